@@ -1,0 +1,142 @@
+/*
+ * sphops_hip.h — C ABI of the MI355X (gfx950) sphops library, libsphops_hip.so.
+ *
+ * This replaces the reference's nanobind module `sph_cuda`
+ * (TheDevilWillBeBee/NPA, sphops/sph_cuda.cu:3380-3441): the eight HashGrid
+ * classes become one opaque handle created with (dim, boundary, mode), and every
+ * method becomes a function taking raw device pointers.  Shapes are fixed by the
+ * handle (B clouds of N particles, G cells per cloud) plus an explicit
+ * feature_dim where the reference read it from an array shape.
+ *
+ * Conventions
+ *  - All pointers are device pointers to contiguous row-major fp32 / int32
+ *    buffers allocated by the caller (the library never allocates user
+ *    tensors; sphops/sph.py allocates every output with torch.empty*).
+ *  - Positions are float2 per particle in 2D and float4 (x, y, z, unused w) in
+ *    3D, as in the reference (positions shape (B, N, 2) or (B, N, 4)).
+ *  - `stream` is a hipStream_t; work is enqueued on it and the call returns
+ *    without synchronising.
+ *  - Return value 0 means success; nonzero means failure, with a message in
+ *    sphops_last_error() (thread-local).  Shape checking is the caller's job
+ *    (the reference's validate_array_shape, sphops/utils.cuh:526-566, lives in
+ *    the Python layer).
+ *  - Results are deterministic: no floating-point atomics are used.
+ */
+#ifndef SPHOPS_HIP_H
+#define SPHOPS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPHOPS_ABI_VERSION 1
+
+#define SPHOPS_CLAMPED 0
+#define SPHOPS_PERIODIC 1
+#define SPHOPS_MODE_GRID 0     /* row-major cell hash  (reference "grid" mode)     */
+#define SPHOPS_MODE_PARTICLE 1 /* Morton cell hash     (reference "particle" mode) */
+
+typedef struct sphops_grid sphops_grid;
+
+/* ABI version of the loaded library (SPHOPS_ABI_VERSION). */
+int sphops_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* sphops_last_error(void);
+
+/* HashGrid{2D,3D}{Periodic,Box} / VHashGrid... constructors
+ * (sphops/sph_cuda.cu:3049-3093 classes, HashGrid::_init sph_cuda.cu:1836-1899;
+ * Python entry sphops/sph.py:48-78).  grid_size has `dim` entries. */
+int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size, float eps,
+                       uint32_t particle_count, uint32_t batch_size, uint32_t max_particles_per_block,
+                       sphops_grid** out);
+void sphops_grid_destroy(sphops_grid* grid);
+
+/* Read-only properties (sph_cuda.cu:3229-3237 `max_blocks`, and the kernel
+ * coefficients HashGrid::_init derives, sph_cuda.cu:1862-1878). */
+int64_t sphops_grid_max_blocks(const sphops_grid* grid);
+int sphops_grid_coefficients(const sphops_grid* grid, float* poly6, float* spiky);
+
+/* HashGrid::initialize (sph_cuda.cu:1926-1992): cell keys, stable sort,
+ * permutation (B,N), bin_offsets (B*G+1, global values), block_info
+ * (max_blocks,4; grid mode only, ignored in particle mode).  total_blocks
+ * (one int32, may be NULL) receives the number of block_info rows in use, kept
+ * per snapshot instead of inside the grid. */
+int sphops_initialize(sphops_grid* grid, const float* positions, int32_t* permutation, int32_t* bin_offsets,
+                      int32_t* block_info, int32_t* total_blocks, void* stream);
+
+/* HashGrid::bin_particles (sph_cuda.cu:1994-2024): out[b, perm[b,i]] = in[b,i]. */
+int sphops_bin_particles(const sphops_grid* grid, const float* in_pos, const float* in_state,
+                         const float* in_mass, const int32_t* permutation, float* out_pos, float* out_state,
+                         float* out_mass, uint32_t feature_dim, void* stream);
+
+/* HashGrid::backward_bin_particles (sph_cuda.cu:2026-2056): out[b,i] = in[b, perm[b,i]]
+ * (also the reference's unbin_particles, sphops/sph.py:187-198). */
+int sphops_backward_bin_particles(const sphops_grid* grid, const float* grad_out_pos,
+                                  const float* grad_out_state, const float* grad_out_mass,
+                                  const int32_t* permutation, float* grad_in_pos, float* grad_in_state,
+                                  float* grad_in_mass, uint32_t feature_dim, void* stream);
+
+/* Forward operators on binned particles (sph_cuda.cu:2058-2499).  `block_info`
+ * is accepted for interface parity and may be NULL: neighbour ranges are read
+ * from bin_offsets alone. */
+int sphops_count_forward(const sphops_grid* grid, const float* x, float* count, const int32_t* bin_offsets,
+                         const int32_t* block_info, void* stream);
+int sphops_density_forward(const sphops_grid* grid, const float* x, const float* mass, float* rho,
+                           const int32_t* bin_offsets, const int32_t* block_info, void* stream);
+int sphops_blur_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                        const float* state_in, float* state_out, uint32_t feature_dim, const int32_t* bin_offsets,
+                        const int32_t* block_info, void* stream);
+int sphops_gradient_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                            const float* state_in, float* state_gradient_out, uint32_t feature_dim,
+                            const int32_t* bin_offsets, const int32_t* block_info, void* stream);
+int sphops_density_gradient_forward(const sphops_grid* grid, const float* x, const float* mass,
+                                    float* density_gradient_out, const int32_t* bin_offsets,
+                                    const int32_t* block_info, void* stream);
+int sphops_moment_matrix_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                                 float* moment_matrix_out, const int32_t* bin_offsets, const int32_t* block_info,
+                                 void* stream);
+
+/* gradient_hybrid forward value raw @ safe_inv(M, tol) in one pass.  No native
+ * counterpart in the reference: it replaces the Python composite
+ * moment_matrix -> safe_inv_sym_mat -> gradient -> matmul (sphops/sph.py:474-484);
+ * its backward is sphops_gradient_backward (straight-through). */
+int sphops_gradient_hybrid_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                                   const float* state_in, float* out, uint32_t feature_dim, float tol,
+                                   const int32_t* bin_offsets, const int32_t* block_info, void* stream);
+
+/* Backward operators (sph_cuda.cu:2501-3046).  The flags say which gradients
+ * the caller needs, as the reference's dLdx/dLds/dLdrho arguments: all false is
+ * a no-op; dLds alone selects the dL/ds-only kernel; anything else computes and
+ * writes every gradient buffer of the operator. */
+int sphops_density_backward(const sphops_grid* grid, const float* x, const float* mass, const float* dL_rho,
+                            float* grad_x, const int32_t* bin_offsets, const int32_t* block_info, int dLdx,
+                            void* stream);
+int sphops_blur_backward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                         const float* state_in, const float* dL_blur, float* grad_x, float* grad_s,
+                         float* grad_rho, uint32_t feature_dim, const int32_t* bin_offsets,
+                         const int32_t* block_info, int dLdx, int dLds, int dLdrho, void* stream);
+int sphops_density_gradient_backward(const sphops_grid* grid, const float* x, const float* mass,
+                                     const float* dL_density_gradient, float* grad_x, const int32_t* bin_offsets,
+                                     const int32_t* block_info, int dLdx, void* stream);
+int sphops_gradient_backward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                             const float* state_in, const float* dL_gradient, float* grad_x, float* grad_s,
+                             float* grad_rho, uint32_t feature_dim, const int32_t* bin_offsets,
+                             const int32_t* block_info, int dLdx, int dLds, int dLdrho, void* stream);
+int sphops_moment_matrix_backward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                                  const float* dL_moment_matrix, float* grad_x, float* grad_rho,
+                                  const int32_t* bin_offsets, const int32_t* block_info, int dLdx, int dLdrho,
+                                  void* stream);
+
+/* Module function safe_inv_sym_mat (sph_cuda.cu:3181-3226): `count` symmetric
+ * dim x dim matrices (dim 2 or 3), identity where |det| < tol. */
+int sphops_safe_inv_sym_mat(const float* in_matrix, float* out_matrix, int64_t count, int dim, float tol,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPHOPS_HIP_H */

@@ -1,0 +1,512 @@
+// Spatial-hash binning for gfx950: cell keys, a stable LSD radix sort with a
+// device-wide scan, bin_offsets from sorted run heads, the grid-mode block
+// table, the permutation, and the bin/unbin row moves.
+//
+// Replaces the reference's atomic counting sort (sphops/sph_cuda.cu:32-206,
+// 1926-2056).  Results are deterministic: within a cell particles keep their
+// input order, which is one of the orders the reference's atomic race can
+// produce.  No dense per-cell counter array is touched: bin_offsets is
+// written once per cell straight from the sorted keys.
+#include "sphops_internal.hpp"
+
+namespace sphops {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kItems = 16;
+constexpr int kTile = kThreads * kItems;  // 4096 keys per radix / scan tile
+constexpr int kRadixBits = 8;
+constexpr int kBins = 1 << kRadixBits;
+constexpr int kChunkLog2 = 10;            // cells per bin_offsets workgroup
+constexpr int kChunk = 1 << kChunkLog2;
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = __lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// ------------------------------------------------------------------ keys
+
+template <int D, bool PERIODIC>
+__global__ __launch_bounds__(kThreads) void k_cell_keys(GridParams g, const float* __restrict__ pos,
+                                                        uint32_t* __restrict__ keys,
+                                                        uint32_t* __restrict__ vals, uint32_t n) {
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= n) return;
+  float x[3];
+  load_pos<D>(pos, k, x);
+  int c[3];
+  pos2cell<D, PERIODIC>(g, x, c);
+  const uint32_t b = k / g.N;
+  keys[k] = b * g.G + cell_hash<D>(g, c);
+  vals[k] = k;
+}
+
+// ------------------------------------------------------- device-wide scan
+
+// Exclusive scan of the 4096 values owned by one workgroup (16 consecutive
+// values per thread).  Returns the workgroup total; `vals` are replaced by
+// their exclusive prefix.
+__device__ uint32_t block_exclusive_scan(uint32_t (&v)[kItems], uint32_t* sm /*[kThreads/64]*/) {
+  uint32_t run = 0;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    uint32_t t = v[i];
+    v[i] = run;
+    run += t;
+  }
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  uint32_t incl = run;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    uint32_t y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) sm[wave] = incl;
+  __syncthreads();
+  uint32_t wave_base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) {
+    uint32_t s = sm[w];
+    if (w < wave) wave_base += s;
+    total += s;
+  }
+  __syncthreads();
+  const uint32_t base = wave_base + incl - run;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) v[i] += base;
+  return total;
+}
+
+__global__ __launch_bounds__(kThreads) void k_scan_reduce(const uint32_t* __restrict__ in, uint64_t n,
+                                                          uint32_t* __restrict__ partials) {
+  __shared__ uint32_t sm[kThreads / 64];
+  const uint64_t base = (uint64_t)blockIdx.x * kTile + (uint64_t)threadIdx.x * kItems;
+  uint32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i)
+    if (base + i < n) s += in[base + i];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+  if (lane == 0) sm[wave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+    for (int w = 0; w < kThreads / 64; ++w) t += sm[w];
+    partials[blockIdx.x] = t;
+  }
+}
+
+// Scan one tile in place-or-out, adding partials[tile] (if given).  When
+// `total_out` is non-null the grand total is stored there by the last tile.
+__global__ __launch_bounds__(kThreads) void k_scan_apply(const uint32_t* in, uint32_t* out, uint64_t n,
+                                                         const uint32_t* __restrict__ partials,
+                                                         uint32_t* total_out) {
+  __shared__ uint32_t sm[kThreads / 64];
+  const uint64_t base = (uint64_t)blockIdx.x * kTile + (uint64_t)threadIdx.x * kItems;
+  uint32_t v[kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) v[i] = (base + i < n) ? in[base + i] : 0u;
+  const uint32_t tot = block_exclusive_scan(v, sm);
+  const uint32_t off = partials ? partials[blockIdx.x] : 0u;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i)
+    if (base + i < n) out[base + i] = v[i] + off;
+  if (total_out && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *total_out = off + tot;
+}
+
+}  // namespace
+
+uint64_t scan_tmp_elems(uint64_t n) {
+  // partial sums for every recursion level, each padded to a tile
+  uint64_t total = 0;
+  while (n > (uint64_t)kTile) {
+    n = (n + kTile - 1) / kTile;
+    total += n + kTile;
+  }
+  return total + 1;
+}
+
+namespace {
+
+// out[i] = sum_{j<i} in[j]; optionally *total = sum of all.  `tmp` holds
+// scan_tmp_elems(n) words.  `in` may equal `out`.
+void device_exclusive_scan(const uint32_t* in, uint32_t* out, uint64_t n, uint32_t* tmp, uint32_t* total,
+                           hipStream_t st) {
+  if (n == 0) return;
+  const uint64_t tiles = (n + kTile - 1) / kTile;
+  if (tiles == 1) {
+    hipLaunchKernelGGL(k_scan_apply, dim3(1), dim3(kThreads), 0, st, in, out, n, nullptr, total);
+    SPHOPS_LAUNCHED();
+    return;
+  }
+  uint32_t* partials = tmp;
+  hipLaunchKernelGGL(k_scan_reduce, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, n, partials);
+  SPHOPS_LAUNCHED();
+  device_exclusive_scan(partials, partials, tiles, tmp + tiles + kTile, nullptr, st);
+  hipLaunchKernelGGL(k_scan_apply, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n, partials, total);
+  SPHOPS_LAUNCHED();
+}
+
+// ------------------------------------------------------------ radix sort
+
+__global__ __launch_bounds__(kThreads) void k_radix_hist(const uint32_t* __restrict__ keys, uint32_t n, int shift,
+                                                         uint32_t* __restrict__ hist, uint32_t ntiles) {
+  __shared__ uint32_t h[kBins];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const uint32_t base = blockIdx.x * kTile;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const uint32_t idx = base + i * kThreads + threadIdx.x;
+    if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & (kBins - 1)], 1u);
+  }
+  __syncthreads();
+  hist[threadIdx.x * ntiles + blockIdx.x] = h[threadIdx.x];
+}
+
+// Stable scatter of one radix digit.  Wave w of the tile owns keys
+// [w*1024, (w+1)*1024) and walks them 64 at a time in index order; lanes with
+// equal digits find each other with 8 ballots, so each key's rank among the
+// equal-digit keys before it is exact and no atomics are involved.
+__global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint32_t* __restrict__ kin,
+                                                            const uint32_t* __restrict__ vin,
+                                                            uint32_t* __restrict__ kout,
+                                                            uint32_t* __restrict__ vout, uint32_t n, int shift,
+                                                            const uint32_t* __restrict__ hist_scan,
+                                                            uint32_t ntiles) {
+  __shared__ uint32_t wcnt[kThreads / 64][kBins];
+  __shared__ uint32_t gbase[kBins];
+  const int wave = threadIdx.x >> 6, lane = __lane_id();
+  for (int i = threadIdx.x; i < (kThreads / 64) * kBins; i += kThreads) (&wcnt[0][0])[i] = 0;
+  gbase[threadIdx.x] = hist_scan[threadIdx.x * ntiles + blockIdx.x];
+  __syncthreads();
+
+  const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
+  const uint64_t below_mask = lanemask_lt();
+  uint32_t key[kItems], val[kItems], rank[kItems];
+#pragma unroll
+  for (int t = 0; t < kItems; ++t) {
+    const uint32_t idx = base + t * 64 + lane;
+    const bool valid = idx < n;
+    key[t] = valid ? kin[idx] : 0u;
+    val[t] = valid ? vin[idx] : 0u;
+    const uint32_t digit = (key[t] >> shift) & (kBins - 1);
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kRadixBits; ++b) {
+      const bool bit = (digit >> b) & 1u;
+      const uint64_t bb = __ballot(bit);
+      peers &= bit ? bb : ~bb;
+    }
+    const uint32_t before = (uint32_t)__popcll(peers & below_mask);
+    const uint32_t prior = wcnt[wave][digit];
+    if (valid && before == 0) wcnt[wave][digit] = prior + (uint32_t)__popcll(peers);
+    rank[t] = prior + before;
+  }
+  __syncthreads();
+  {
+    // exclusive prefix of the per-wave counts, digit by digit
+    const int d = threadIdx.x;
+    uint32_t run = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+      const uint32_t c = wcnt[w][d];
+      wcnt[w][d] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < kItems; ++t) {
+    const uint32_t idx = base + t * 64 + lane;
+    if (idx < n) {
+      const uint32_t digit = (key[t] >> shift) & (kBins - 1);
+      const uint32_t dst = gbase[digit] + wcnt[wave][digit] + rank[t];
+      kout[dst] = key[t];
+      vout[dst] = val[t];
+    }
+  }
+}
+
+// ------------------------------------------------------- bin_offsets
+
+__global__ __launch_bounds__(kThreads) void k_fill_u32(uint32_t* __restrict__ p, uint64_t n, uint32_t v) {
+  const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// First and one-past-last sorted position of every non-empty cell chunk.
+__global__ __launch_bounds__(kThreads) void k_chunk_marks(const uint32_t* __restrict__ keys, uint32_t n,
+                                                          uint32_t* __restrict__ cfirst,
+                                                          uint32_t* __restrict__ cend) {
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= n) return;
+  const uint32_t ch = keys[k] >> kChunkLog2;
+  if (k == 0 || (keys[k - 1] >> kChunkLog2) != ch) cfirst[ch] = k;
+  if (k == n - 1 || (keys[k + 1] >> kChunkLog2) != ch) cend[ch] = k + 1;
+}
+
+__global__ __launch_bounds__(kThreads) void k_chunk_counts(const uint32_t* __restrict__ cfirst,
+                                                           const uint32_t* __restrict__ cend,
+                                                           uint32_t* __restrict__ cnt, uint32_t nch) {
+  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < nch) cnt[i] = cend[i] - cfirst[i];
+}
+
+// bin_offsets[c] = number of sorted keys < c, for the 1024 cells of one chunk.
+// Run heads inside the chunk mark their cell; empty cells take the next run
+// head (suffix minimum), the chunk end being the sentinel.
+__global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint32_t* __restrict__ keys,
+                                                          const uint32_t* __restrict__ chunk_lo,
+                                                          int32_t* __restrict__ bo, uint64_t ncells_p1) {
+  __shared__ uint32_t first[kChunk];
+  __shared__ uint32_t wmin[kThreads / 64];
+  const uint32_t ch = blockIdx.x;
+  const uint32_t lo = chunk_lo[ch], hi = chunk_lo[ch + 1];
+  const uint64_t c0 = (uint64_t)ch << kChunkLog2;
+  const int t = threadIdx.x;
+  uint32_t s[4];
+  if (lo == hi) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s[q] = lo;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) first[t * 4 + q] = hi;
+    __syncthreads();
+    for (uint32_t p = lo + t; p < hi; p += kThreads) {
+      const uint32_t key = keys[p];
+      if (p == lo || keys[p - 1] != key) first[key - (uint32_t)c0] = p;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s[q] = first[t * 4 + q];
+    s[2] = min(s[2], s[3]);
+    s[1] = min(s[1], s[2]);
+    s[0] = min(s[0], s[1]);
+    // exclusive suffix minimum over threads
+    const int lane = __lane_id(), wave = t >> 6;
+    uint32_t incl = s[0];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = __shfl_down(incl, off, 64);
+      if (lane + off < 64) incl = min(incl, y);
+    }
+    if (lane == 0) wmin[wave] = incl;
+    __syncthreads();
+    uint32_t after = hi;
+    for (int w = wave + 1; w < kThreads / 64; ++w) after = min(after, wmin[w]);
+    uint32_t nxt = __shfl_down(incl, 1, 64);
+    if (lane == 63) nxt = hi;
+    after = min(after, nxt);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s[q] = min(s[q], after);
+  }
+  const uint64_t c = c0 + (uint64_t)t * 4;
+  if (c + 3 < ncells_p1) {
+    *reinterpret_cast<int4*>(bo + c) = make_int4((int)s[0], (int)s[1], (int)s[2], (int)s[3]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (c + q < ncells_p1) bo[c + q] = (int)s[q];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void k_permutation(const uint32_t* __restrict__ vals, uint32_t n,
+                                                          uint32_t N, int32_t* __restrict__ perm) {
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= n) return;
+  const uint32_t src = vals[k];
+  perm[src] = (int32_t)(k - (src / N) * N);
+}
+
+// --------------------------------------------------------- block table
+
+__global__ __launch_bounds__(kThreads) void k_block_flags(const uint32_t* __restrict__ keys, uint32_t n,
+                                                          const int32_t* __restrict__ bo, uint32_t maxp,
+                                                          uint32_t* __restrict__ flags) {
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= n) return;
+  const uint32_t rs = (uint32_t)bo[keys[k]];
+  flags[k] = ((k - rs) % maxp == 0) ? 1u : 0u;
+}
+
+// rows {global_cell, offset_in_cell, count, batch} (sphops/utils.cuh:295-301)
+__global__ __launch_bounds__(kThreads) void k_block_rows(const uint32_t* __restrict__ keys, uint32_t n,
+                                                         const int32_t* __restrict__ bo,
+                                                         const uint32_t* __restrict__ rowidx, uint32_t maxp,
+                                                         uint32_t G, int4* __restrict__ info) {
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= n) return;
+  const uint32_t key = keys[k];
+  const uint32_t rs = (uint32_t)bo[key];
+  const uint32_t off = k - rs;
+  if (off % maxp != 0) return;
+  const uint32_t cnt = (uint32_t)bo[key + 1] - rs;
+  info[rowidx[k]] = make_int4((int)key, (int)off, (int)min(maxp, cnt - off), (int)(key / G));
+}
+
+__global__ __launch_bounds__(kThreads) void k_block_tail(const uint32_t* __restrict__ total, uint64_t max_blocks,
+                                                         int4* __restrict__ info, int32_t* __restrict__ total_out) {
+  const uint64_t r = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t t = *total;
+  if (r == 0 && total_out) *total_out = (int32_t)t;
+  if (r < max_blocks && r >= t) info[r] = make_int4(0, 0, 0, 0);
+}
+
+// ----------------------------------------------------------- bin / unbin
+
+// One group of `lanes` threads moves one particle row.  forward: scatter
+// in[b,i] -> out[b,perm[b,i]];  backward: gather out[b,i] = in[b,perm[b,i]].
+template <int P, bool VEC4>
+__global__ __launch_bounds__(kThreads) void k_move_rows(const float* __restrict__ in_pos,
+                                                        const float* __restrict__ in_state,
+                                                        const float* __restrict__ in_mass,
+                                                        const int32_t* __restrict__ perm, float* __restrict__ out_pos,
+                                                        float* __restrict__ out_state, float* __restrict__ out_mass,
+                                                        uint32_t n, uint32_t N, uint32_t C, int lanes_log2,
+                                                        int forward) {
+  const uint64_t gid = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  const uint64_t k = gid >> lanes_log2;
+  const uint32_t q = (uint32_t)(gid & ((1u << lanes_log2) - 1));
+  if (k >= n) return;
+  const uint64_t b = k / N;
+  const uint64_t slot = b * N + (uint32_t)perm[k];
+  const uint64_t src = forward ? k : slot;
+  const uint64_t dst = forward ? slot : k;
+  if (q == 0) {
+    if constexpr (P == 2)
+      reinterpret_cast<float2*>(out_pos)[dst] = reinterpret_cast<const float2*>(in_pos)[src];
+    else
+      reinterpret_cast<float4*>(out_pos)[dst] = reinterpret_cast<const float4*>(in_pos)[src];
+    out_mass[dst] = in_mass[src];
+  }
+  const uint32_t lanes = 1u << lanes_log2;
+  if constexpr (VEC4) {
+    const uint32_t U = C >> 2;
+    const float4* s4 = reinterpret_cast<const float4*>(in_state) + src * U;
+    float4* d4 = reinterpret_cast<float4*>(out_state) + dst * U;
+    for (uint32_t u = q; u < U; u += lanes) d4[u] = s4[u];
+  } else {
+    const float* s1 = in_state + src * C;
+    float* d1 = out_state + dst * C;
+    for (uint32_t u = q; u < C; u += lanes) d1[u] = s1[u];
+  }
+}
+
+template <int D>
+void launch_keys(const Grid& g, const float* pos, uint32_t n, hipStream_t st) {
+  const dim3 grid((n + kThreads - 1) / kThreads);
+  if (g.periodic)
+    hipLaunchKernelGGL((k_cell_keys<D, true>), grid, dim3(kThreads), 0, st, g.p, pos, g.keys[0], g.vals[0], n);
+  else
+    hipLaunchKernelGGL((k_cell_keys<D, false>), grid, dim3(kThreads), 0, st, g.p, pos, g.keys[0], g.vals[0], n);
+  SPHOPS_LAUNCHED();
+}
+
+inline dim3 blocks_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) / kThreads)); }
+
+}  // namespace
+
+void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int32_t* block_info,
+                     int32_t* total_blocks, hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  const uint64_t ncp1 = g.n_cells + 1;
+  if (n == 0) {
+    hipLaunchKernelGGL(k_fill_u32, blocks_for(ncp1), dim3(kThreads), 0, st, reinterpret_cast<uint32_t*>(bo),
+                       ncp1, 0u);
+    SPHOPS_LAUNCHED();
+    if (!g.particle_mode) {
+      hipLaunchKernelGGL(k_fill_u32, blocks_for(g.max_blocks * 4 + 1), dim3(kThreads), 0, st,
+                         reinterpret_cast<uint32_t*>(block_info), g.max_blocks * 4, 0u);
+      SPHOPS_LAUNCHED();
+    }
+    if (total_blocks) SPHOPS_HIP(hipMemsetAsync(total_blocks, 0, sizeof(int32_t), st));
+    return;
+  }
+  // 1. keys
+  if (g.dim == 2) launch_keys<2>(g, pos, n, st);
+  else launch_keys<3>(g, pos, n, st);
+
+  // 2. stable LSD radix sort of (key, index)
+  int bits = 1;
+  while (bits < 32 && (g.n_cells - 1) >> bits) ++bits;
+  const int passes = (bits + kRadixBits - 1) / kRadixBits;
+  const uint32_t ntiles = (uint32_t)g.n_tiles;
+  int cur = 0;
+  for (int p = 0; p < passes; ++p) {
+    const int shift = p * kRadixBits;
+    hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kThreads), 0, st, g.keys[cur], n, shift, g.hist, ntiles);
+    SPHOPS_LAUNCHED();
+    device_exclusive_scan(g.hist, g.hist, (uint64_t)kBins * ntiles, g.scan_tmp, nullptr, st);
+    hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kThreads), 0, st, g.keys[cur], g.vals[cur],
+                       g.keys[cur ^ 1], g.vals[cur ^ 1], n, shift, g.hist, ntiles);
+    SPHOPS_LAUNCHED();
+    cur ^= 1;
+  }
+  const uint32_t* skeys = g.keys[cur];
+  const uint32_t* svals = g.vals[cur];
+
+  // 3. bin_offsets via per-chunk key ranges
+  const uint32_t nch = (uint32_t)g.n_chunks;
+  hipLaunchKernelGGL(k_fill_u32, blocks_for(nch), dim3(kThreads), 0, st, g.chunk_first, (uint64_t)nch, 0u);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL(k_fill_u32, blocks_for(nch), dim3(kThreads), 0, st, g.chunk_end, (uint64_t)nch, 0u);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL(k_chunk_marks, blocks_for(n), dim3(kThreads), 0, st, skeys, n, g.chunk_first, g.chunk_end);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL(k_chunk_counts, blocks_for(nch), dim3(kThreads), 0, st, g.chunk_first, g.chunk_end,
+                     g.chunk_lo, nch);
+  SPHOPS_LAUNCHED();
+  device_exclusive_scan(g.chunk_lo, g.chunk_lo, nch, g.scan_tmp, g.chunk_lo + nch, st);
+  hipLaunchKernelGGL(k_bin_offsets, dim3(nch), dim3(kThreads), 0, st, skeys, g.chunk_lo, bo, ncp1);
+  SPHOPS_LAUNCHED();
+
+  // 4. permutation (destination slot of each input particle)
+  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, svals, n, g.p.N, perm);
+  SPHOPS_LAUNCHED();
+
+  // 5. block table (grid mode)
+  if (!g.particle_mode) {
+    hipLaunchKernelGGL(k_block_flags, blocks_for(n), dim3(kThreads), 0, st, skeys, n, bo, g.p.maxp, g.flags);
+    SPHOPS_LAUNCHED();
+    device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, g.flags + n, st);
+    hipLaunchKernelGGL(k_block_rows, blocks_for(n), dim3(kThreads), 0, st, skeys, n, bo, g.flags, g.p.maxp,
+                       g.p.G, reinterpret_cast<int4*>(block_info));
+    SPHOPS_LAUNCHED();
+    hipLaunchKernelGGL(k_block_tail, blocks_for(g.max_blocks), dim3(kThreads), 0, st, g.flags + n, g.max_blocks,
+                       reinterpret_cast<int4*>(block_info), total_blocks);
+    SPHOPS_LAUNCHED();
+  } else if (total_blocks) {
+    SPHOPS_HIP(hipMemsetAsync(total_blocks, 0, sizeof(int32_t), st));
+  }
+}
+
+void run_bin_particles(const Grid& g, const float* in_pos, const float* in_state, const float* in_mass,
+                       const int32_t* perm, float* out_pos, float* out_state, float* out_mass, uint32_t C,
+                       bool forward, hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  if (n == 0) return;
+  const bool vec4 = (C % 4 == 0) && (reinterpret_cast<uintptr_t>(in_state) % 16 == 0) &&
+                    (reinterpret_cast<uintptr_t>(out_state) % 16 == 0);
+  const uint32_t units = vec4 ? C / 4 : C;
+  int lanes_log2 = 0;
+  while ((1u << lanes_log2) < units && lanes_log2 < 4) ++lanes_log2;
+  const uint64_t threads = (uint64_t)n << lanes_log2;
+  const dim3 grid = blocks_for(threads);
+  const int fw = forward ? 1 : 0;
+#define SPHOPS_MOVE(P, V)                                                                                 \
+  hipLaunchKernelGGL((k_move_rows<P, V>), grid, dim3(kThreads), 0, st, in_pos, in_state, in_mass, perm, \
+                     out_pos, out_state, out_mass, n, g.p.N, C, lanes_log2, fw)
+  if (g.dim == 2) {
+    if (vec4) SPHOPS_MOVE(2, true); else SPHOPS_MOVE(2, false);
+  } else {
+    if (vec4) SPHOPS_MOVE(4, true); else SPHOPS_MOVE(4, false);
+  }
+#undef SPHOPS_MOVE
+  SPHOPS_LAUNCHED();
+}
+
+}  // namespace sphops

@@ -1,0 +1,481 @@
+// extern "C" entry points of libsphops_hip.so (declared in include/sphops_hip.h).
+#include <cmath>
+#include <string>
+
+#include "../../include/sphops_hip.h"
+#include "perception_kernels.hpp"
+
+namespace sphops {
+
+void run_forward_2d(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, hipStream_t st);
+void run_forward_3d(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, hipStream_t st);
+void run_backward_2d(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a, hipStream_t st);
+void run_backward_3d(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a, hipStream_t st);
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return 0;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+  } catch (...) {
+    g_last_error = "unknown error";
+  }
+  return -1;
+}
+
+void require(bool ok, const std::string& msg) {
+  if (!ok) throw Error(msg);
+}
+
+template <class T>
+T* dalloc(uint64_t n) {
+  void* p = nullptr;
+  SPHOPS_HIP(hipMalloc(&p, sizeof(T) * (n ? n : 1)));
+  return static_cast<T*>(p);
+}
+
+uint32_t spread_host(uint32_t v, int dim) {
+  uint32_t out = 0;
+  for (int b = 0; b < 10; ++b) out |= ((v >> b) & 1u) << (b * dim);
+  return out;
+}
+
+void free_grid(Grid* g) {
+  if (!g) return;
+  for (int i = 0; i < 2; ++i) {
+    (void)hipFree(g->keys[i]);
+    (void)hipFree(g->vals[i]);
+  }
+  (void)hipFree(g->hist);
+  (void)hipFree(g->scan_tmp);
+  (void)hipFree(g->chunk_first);
+  (void)hipFree(g->chunk_end);
+  (void)hipFree(g->chunk_lo);
+  (void)hipFree(g->flags);
+  delete g;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+void check_channels(uint32_t C) {
+  require(C >= 1 && C <= kMaxChannels,
+          "feature_dim must be in [1, " + std::to_string(kMaxChannels) + "], got " + std::to_string(C));
+}
+
+void forward(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+  if (g.dim == 2) run_forward_2d(g, op, bo, a, st);
+  else run_forward_3d(g, op, bo, a, st);
+}
+
+void backward(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+  if (g.dim == 2) run_backward_2d(g, op, full, bo, a, st);
+  else run_backward_3d(g, op, full, bo, a, st);
+}
+
+__global__ __launch_bounds__(256) void k_safe_inv2(const float4* __restrict__ in, float4* __restrict__ out,
+                                                   uint64_t count, float tol) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const float4 m = in[i];
+  float M[4] = {m.x, m.y, m.z, m.w}, L[4];
+  pk::safe_inv_sym<2>(M, tol, L);
+  out[i] = make_float4(L[0], L[1], L[2], L[3]);
+}
+
+__global__ __launch_bounds__(256) void k_safe_inv3(const float* __restrict__ in, float* __restrict__ out,
+                                                   uint64_t count, float tol) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  float M[9], L[9];
+#pragma unroll
+  for (int q = 0; q < 9; ++q) M[q] = in[i * 9 + q];
+  pk::safe_inv_sym<3>(M, tol, L);
+#pragma unroll
+  for (int q = 0; q < 9; ++q) out[i * 9 + q] = L[q];
+}
+
+}  // namespace
+
+void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st) {
+  if (count == 0) return;
+  const dim3 grid((uint32_t)((count + 255) / 256));
+  if (dim == 2) {
+    require(pk::aligned16(in) && pk::aligned16(out), "safe_inv_sym_mat: 2x2 matrices must be 16-byte aligned");
+    hipLaunchKernelGGL(k_safe_inv2, grid, dim3(256), 0, st, reinterpret_cast<const float4*>(in),
+                       reinterpret_cast<float4*>(out), count, tol);
+  } else {
+    hipLaunchKernelGGL(k_safe_inv3, grid, dim3(256), 0, st, in, out, count, tol);
+  }
+  SPHOPS_LAUNCHED();
+}
+
+}  // namespace sphops
+
+using sphops::Grid;
+using sphops::Op;
+using sphops::OpPtrs;
+using sphops::guarded;
+using sphops::require;
+using sphops::spread_host;
+using sphops::dalloc;
+
+struct sphops_grid : Grid {};
+
+extern "C" {
+
+int sphops_abi_version(void) { return SPHOPS_ABI_VERSION; }
+
+const char* sphops_last_error(void) { return sphops::g_last_error.c_str(); }
+
+int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size, float eps, uint32_t particle_count,
+                       uint32_t batch_size, uint32_t max_particles_per_block, sphops_grid** out) {
+  return guarded([&] {
+    require(out != nullptr, "out must not be NULL");
+    *out = nullptr;
+    require(dim == 2 || dim == 3, "dim must be 2 or 3");
+    require(boundary == SPHOPS_CLAMPED || boundary == SPHOPS_PERIODIC, "boundary must be clamped or periodic");
+    require(mode == SPHOPS_MODE_GRID || mode == SPHOPS_MODE_PARTICLE, "mode must be grid or particle");
+    require(grid_size != nullptr, "grid_size must not be NULL");
+    require(std::isfinite(eps) && eps > 0.0f, "eps must be a positive finite number");
+    require(max_particles_per_block >= 1, "max_particles_per_block must be >= 1");
+    uint64_t G = 1;
+    for (int d = 0; d < dim; ++d) {
+      require(grid_size[d] >= 1, "grid sizes must be >= 1");
+      if (boundary == SPHOPS_PERIODIC)
+        require(grid_size[d] >= 3, "periodic grids need at least 3 cells per axis (fewer double-count neighbours)");
+      G *= (uint64_t)grid_size[d];
+    }
+    const uint64_t BG = G * batch_size, BN = (uint64_t)particle_count * batch_size;
+    require(BG + 1 < (1ull << 32), "batch_size * cell_count must be below 2^32 - 1");
+    require(BN < (1ull << 31), "batch_size * particle_count must be below 2^31");
+    if (mode == SPHOPS_MODE_PARTICLE) {
+      uint32_t hmax = 0;
+      for (int d = 0; d < dim; ++d) {
+        const int gsz = grid_size[d];
+        require((gsz & (gsz - 1)) == 0, "particle mode needs power-of-two grid sizes");
+        require(gsz <= 1024, "particle mode supports at most 1024 cells per axis");
+        hmax |= spread_host((uint32_t)gsz - 1, dim) << d;
+      }
+      require(hmax < G, "particle mode: the Morton hash of this grid shape exceeds the cell count "
+                        "(use equal sizes, or sizes non-increasing along x, y, z)");
+    }
+    auto* g = new sphops_grid();
+    try {
+      SPHOPS_HIP(hipGetDevice(&g->device));
+      g->dim = dim;
+      g->periodic = boundary == SPHOPS_PERIODIC;
+      g->particle_mode = mode == SPHOPS_MODE_PARTICLE;
+      auto& p = g->p;
+      for (int d = 0; d < 3; ++d) {
+        p.gs[d] = d < dim ? grid_size[d] : 1;
+        p.half_gs[d] = p.gs[d] / 2;
+      }
+      p.eps = eps;
+      p.inv_eps = 1.0f / eps;
+      p.eps2 = eps * eps;
+      for (int d = 0; d < 3; ++d) {
+        p.L[d] = static_cast<float>(p.gs[d]) * eps;
+        p.half_L[d] = 0.5f * p.L[d];
+      }
+      // coefficients exactly as HashGrid::_init derives them (fp32 powers of
+      // 1/eps, double constant, rounded to fp32)
+      const float ie = p.inv_eps, ie2 = ie * ie, ie4 = ie2 * ie2;
+      if (dim == 2) {
+        const float ie5 = ie4 * ie, ie8 = ie4 * ie4;
+        p.c6 = (float)(4.0 / M_PI * (double)ie8);
+        p.cs = (float)(10.0 / M_PI * (double)ie5);
+      } else {
+        const float ie6 = ie4 * ie2, ie9 = ie4 * ie4 * ie;
+        p.c6 = (float)((315.0 / (64.0 * M_PI)) * (double)ie9);
+        p.cs = (float)((15.0 / M_PI) * (double)ie6);
+      }
+      p.N = particle_count;
+      p.B = batch_size;
+      p.G = (uint32_t)G;
+      p.maxp = max_particles_per_block;
+      p.morton = g->particle_mode ? 1 : 0;
+      if (!g->particle_mode) {
+        const uint64_t per = std::min<uint64_t>(particle_count,
+                                                G + (particle_count + max_particles_per_block - 1) /
+                                                        max_particles_per_block);
+        g->max_blocks = per * batch_size;
+      } else {
+        g->max_blocks = 1;
+      }
+      g->n_keys = BN;
+      g->n_cells = BG;
+      g->n_tiles = (BN + 4095) / 4096;
+      g->n_chunks = (BG + 1 + 1023) / 1024;
+      for (int i = 0; i < 2; ++i) {
+        g->keys[i] = dalloc<uint32_t>(BN);
+        g->vals[i] = dalloc<uint32_t>(BN);
+      }
+      g->hist = dalloc<uint32_t>(256 * g->n_tiles);
+      const uint64_t scan_n = std::max<uint64_t>(std::max<uint64_t>(256 * g->n_tiles, BN + 1), g->n_chunks + 1);
+      g->scan_tmp_len = sphops::scan_tmp_elems(scan_n);
+      g->scan_tmp = dalloc<uint32_t>(g->scan_tmp_len);
+      g->chunk_first = dalloc<uint32_t>(g->n_chunks);
+      g->chunk_end = dalloc<uint32_t>(g->n_chunks);
+      g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
+      g->flags = dalloc<uint32_t>(BN + 1);
+    } catch (...) {
+      sphops::free_grid(g);
+      throw;
+    }
+    *out = g;
+  });
+}
+
+void sphops_grid_destroy(sphops_grid* grid) { sphops::free_grid(grid); }
+
+int64_t sphops_grid_max_blocks(const sphops_grid* grid) { return grid ? (int64_t)grid->max_blocks : -1; }
+
+int sphops_grid_coefficients(const sphops_grid* grid, float* poly6, float* spiky) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    if (poly6) *poly6 = grid->p.c6;
+    if (spiky) *spiky = grid->p.cs;
+  });
+}
+
+int sphops_initialize(sphops_grid* grid, const float* positions, int32_t* permutation, int32_t* bin_offsets,
+                      int32_t* block_info, int32_t* total_blocks, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(bin_offsets != nullptr, "bin_offsets must not be NULL");
+    require(grid->n_keys == 0 || (positions && permutation), "positions and permutation must not be NULL");
+    require(grid->particle_mode || block_info != nullptr, "block_info must not be NULL in grid mode");
+    require(sphops::pk::aligned16(bin_offsets), "bin_offsets must be 16-byte aligned");
+    require(grid->particle_mode || sphops::pk::aligned16(block_info), "block_info must be 16-byte aligned");
+    require(grid->dim == 2 || sphops::pk::aligned16(positions), "3D positions must be 16-byte aligned");
+    sphops::run_instantiate(*grid, positions, permutation, bin_offsets, block_info, total_blocks,
+                            sphops::as_stream(stream));
+  });
+}
+
+static int move_rows(const sphops_grid* grid, const float* ip, const float* is, const float* im, const int32_t* perm,
+                     float* op, float* os, float* om, uint32_t C, bool fwd, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    sphops::check_channels(C == 0 ? 1 : C);
+    require(grid->n_keys == 0 || (ip && is && im && perm && op && os && om), "null buffer");
+    sphops::run_bin_particles(*grid, ip, is, im, perm, op, os, om, C, fwd, sphops::as_stream(stream));
+  });
+}
+
+int sphops_bin_particles(const sphops_grid* grid, const float* in_pos, const float* in_state, const float* in_mass,
+                         const int32_t* permutation, float* out_pos, float* out_state, float* out_mass,
+                         uint32_t feature_dim, void* stream) {
+  return move_rows(grid, in_pos, in_state, in_mass, permutation, out_pos, out_state, out_mass, feature_dim, true,
+                   stream);
+}
+
+int sphops_backward_bin_particles(const sphops_grid* grid, const float* grad_out_pos, const float* grad_out_state,
+                                  const float* grad_out_mass, const int32_t* permutation, float* grad_in_pos,
+                                  float* grad_in_state, float* grad_in_mass, uint32_t feature_dim, void* stream) {
+  return move_rows(grid, grad_out_pos, grad_out_state, grad_out_mass, permutation, grad_in_pos, grad_in_state,
+                   grad_in_mass, feature_dim, false, stream);
+}
+
+static int fwd_op(const sphops_grid* grid, Op op, const int32_t* bo, OpPtrs a, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(bo != nullptr && a.x != nullptr && a.out0 != nullptr, "null buffer");
+    if (op == Op::Blur || op == Op::Gradient || op == Op::GradientHybrid) {
+      sphops::check_channels(a.C);
+      require(a.s != nullptr, "state must not be NULL");
+    }
+    if (op != Op::Count) require(a.m != nullptr, "mass must not be NULL");
+    if (op == Op::Blur || op == Op::Gradient || op == Op::GradientHybrid || op == Op::MomentMatrix)
+      require(a.rho != nullptr, "rho must not be NULL");
+    require(grid->dim == 2 || sphops::pk::aligned16(a.x), "3D positions must be 16-byte aligned");
+    sphops::forward(*grid, op, bo, a, sphops::as_stream(stream));
+  });
+}
+
+int sphops_count_forward(const sphops_grid* grid, const float* x, float* count, const int32_t* bo, const int32_t*,
+                         void* stream) {
+  OpPtrs a;
+  a.x = x;
+  a.out0 = count;
+  return fwd_op(grid, Op::Count, bo, a, stream);
+}
+
+int sphops_density_forward(const sphops_grid* grid, const float* x, const float* mass, float* rho, const int32_t* bo,
+                           const int32_t*, void* stream) {
+  OpPtrs a;
+  a.x = x;
+  a.m = mass;
+  a.out0 = rho;
+  return fwd_op(grid, Op::Density, bo, a, stream);
+}
+
+int sphops_blur_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                        const float* state_in, float* state_out, uint32_t C, const int32_t* bo, const int32_t*,
+                        void* stream) {
+  OpPtrs a;
+  a.x = x;
+  a.rho = rho;
+  a.m = mass;
+  a.s = state_in;
+  a.out0 = state_out;
+  a.C = C;
+  return fwd_op(grid, Op::Blur, bo, a, stream);
+}
+
+int sphops_gradient_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                            const float* state_in, float* out, uint32_t C, const int32_t* bo, const int32_t*,
+                            void* stream) {
+  OpPtrs a;
+  a.x = x;
+  a.rho = rho;
+  a.m = mass;
+  a.s = state_in;
+  a.out0 = out;
+  a.C = C;
+  return fwd_op(grid, Op::Gradient, bo, a, stream);
+}
+
+int sphops_density_gradient_forward(const sphops_grid* grid, const float* x, const float* mass, float* out,
+                                    const int32_t* bo, const int32_t*, void* stream) {
+  OpPtrs a;
+  a.x = x;
+  a.m = mass;
+  a.out0 = out;
+  return fwd_op(grid, Op::DensityGradient, bo, a, stream);
+}
+
+int sphops_moment_matrix_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                                 float* out, const int32_t* bo, const int32_t*, void* stream) {
+  OpPtrs a;
+  a.x = x;
+  a.rho = rho;
+  a.m = mass;
+  a.out0 = out;
+  return fwd_op(grid, Op::MomentMatrix, bo, a, stream);
+}
+
+int sphops_gradient_hybrid_forward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                                   const float* state_in, float* out, uint32_t C, float tol, const int32_t* bo,
+                                   const int32_t*, void* stream) {
+  OpPtrs a;
+  a.x = x;
+  a.rho = rho;
+  a.m = mass;
+  a.s = state_in;
+  a.out0 = out;
+  a.C = C;
+  a.tol = tol;
+  return fwd_op(grid, Op::GradientHybrid, bo, a, stream);
+}
+
+static int bwd_op(const sphops_grid* grid, Op op, bool full, const int32_t* bo, OpPtrs a, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(bo != nullptr && a.x != nullptr && a.m != nullptr && a.g != nullptr, "null buffer");
+    if (op == Op::Blur || op == Op::Gradient) {
+      sphops::check_channels(a.C);
+      require(a.rho != nullptr && a.s != nullptr && a.out1 != nullptr, "null buffer");
+      if (full) require(a.out0 != nullptr && a.out2 != nullptr, "null buffer");
+    } else if (op == Op::MomentMatrix) {
+      require(a.rho != nullptr && a.out0 != nullptr && a.out2 != nullptr, "null buffer");
+    } else {
+      require(a.out0 != nullptr, "null buffer");
+    }
+    require(grid->dim == 2 || (sphops::pk::aligned16(a.x) && (!a.out0 || sphops::pk::aligned16(a.out0))),
+            "3D positions must be 16-byte aligned");
+    sphops::backward(*grid, op, full, bo, a, sphops::as_stream(stream));
+  });
+}
+
+int sphops_density_backward(const sphops_grid* grid, const float* x, const float* mass, const float* dL_rho,
+                            float* grad_x, const int32_t* bo, const int32_t*, int dLdx, void* stream) {
+  if (!dLdx) return 0;
+  OpPtrs a;
+  a.x = x;
+  a.m = mass;
+  a.g = dL_rho;
+  a.out0 = grad_x;
+  return bwd_op(grid, Op::Density, true, bo, a, stream);
+}
+
+int sphops_blur_backward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                         const float* state_in, const float* dL, float* grad_x, float* grad_s, float* grad_rho,
+                         uint32_t C, const int32_t* bo, const int32_t*, int dLdx, int dLds, int dLdrho,
+                         void* stream) {
+  if (!dLdx && !dLds && !dLdrho) return 0;
+  const bool ds_only = dLds && !dLdx && !dLdrho;
+  OpPtrs a;
+  a.x = x;
+  a.rho = rho;
+  a.m = mass;
+  a.s = state_in;
+  a.g = dL;
+  a.out0 = grad_x;
+  a.out1 = grad_s;
+  a.out2 = grad_rho;
+  a.C = C;
+  return bwd_op(grid, Op::Blur, !ds_only, bo, a, stream);
+}
+
+int sphops_density_gradient_backward(const sphops_grid* grid, const float* x, const float* mass, const float* dL,
+                                     float* grad_x, const int32_t* bo, const int32_t*, int dLdx, void* stream) {
+  if (!dLdx) return 0;
+  OpPtrs a;
+  a.x = x;
+  a.m = mass;
+  a.g = dL;
+  a.out0 = grad_x;
+  return bwd_op(grid, Op::DensityGradient, true, bo, a, stream);
+}
+
+int sphops_gradient_backward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                             const float* state_in, const float* dL, float* grad_x, float* grad_s, float* grad_rho,
+                             uint32_t C, const int32_t* bo, const int32_t*, int dLdx, int dLds, int dLdrho,
+                             void* stream) {
+  if (!dLdx && !dLds && !dLdrho) return 0;
+  const bool ds_only = dLds && !dLdx && !dLdrho;
+  OpPtrs a;
+  a.x = x;
+  a.rho = rho;
+  a.m = mass;
+  a.s = state_in;
+  a.g = dL;
+  a.out0 = grad_x;
+  a.out1 = grad_s;
+  a.out2 = grad_rho;
+  a.C = C;
+  return bwd_op(grid, Op::Gradient, !ds_only, bo, a, stream);
+}
+
+int sphops_moment_matrix_backward(const sphops_grid* grid, const float* x, const float* rho, const float* mass,
+                                  const float* dL, float* grad_x, float* grad_rho, const int32_t* bo, const int32_t*,
+                                  int dLdx, int dLdrho, void* stream) {
+  if (!dLdx && !dLdrho) return 0;
+  OpPtrs a;
+  a.x = x;
+  a.rho = rho;
+  a.m = mass;
+  a.g = dL;
+  a.out0 = grad_x;
+  a.out2 = grad_rho;
+  return bwd_op(grid, Op::MomentMatrix, true, bo, a, stream);
+}
+
+int sphops_safe_inv_sym_mat(const float* in, float* out, int64_t count, int dim, float tol, void* stream) {
+  return guarded([&] {
+    require(dim == 2 || dim == 3, "safe_inverse only supports 2x2 or 3x3 matrices.");
+    require(count >= 0, "count must be >= 0");
+    require(count == 0 || (in && out), "null buffer");
+    sphops::run_safe_inv(in, out, (uint64_t)count, dim, tol, sphops::as_stream(stream));
+  });
+}
+
+}  // extern "C"

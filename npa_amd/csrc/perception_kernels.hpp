@@ -1,0 +1,733 @@
+// SPH neighbour perception kernels (forward and gather-form backward) for gfx950.
+//
+// One lane owns one binned particle i and writes only i's outputs, so no
+// atomics are used and every result is deterministic.  The candidate set of i
+// is the 3^D cell stencil of its cell, read as contiguous slices of the
+// sorted particle arrays through bin_offsets: in grid mode 3^(D-1) rows of up
+// to three x-adjacent cells (plus the periodic wrap cell), as the reference
+// traverses them (sphops/sph_cuda.cu:1561-1640); in particle mode the 3^D
+// Morton cells (sphops/sph_cuda.cu:324-346).
+//
+// Operators with per-channel work run in two phases per round: every lane
+// first scans its candidates and appends in-radius neighbours to its own
+// column of a per-wave LDS list (kCap entries), then all lanes walk their
+// lists together, so the channel loops execute with the wave converged
+// instead of under the ~1-in-6 in-radius branch.  The formulas are the
+// reference's (sphops/sph_cuda.cu:218-721 and 1160-1375, sphops/utils.cuh:199-279),
+// with per-pair work hoisted out of the channel loops.
+#pragma once
+
+#include "sphops_internal.hpp"
+
+namespace sphops {
+namespace pk {
+
+constexpr int kThreads = 256;
+constexpr int kCap = 32;
+
+// ------------------------------------------------------------- traversal
+
+template <int D, bool PERIODIC>
+struct Walker {
+  int c[3];
+  uint32_t base;  // b * G
+  int r;          // next range to fetch
+  uint32_t j, jend;
+
+  static constexpr int kRowRanges = (D == 2 ? 3 : 9) * (PERIODIC ? 2 : 1);
+  static constexpr int kCellRanges = (D == 2 ? 9 : 27);
+
+  __device__ __forceinline__ void init(const GridParams& g, const float* xi, uint32_t k) {
+    pos2cell<D, PERIODIC>(g, xi, c);
+    base = (k / g.N) * g.G;
+    r = 0;
+    j = 0;
+    jend = 0;
+  }
+
+  __device__ __forceinline__ bool fetch(const GridParams& g, const int32_t* __restrict__ bo, int rr) {
+    int nc[3] = {c[0], c[1], D == 3 ? c[2] : 0};
+    if (!g.morton) {
+      if (rr >= kRowRanges) return false;
+      const int row = PERIODIC ? (rr >> 1) : rr;
+      const int chunk = PERIODIC ? (rr & 1) : 0;
+      j = jend = 0;
+      if constexpr (D == 2) {
+        nc[1] = c[1] + row - 1;
+      } else {
+        nc[1] = c[1] + row % 3 - 1;
+        nc[2] = c[2] + row / 3 - 1;
+      }
+#pragma unroll
+      for (int d = 1; d < D; ++d) {
+        if (PERIODIC) {
+          nc[d] = bound_axis(nc[d], g.gs[d], true);
+        } else if (nc[d] < 0 || nc[d] >= g.gs[d]) {
+          return true;
+        }
+      }
+      int x0, x1;
+      if (chunk == 0) {
+        x0 = max(0, c[0] - 1);
+        x1 = min(g.gs[0] - 1, c[0] + 1);
+      } else if (c[0] == 0) {
+        x0 = x1 = g.gs[0] - 1;
+      } else if (c[0] == g.gs[0] - 1) {
+        x0 = x1 = 0;
+      } else {
+        return true;
+      }
+      nc[0] = x0;
+      const uint32_t h0 = cell_hash<D>(g, nc);
+      const uint32_t h1 = h0 + (uint32_t)(x1 - x0);
+      j = (uint32_t)bo[base + h0];
+      jend = (uint32_t)bo[base + h1 + 1];
+      return true;
+    }
+    if (rr >= kCellRanges) return false;
+    j = jend = 0;
+    nc[0] = c[0] + rr % 3 - 1;
+    nc[1] = c[1] + (rr / 3) % 3 - 1;
+    if constexpr (D == 3) nc[2] = c[2] + rr / 9 - 1;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (PERIODIC) {
+        nc[d] = bound_axis(nc[d], g.gs[d], true);
+      } else if (nc[d] < 0 || nc[d] >= g.gs[d]) {
+        return true;
+      }
+    }
+    const uint32_t h = cell_hash<D>(g, nc);
+    j = (uint32_t)bo[base + h];
+    jend = (uint32_t)bo[base + h + 1];
+    return true;
+  }
+
+  // Position on the next candidate; false once the stencil is exhausted.
+  __device__ __forceinline__ bool next(const GridParams& g, const int32_t* __restrict__ bo) {
+    while (j >= jend) {
+      if (!fetch(g, bo, r)) return false;
+      ++r;
+    }
+    return true;
+  }
+};
+
+// ------------------------------------------------------------- row loads
+
+// Load one row of `n` floats (compile-time) starting at p + row*stride.
+template <int N, bool VEC>
+__device__ __forceinline__ void load_row(const float* __restrict__ p, uint64_t row, float* v) {
+  if constexpr (VEC) {
+    const float4* q = reinterpret_cast<const float4*>(p + row * N);
+#pragma unroll
+    for (int u = 0; u < N / 4; ++u) {
+      const float4 t = q[u];
+      v[4 * u + 0] = t.x;
+      v[4 * u + 1] = t.y;
+      v[4 * u + 2] = t.z;
+      v[4 * u + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < N; ++u) v[u] = p[row * N + u];
+  }
+}
+
+// Channel configuration: CM channels in registers; EXACT means C == CM and rows
+// can be loaded with 16-byte vectors, otherwise C <= CM with predication.
+template <int CM, bool EXACT>
+struct Chan {
+  static constexpr int kMax = CM;
+  static constexpr bool kVec = EXACT && (CM % 4 == 0);
+  __device__ static __forceinline__ void load(const float* __restrict__ p, uint64_t row, uint32_t C, float* v) {
+    if constexpr (EXACT) {
+      load_row<CM, kVec>(p, row, v);
+    } else {
+#pragma unroll
+      for (int f = 0; f < CM; ++f) v[f] = (f < (int)C) ? p[row * C + f] : 0.0f;
+    }
+  }
+  // row of CM*D floats (gradient-shaped tensors)
+  template <int D>
+  __device__ static __forceinline__ void load_cd(const float* __restrict__ p, uint64_t row, uint32_t C, float* v) {
+    if constexpr (EXACT) {
+      load_row<CM * D, (CM * D) % 4 == 0 && kVec>(p, row, v);
+    } else {
+#pragma unroll
+      for (int f = 0; f < CM * D; ++f) v[f] = (f < (int)C * D) ? p[row * C * D + f] : 0.0f;
+    }
+  }
+};
+
+template <int D>
+__device__ __forceinline__ void store_pos_grad(float* __restrict__ out, uint32_t k, const float* v, float scale) {
+  if constexpr (D == 2) {
+    reinterpret_cast<float2*>(out)[k] = make_float2(v[0] * scale, v[1] * scale);
+  } else {
+    reinterpret_cast<float4*>(out)[k] = make_float4(v[0] * scale, v[1] * scale, v[2] * scale, 0.0f);
+  }
+}
+
+// Adjugate inverse of a symmetric 2x2 / 3x3 matrix read from its upper
+// triangle, identity when |det| < tol (sphops/sph_cuda.cu:3095-3179).
+template <int D>
+__device__ __forceinline__ void safe_inv_sym(const float* M, float tol, float* L) {
+  if constexpr (D == 2) {
+    const float a = M[0], b = M[1], d = M[3];
+    const float det = a * d - b * b;
+    if (fabsf(det) < tol) {
+      L[0] = 1.0f; L[1] = 0.0f; L[2] = 0.0f; L[3] = 1.0f;
+      return;
+    }
+    const float id = 1.0f / det;
+    L[0] = d * id; L[1] = -b * id; L[2] = -b * id; L[3] = a * id;
+  } else {
+    const float a = M[0], b = M[1], c = M[2], d = M[4], e = M[5], f = M[8];
+    const float t1 = d * f - e * e, t2 = c * e - b * f, t3 = b * e - c * d;
+    const float det = a * t1 + b * t2 + c * t3;
+    if (fabsf(det) < tol) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) L[q] = (q % 4 == 0) ? 1.0f : 0.0f;
+      return;
+    }
+    const float id = 1.0f / det;
+    const float u = (b * c - a * e) * id;
+    L[0] = t1 * id; L[1] = t2 * id; L[2] = t3 * id;
+    L[3] = t2 * id; L[4] = (a * f - c * c) * id; L[5] = u;
+    L[6] = t3 * id; L[7] = u; L[8] = (a * d - b * b) * id;
+  }
+}
+
+// ------------------------------------------------------------- operators
+
+// Single-phase operators receive (x_j, r = x_j - x_i, |r|^2) for every
+// in-radius candidate; two-phase operators receive j and reload what they need.
+
+template <int D, bool P>
+struct OpCount {
+  static constexpr bool kTwoPhase = false;
+  float acc = 0.0f;
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
+  __device__ void pair(const GridParams&, const OpPtrs&, const float*, const float*, const float*, float, uint32_t) {
+    acc += 1.0f;
+  }
+  __device__ void finish(const GridParams&, const OpPtrs& a, uint32_t k) { a.out0[k] = acc; }
+};
+
+template <int D, bool P>
+struct OpDensity {
+  static constexpr bool kTwoPhase = false;
+  float acc = 0.0f;
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, const float*, float d2,
+                       uint32_t j) {
+    acc += poly6(g.eps2, d2) * a.m[j];
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { a.out0[k] = acc * g.c6; }
+};
+
+template <int D, bool P>
+struct OpDensityGradient {
+  static constexpr bool kTwoPhase = false;
+  float acc[D] = {};
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, const float* r, float d2,
+                       uint32_t j) {
+    float d;
+    const float t = spiky_mag(g.eps, d2, &d) * a.m[j];
+#pragma unroll
+    for (int e = 0; e < D; ++e) acc[e] += t * r[e];
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+#pragma unroll
+    for (int e = 0; e < D; ++e) a.out0[(uint64_t)k * D + e] = acc[e] * g.cs;
+  }
+};
+
+template <int D, bool P>
+struct OpMomentMatrix {
+  static constexpr bool kTwoPhase = false;
+  float acc[D * D] = {};
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, const float* r, float d2,
+                       uint32_t j) {
+    float d;
+    const float t = spiky_mag(g.eps, d2, &d) * (a.m[j] / a.rho[j]);
+#pragma unroll
+    for (int p = 0; p < D; ++p)
+#pragma unroll
+      for (int q = 0; q < D; ++q) acc[p * D + q] += t * r[p] * r[q];
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+#pragma unroll
+    for (int q = 0; q < D * D; ++q) a.out0[(uint64_t)k * D * D + q] = acc[q] * g.cs;
+  }
+};
+
+template <int D, bool P, int CM, bool EX>
+struct OpBlur {
+  static constexpr bool kTwoPhase = true;
+  using Ch = Chan<CM, EX>;
+  float acc[CM] = {};
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
+  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
+    float xj[3], r[3];
+    load_pos<D>(a.x, j, xj);
+    const float d2 = displacement<D, P>(g, xi, xj, r);
+    const float w = poly6(g.eps2, d2) * (a.m[j] / a.rho[j]);
+    float sj[CM];
+    Ch::load(a.s, j, a.C, sj);
+#pragma unroll
+    for (int f = 0; f < CM; ++f) acc[f] += w * sj[f];
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    const uint32_t C = EX ? CM : a.C;
+#pragma unroll
+    for (int f = 0; f < CM; ++f)
+      if (f < (int)C) a.out0[(uint64_t)k * C + f] = acc[f] * g.c6;
+  }
+};
+
+template <int D, bool P, int CM, bool EX>
+struct OpGradient {
+  static constexpr bool kTwoPhase = true;
+  using Ch = Chan<CM, EX>;
+  float si[CM];
+  float acc[CM * D] = {};
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) { Ch::load(a.s, k, a.C, si); }
+  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
+    float xj[3], r[3];
+    load_pos<D>(a.x, j, xj);
+    const float d2 = displacement<D, P>(g, xi, xj, r);
+    float d;
+    const float t = spiky_mag(g.eps, d2, &d) * (a.m[j] / a.rho[j]);
+    float sj[CM];
+    Ch::load(a.s, j, a.C, sj);
+#pragma unroll
+    for (int f = 0; f < CM; ++f) {
+      const float q = t * (sj[f] - si[f]);
+#pragma unroll
+      for (int e = 0; e < D; ++e) acc[f * D + e] += q * r[e];
+    }
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    const uint32_t C = EX ? CM : a.C;
+#pragma unroll
+    for (int f = 0; f < CM * D; ++f)
+      if (f < (int)(C * D)) a.out0[(uint64_t)k * C * D + f] = acc[f] * g.cs;
+  }
+};
+
+// gradient_hybrid forward fused: raw gradient and moment matrix in one sweep,
+// then raw @ safe_inv(M) in registers (sphops/sph.py:474-484).
+template <int D, bool P, int CM, bool EX>
+struct OpGradientHybrid {
+  static constexpr bool kTwoPhase = true;
+  using Ch = Chan<CM, EX>;
+  float si[CM];
+  float acc[CM * D] = {};
+  float M[D * D] = {};
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) { Ch::load(a.s, k, a.C, si); }
+  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
+    float xj[3], r[3];
+    load_pos<D>(a.x, j, xj);
+    const float d2 = displacement<D, P>(g, xi, xj, r);
+    float d;
+    const float t = spiky_mag(g.eps, d2, &d) * (a.m[j] / a.rho[j]);
+#pragma unroll
+    for (int p = 0; p < D; ++p)
+#pragma unroll
+      for (int q = p; q < D; ++q) M[p * D + q] += t * r[p] * r[q];
+    float sj[CM];
+    Ch::load(a.s, j, a.C, sj);
+#pragma unroll
+    for (int f = 0; f < CM; ++f) {
+      const float q = t * (sj[f] - si[f]);
+#pragma unroll
+      for (int e = 0; e < D; ++e) acc[f * D + e] += q * r[e];
+    }
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    float Ms[D * D], L[D * D];
+#pragma unroll
+    for (int p = 0; p < D; ++p)
+#pragma unroll
+      for (int q = 0; q < D; ++q) Ms[p * D + q] = (q >= p ? M[p * D + q] : M[q * D + p]) * g.cs;
+    safe_inv_sym<D>(Ms, a.tol, L);
+    const uint32_t C = EX ? CM : a.C;
+#pragma unroll
+    for (int f = 0; f < CM; ++f) {
+      if (f >= (int)C) continue;
+      float raw[D];
+#pragma unroll
+      for (int e = 0; e < D; ++e) raw[e] = acc[f * D + e] * g.cs;
+#pragma unroll
+      for (int e = 0; e < D; ++e) {
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < D; ++q) o += raw[q] * L[q * D + e];
+        a.out0[((uint64_t)k * C + f) * D + e] = o;
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------- backward ops
+
+// displacement x_i - x_j as the reference's backward evaluates it
+template <int D, bool P>
+__device__ __forceinline__ float back_disp(const GridParams& g, const float* xi, const float* xj, const float* r_fwd,
+                                           float d2_fwd, float* rb) {
+  if constexpr (!P) {
+#pragma unroll
+    for (int e = 0; e < D; ++e) rb[e] = -r_fwd[e];
+    return d2_fwd;
+  } else {
+    return displacement<D, P>(g, xj, xi, rb);
+  }
+}
+
+template <int D, bool P>
+struct OpDensityBwd {
+  static constexpr bool kTwoPhase = false;
+  float gi = 0.0f, mi = 0.0f;
+  float dx[D] = {};
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+    gi = a.g[k];
+    mi = a.m[k];
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, const float* r,
+                       float d2, uint32_t j) {
+    float rb[3];
+    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
+    if (db == 0.0f || !(db < g.eps2)) return;
+    const float t = g.eps2 - db;
+    const float coef = gi * a.m[j] + a.g[j] * mi;
+    const float mag = -coef * 6.0f * t * t;
+#pragma unroll
+    for (int e = 0; e < D; ++e) dx[e] += mag * rb[e];
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { store_pos_grad<D>(a.out0, k, dx, g.c6); }
+};
+
+template <int D, bool P>
+struct OpDensityGradientBwd {
+  static constexpr bool kTwoPhase = false;
+  float gi[D], mi = 0.0f;
+  float dx[D] = {};
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+#pragma unroll
+    for (int e = 0; e < D; ++e) gi[e] = a.g[(uint64_t)k * D + e];
+    mi = a.m[k];
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, const float* r,
+                       float d2, uint32_t j) {
+    float rb[3];
+    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
+    const float mj = a.m[j];
+    float diff[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) diff[e] = a.g[(uint64_t)j * D + e] * mi - gi[e] * mj;
+    spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, diff, dx);
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { store_pos_grad<D>(a.out0, k, dx, g.cs); }
+};
+
+template <int D, bool P>
+struct OpMomentMatrixBwd {
+  static constexpr bool kTwoPhase = false;
+  float gi[D * D], vi = 0.0f, mr2 = 0.0f;
+  float dx[D] = {};
+  float drho = 0.0f;
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+#pragma unroll
+    for (int q = 0; q < D * D; ++q) gi[q] = a.g[(uint64_t)k * D * D + q];
+    const float mi = a.m[k], ri = a.rho[k];
+    vi = mi / ri;
+    mr2 = mi / (ri * ri);
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, const float* r,
+                       float d2, uint32_t j) {
+    float rb[3];
+    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
+    float d;
+    const float mag = spiky_mag(g.eps, db, &d);
+    float w[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) w[e] = mag * rb[e];
+    const float vj = a.m[j] / a.rho[j];
+    float gd[D * D];
+#pragma unroll
+    for (int p = 0; p < D; ++p) {
+#pragma unroll
+      for (int q = 0; q < D; ++q) {
+        const float gj = a.g[(uint64_t)j * D * D + p * D + q];
+        drho += gj * rb[p] * w[q];
+        const float c = gi[p * D + q] * vj + gj * vi;
+        dx[p] += w[q] * c;
+        gd[p * D + q] = rb[p] * c;
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < D; ++p) spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, &gd[p * D], dx);
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    store_pos_grad<D>(a.out0, k, dx, g.cs);
+    a.out2[k] = -drho * mr2 * g.cs;
+  }
+};
+
+template <int D, bool P, int CM, bool EX, bool FULL>
+struct OpBlurBwd {
+  static constexpr bool kTwoPhase = true;
+  using Ch = Chan<CM, EX>;
+  float vi = 0.0f, mr2 = 0.0f;
+  float si[FULL ? CM : 1], gi[FULL ? CM : 1];
+  float ds[CM] = {};
+  float dx[D] = {};
+  float drho = 0.0f;
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+    const float mi = a.m[k], ri = a.rho[k];
+    vi = mi / ri;
+    mr2 = mi / (ri * ri);
+    if constexpr (FULL) {
+      Ch::load(a.s, k, a.C, si);
+      Ch::load(a.g, k, a.C, gi);
+    }
+  }
+  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
+    float xj[3], r[3], rb[3];
+    load_pos<D>(a.x, j, xj);
+    const float d2 = displacement<D, P>(g, xi, xj, r);
+    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
+    const float W = poly6(g.eps2, db);
+    float gj[CM];
+    Ch::load(a.g, j, a.C, gj);
+#pragma unroll
+    for (int f = 0; f < CM; ++f) ds[f] += W * gj[f];
+    if constexpr (FULL) {
+      float sj[CM];
+      Ch::load(a.s, j, a.C, sj);
+      float A = 0.0f, Bv = 0.0f;
+#pragma unroll
+      for (int f = 0; f < CM; ++f) {
+        A += gi[f] * sj[f];
+        Bv += gj[f] * si[f];
+      }
+      drho += W * Bv;
+      if (db != 0.0f && db < g.eps2) {
+        const float vj = a.m[j] / a.rho[j];
+        const float t = g.eps2 - db;
+        const float mag = -6.0f * t * t * (A * vj + Bv * vi);
+#pragma unroll
+        for (int e = 0; e < D; ++e) dx[e] += mag * rb[e];
+      }
+    }
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    const uint32_t C = EX ? CM : a.C;
+    const float sc = vi * g.c6;
+#pragma unroll
+    for (int f = 0; f < CM; ++f)
+      if (f < (int)C) a.out1[(uint64_t)k * C + f] = ds[f] * sc;
+    if constexpr (FULL) {
+      a.out2[k] = -drho * mr2 * g.c6;
+      store_pos_grad<D>(a.out0, k, dx, g.c6);
+    }
+  }
+};
+
+template <int D, bool P, int CM, bool EX, bool FULL>
+struct OpGradientBwd {
+  static constexpr bool kTwoPhase = true;
+  using Ch = Chan<CM, EX>;
+  float vi = 0.0f, mr2 = 0.0f;
+  float gi[CM * D];
+  float si[FULL ? CM : 1];
+  float ds[CM] = {};
+  float wsum[D] = {};
+  float dx[D] = {};
+  float drho = 0.0f;
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+    const float mi = a.m[k], ri = a.rho[k];
+    vi = mi / ri;
+    mr2 = mi / (ri * ri);
+    Ch::template load_cd<D>(a.g, k, a.C, gi);
+    if constexpr (FULL) Ch::load(a.s, k, a.C, si);
+  }
+  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
+    float xj[3], r[3], rb[3];
+    load_pos<D>(a.x, j, xj);
+    const float d2 = displacement<D, P>(g, xi, xj, r);
+    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
+    float d;
+    const float mag = spiky_mag(g.eps, db, &d);
+    float w[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) w[e] = mag * rb[e];
+    const float vj = a.m[j] / a.rho[j];
+#pragma unroll
+    for (int e = 0; e < D; ++e) wsum[e] += vj * w[e];
+    float gj[CM * D];
+    Ch::template load_cd<D>(a.g, j, a.C, gj);
+    if constexpr (!FULL) {
+#pragma unroll
+      for (int f = 0; f < CM; ++f) {
+        float pf = 0.0f;
+#pragma unroll
+        for (int e = 0; e < D; ++e) pf += gj[f * D + e] * w[e];
+        ds[f] += pf;
+      }
+    } else {
+      float sj[CM];
+      Ch::load(a.s, j, a.C, sj);
+      float u1[D] = {}, u2[D] = {};
+#pragma unroll
+      for (int f = 0; f < CM; ++f) {
+        float pf = 0.0f;
+        const float df = si[f] - sj[f];
+#pragma unroll
+        for (int e = 0; e < D; ++e) {
+          pf += gj[f * D + e] * w[e];
+          u1[e] += df * gj[f * D + e];
+          u2[e] += df * gi[f * D + e];
+        }
+        ds[f] += pf;
+      }
+      float u[D], uw = 0.0f;
+#pragma unroll
+      for (int e = 0; e < D; ++e) {
+        uw += u1[e] * w[e];
+        u[e] = vi * u1[e] + vj * u2[e];
+      }
+      drho += uw;
+      spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, u, dx);
+    }
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    const uint32_t C = EX ? CM : a.C;
+#pragma unroll
+    for (int f = 0; f < CM; ++f) {
+      if (f >= (int)C) continue;
+      float t = vi * ds[f];
+#pragma unroll
+      for (int e = 0; e < D; ++e) t += gi[f * D + e] * wsum[e];
+      a.out1[(uint64_t)k * C + f] = t * g.cs;
+    }
+    if constexpr (FULL) {
+      a.out2[k] = -drho * mr2 * g.cs;
+      store_pos_grad<D>(a.out0, k, dx, g.cs);
+    }
+  }
+};
+
+// ---------------------------------------------------------------- driver
+
+template <int D, bool P, class OP>
+__global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t* __restrict__ bo, OpPtrs a) {
+  const uint32_t n = g.B * g.N;
+  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
+  const bool active = k < n;
+  OP op;
+  float xi[3] = {0.0f, 0.0f, 0.0f};
+  Walker<D, P> w;
+  if (active) {
+    load_pos<D>(a.x, k, xi);
+    op.init(g, a, k, xi);
+    w.init(g, xi, k);
+  }
+  bool more = active && w.next(g, bo);
+  if constexpr (OP::kTwoPhase) {
+    __shared__ uint32_t list[kThreads / kWave][kCap][kWave];
+    const int wv = threadIdx.x >> 6, ln = __lane_id();
+    while (__any(more)) {
+      int cnt = 0;
+      while (more && cnt < kCap) {
+        float xj[3], r[3];
+        load_pos<D>(a.x, w.j, xj);
+        const float d2 = displacement<D, P>(g, xi, xj, r);
+        if (d2 < g.eps2) list[wv][cnt++][ln] = w.j;
+        ++w.j;
+        more = w.next(g, bo);
+      }
+      for (int t = 0; t < cnt; ++t) op.pair2(g, a, xi, list[wv][t][ln]);
+    }
+  } else {
+    while (more) {
+      float xj[3], r[3];
+      load_pos<D>(a.x, w.j, xj);
+      const float d2 = displacement<D, P>(g, xi, xj, r);
+      if (d2 < g.eps2) op.pair(g, a, xi, xj, r, d2, w.j);
+      ++w.j;
+      more = w.next(g, bo);
+    }
+  }
+  if (active) op.finish(g, a, k);
+}
+
+template <int D, bool P, class OP>
+void launch_pairs(const Grid& g, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+  const uint64_t n = g.n_keys;
+  if (n == 0) return;
+  hipLaunchKernelGGL((k_pairs<D, P, OP>), dim3((uint32_t)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, st,
+                     g.p, bo, a);
+  SPHOPS_LAUNCHED();
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Pick the register-channel configuration for C.
+template <int D, bool P, template <int, bool, int, bool> class OPT>
+void launch_channels(const Grid& g, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+  const uint32_t C = a.C;
+  const bool al = aligned16(a.s) && aligned16(a.g);
+  if (al && C == 16) return launch_pairs<D, P, OPT<D, P, 16, true>>(g, bo, a, st);
+  if (al && C == 12) return launch_pairs<D, P, OPT<D, P, 12, true>>(g, bo, a, st);
+  if (al && C == 32) return launch_pairs<D, P, OPT<D, P, 32, true>>(g, bo, a, st);
+  if (C <= 8) return launch_pairs<D, P, OPT<D, P, 8, false>>(g, bo, a, st);
+  if (C <= 16) return launch_pairs<D, P, OPT<D, P, 16, false>>(g, bo, a, st);
+  if (C <= 32) return launch_pairs<D, P, OPT<D, P, 32, false>>(g, bo, a, st);
+  return launch_pairs<D, P, OPT<D, P, 64, false>>(g, bo, a, st);
+}
+
+template <int D, bool P, int CM, bool EX> using BlurBwdFull = OpBlurBwd<D, P, CM, EX, true>;
+template <int D, bool P, int CM, bool EX> using BlurBwdDs = OpBlurBwd<D, P, CM, EX, false>;
+template <int D, bool P, int CM, bool EX> using GradientBwdFull = OpGradientBwd<D, P, CM, EX, true>;
+template <int D, bool P, int CM, bool EX> using GradientBwdDs = OpGradientBwd<D, P, CM, EX, false>;
+
+template <int D, bool P>
+void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+  switch (op) {
+    case Op::Count: return launch_pairs<D, P, OpCount<D, P>>(g, bo, a, st);
+    case Op::Density: return launch_pairs<D, P, OpDensity<D, P>>(g, bo, a, st);
+    case Op::DensityGradient: return launch_pairs<D, P, OpDensityGradient<D, P>>(g, bo, a, st);
+    case Op::MomentMatrix: return launch_pairs<D, P, OpMomentMatrix<D, P>>(g, bo, a, st);
+    case Op::Blur: return launch_channels<D, P, OpBlur>(g, bo, a, st);
+    case Op::Gradient: return launch_channels<D, P, OpGradient>(g, bo, a, st);
+    case Op::GradientHybrid: return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
+  }
+  throw Error("unknown forward operator");
+}
+
+template <int D, bool P>
+void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+  switch (op) {
+    case Op::Density: return launch_pairs<D, P, OpDensityBwd<D, P>>(g, bo, a, st);
+    case Op::DensityGradient: return launch_pairs<D, P, OpDensityGradientBwd<D, P>>(g, bo, a, st);
+    case Op::MomentMatrix: return launch_pairs<D, P, OpMomentMatrixBwd<D, P>>(g, bo, a, st);
+    case Op::Blur:
+      if (full) return launch_channels<D, P, BlurBwdFull>(g, bo, a, st);
+      return launch_channels<D, P, BlurBwdDs>(g, bo, a, st);
+    case Op::Gradient:
+    case Op::GradientHybrid:
+      if (full) return launch_channels<D, P, GradientBwdFull>(g, bo, a, st);
+      return launch_channels<D, P, GradientBwdDs>(g, bo, a, st);
+    default:
+      break;
+  }
+  throw Error("operator has no backward");
+}
+
+}  // namespace pk
+}  // namespace sphops

@@ -1,0 +1,93 @@
+// Host-side internals shared by the sphops translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdexcept>
+#include <string>
+
+#include "sphops_device.hpp"
+
+namespace sphops {
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+#define SPHOPS_HIP(call)                                                                  \
+  do {                                                                                    \
+    hipError_t e_ = (call);                                                               \
+    if (e_ != hipSuccess)                                                                 \
+      throw ::sphops::Error(std::string("HIP error at ") + __FILE__ + ":" +               \
+                            std::to_string(__LINE__) + " - " + hipGetErrorString(e_));    \
+  } while (0)
+
+#define SPHOPS_LAUNCHED() SPHOPS_HIP(hipGetLastError())
+
+// Grid object: static parameters plus the scratch buffers binning needs
+// (the reference's HashGrid::_init allocations, sphops/sph_cuda.cu:1880-1895).
+struct Grid {
+  GridParams p{};
+  int dim = 2;
+  bool periodic = false;
+  bool particle_mode = false;
+  uint64_t max_blocks = 1;
+  int device = 0;
+
+  // scratch, sized at creation for B*N keys and B*G+1 cells
+  uint64_t n_keys = 0;        // B*N
+  uint64_t n_cells = 0;       // B*G
+  uint64_t n_tiles = 0;       // radix tiles
+  uint64_t n_chunks = 0;      // cell chunks for bin_offsets
+  uint32_t* keys[2] = {nullptr, nullptr};
+  uint32_t* vals[2] = {nullptr, nullptr};
+  uint32_t* hist = nullptr;       // 256 * n_tiles (+1)
+  uint32_t* scan_tmp = nullptr;   // partial sums for device scans
+  uint64_t scan_tmp_len = 0;
+  uint32_t* chunk_first = nullptr;
+  uint32_t* chunk_end = nullptr;
+  uint32_t* chunk_lo = nullptr;   // n_chunks + 1
+  uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
+};
+
+// binning.hip
+void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bin_offsets,
+                     int32_t* block_info, int32_t* total_blocks, hipStream_t st);
+void run_bin_particles(const Grid& g, const float* in_pos, const float* in_state, const float* in_mass,
+                       const int32_t* perm, float* out_pos, float* out_state, float* out_mass,
+                       uint32_t C, bool forward, hipStream_t st);
+uint64_t scan_tmp_elems(uint64_t n);
+
+// perception.hip
+enum class Op : int {
+  Count = 0,
+  Density = 1,
+  DensityGradient = 2,
+  MomentMatrix = 3,
+  Blur = 4,
+  Gradient = 5,
+  GradientHybrid = 6,
+};
+
+struct OpPtrs {
+  const float* x = nullptr;
+  const float* m = nullptr;
+  const float* rho = nullptr;
+  const float* s = nullptr;
+  const float* g = nullptr;   // upstream gradient (backward)
+  float* out0 = nullptr;      // forward output / grad_x
+  float* out1 = nullptr;      // grad_s
+  float* out2 = nullptr;      // grad_rho
+  uint32_t C = 0;
+  float tol = 1e-3f;
+};
+
+void run_forward(const Grid& g, Op op, const int32_t* bin_offsets, const OpPtrs& a, hipStream_t st);
+// full = false selects the dL/ds-only variant (Blur, Gradient)
+void run_backward(const Grid& g, Op op, bool full, const int32_t* bin_offsets, const OpPtrs& a,
+                  hipStream_t st);
+void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
+
+constexpr uint32_t kMaxChannels = 64;
+
+}  // namespace sphops

@@ -1,0 +1,69 @@
+"""ctypes binding of libsphops_hip.so (the C ABI in include/sphops_hip.h).
+
+The library is built in-tree (``npa_amd/_lib``) by ``__graft_entry__.build()``
+or ``make -C npa_amd/csrc``.  There is no fallback: if the library is missing
+or cannot be loaded, importing this module raises ImportError.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get(
+    "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
+ABI_VERSION = 1
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"libsphops_hip.so not found at {LIB_PATH}; build it with "
+        "`python -c 'import __graft_entry__ as g; g.build()'` or `make -C npa_amd/csrc`")
+
+lib = ctypes.CDLL(LIB_PATH)
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int
+_u32 = ctypes.c_uint32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+_SIGNATURES = {
+    "sphops_abi_version": ([], _i32),
+    "sphops_last_error": ([], ctypes.c_char_p),
+    "sphops_grid_create": ([_i32, _i32, _i32, ctypes.POINTER(ctypes.c_int32), _f32, _u32, _u32, _u32,
+                            ctypes.POINTER(_p)], _i32),
+    "sphops_grid_destroy": ([_p], None),
+    "sphops_grid_max_blocks": ([_p], _i64),
+    "sphops_grid_coefficients": ([_p, ctypes.POINTER(_f32), ctypes.POINTER(_f32)], _i32),
+    "sphops_initialize": ([_p, _p, _p, _p, _p, _p, _p], _i32),
+    "sphops_bin_particles": ([_p, _p, _p, _p, _p, _p, _p, _p, _u32, _p], _i32),
+    "sphops_backward_bin_particles": ([_p, _p, _p, _p, _p, _p, _p, _p, _u32, _p], _i32),
+    "sphops_count_forward": ([_p, _p, _p, _p, _p, _p], _i32),
+    "sphops_density_forward": ([_p, _p, _p, _p, _p, _p, _p], _i32),
+    "sphops_blur_forward": ([_p, _p, _p, _p, _p, _p, _u32, _p, _p, _p], _i32),
+    "sphops_gradient_forward": ([_p, _p, _p, _p, _p, _p, _u32, _p, _p, _p], _i32),
+    "sphops_density_gradient_forward": ([_p, _p, _p, _p, _p, _p, _p], _i32),
+    "sphops_moment_matrix_forward": ([_p, _p, _p, _p, _p, _p, _p, _p], _i32),
+    "sphops_gradient_hybrid_forward": ([_p, _p, _p, _p, _p, _p, _u32, _f32, _p, _p, _p], _i32),
+    "sphops_density_backward": ([_p, _p, _p, _p, _p, _p, _p, _i32, _p], _i32),
+    "sphops_blur_backward": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _p, _p, _i32, _i32, _i32, _p], _i32),
+    "sphops_density_gradient_backward": ([_p, _p, _p, _p, _p, _p, _p, _i32, _p], _i32),
+    "sphops_gradient_backward": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _u32, _p, _p, _i32, _i32, _i32, _p],
+                                 _i32),
+    "sphops_moment_matrix_backward": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p], _i32),
+    "sphops_safe_inv_sym_mat": ([_p, _p, _i64, _i32, _f32, _p], _i32),
+}
+
+for _name, (_args, _res) in _SIGNATURES.items():
+    _fn = getattr(lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _res
+
+if lib.sphops_abi_version() != ABI_VERSION:
+    raise ImportError(f"{LIB_PATH}: ABI version {lib.sphops_abi_version()} != expected {ABI_VERSION}")
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+def check(status):
+    """Raise RuntimeError with the library's message on a nonzero status."""
+    if status != 0:
+        raise RuntimeError(lib.sphops_last_error().decode("utf-8", "replace"))

@@ -1,0 +1,371 @@
+"""Public sphops API on the gfx950 library (drop-in for the reference's ``sphops/sph.py``).
+
+Same classes, functions, argument order and autograd contract as the
+reference (``sphops/sph.py:11-484``):
+
+* ``HashGrid(dim, boundary, mode, grid_size, eps, num_particles, batch_size,
+  max_particles_per_block)`` with ``instantiate(x) -> HashGridSnapshot`` and
+  ``wrap_positions(x)``;
+* ``bin_particles``/``unbin_particles``, ``count``, ``density``, ``blur``,
+  ``gradient``, ``density_gradient``, ``moment_matrix``, ``safe_inv_sym_mat``
+  and ``gradient_hybrid``, each a ``torch.autograd.Function`` whose backward
+  calls the native gather-form kernel with the ``dLdx/dLds/dLdrho`` flags the
+  reference passes.
+
+Differences, all compatible with callers of the reference:
+* ``HashGridSnapshot`` carries ``total_blocks`` (device int32) so a snapshot's
+  block count is not overwritten by later ``instantiate`` calls;
+* ``gradient_hybrid`` runs as one fused kernel (same forward value
+  ``raw @ safe_inv(M)``, same straight-through backward);
+* ``Count.backward`` returns a zero gradient instead of failing;
+* the default unit mass tensor is cached per shape instead of re-allocated.
+"""
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import sph_hip
+
+_MASS_CACHE = {}
+
+
+def _default_mass(x, mass):
+    """``mass=None`` means unit masses (``sphops/sph.py:11-17``)."""
+    if mass is None:
+        B, N = x.shape[0], x.shape[1]
+        key = (B, N, x.device, x.dtype)
+        m = _MASS_CACHE.get(key)
+        if m is None:
+            m = x.new_full((B, N), 1.0)
+            _MASS_CACHE[key] = m
+        return m
+    if mass.dim() == 3 and mass.shape[-1] == 1:
+        return mass.squeeze(-1)
+    return mass
+
+
+def get_hashgrid_cls(dim, boundary, mode):
+    return {
+        (2, "periodic", "grid"): sph_hip.HashGrid2DPeriodic,
+        (3, "periodic", "grid"): sph_hip.HashGrid3DPeriodic,
+        (2, "clamped", "grid"): sph_hip.HashGrid2DBox,
+        (3, "clamped", "grid"): sph_hip.HashGrid3DBox,
+        (2, "periodic", "particle"): sph_hip.VHashGrid2DPeriodic,
+        (3, "periodic", "particle"): sph_hip.VHashGrid3DPeriodic,
+        (2, "clamped", "particle"): sph_hip.VHashGrid2DBox,
+        (3, "clamped", "particle"): sph_hip.VHashGrid3DBox,
+    }[(dim, boundary, mode)]
+
+
+@dataclass
+class HashGridSnapshot:
+    grid: object
+    bin_offsets: torch.Tensor
+    permutation: torch.Tensor
+    block_info: torch.Tensor
+    dim: int
+    total_blocks: torch.Tensor = None
+
+
+class HashGrid:
+    """Spatial hash grid over B clouds of N particles (``sphops/sph.py:42-123``)."""
+
+    def __init__(self, dim=2, boundary="periodic", mode="grid", grid_size=(16, 16), eps=0.1,
+                 num_particles=4096, batch_size=8, max_particles_per_block=64):
+        self.dim = dim
+        self.boundary = boundary
+        self.mode = mode
+        self.grid_size = grid_size
+        self.eps = eps
+        self.num_particles = num_particles
+        self.batch_size = batch_size
+        self.max_particles_per_block = max_particles_per_block
+        if mode == "particle":
+            for size in grid_size:
+                assert (size & (size - 1)) == 0, "grid_size must be a power of 2"
+        self.num_cells = math.prod(grid_size)
+        self.hashgrid_cls = get_hashgrid_cls(dim, boundary, mode)
+        self.hashgrid = self.hashgrid_cls(*grid_size, eps, num_particles, batch_size, max_particles_per_block)
+        self.device = torch.device("cuda", torch.cuda.current_device())
+
+    def instantiate(self, x):
+        """Bin positions ``x`` (B, N, 2|4) and return the snapshot."""
+        B, N, _ = x.shape
+        dev = x.device
+        permutation = torch.empty(B, N, dtype=torch.int32, device=dev)
+        bin_offsets = torch.empty(B * self.num_cells + 1, dtype=torch.int32, device=dev)
+        block_info = torch.empty(self.hashgrid.max_blocks, 4, dtype=torch.int32, device=dev)
+        total_blocks = torch.empty(1, dtype=torch.int32, device=dev)
+        self.hashgrid.initialize(x, permutation, bin_offsets, block_info, total_blocks)
+        return HashGridSnapshot(grid=self.hashgrid, bin_offsets=bin_offsets, permutation=permutation,
+                                block_info=block_info, dim=self.dim, total_blocks=total_blocks)
+
+    def wrap_positions(self, x):
+        """Wrap positions into ``[-L/2, L/2)`` per axis when periodic
+        (``sphops/sph.py:107-123``); identity when clamped."""
+        if self.boundary == "periodic":
+            out = []
+            for d in range(self.dim):
+                L = torch.tensor(self.grid_size[d] * self.eps, device=x.device)
+                half_L = 0.5 * L
+                out.append(torch.remainder(x[..., d] + half_L, L) - half_L)
+            return torch.stack(out, dim=-1)
+        return x
+
+
+def _c(t):
+    return t if t.is_contiguous() else t.contiguous()
+
+
+class Permute(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, s, mass, snapshot):
+        x_bin = torch.empty_like(x)
+        s_bin = torch.empty_like(s)
+        mass_bin = torch.empty_like(mass)
+        snapshot.grid.bin_particles(x, s, mass, snapshot.permutation, x_bin, s_bin, mass_bin)
+        ctx.snapshot = snapshot
+        ctx.x_shape, ctx.s_shape, ctx.m_shape = x.shape, s.shape, mass.shape
+        ctx.dtype, ctx.device = x.dtype, x.device
+        ctx.dLdx, ctx.dLds, ctx.dLdm = x.requires_grad, s.requires_grad, mass.requires_grad
+        return x_bin, s_bin, mass_bin
+
+    @staticmethod
+    def backward(ctx, dL_dx_bin, dL_ds_bin, dL_dm_bin):
+        if dL_dx_bin is None:
+            dL_dx_bin = torch.zeros(ctx.x_shape, dtype=ctx.dtype, device=ctx.device)
+        if dL_ds_bin is None:
+            dL_ds_bin = torch.zeros(ctx.s_shape, dtype=ctx.dtype, device=ctx.device)
+        if dL_dm_bin is None:
+            dL_dm_bin = torch.zeros(ctx.m_shape, dtype=ctx.dtype, device=ctx.device)
+        dL_dx_bin, dL_ds_bin, dL_dm_bin = _c(dL_dx_bin), _c(dL_ds_bin), _c(dL_dm_bin)
+        grad_x = torch.empty_like(dL_dx_bin)
+        grad_s = torch.empty_like(dL_ds_bin)
+        grad_m = torch.empty_like(dL_dm_bin)
+        ctx.snapshot.grid.backward_bin_particles(dL_dx_bin, dL_ds_bin, dL_dm_bin, ctx.snapshot.permutation,
+                                                 grad_x, grad_s, grad_m)
+        return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
+                grad_m if ctx.dLdm else None, None)
+
+
+def bin_particles(x, s, snapshot, mass=None):
+    mass_is_none = mass is None
+    mass = _default_mass(x, mass)
+    x_bin, s_bin, mass_bin = Permute.apply(x, s, mass, snapshot)
+    if mass_is_none:
+        return x_bin, s_bin
+    return x_bin, s_bin, mass_bin
+
+
+def unbin_particles(x_bin, s_bin, snapshot, mass_bin=None):
+    x = torch.empty_like(x_bin)
+    s = torch.empty_like(s_bin)
+    mass_is_none = mass_bin is None
+    mass_bin = _default_mass(x_bin, mass_bin)
+    mass = torch.empty_like(mass_bin)
+    snapshot.grid.backward_bin_particles(_c(x_bin), _c(s_bin), _c(mass_bin), snapshot.permutation, x, s, mass)
+    if mass_is_none:
+        return x, s
+    return x, s, mass
+
+
+class Count(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x_bin, snapshot):
+        count = torch.empty(x_bin.shape[:-1], dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.count_forward(x_bin, count, snapshot.bin_offsets, snapshot.block_info)
+        return count
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        # the neighbour count is piecewise constant in x
+        return None, None
+
+
+def count(x_bin, snapshot):
+    return Count.apply(x_bin, snapshot)
+
+
+class Density(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x_bin, mass, snapshot):
+        rho = torch.empty(x_bin.shape[:-1], dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.density_forward(x_bin, mass, rho, snapshot.bin_offsets, snapshot.block_info)
+        ctx.save_for_backward(x_bin, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx = x_bin.requires_grad
+        return rho
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        if not ctx.dLdx:
+            return None, None, None
+        x_bin, mass = ctx.saved_tensors
+        snap = ctx.snapshot
+        grad_x = torch.empty_like(x_bin)
+        snap.grid.density_backward(x_bin, mass, _c(grad_output), grad_x, snap.bin_offsets, snap.block_info,
+                                   ctx.dLdx)
+        return grad_x, None, None
+
+
+def density(x_bin, snapshot, mass=None):
+    mass = _default_mass(x_bin, mass)
+    return Density.apply(x_bin, mass, snapshot)
+
+
+class Blur(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x_bin, s_bin, rho, mass, snapshot):
+        s_blur = torch.empty_like(s_bin)
+        snapshot.grid.blur_forward(x_bin, rho, mass, s_bin, s_blur, snapshot.bin_offsets, snapshot.block_info)
+        ctx.save_for_backward(x_bin, s_bin, rho, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
+        return s_blur
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x_bin, s_bin, rho, mass = ctx.saved_tensors
+        snap = ctx.snapshot
+        grad_s = torch.empty_like(s_bin)
+        grad_x = torch.empty_like(x_bin)
+        grad_rho = torch.empty_like(rho)
+        snap.grid.blur_backward(x_bin, rho, mass, s_bin, _c(grad_output), grad_x, grad_s, grad_rho,
+                                snap.bin_offsets, snap.block_info, ctx.dLdx, ctx.dLds, ctx.dLdrho)
+        return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
+                grad_rho if ctx.dLdrho else None, None, None)
+
+
+def blur(x_bin, rho, s_bin, snapshot, mass=None):
+    mass = _default_mass(x_bin, mass)
+    return Blur.apply(x_bin, s_bin, rho, mass, snapshot)
+
+
+def _gradient_backward(ctx, grad_output):
+    x_bin, s_bin, rho, mass = ctx.saved_tensors
+    snap = ctx.snapshot
+    grad_s = torch.empty_like(s_bin)
+    grad_x = torch.empty_like(x_bin)
+    grad_rho = torch.empty_like(rho)
+    snap.grid.gradient_backward(x_bin, rho, mass, s_bin, _c(grad_output), grad_x, grad_s, grad_rho,
+                                snap.bin_offsets, snap.block_info, ctx.dLdx, ctx.dLds, ctx.dLdrho)
+    return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
+            grad_rho if ctx.dLdrho else None, None, None)
+
+
+class Gradient(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x_bin, s_bin, rho, mass, snapshot):
+        grad_s = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.gradient_forward(x_bin, rho, mass, s_bin, grad_s, snapshot.bin_offsets, snapshot.block_info)
+        ctx.save_for_backward(x_bin, s_bin, rho, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
+        return grad_s
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return _gradient_backward(ctx, grad_output)
+
+
+def gradient(x_bin, rho, s_bin, snapshot, mass=None):
+    mass = _default_mass(x_bin, mass)
+    return Gradient.apply(x_bin, s_bin, rho, mass, snapshot)
+
+
+class DensityGradient(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x_bin, mass, snapshot):
+        out = torch.empty(*x_bin.shape[:-1], snapshot.dim, dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.density_gradient_forward(x_bin, mass, out, snapshot.bin_offsets, snapshot.block_info)
+        ctx.save_for_backward(x_bin, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx = x_bin.requires_grad
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        if not ctx.dLdx:
+            return None, None, None
+        x_bin, mass = ctx.saved_tensors
+        snap = ctx.snapshot
+        grad_x = torch.empty_like(x_bin)
+        snap.grid.density_gradient_backward(x_bin, mass, _c(grad_output), grad_x, snap.bin_offsets,
+                                            snap.block_info, ctx.dLdx)
+        return grad_x, None, None
+
+
+def density_gradient(x_bin, snapshot, mass=None):
+    mass = _default_mass(x_bin, mass)
+    return DensityGradient.apply(x_bin, mass, snapshot)
+
+
+class MomentMatrix(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x_bin, rho, mass, snapshot):
+        D = snapshot.dim
+        M = torch.empty(*x_bin.shape[:-1], D, D, dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.moment_matrix_forward(x_bin, rho, mass, M, snapshot.bin_offsets, snapshot.block_info)
+        ctx.save_for_backward(x_bin, rho, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx, ctx.dLdrho = x_bin.requires_grad, rho.requires_grad
+        return M
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x_bin, rho, mass = ctx.saved_tensors
+        snap = ctx.snapshot
+        grad_x = torch.empty_like(x_bin)
+        grad_rho = torch.empty_like(rho)
+        snap.grid.moment_matrix_backward(x_bin, rho, mass, _c(grad_output), grad_x, grad_rho, snap.bin_offsets,
+                                         snap.block_info, ctx.dLdx, ctx.dLdrho)
+        return grad_x if ctx.dLdx else None, grad_rho if ctx.dLdrho else None, None, None
+
+
+def moment_matrix(x_bin, rho, snapshot, mass=None):
+    mass = _default_mass(x_bin, mass)
+    return MomentMatrix.apply(x_bin, rho, mass, snapshot)
+
+
+@torch.no_grad()
+def safe_inv_sym_mat(M, rtol=1e-6):
+    """Inverse of symmetric 2x2/3x3 matrices, identity where ``|det| < rtol``
+    (an absolute threshold, as in the reference, ``sphops/sph.py:467-471``)."""
+    M_inv = torch.empty_like(M)
+    sph_hip.safe_inv_sym_mat(_c(M), M_inv, rtol)
+    return M_inv
+
+
+class GradientHybrid(torch.autograd.Function):
+    """Forward ``raw @ safe_inv(M)`` in one kernel; backward is the gradient
+    operator's backward applied to the upstream gradient unchanged (the
+    reference's ``raw + (raw @ L - raw).detach()``)."""
+
+    @staticmethod
+    def forward(ctx, x_bin, s_bin, rho, mass, snapshot, tol):
+        out = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.gradient_hybrid_forward(x_bin, rho, mass, s_bin, out, snapshot.bin_offsets,
+                                              snapshot.block_info, tol)
+        ctx.save_for_backward(x_bin, s_bin, rho, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return _gradient_backward(ctx, grad_output) + (None,)
+
+
+def gradient_hybrid(x_bin, rho, s_bin, snapshot, mass=None):
+    """Moment-corrected state gradient (``sphops/sph.py:474-484``): the value
+    is ``gradient(...) @ safe_inv_sym_mat(moment_matrix(...), 1e-3)`` and the
+    gradient flows straight through to the raw gradient."""
+    if snapshot.dim not in (2, 3):
+        with torch.no_grad():
+            M = moment_matrix(x_bin, rho, snapshot, mass=mass)
+            L = torch.linalg.pinv(M, hermitian=True, rtol=1e-3)
+        raw = gradient(x_bin, rho, s_bin, snapshot, mass=mass)
+        return raw + (raw @ L - raw).detach()
+    mass = _default_mass(x_bin, mass)
+    return GradientHybrid.apply(x_bin, s_bin, rho, mass, snapshot, 1e-3)

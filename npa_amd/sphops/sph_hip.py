@@ -1,0 +1,371 @@
+"""Native class surface of the gfx950 sphops library.
+
+Mirrors the reference's nanobind module ``sph_cuda``
+(``sphops/sph_cuda.cu:3228-3441``): the classes ``HashGrid2DPeriodic``,
+``HashGrid2DBox``, ``HashGrid3DPeriodic``, ``HashGrid3DBox`` and their
+particle-mode ``VHashGrid*`` twins, with the same constructor arguments,
+read-only properties and method argument order, plus the module function
+``safe_inv_sym_mat``.
+
+Argument checks follow the reference: a tensor of the wrong dtype, device,
+layout or rank raises ``TypeError`` (nanobind's ndarray type check,
+``sph_cuda.cu:12-18``); a wrong size raises ``RuntimeError`` with the
+reference's message (``validate_array_shape``, ``utils.cuh:526-566``); a
+failure inside the library raises ``RuntimeError``.
+
+Every call enqueues work on the current HIP stream of the tensor's device and
+returns without synchronising.
+"""
+import ctypes
+
+import torch
+
+from . import _native
+
+_lib = _native.lib
+_check = _native.check
+
+CLAMPED, PERIODIC = 0, 1
+MODE_GRID, MODE_PARTICLE = 0, 1
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _arr(t, name, dtype, ndim):
+    """nanobind-style type check: dtype, device, C-contiguity and rank."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise TypeError(f"{name}: expected a GPU tensor, got device {t.device}")
+    if not t.is_contiguous():
+        raise TypeError(f"{name}: expected a C-contiguous tensor")
+    if t.dim() != ndim:
+        raise TypeError(f"{name}: expected {ndim} dimensions, got {t.dim()}")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _validate_shape(t, expected, name):
+    """``validate_array_shape`` (``sphops/utils.cuh:526-566``)."""
+    if t.dim() != len(expected):
+        raise RuntimeError(f"{name} must have {len(expected)} dimensions, got {t.dim()}")
+    for got, want in zip(t.shape, expected):
+        if got != want:
+            exp = "(" + ", ".join(str(v) for v in expected) + ")"
+            act = "(" + ", ".join(str(v) for v in t.shape) + ")"
+            raise RuntimeError(f"{name} must have shape {exp}, got {act}")
+
+
+_F32, _I32 = torch.float32, torch.int32
+
+
+class _HashGridNative:
+    """Common implementation of the eight grid classes."""
+
+    _dim = 2
+    _boundary = CLAMPED
+    _mode = MODE_GRID
+
+    def __init__(self, *args, **kwargs):
+        names = ["grid_size_x", "grid_size_y"] + (["grid_size_z"] if self._dim == 3 else []) + [
+            "eps", "particle_count", "batch_size", "max_particles_per_block"]
+        vals = dict(zip(names, args))
+        for k, v in kwargs.items():
+            if k not in names:
+                raise TypeError(f"unexpected keyword argument {k!r}")
+            if k in vals:
+                raise TypeError(f"duplicate argument {k!r}")
+            vals[k] = v
+        vals.setdefault("max_particles_per_block", 64)
+        missing = [n for n in names if n not in vals]
+        if missing:
+            raise TypeError(f"missing arguments: {missing}")
+        self._sizes = [int(vals[n]) for n in names[: self._dim]]
+        self._eps = float(torch.tensor(float(vals["eps"]), dtype=torch.float32))
+        self._n = int(vals["particle_count"])
+        self._b = int(vals["batch_size"])
+        self._maxp = int(vals["max_particles_per_block"])
+        for name, v in (("particle_count", self._n), ("batch_size", self._b),
+                        ("max_particles_per_block", self._maxp)):
+            if v < 0 or v >= 2 ** 32:
+                raise TypeError(f"{name} must fit an unsigned 32-bit integer")
+        gs = (ctypes.c_int32 * self._dim)(*self._sizes)
+        handle = ctypes.c_void_p()
+        self._h = None
+        _check(_lib.sphops_grid_create(self._dim, self._boundary, self._mode, gs, ctypes.c_float(self._eps),
+                                       self._n, self._b, self._maxp, ctypes.byref(handle)))
+        self._h = handle
+        self._device = torch.device("cuda", torch.cuda.current_device())
+        self._pw = 2 if self._dim == 2 else 4
+        self._cells = 1
+        for s in self._sizes:
+            self._cells *= s
+        c6, cs = ctypes.c_float(), ctypes.c_float()
+        _check(_lib.sphops_grid_coefficients(self._h, ctypes.byref(c6), ctypes.byref(cs)))
+        self.smoothing_coef, self.spiky_coef = c6.value, cs.value
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.sphops_grid_destroy(h)
+            self._h = None
+
+    # ---- properties (sph_cuda.cu:3229-3237)
+    @property
+    def grid_size_x(self):
+        return self._sizes[0]
+
+    @property
+    def grid_size_y(self):
+        return self._sizes[1]
+
+    @property
+    def eps(self):
+        return self._eps
+
+    @property
+    def particle_count(self):
+        return self._n
+
+    @property
+    def batch_size(self):
+        return self._b
+
+    @property
+    def max_blocks(self):
+        return int(_lib.sphops_grid_max_blocks(self._h))
+
+    @property
+    def max_particles_per_block(self):
+        return self._maxp
+
+    @property
+    def cell_count(self):
+        return self._cells
+
+    # ---- shape helpers
+    def _pos(self, t, name):
+        p = _arr(t, name, _F32, 3)
+        _validate_shape(t, (self._b, self._n, self._pw), name)
+        return p
+
+    def _bn(self, t, name):
+        p = _arr(t, name, _F32, 2)
+        _validate_shape(t, (self._b, self._n), name)
+        return p
+
+    def _state(self, t, name, C):
+        p = _arr(t, name, _F32, 3)
+        _validate_shape(t, (self._b, self._n, C), name)
+        return p
+
+    def _offsets(self, t):
+        p = _arr(t, "bin_offsets", _I32, 1)
+        _validate_shape(t, (self._b * self._cells + 1,), "bin_offsets")
+        return p
+
+    def _blocks(self, t):
+        if t is None:
+            return ctypes.c_void_p()
+        if not isinstance(t, torch.Tensor) or t.dtype != _I32 or t.dim() != 2 or t.shape[-1] != 4:
+            raise TypeError("block_info: expected an int32 tensor of shape (max_blocks, 4)")
+        if self._mode == MODE_GRID:
+            _validate_shape(t, (self.max_blocks, 4), "block_info")
+        return ctypes.c_void_p(t.data_ptr())
+
+    # ---- binning (sph_cuda.cu:1926-2056)
+    def initialize(self, positions, permutation, bin_offsets, block_info, total_blocks=None):
+        x = self._pos(positions, "positions")
+        bo = self._offsets(bin_offsets)
+        pm = _arr(permutation, "permutation", _I32, 2)
+        _validate_shape(permutation, (self._b, self._n), "permutation")
+        if self._mode == MODE_GRID:
+            bi = _arr(block_info, "block_info", _I32, 2)
+            _validate_shape(block_info, (self.max_blocks, 4), "block_info")
+        else:
+            bi = ctypes.c_void_p(block_info.data_ptr()) if block_info is not None else ctypes.c_void_p()
+        tb = ctypes.c_void_p()
+        if total_blocks is not None:
+            tb = _arr(total_blocks, "total_blocks", _I32, 1)
+        _check(_lib.sphops_initialize(self._h, x, pm, bo, bi, tb, _stream(positions)))
+
+    def bin_particles(self, input_positions, input_state, input_mass, permutation, output_positions,
+                      output_state, output_mass):
+        C = input_state.shape[2] if input_state.dim() == 3 else -1
+        args = self._move_args(input_positions, input_state, input_mass, permutation, output_positions,
+                               output_state, output_mass, C,
+                               ("input_positions", "input_state", "input_mass", "permutation",
+                                "output_positions", "output_state", "output_mass"))
+        _check(_lib.sphops_bin_particles(self._h, *args, C, _stream(input_positions)))
+
+    def backward_bin_particles(self, grad_output_positions, grad_output_state, grad_output_mass, permutation,
+                               grad_input_positions, grad_input_state, grad_input_mass):
+        C = grad_output_state.shape[2] if grad_output_state.dim() == 3 else -1
+        args = self._move_args(grad_output_positions, grad_output_state, grad_output_mass, permutation,
+                               grad_input_positions, grad_input_state, grad_input_mass, C,
+                               ("grad_output_positions", "grad_output_state", "grad_output_mass", "permutation",
+                                "grad_input_positions", "grad_input_state", "grad_input_mass"))
+        _check(_lib.sphops_backward_bin_particles(self._h, *args, C, _stream(grad_output_positions)))
+
+    def _move_args(self, ip, is_, im, perm, op, os_, om, C, names):
+        out = [self._pos(ip, names[0]), self._state(is_, names[1], C), self._bn(im, names[2])]
+        out.append(_arr(perm, names[3], _I32, 2))
+        _validate_shape(perm, (self._b, self._n), names[3])
+        out += [self._pos(op, names[4]), self._state(os_, names[5], C), self._bn(om, names[6])]
+        return out
+
+    # ---- forward operators (sph_cuda.cu:2058-2499)
+    def density_forward(self, binned_positions, mass, rho, bin_offsets, block_info):
+        _check(_lib.sphops_density_forward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(mass, "mass"),
+            self._bn(rho, "rho"), self._offsets(bin_offsets), self._blocks(block_info),
+            _stream(binned_positions)))
+
+    def count_forward(self, binned_positions, count, bin_offsets, block_info):
+        _check(_lib.sphops_count_forward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(count, "count"),
+            self._offsets(bin_offsets), self._blocks(block_info), _stream(binned_positions)))
+
+    def blur_forward(self, binned_positions, rho, mass, state_in, state_out, bin_offsets, block_info):
+        C = state_in.shape[2] if state_in.dim() == 3 else -1
+        _check(_lib.sphops_blur_forward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(rho, "rho"),
+            self._bn(mass, "mass"), self._state(state_in, "state_in", C),
+            self._state(state_out, "state_out", C), C, self._offsets(bin_offsets), self._blocks(block_info),
+            _stream(binned_positions)))
+
+    def gradient_forward(self, binned_positions, rho, mass, state_in, state_gradient_out, bin_offsets, block_info):
+        C = state_in.shape[2] if state_in.dim() == 3 else -1
+        go = _arr(state_gradient_out, "state_gradient_out", _F32, 4)
+        _validate_shape(state_gradient_out, (self._b, self._n, C, self._dim), "state_gradient_out")
+        _check(_lib.sphops_gradient_forward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(rho, "rho"),
+            self._bn(mass, "mass"), self._state(state_in, "state_in", C), go, C, self._offsets(bin_offsets),
+            self._blocks(block_info), _stream(binned_positions)))
+
+    def gradient_hybrid_forward(self, binned_positions, rho, mass, state_in, out, bin_offsets, block_info,
+                                tol=1e-3):
+        """Fused ``raw @ safe_inv(M, tol)`` (no native counterpart in the
+        reference; replaces the composite of ``sphops/sph.py:474-484``)."""
+        C = state_in.shape[2] if state_in.dim() == 3 else -1
+        go = _arr(out, "out", _F32, 4)
+        _validate_shape(out, (self._b, self._n, C, self._dim), "out")
+        _check(_lib.sphops_gradient_hybrid_forward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(rho, "rho"),
+            self._bn(mass, "mass"), self._state(state_in, "state_in", C), go, C, ctypes.c_float(tol),
+            self._offsets(bin_offsets), self._blocks(block_info), _stream(binned_positions)))
+
+    def density_gradient_forward(self, binned_positions, mass, density_gradient_out, bin_offsets, block_info):
+        go = _arr(density_gradient_out, "density_gradient_out", _F32, 3)
+        _validate_shape(density_gradient_out, (self._b, self._n, self._dim), "density_gradient_out")
+        _check(_lib.sphops_density_gradient_forward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(mass, "mass"), go,
+            self._offsets(bin_offsets), self._blocks(block_info), _stream(binned_positions)))
+
+    def moment_matrix_forward(self, binned_positions, rho, mass, moment_matrix_out, bin_offsets, block_info):
+        mo = _arr(moment_matrix_out, "moment_matrix_out", _F32, 4)
+        _validate_shape(moment_matrix_out, (self._b, self._n, self._dim, self._dim), "moment_matrix_out")
+        _check(_lib.sphops_moment_matrix_forward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(rho, "rho"),
+            self._bn(mass, "mass"), mo, self._offsets(bin_offsets), self._blocks(block_info),
+            _stream(binned_positions)))
+
+    # ---- backward operators (sph_cuda.cu:2501-3046)
+    def density_backward(self, binned_positions, mass, dL_rho_out, grad_x, bin_offsets, block_info, dLdx=True):
+        if not dLdx:
+            return
+        _check(_lib.sphops_density_backward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(mass, "mass"),
+            self._bn(dL_rho_out, "grad_output_rho"), self._pos(grad_x, "grad_x"), self._offsets(bin_offsets),
+            self._blocks(block_info), 1, _stream(binned_positions)))
+
+    def blur_backward(self, binned_positions, rho, mass, state_in, dL_blur_state_out, grad_x, grad_s, grad_rho,
+                      bin_offsets, block_info, dLdx=True, dLds=True, dLdrho=True):
+        if not (dLdx or dLds or dLdrho):
+            return
+        C = state_in.shape[2] if state_in.dim() == 3 else -1
+        ds_only = dLds and not dLdx and not dLdrho
+        gx = ctypes.c_void_p() if ds_only else self._pos(grad_x, "grad_x")
+        gr = ctypes.c_void_p() if ds_only else self._bn(grad_rho, "grad_rho")
+        _check(_lib.sphops_blur_backward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(rho, "rho"),
+            self._bn(mass, "mass"), self._state(state_in, "state_in", C),
+            self._state(dL_blur_state_out, "dL_blur_state_out", C), gx, self._state(grad_s, "grad_s", C), gr, C,
+            self._offsets(bin_offsets), self._blocks(block_info), int(bool(dLdx)), int(bool(dLds)),
+            int(bool(dLdrho)), _stream(binned_positions)))
+
+    def density_gradient_backward(self, binned_positions, mass, dL_density_gradient_out, grad_x, bin_offsets,
+                                  block_info, dLdx=True):
+        if not dLdx:
+            return
+        dl = _arr(dL_density_gradient_out, "dL_density_gradient_out", _F32, 3)
+        _validate_shape(dL_density_gradient_out, (self._b, self._n, self._dim), "dL_density_gradient_out")
+        _check(_lib.sphops_density_gradient_backward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(mass, "mass"), dl,
+            self._pos(grad_x, "grad_x"), self._offsets(bin_offsets), self._blocks(block_info), 1,
+            _stream(binned_positions)))
+
+    def gradient_backward(self, binned_positions, rho, mass, state_in, dL_grad_state_out, grad_x, grad_s, grad_rho,
+                          bin_offsets, block_info, dLdx=True, dLds=True, dLdrho=True):
+        if not (dLdx or dLds or dLdrho):
+            return
+        C = state_in.shape[2] if state_in.dim() == 3 else -1
+        dl = _arr(dL_grad_state_out, "dL_grad_state_out", _F32, 4)
+        _validate_shape(dL_grad_state_out, (self._b, self._n, C, self._dim), "dL_grad_state_out")
+        ds_only = dLds and not dLdx and not dLdrho
+        gx = ctypes.c_void_p() if ds_only else self._pos(grad_x, "grad_x")
+        gr = ctypes.c_void_p() if ds_only else self._bn(grad_rho, "grad_rho")
+        _check(_lib.sphops_gradient_backward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(rho, "rho"),
+            self._bn(mass, "mass"), self._state(state_in, "state_in", C), dl, gx,
+            self._state(grad_s, "grad_s", C), gr, C, self._offsets(bin_offsets), self._blocks(block_info),
+            int(bool(dLdx)), int(bool(dLds)), int(bool(dLdrho)), _stream(binned_positions)))
+
+    def moment_matrix_backward(self, binned_positions, rho, mass, dL_moment_matrix_out, grad_x, grad_rho,
+                               bin_offsets, block_info, dLdx=True, dLdrho=True):
+        if not (dLdx or dLdrho):
+            return
+        dl = _arr(dL_moment_matrix_out, "dL_moment_matrix_out", _F32, 4)
+        _validate_shape(dL_moment_matrix_out, (self._b, self._n, self._dim, self._dim), "dL_moment_matrix_out")
+        _check(_lib.sphops_moment_matrix_backward(
+            self._h, self._pos(binned_positions, "binned_positions"), self._bn(rho, "rho"),
+            self._bn(mass, "mass"), dl, self._pos(grad_x, "grad_x"), self._bn(grad_rho, "grad_rho"),
+            self._offsets(bin_offsets), self._blocks(block_info), 1, 1, _stream(binned_positions)))
+
+
+class _Grid3DProps:
+    @property
+    def grid_size_z(self):
+        return self._sizes[2]
+
+
+def _make(name, dim, boundary, mode):
+    bases = (_Grid3DProps, _HashGridNative) if dim == 3 else (_HashGridNative,)
+    return type(name, bases, {"_dim": dim, "_boundary": boundary, "_mode": mode, "__module__": __name__})
+
+
+HashGrid2DPeriodic = _make("HashGrid2DPeriodic", 2, PERIODIC, MODE_GRID)
+HashGrid2DBox = _make("HashGrid2DBox", 2, CLAMPED, MODE_GRID)
+VHashGrid2DPeriodic = _make("VHashGrid2DPeriodic", 2, PERIODIC, MODE_PARTICLE)
+VHashGrid2DBox = _make("VHashGrid2DBox", 2, CLAMPED, MODE_PARTICLE)
+HashGrid3DPeriodic = _make("HashGrid3DPeriodic", 3, PERIODIC, MODE_GRID)
+HashGrid3DBox = _make("HashGrid3DBox", 3, CLAMPED, MODE_GRID)
+VHashGrid3DPeriodic = _make("VHashGrid3DPeriodic", 3, PERIODIC, MODE_PARTICLE)
+VHashGrid3DBox = _make("VHashGrid3DBox", 3, CLAMPED, MODE_PARTICLE)
+
+
+def safe_inv_sym_mat(in_matrix, out_matrix, tol=1e-3):
+    """Module function ``safe_inv_sym_mat(in, out, tol)`` (``sph_cuda.cu:3181-3226``)."""
+    if not isinstance(in_matrix, torch.Tensor) or in_matrix.dim() != 4:
+        raise TypeError("in_matrix: expected a 4-d float32 tensor")
+    B, N, D = in_matrix.shape[0], in_matrix.shape[1], in_matrix.shape[2]
+    if D not in (2, 3):
+        raise RuntimeError("safe_inverse only supports 2x2 or 3x3 matrices.")
+    pi = _arr(in_matrix, "in_matrix", _F32, 4)
+    po = _arr(out_matrix, "out_matrix", _F32, 4)
+    _validate_shape(in_matrix, (B, N, D, D), "in_matrix")
+    _validate_shape(out_matrix, (B, N, D, D), "out_matrix")
+    _check(_lib.sphops_safe_inv_sym_mat(pi, po, B * N, D, ctypes.c_float(tol), _stream(in_matrix)))

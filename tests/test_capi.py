@@ -1,0 +1,52 @@
+"""The C-ABI library loads and exports every symbol include/sphops_hip.h declares
+(no compute calls: this runs without a GPU)."""
+import ctypes
+import os
+import re
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "sphops_hip.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sphops_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_reference_surface():
+    names = declared()
+    for meth in ("initialize", "bin_particles", "backward_bin_particles", "count_forward", "density_forward",
+                 "blur_forward", "gradient_forward", "density_gradient_forward", "moment_matrix_forward",
+                 "density_backward", "blur_backward", "density_gradient_backward", "gradient_backward",
+                 "moment_matrix_backward", "safe_inv_sym_mat"):
+        assert f"sphops_{meth}" in names
+
+
+def test_library_exports_every_declared_symbol():
+    from npa_amd.sphops import _native
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(declared()) == set(_native.EXPORTED)
+
+
+def test_abi_version_and_error_channel():
+    from npa_amd.sphops import _native
+    assert _native.lib.sphops_abi_version() == 1
+    # a failing call without touching the GPU: invalid dimension
+    h = ctypes.c_void_p()
+    gs = (ctypes.c_int32 * 2)(4, 4)
+    st = _native.lib.sphops_grid_create(5, 0, 0, gs, ctypes.c_float(0.1), 10, 1, 64, ctypes.byref(h))
+    assert st != 0
+    assert b"dim must be 2 or 3" in _native.lib.sphops_last_error()
+    st = _native.lib.sphops_grid_create(2, 1, 0, gs, ctypes.c_float(0.1), 10, 1, 64, ctypes.byref(h))
+    gs2 = (ctypes.c_int32 * 2)(2, 4)
+    st = _native.lib.sphops_grid_create(2, 1, 0, gs2, ctypes.c_float(0.1), 10, 1, 64, ctypes.byref(h))
+    assert st != 0 and b"at least 3 cells" in _native.lib.sphops_last_error()
+    gs3 = (ctypes.c_int32 * 2)(8, 16)
+    st = _native.lib.sphops_grid_create(2, 0, 1, gs3, ctypes.c_float(0.1), 10, 1, 64, ctypes.byref(h))
+    assert st != 0 and b"Morton" in _native.lib.sphops_last_error()
+    st = _native.lib.sphops_safe_inv_sym_mat(None, None, 4, 4, ctypes.c_float(1e-3), None)
+    assert st != 0 and b"2x2 or 3x3" in _native.lib.sphops_last_error()
