@@ -130,6 +130,69 @@ int sphops_moment_matrix_backward(const sphops_grid* grid, const float* x, const
                                   const int32_t* bin_offsets, const int32_t* block_info, int dLdx, int dLdrho,
                                   void* stream);
 
+/* ---- generic operator interface (the path the Python layer uses) -------
+ *
+ * One entry point per direction for every perception operator, with an
+ * optional per-snapshot neighbour list.  The reference has no counterpart:
+ * its methods above traverse the cell stencil on every call.  Building the
+ * list once per snapshot (sphops_neighbor_count + sphops_neighbor_fill) and
+ * passing it here makes every later operator walk only in-radius pairs;
+ * results are identical (same pairs, same order, same arithmetic). */
+
+#define SPHOPS_OP_COUNT 0
+#define SPHOPS_OP_DENSITY 1
+#define SPHOPS_OP_DENSITY_GRADIENT 2
+#define SPHOPS_OP_MOMENT_MATRIX 3
+#define SPHOPS_OP_BLUR 4
+#define SPHOPS_OP_GRADIENT 5
+#define SPHOPS_OP_GRADIENT_HYBRID 6
+
+typedef struct sphops_args {
+  const float* x;              /* binned positions (B,N,2|4) */
+  const float* mass;           /* (B,N) */
+  const float* rho;            /* (B,N): blur, gradient, gradient_hybrid, moment_matrix */
+  const float* state;          /* (B,N,C): blur, gradient, gradient_hybrid */
+  const float* upstream;       /* backward: dL/d(output), shaped like the forward output */
+  float* out;                  /* forward: the output; backward: dL/dx (B,N,2|4) */
+  float* grad_state;           /* backward: dL/ds (B,N,C) */
+  float* grad_rho;             /* backward: dL/drho (B,N) */
+  uint32_t feature_dim;        /* C */
+  float tol;                   /* gradient_hybrid: safe-inverse threshold */
+  const int32_t* bin_offsets;  /* (B*G+1) from sphops_initialize */
+  const int32_t* nbr_offsets;  /* optional (B*N+1) CSR offsets from sphops_neighbor_count */
+  const int32_t* nbr_index;    /* optional CSR indices from sphops_neighbor_fill; NULL: scan the stencil */
+  const int32_t* nbr_order;    /* optional particle order by list-length class (sphops_neighbor_schedule) */
+  int32_t nbr_class_count[4];  /* host copy of the class sizes written by sphops_neighbor_schedule */
+} sphops_args;
+
+/* Forward operator `op` (SPHOPS_OP_*) on binned particles. */
+int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream);
+
+/* Backward of operator `op` (not COUNT); flags as in the per-operator
+ * functions above.  For SPHOPS_OP_GRADIENT_HYBRID it is the gradient
+ * operator's backward (straight-through, sphops/sph.py:482). */
+int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLdrho, const sphops_args* args,
+                    void* stream);
+
+/* In-radius neighbour count of every binned particle (pairs |r| < eps incl.
+ * self, the reference's `count` as integers) written to nbr_offsets[0..B*N),
+ * then scanned in place: nbr_offsets becomes the exclusive prefix sum with the
+ * total number of pairs in nbr_offsets[B*N]. */
+int sphops_neighbor_count(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
+                          int32_t* nbr_offsets, void* stream);
+
+/* Fill nbr_index[nbr_offsets[i] .. nbr_offsets[i+1]) with the binned indices
+ * of i's in-radius neighbours in stencil order. */
+int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
+                         const int32_t* nbr_offsets, int32_t* nbr_index, void* stream);
+
+/* Schedule for list traversal: a stable partition of the binned particles by
+ * list length into four classes (<=4, <=32, <=128, >128 neighbours), served by
+ * groups of 1, 4, 16 and 64 lanes per particle.  nbr_order (B*N) receives the
+ * particles class by class; class_counts (4 device int32) the class sizes. */
+int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_offsets, int32_t* nbr_order,
+                             int32_t* class_counts, void* stream);
+
 /* Module function safe_inv_sym_mat (sph_cuda.cu:3181-3226): `count` symmetric
  * dim x dim matrices (dim 2 or 3), identity where |det| < tol. */
 int sphops_safe_inv_sym_mat(const float* in_matrix, float* out_matrix, int64_t count, int dim, float tol,

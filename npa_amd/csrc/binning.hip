@@ -410,6 +410,123 @@ inline dim3 blocks_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) /
 
 }  // namespace
 
+// ------------------------------------------------ neighbour-list schedule
+//
+// Stable partition of the binned particles into four classes by neighbour
+// list length (<=4, <=32, <=128, more), which the pair kernels serve with
+// groups of 1, 4, 16 and 64 lanes per particle.
+
+namespace {
+
+__device__ __forceinline__ uint32_t length_class(int32_t len) {
+  return len <= 4 ? 0u : (len <= 32 ? 1u : (len <= 128 ? 2u : 3u));
+}
+
+__global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restrict__ nptr, uint32_t n,
+                                                          uint32_t* __restrict__ cnt, uint32_t ntiles) {
+  __shared__ uint32_t h[4];
+  if (threadIdx.x < 4) h[threadIdx.x] = 0;
+  __syncthreads();
+  const uint32_t base = blockIdx.x * kTile;
+  uint32_t c[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const uint32_t idx = base + i * kThreads + threadIdx.x;
+    if (idx < n) {
+      const uint32_t k = length_class(nptr[idx + 1] - nptr[idx]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[q] += (k == (uint32_t)q);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t v = c[q];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+    if (__lane_id() == 0) atomicAdd(&h[q], v);
+  }
+  __syncthreads();
+  if (threadIdx.x < 4) cnt[threadIdx.x * ntiles + blockIdx.x] = h[threadIdx.x];
+}
+
+// Same tile walk as the radix scatter: wave w owns items [w*1024, (w+1)*1024)
+// in index order; two ballots identify lanes of the same class.
+__global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __restrict__ nptr, uint32_t n,
+                                                            const uint32_t* __restrict__ cnt_scan, uint32_t ntiles,
+                                                            int32_t* __restrict__ order) {
+  __shared__ uint32_t wcnt[kThreads / 64][4];
+  __shared__ uint32_t gbase[4];
+  const int wave = threadIdx.x >> 6, lane = __lane_id();
+  if (threadIdx.x < (kThreads / 64) * 4) (&wcnt[0][0])[threadIdx.x] = 0;
+  if (threadIdx.x < 4) gbase[threadIdx.x] = cnt_scan[threadIdx.x * ntiles + blockIdx.x];
+  __syncthreads();
+  const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
+  const uint64_t below_mask = lanemask_lt();
+  uint32_t cls[kItems], rank[kItems];
+#pragma unroll
+  for (int t = 0; t < kItems; ++t) {
+    const uint32_t idx = base + t * 64 + lane;
+    const bool valid = idx < n;
+    const uint32_t k = valid ? length_class(nptr[idx + 1] - nptr[idx]) : 0u;
+    cls[t] = k;
+    uint64_t peers = __ballot(valid);
+    const uint64_t b0 = __ballot(k & 1u), b1 = __ballot((k >> 1) & 1u);
+    peers &= (k & 1u) ? b0 : ~b0;
+    peers &= (k & 2u) ? b1 : ~b1;
+    const uint32_t before = (uint32_t)__popcll(peers & below_mask);
+    const uint32_t prior = wcnt[wave][k];
+    if (valid && before == 0) wcnt[wave][k] = prior + (uint32_t)__popcll(peers);
+    rank[t] = prior + before;
+  }
+  __syncthreads();
+  if (threadIdx.x < 4) {
+    uint32_t run = 0;
+    for (int w = 0; w < kThreads / 64; ++w) {
+      const uint32_t c = wcnt[w][threadIdx.x];
+      wcnt[w][threadIdx.x] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < kItems; ++t) {
+    const uint32_t idx = base + t * 64 + lane;
+    if (idx < n) order[gbase[cls[t]] + wcnt[wave][cls[t]] + rank[t]] = (int32_t)idx;
+  }
+}
+
+__global__ void k_class_totals(const uint32_t* __restrict__ cnt_scan, uint32_t ntiles, uint32_t n,
+                               int32_t* __restrict__ out) {
+  // class q holds [cnt_scan[q*ntiles], cnt_scan[(q+1)*ntiles]) of the order
+  const int q = threadIdx.x;
+  if (q < 4) {
+    const uint32_t lo = cnt_scan[q * ntiles];
+    const uint32_t hi = q < 3 ? cnt_scan[(q + 1) * ntiles] : n;
+    out[q] = (int32_t)(hi - lo);
+  }
+}
+
+}  // namespace
+
+void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, int32_t* class_counts,
+                            hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  if (n == 0) return;
+  const uint32_t ntiles = (uint32_t)g.n_tiles;
+  uint32_t* cnt = g.hist;  // 4 * ntiles <= 256 * ntiles words
+  hipLaunchKernelGGL(k_class_count, dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cnt, ntiles);
+  SPHOPS_LAUNCHED();
+  device_exclusive_scan(cnt, cnt, 4ull * ntiles, g.scan_tmp, nullptr, st);
+  hipLaunchKernelGGL(k_class_scatter, dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cnt, ntiles, order);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL(k_class_totals, dim3(1), dim3(64), 0, st, cnt, ntiles, n, class_counts);
+  SPHOPS_LAUNCHED();
+}
+
+void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* total, hipStream_t st) {
+  device_exclusive_scan(data, data, n, g.scan_tmp, total, st);
+}
+
 void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int32_t* block_info,
                      int32_t* total_blocks, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;

@@ -59,6 +59,7 @@ void free_grid(Grid* g) {
   (void)hipFree(g->chunk_end);
   (void)hipFree(g->chunk_lo);
   (void)hipFree(g->flags);
+  (void)hipFree(g->packed);
   delete g;
 }
 
@@ -225,6 +226,7 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->chunk_end = dalloc<uint32_t>(g->n_chunks);
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
       g->flags = dalloc<uint32_t>(BN + 1);
+      g->packed = dalloc<float4>(BN);
     } catch (...) {
       sphops::free_grid(g);
       throw;
@@ -467,6 +469,126 @@ int sphops_moment_matrix_backward(const sphops_grid* grid, const float* x, const
   a.out0 = grad_x;
   a.out2 = grad_rho;
   return bwd_op(grid, Op::MomentMatrix, true, bo, a, stream);
+}
+
+static OpPtrs from_args(const sphops_args* a) {
+  OpPtrs p;
+  p.x = a->x;
+  p.m = a->mass;
+  p.rho = a->rho;
+  p.s = a->state;
+  p.g = a->upstream;
+  p.out0 = a->out;
+  p.out1 = a->grad_state;
+  p.out2 = a->grad_rho;
+  p.C = a->feature_dim;
+  p.tol = a->tol;
+  p.nptr = a->nbr_offsets;
+  p.nidx = a->nbr_index;
+  p.order = a->nbr_order;
+  for (int c = 0; c < 4; ++c) p.class_count[c] = a->nbr_class_count[c];
+  return p;
+}
+
+static void check_list(const sphops_args* a) {
+  require(a->nbr_index == nullptr || a->nbr_offsets != nullptr, "nbr_index needs nbr_offsets");
+  require(a->nbr_order == nullptr || a->nbr_index != nullptr, "nbr_order needs nbr_index");
+  for (int c = 0; c < 4; ++c) require(a->nbr_class_count[c] >= 0, "negative class count");
+}
+
+int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream) {
+  if (args == nullptr) {
+    sphops::g_last_error = "args must not be NULL";
+    return -1;
+  }
+  if (op < SPHOPS_OP_COUNT || op > SPHOPS_OP_GRADIENT_HYBRID) {
+    sphops::g_last_error = "unknown operator " + std::to_string(op);
+    return -1;
+  }
+  int st = guarded([&] { check_list(args); });
+  if (st) return st;
+  return fwd_op(grid, static_cast<Op>(op), args->bin_offsets, from_args(args), stream);
+}
+
+int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLdrho, const sphops_args* args,
+                    void* stream) {
+  if (args == nullptr) {
+    sphops::g_last_error = "args must not be NULL";
+    return -1;
+  }
+  if (op <= SPHOPS_OP_COUNT || op > SPHOPS_OP_GRADIENT_HYBRID) {
+    sphops::g_last_error = "operator " + std::to_string(op) + " has no backward";
+    return -1;
+  }
+  int st = guarded([&] { check_list(args); });
+  if (st) return st;
+  const Op o = static_cast<Op>(op);
+  OpPtrs a = from_args(args);
+  switch (o) {
+    case Op::Density:
+    case Op::DensityGradient:
+      if (!dLdx) return 0;
+      return bwd_op(grid, o, true, args->bin_offsets, a, stream);
+    case Op::MomentMatrix:
+      if (!dLdx && !dLdrho) return 0;
+      return bwd_op(grid, o, true, args->bin_offsets, a, stream);
+    default: {
+      if (!dLdx && !dLds && !dLdrho) return 0;
+      const bool ds_only = dLds && !dLdx && !dLdrho;
+      return bwd_op(grid, o == Op::GradientHybrid ? Op::Gradient : o, !ds_only, args->bin_offsets, a, stream);
+    }
+  }
+}
+
+int sphops_neighbor_count(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* nbr_offsets,
+                          void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(bo != nullptr && nbr_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
+    require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
+    const hipStream_t st = sphops::as_stream(stream);
+    if (grid->n_keys == 0) {
+      SPHOPS_HIP(hipMemsetAsync(nbr_offsets, 0, sizeof(int32_t), st));
+      return;
+    }
+    OpPtrs a;
+    a.x = x;
+    a.iout = nbr_offsets;
+    sphops::forward(*grid, Op::NeighbourCount, bo, a, st);
+    sphops::exclusive_scan_u32(*grid, reinterpret_cast<uint32_t*>(nbr_offsets), grid->n_keys,
+                               reinterpret_cast<uint32_t*>(nbr_offsets) + grid->n_keys, st);
+  });
+}
+
+int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, const int32_t* nbr_offsets,
+                         int32_t* nbr_index, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(bo != nullptr && nbr_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
+    require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
+    if (grid->n_keys == 0) return;
+    require(nbr_index != nullptr, "nbr_index must not be NULL");
+    OpPtrs a;
+    a.x = x;
+    a.nptr = nbr_offsets;
+    a.iout = nbr_index;
+    sphops::forward(*grid, Op::NeighbourFill, bo, a, sphops::as_stream(stream));
+  });
+}
+
+int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_offsets, int32_t* nbr_order,
+                             int32_t* class_counts, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(nbr_offsets != nullptr && class_counts != nullptr && (nbr_order != nullptr || grid->n_keys == 0),
+            "null buffer");
+    const hipStream_t st = sphops::as_stream(stream);
+    if (grid->n_keys == 0) {
+      SPHOPS_HIP(hipMemsetAsync(class_counts, 0, 4 * sizeof(int32_t), st));
+      return;
+    }
+    sphops::run_neighbour_schedule(*grid, nbr_offsets, nbr_order, class_counts, st);
+  });
 }
 
 int sphops_safe_inv_sym_mat(const float* in, float* out, int64_t count, int dim, float tol, void* stream) {

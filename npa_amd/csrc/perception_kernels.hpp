@@ -1,20 +1,26 @@
 // SPH neighbour perception kernels (forward and gather-form backward) for gfx950.
 //
-// One lane owns one binned particle i and writes only i's outputs, so no
-// atomics are used and every result is deterministic.  The candidate set of i
-// is the 3^D cell stencil of its cell, read as contiguous slices of the
-// sorted particle arrays through bin_offsets: in grid mode 3^(D-1) rows of up
-// to three x-adjacent cells (plus the periodic wrap cell), as the reference
-// traverses them (sphops/sph_cuda.cu:1561-1640); in particle mode the 3^D
-// Morton cells (sphops/sph_cuda.cu:324-346).
+// One lane owns one binned particle i and writes only i's outputs: no atomics,
+// deterministic results.  Neighbour data is read through a packed float4 per
+// particle (x, y, z|0, weight), weight = mass or mass/rho depending on the
+// operator, so one 16-byte load gives a neighbour's position and weight.
 //
-// Operators with per-channel work run in two phases per round: every lane
-// first scans its candidates and appends in-radius neighbours to its own
-// column of a per-wave LDS list (kCap entries), then all lanes walk their
-// lists together, so the channel loops execute with the wave converged
-// instead of under the ~1-in-6 in-radius branch.  The formulas are the
-// reference's (sphops/sph_cuda.cu:218-721 and 1160-1375, sphops/utils.cuh:199-279),
-// with per-pair work hoisted out of the channel loops.
+// Three traversals of i's neighbours:
+//  * kList     — walk i's precomputed in-radius list (CSR, built once per
+//                snapshot by the count/fill operators below); no distance
+//                tests, no divergence beyond list length.
+//  * kStencil  — test every candidate of the 3^D cell stencil, four loads in
+//                flight per lane, and call the operator for in-radius pairs.
+//  * kStencil2 — the same scan, but in-radius neighbours are first appended to
+//                the lane's column of a per-wave LDS list and processed after,
+//                so channel loops run with the wave converged.
+// The stencil is read as contiguous slices of the sorted arrays through
+// bin_offsets: in grid mode 3^(D-1) rows of up to three x-adjacent cells (plus
+// the periodic wrap cell), as the reference traverses them
+// (sphops/sph_cuda.cu:1561-1640); in particle mode the 3^D Morton cells
+// (sphops/sph_cuda.cu:324-346).  Operator formulas are the reference's
+// (sphops/sph_cuda.cu:218-721, 1160-1375; sphops/utils.cuh:199-279) with
+// per-pair work hoisted out of the channel loops.
 #pragma once
 
 #include "sphops_internal.hpp"
@@ -24,6 +30,9 @@ namespace pk {
 
 constexpr int kThreads = 256;
 constexpr int kCap = 32;
+
+enum Trav { kList = 0, kStencil = 1, kStencil2 = 2 };
+enum Weight { kWNone = 0, kWMass = 1, kWVolume = 2 };
 
 // ------------------------------------------------------------- traversal
 
@@ -115,7 +124,6 @@ struct Walker {
 
 // ------------------------------------------------------------- row loads
 
-// Load one row of `n` floats (compile-time) starting at p + row*stride.
 template <int N, bool VEC>
 __device__ __forceinline__ void load_row(const float* __restrict__ p, uint64_t row, float* v) {
   if constexpr (VEC) {
@@ -134,11 +142,10 @@ __device__ __forceinline__ void load_row(const float* __restrict__ p, uint64_t r
   }
 }
 
-// Channel configuration: CM channels in registers; EXACT means C == CM and rows
-// can be loaded with 16-byte vectors, otherwise C <= CM with predication.
+// CM channels in registers; EXACT means C == CM (rows loaded as 16-byte
+// vectors when CM % 4 == 0), otherwise C <= CM with predication.
 template <int CM, bool EXACT>
 struct Chan {
-  static constexpr int kMax = CM;
   static constexpr bool kVec = EXACT && (CM % 4 == 0);
   __device__ static __forceinline__ void load(const float* __restrict__ p, uint64_t row, uint32_t C, float* v) {
     if constexpr (EXACT) {
@@ -148,7 +155,6 @@ struct Chan {
       for (int f = 0; f < CM; ++f) v[f] = (f < (int)C) ? p[row * C + f] : 0.0f;
     }
   }
-  // row of CM*D floats (gradient-shaped tensors)
   template <int D>
   __device__ static __forceinline__ void load_cd(const float* __restrict__ p, uint64_t row, uint32_t C, float* v) {
     if constexpr (EXACT) {
@@ -199,46 +205,109 @@ __device__ __forceinline__ void safe_inv_sym(const float* M, float tol, float* L
   }
 }
 
-// ------------------------------------------------------------- operators
+// displacement x_i - x_j as the reference's backward evaluates it
+template <int D, bool P>
+__device__ __forceinline__ float back_disp(const GridParams& g, const float* xi, const float* xj, const float* r_fwd,
+                                           float d2_fwd, float* rb) {
+  if constexpr (!P) {
+#pragma unroll
+    for (int e = 0; e < D; ++e) rb[e] = -r_fwd[e];
+    return d2_fwd;
+  } else {
+    return displacement<D, P>(g, xj, xi, rb);
+  }
+}
 
-// Single-phase operators receive (x_j, r = x_j - x_i, |r|^2) for every
-// in-radius candidate; two-phase operators receive j and reload what they need.
+// Sum over the aligned group of G lanes (G a power of two <= 64); every lane
+// of the group receives the same total (xor butterfly, fixed order).
+__device__ __forceinline__ float grp_sum(float v, int G) {
+  for (int off = 1; off < G; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void grp_sum(float (&v)[N], int G) {
+#pragma unroll
+  for (int q = 0; q < N; ++q) v[q] = grp_sum(v[q], G);
+}
+
+// ------------------------------------------------------------- operators
+//
+// Interface: init(g, a, k) at the owning lane, pair(g, a, xi, xj, wj, r, d2, j)
+// for every in-radius neighbour j (r = x_j - x_i wrapped, d2 = |r|^2 in fp32,
+// wj = the packed weight of j), finish(g, a, k).  kWeightKind selects what the
+// packed float4 carries in .w.
+
+template <int D, bool P>
+struct OpNeighbourCount {
+  static constexpr int kWeightKind = kWNone;
+  static constexpr bool kChannels = false;
+  int32_t n = 0;
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
+  __device__ void pair(const GridParams&, const OpPtrs&, const float*, const float*, float, const float*, float,
+                       uint32_t) {
+    ++n;
+  }
+  __device__ void reduce(int G) { (void)G; }
+  __device__ void finish(const GridParams&, const OpPtrs& a, uint32_t k) { a.iout[k] = n; }
+};
+
+template <int D, bool P>
+struct OpNeighbourFill {
+  static constexpr int kWeightKind = kWNone;
+  static constexpr bool kChannels = false;
+  int32_t pos = 0;
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) { pos = a.nptr[k]; }
+  __device__ void pair(const GridParams&, const OpPtrs& a, const float*, const float*, float, const float*, float,
+                       uint32_t j) {
+    a.iout[pos++] = (int32_t)j;
+  }
+  __device__ void reduce(int G) { (void)G; }
+  __device__ void finish(const GridParams&, const OpPtrs&, uint32_t) {}
+};
 
 template <int D, bool P>
 struct OpCount {
-  static constexpr bool kTwoPhase = false;
+  static constexpr int kWeightKind = kWNone;
+  static constexpr bool kChannels = false;
   float acc = 0.0f;
-  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
-  __device__ void pair(const GridParams&, const OpPtrs&, const float*, const float*, const float*, float, uint32_t) {
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
+  __device__ void pair(const GridParams&, const OpPtrs&, const float*, const float*, float, const float*, float,
+                       uint32_t) {
     acc += 1.0f;
   }
+  __device__ void reduce(int G) { (void)G; }
   __device__ void finish(const GridParams&, const OpPtrs& a, uint32_t k) { a.out0[k] = acc; }
 };
 
 template <int D, bool P>
 struct OpDensity {
-  static constexpr bool kTwoPhase = false;
+  static constexpr int kWeightKind = kWMass;
+  static constexpr bool kChannels = false;
   float acc = 0.0f;
-  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
-  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, const float*, float d2,
-                       uint32_t j) {
-    acc += poly6(g.eps2, d2) * a.m[j];
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
+  __device__ void pair(const GridParams& g, const OpPtrs&, const float*, const float*, float wj, const float*,
+                       float d2, uint32_t) {
+    acc += poly6(g.eps2, d2) * wj;
   }
+  __device__ void reduce(int G) { acc = grp_sum(acc, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { a.out0[k] = acc * g.c6; }
 };
 
 template <int D, bool P>
 struct OpDensityGradient {
-  static constexpr bool kTwoPhase = false;
+  static constexpr int kWeightKind = kWMass;
+  static constexpr bool kChannels = false;
   float acc[D] = {};
-  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
-  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, const float* r, float d2,
-                       uint32_t j) {
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
+  __device__ void pair(const GridParams& g, const OpPtrs&, const float*, const float*, float wj, const float* r,
+                       float d2, uint32_t) {
     float d;
-    const float t = spiky_mag(g.eps, d2, &d) * a.m[j];
+    const float t = spiky_mag(g.eps, d2, &d) * wj;
 #pragma unroll
     for (int e = 0; e < D; ++e) acc[e] += t * r[e];
   }
+  __device__ void reduce(int G) { grp_sum(acc, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
 #pragma unroll
     for (int e = 0; e < D; ++e) a.out0[(uint64_t)k * D + e] = acc[e] * g.cs;
@@ -247,18 +316,20 @@ struct OpDensityGradient {
 
 template <int D, bool P>
 struct OpMomentMatrix {
-  static constexpr bool kTwoPhase = false;
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = false;
   float acc[D * D] = {};
-  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
-  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, const float* r, float d2,
-                       uint32_t j) {
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
+  __device__ void pair(const GridParams& g, const OpPtrs&, const float*, const float*, float wj, const float* r,
+                       float d2, uint32_t) {
     float d;
-    const float t = spiky_mag(g.eps, d2, &d) * (a.m[j] / a.rho[j]);
+    const float t = spiky_mag(g.eps, d2, &d) * wj;
 #pragma unroll
     for (int p = 0; p < D; ++p)
 #pragma unroll
       for (int q = 0; q < D; ++q) acc[p * D + q] += t * r[p] * r[q];
   }
+  __device__ void reduce(int G) { grp_sum(acc, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
 #pragma unroll
     for (int q = 0; q < D * D; ++q) a.out0[(uint64_t)k * D * D + q] = acc[q] * g.cs;
@@ -267,20 +338,20 @@ struct OpMomentMatrix {
 
 template <int D, bool P, int CM, bool EX>
 struct OpBlur {
-  static constexpr bool kTwoPhase = true;
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = true;
   using Ch = Chan<CM, EX>;
   float acc[CM] = {};
-  __device__ void init(const GridParams&, const OpPtrs&, uint32_t, const float*) {}
-  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
-    float xj[3], r[3];
-    load_pos<D>(a.x, j, xj);
-    const float d2 = displacement<D, P>(g, xi, xj, r);
-    const float w = poly6(g.eps2, d2) * (a.m[j] / a.rho[j]);
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, float wj, const float*,
+                       float d2, uint32_t j) {
+    const float w = poly6(g.eps2, d2) * wj;
     float sj[CM];
     Ch::load(a.s, j, a.C, sj);
 #pragma unroll
     for (int f = 0; f < CM; ++f) acc[f] += w * sj[f];
   }
+  __device__ void reduce(int G) { grp_sum(acc, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
 #pragma unroll
@@ -291,17 +362,16 @@ struct OpBlur {
 
 template <int D, bool P, int CM, bool EX>
 struct OpGradient {
-  static constexpr bool kTwoPhase = true;
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = true;
   using Ch = Chan<CM, EX>;
   float si[CM];
   float acc[CM * D] = {};
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) { Ch::load(a.s, k, a.C, si); }
-  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
-    float xj[3], r[3];
-    load_pos<D>(a.x, j, xj);
-    const float d2 = displacement<D, P>(g, xi, xj, r);
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) { Ch::load(a.s, k, a.C, si); }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, float wj, const float* r,
+                       float d2, uint32_t j) {
     float d;
-    const float t = spiky_mag(g.eps, d2, &d) * (a.m[j] / a.rho[j]);
+    const float t = spiky_mag(g.eps, d2, &d) * wj;
     float sj[CM];
     Ch::load(a.s, j, a.C, sj);
 #pragma unroll
@@ -311,6 +381,7 @@ struct OpGradient {
       for (int e = 0; e < D; ++e) acc[f * D + e] += q * r[e];
     }
   }
+  __device__ void reduce(int G) { grp_sum(acc, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
 #pragma unroll
@@ -323,18 +394,17 @@ struct OpGradient {
 // then raw @ safe_inv(M) in registers (sphops/sph.py:474-484).
 template <int D, bool P, int CM, bool EX>
 struct OpGradientHybrid {
-  static constexpr bool kTwoPhase = true;
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = true;
   using Ch = Chan<CM, EX>;
   float si[CM];
   float acc[CM * D] = {};
   float M[D * D] = {};
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) { Ch::load(a.s, k, a.C, si); }
-  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
-    float xj[3], r[3];
-    load_pos<D>(a.x, j, xj);
-    const float d2 = displacement<D, P>(g, xi, xj, r);
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) { Ch::load(a.s, k, a.C, si); }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, float wj, const float* r,
+                       float d2, uint32_t j) {
     float d;
-    const float t = spiky_mag(g.eps, d2, &d) * (a.m[j] / a.rho[j]);
+    const float t = spiky_mag(g.eps, d2, &d) * wj;
 #pragma unroll
     for (int p = 0; p < D; ++p)
 #pragma unroll
@@ -348,6 +418,7 @@ struct OpGradientHybrid {
       for (int e = 0; e < D; ++e) acc[f * D + e] += q * r[e];
     }
   }
+  __device__ void reduce(int G) { grp_sum(acc, G); grp_sum(M, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     float Ms[D * D], L[D * D];
 #pragma unroll
@@ -375,80 +446,71 @@ struct OpGradientHybrid {
 
 // ---------------------------------------------------------- backward ops
 
-// displacement x_i - x_j as the reference's backward evaluates it
-template <int D, bool P>
-__device__ __forceinline__ float back_disp(const GridParams& g, const float* xi, const float* xj, const float* r_fwd,
-                                           float d2_fwd, float* rb) {
-  if constexpr (!P) {
-#pragma unroll
-    for (int e = 0; e < D; ++e) rb[e] = -r_fwd[e];
-    return d2_fwd;
-  } else {
-    return displacement<D, P>(g, xj, xi, rb);
-  }
-}
-
 template <int D, bool P>
 struct OpDensityBwd {
-  static constexpr bool kTwoPhase = false;
+  static constexpr int kWeightKind = kWMass;
+  static constexpr bool kChannels = false;
   float gi = 0.0f, mi = 0.0f;
   float dx[D] = {};
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) {
     gi = a.g[k];
     mi = a.m[k];
   }
-  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, const float* r,
-                       float d2, uint32_t j) {
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float wj,
+                       const float* r, float d2, uint32_t j) {
     float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
     if (db == 0.0f || !(db < g.eps2)) return;
     const float t = g.eps2 - db;
-    const float coef = gi * a.m[j] + a.g[j] * mi;
+    const float coef = gi * wj + a.g[j] * mi;
     const float mag = -coef * 6.0f * t * t;
 #pragma unroll
     for (int e = 0; e < D; ++e) dx[e] += mag * rb[e];
   }
+  __device__ void reduce(int G) { grp_sum(dx, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { store_pos_grad<D>(a.out0, k, dx, g.c6); }
 };
 
 template <int D, bool P>
 struct OpDensityGradientBwd {
-  static constexpr bool kTwoPhase = false;
+  static constexpr int kWeightKind = kWMass;
+  static constexpr bool kChannels = false;
   float gi[D], mi = 0.0f;
   float dx[D] = {};
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) {
 #pragma unroll
     for (int e = 0; e < D; ++e) gi[e] = a.g[(uint64_t)k * D + e];
     mi = a.m[k];
   }
-  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, const float* r,
-                       float d2, uint32_t j) {
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float wj,
+                       const float* r, float d2, uint32_t j) {
     float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
-    const float mj = a.m[j];
     float diff[D];
 #pragma unroll
-    for (int e = 0; e < D; ++e) diff[e] = a.g[(uint64_t)j * D + e] * mi - gi[e] * mj;
+    for (int e = 0; e < D; ++e) diff[e] = a.g[(uint64_t)j * D + e] * mi - gi[e] * wj;
     spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, diff, dx);
   }
+  __device__ void reduce(int G) { grp_sum(dx, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { store_pos_grad<D>(a.out0, k, dx, g.cs); }
 };
 
 template <int D, bool P>
 struct OpMomentMatrixBwd {
-  static constexpr bool kTwoPhase = false;
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = false;
   float gi[D * D], vi = 0.0f, mr2 = 0.0f;
   float dx[D] = {};
   float drho = 0.0f;
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) {
 #pragma unroll
     for (int q = 0; q < D * D; ++q) gi[q] = a.g[(uint64_t)k * D * D + q];
     const float mi = a.m[k], ri = a.rho[k];
     vi = mi / ri;
     mr2 = mi / (ri * ri);
   }
-  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, const float* r,
-                       float d2, uint32_t j) {
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float vj,
+                       const float* r, float d2, uint32_t j) {
     float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
     float d;
@@ -456,7 +518,6 @@ struct OpMomentMatrixBwd {
     float w[D];
 #pragma unroll
     for (int e = 0; e < D; ++e) w[e] = mag * rb[e];
-    const float vj = a.m[j] / a.rho[j];
     float gd[D * D];
 #pragma unroll
     for (int p = 0; p < D; ++p) {
@@ -472,6 +533,7 @@ struct OpMomentMatrixBwd {
 #pragma unroll
     for (int p = 0; p < D; ++p) spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, &gd[p * D], dx);
   }
+  __device__ void reduce(int G) { grp_sum(dx, G); drho = grp_sum(drho, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     store_pos_grad<D>(a.out0, k, dx, g.cs);
     a.out2[k] = -drho * mr2 * g.cs;
@@ -480,14 +542,15 @@ struct OpMomentMatrixBwd {
 
 template <int D, bool P, int CM, bool EX, bool FULL>
 struct OpBlurBwd {
-  static constexpr bool kTwoPhase = true;
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = true;
   using Ch = Chan<CM, EX>;
   float vi = 0.0f, mr2 = 0.0f;
   float si[FULL ? CM : 1], gi[FULL ? CM : 1];
   float ds[CM] = {};
   float dx[D] = {};
   float drho = 0.0f;
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) {
     const float mi = a.m[k], ri = a.rho[k];
     vi = mi / ri;
     mr2 = mi / (ri * ri);
@@ -496,10 +559,9 @@ struct OpBlurBwd {
       Ch::load(a.g, k, a.C, gi);
     }
   }
-  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
-    float xj[3], r[3], rb[3];
-    load_pos<D>(a.x, j, xj);
-    const float d2 = displacement<D, P>(g, xi, xj, r);
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float vj,
+                       const float* r, float d2, uint32_t j) {
+    float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
     const float W = poly6(g.eps2, db);
     float gj[CM];
@@ -517,7 +579,6 @@ struct OpBlurBwd {
       }
       drho += W * Bv;
       if (db != 0.0f && db < g.eps2) {
-        const float vj = a.m[j] / a.rho[j];
         const float t = g.eps2 - db;
         const float mag = -6.0f * t * t * (A * vj + Bv * vi);
 #pragma unroll
@@ -525,6 +586,7 @@ struct OpBlurBwd {
       }
     }
   }
+  __device__ void reduce(int G) { grp_sum(ds, G); grp_sum(dx, G); drho = grp_sum(drho, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
     const float sc = vi * g.c6;
@@ -540,7 +602,8 @@ struct OpBlurBwd {
 
 template <int D, bool P, int CM, bool EX, bool FULL>
 struct OpGradientBwd {
-  static constexpr bool kTwoPhase = true;
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = true;
   using Ch = Chan<CM, EX>;
   float vi = 0.0f, mr2 = 0.0f;
   float gi[CM * D];
@@ -549,24 +612,22 @@ struct OpGradientBwd {
   float wsum[D] = {};
   float dx[D] = {};
   float drho = 0.0f;
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, const float*) {
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) {
     const float mi = a.m[k], ri = a.rho[k];
     vi = mi / ri;
     mr2 = mi / (ri * ri);
     Ch::template load_cd<D>(a.g, k, a.C, gi);
     if constexpr (FULL) Ch::load(a.s, k, a.C, si);
   }
-  __device__ void pair2(const GridParams& g, const OpPtrs& a, const float* xi, uint32_t j) {
-    float xj[3], r[3], rb[3];
-    load_pos<D>(a.x, j, xj);
-    const float d2 = displacement<D, P>(g, xi, xj, r);
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float vj,
+                       const float* r, float d2, uint32_t j) {
+    float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
     float d;
     const float mag = spiky_mag(g.eps, db, &d);
     float w[D];
 #pragma unroll
     for (int e = 0; e < D; ++e) w[e] = mag * rb[e];
-    const float vj = a.m[j] / a.rho[j];
 #pragma unroll
     for (int e = 0; e < D; ++e) wsum[e] += vj * w[e];
     float gj[CM * D];
@@ -605,6 +666,7 @@ struct OpGradientBwd {
       spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, u, dx);
     }
   }
+  __device__ void reduce(int G) { grp_sum(ds, G); grp_sum(wsum, G); grp_sum(dx, G); drho = grp_sum(drho, G); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
 #pragma unroll
@@ -624,54 +686,214 @@ struct OpGradientBwd {
 
 // ---------------------------------------------------------------- driver
 
-template <int D, bool P, class OP>
+// (x, y, z|0, weight) per particle into the scratch array the pair kernels read.
+template <int D, int WK>
+__global__ __launch_bounds__(kThreads) void k_pack(const float* __restrict__ x, const float* __restrict__ m,
+                                                   const float* __restrict__ rho, float4* __restrict__ xw,
+                                                   uint32_t n) {
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= n) return;
+  float p[3];
+  load_pos<D>(x, k, p);
+  float w = 0.0f;
+  if constexpr (WK == kWMass) w = m[k];
+  if constexpr (WK == kWVolume) w = m[k] / rho[k];
+  xw[k] = make_float4(p[0], p[1], D == 3 ? p[2] : 0.0f, w);
+}
+
+__device__ __forceinline__ void unpack(const float4 v, float* p) {
+  p[0] = v.x;
+  p[1] = v.y;
+  p[2] = v.z;
+}
+
+template <int D, bool P, int TRAV, class OP>
 __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t* __restrict__ bo, OpPtrs a) {
   const uint32_t n = g.B * g.N;
   const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
   const bool active = k < n;
+  const float4* __restrict__ xw = a.xw;
   OP op;
   float xi[3] = {0.0f, 0.0f, 0.0f};
-  Walker<D, P> w;
   if (active) {
-    load_pos<D>(a.x, k, xi);
-    op.init(g, a, k, xi);
-    w.init(g, xi, k);
+    unpack(xw[k], xi);
+    op.init(g, a, k);
   }
-  bool more = active && w.next(g, bo);
-  if constexpr (OP::kTwoPhase) {
-    __shared__ uint32_t list[kThreads / kWave][kCap][kWave];
-    const int wv = threadIdx.x >> 6, ln = __lane_id();
-    while (__any(more)) {
-      int cnt = 0;
-      while (more && cnt < kCap) {
-        float xj[3], r[3];
-        load_pos<D>(a.x, w.j, xj);
-        const float d2 = displacement<D, P>(g, xi, xj, r);
-        if (d2 < g.eps2) list[wv][cnt++][ln] = w.j;
-        ++w.j;
-        more = w.next(g, bo);
+  if constexpr (TRAV == kList) {
+    if (active) {
+      const int32_t* __restrict__ nidx = a.nidx;
+      int t = a.nptr[k];
+      const int end = a.nptr[k + 1];
+      for (; t + 1 < end; t += 2) {
+        const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + 1];
+        const float4 p0 = xw[j0], p1 = xw[j1];
+        float x0[3], x1[3], r0[3], r1[3];
+        unpack(p0, x0);
+        unpack(p1, x1);
+        const float d0 = displacement<D, P>(g, xi, x0, r0);
+        const float d1 = displacement<D, P>(g, xi, x1, r1);
+        op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+        op.pair(g, a, xi, x1, p1.w, r1, d1, j1);
       }
-      for (int t = 0; t < cnt; ++t) op.pair2(g, a, xi, list[wv][t][ln]);
+      if (t < end) {
+        const uint32_t j0 = (uint32_t)nidx[t];
+        const float4 p0 = xw[j0];
+        float x0[3], r0[3];
+        unpack(p0, x0);
+        const float d0 = displacement<D, P>(g, xi, x0, r0);
+        op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+      }
     }
   } else {
-    while (more) {
-      float xj[3], r[3];
-      load_pos<D>(a.x, w.j, xj);
-      const float d2 = displacement<D, P>(g, xi, xj, r);
-      if (d2 < g.eps2) op.pair(g, a, xi, xj, r, d2, w.j);
-      ++w.j;
-      more = w.next(g, bo);
+    Walker<D, P> w;
+    if (active) w.init(g, xi, k);
+    bool more = active && w.next(g, bo);
+    if constexpr (TRAV == kStencil) {
+      while (more) {
+        const uint32_t last = w.jend - 1;
+        float4 p[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = xw[min(w.j + q, last)];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (w.j + q <= last) {
+            float xj[3], r[3];
+            unpack(p[q], xj);
+            const float d2 = displacement<D, P>(g, xi, xj, r);
+            if (d2 < g.eps2) op.pair(g, a, xi, xj, p[q].w, r, d2, w.j + q);
+          }
+        }
+        w.j = min(w.j + 4, w.jend);
+        more = w.next(g, bo);
+      }
+    } else {
+      __shared__ uint32_t list[kThreads / kWave][kCap][kWave];
+      const int wv = threadIdx.x >> 6, ln = __lane_id();
+      while (__any(more)) {
+        int cnt = 0;
+        while (more && cnt <= kCap - 4) {
+          const uint32_t last = w.jend - 1;
+          float4 p[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) p[q] = xw[min(w.j + q, last)];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (w.j + q <= last) {
+              float xj[3], r[3];
+              unpack(p[q], xj);
+              const float d2 = displacement<D, P>(g, xi, xj, r);
+              if (d2 < g.eps2) list[wv][cnt++][ln] = w.j + q;
+            }
+          }
+          w.j = min(w.j + 4, w.jend);
+          more = w.next(g, bo);
+        }
+        for (int t = 0; t < cnt; ++t) {
+          const uint32_t j = list[wv][t][ln];
+          const float4 pj = xw[j];
+          float xj[3], r[3];
+          unpack(pj, xj);
+          const float d2 = displacement<D, P>(g, xi, xj, r);
+          op.pair(g, a, xi, xj, pj.w, r, d2, j);
+        }
+      }
     }
   }
   if (active) op.finish(g, a, k);
 }
 
+// List traversal with a group of G lanes per particle, G by list-length class
+// (particles ordered by class in a.order): lane `sub` of the group takes pairs
+// sub, sub+G, ... of the particle's list, so consecutive lanes read
+// consecutive neighbours; the group then sums its partials.
+struct GroupSched {
+  uint32_t wave_start[5];  // first wave of each class; wave_start[4] = total waves
+  uint32_t part_start[4];  // first slot of each class in a.order
+};
+
 template <int D, bool P, class OP>
-void launch_pairs(const Grid& g, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+__global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs a, GroupSched sc) {
+  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (wave >= sc.wave_start[4]) return;
+  int c = 0;
+  while (c < 3 && wave >= sc.wave_start[c + 1]) ++c;
+  const int G = kGroupSizes[c];
+  const int lane = __lane_id();
+  const uint32_t slot = (wave - sc.wave_start[c]) * (uint32_t)(kWave / G) + (uint32_t)(lane / G);
+  const int sub = lane & (G - 1);
+  const bool active = slot < (uint32_t)a.class_count[c];
+  const uint32_t k = active ? (uint32_t)a.order[sc.part_start[c] + slot] : 0u;
+  const float4* __restrict__ xw = a.xw;
+  OP op;
+  float xi[3] = {0.0f, 0.0f, 0.0f};
+  if (active) {
+    unpack(xw[k], xi);
+    op.init(g, a, k);
+    const int32_t* __restrict__ nidx = a.nidx;
+    const int end = a.nptr[k + 1];
+    int t = a.nptr[k] + sub;
+    for (; t + G < end; t += 2 * G) {
+      const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + G];
+      const float4 p0 = xw[j0], p1 = xw[j1];
+      float x0[3], x1[3], r0[3], r1[3];
+      unpack(p0, x0);
+      unpack(p1, x1);
+      const float d0 = displacement<D, P>(g, xi, x0, r0);
+      const float d1 = displacement<D, P>(g, xi, x1, r1);
+      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+      op.pair(g, a, xi, x1, p1.w, r1, d1, j1);
+    }
+    if (t < end) {
+      const uint32_t j0 = (uint32_t)nidx[t];
+      const float4 p0 = xw[j0];
+      float x0[3], r0[3];
+      unpack(p0, x0);
+      const float d0 = displacement<D, P>(g, xi, x0, r0);
+      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+    }
+  }
+  op.reduce(G);
+  if (active && sub == 0) op.finish(g, a, k);
+}
+
+inline dim3 grid_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) / kThreads)); }
+
+template <int D, class OP>
+void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
+  constexpr int WK = OP::kWeightKind;
+  hipLaunchKernelGGL((k_pack<D, WK>), grid_for(g.n_keys), dim3(kThreads), 0, st, a.x, a.m, a.rho, g.packed,
+                     (uint32_t)g.n_keys);
+  SPHOPS_LAUNCHED();
+  a.xw = g.packed;
+}
+
+template <int D, bool P, class OP>
+void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
   const uint64_t n = g.n_keys;
   if (n == 0) return;
-  hipLaunchKernelGGL((k_pairs<D, P, OP>), dim3((uint32_t)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, st,
-                     g.p, bo, a);
+  pack_for<D, OP>(g, a, st);
+  if (a.nidx != nullptr && a.order != nullptr) {
+    GroupSched sc{};
+    uint32_t waves = 0, part = 0;
+    for (int c = 0; c < 4; ++c) {
+      sc.wave_start[c] = waves;
+      sc.part_start[c] = part;
+      const uint32_t per_wave = (uint32_t)(kWave / kGroupSizes[c]);
+      waves += ((uint32_t)a.class_count[c] + per_wave - 1) / per_wave;
+      part += (uint32_t)a.class_count[c];
+    }
+    sc.wave_start[4] = waves;
+    if (part != n) throw Error("neighbour schedule class counts do not add up to the particle count");
+    const uint32_t wgs = (waves + (kThreads / kWave) - 1) / (kThreads / kWave);
+    if (wgs == 0) return;
+    hipLaunchKernelGGL((k_pairs_grouped<D, P, OP>), dim3(wgs), dim3(kThreads), 0, st, g.p, a, sc);
+  } else if (a.nidx != nullptr) {
+    hipLaunchKernelGGL((k_pairs<D, P, kList, OP>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, a);
+  } else if (OP::kChannels) {
+    hipLaunchKernelGGL((k_pairs<D, P, kStencil2, OP>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, a);
+  } else {
+    hipLaunchKernelGGL((k_pairs<D, P, kStencil, OP>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, a);
+  }
   SPHOPS_LAUNCHED();
 }
 
@@ -706,6 +928,16 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
     case Op::Blur: return launch_channels<D, P, OpBlur>(g, bo, a, st);
     case Op::Gradient: return launch_channels<D, P, OpGradient>(g, bo, a, st);
     case Op::GradientHybrid: return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
+    case Op::NeighbourCount: {
+      OpPtrs b = a;
+      b.nidx = nullptr;  // counting always scans the stencil
+      return launch_pairs<D, P, OpNeighbourCount<D, P>>(g, bo, b, st);
+    }
+    case Op::NeighbourFill: {
+      OpPtrs b = a;
+      b.nidx = nullptr;
+      return launch_pairs<D, P, OpNeighbourFill<D, P>>(g, bo, b, st);
+    }
   }
   throw Error("unknown forward operator");
 }

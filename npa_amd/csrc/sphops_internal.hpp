@@ -48,6 +48,7 @@ struct Grid {
   uint32_t* chunk_end = nullptr;
   uint32_t* chunk_lo = nullptr;   // n_chunks + 1
   uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
+  float4* packed = nullptr;       // B*N (x, y, z|0, weight) read by the pair kernels
 };
 
 // binning.hip
@@ -57,6 +58,8 @@ void run_bin_particles(const Grid& g, const float* in_pos, const float* in_state
                        const int32_t* perm, float* out_pos, float* out_state, float* out_mass,
                        uint32_t C, bool forward, hipStream_t st);
 uint64_t scan_tmp_elems(uint64_t n);
+// in-place exclusive scan of n <= B*N+1 words with the grid's scratch
+void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* total, hipStream_t st);
 
 // perception.hip
 enum class Op : int {
@@ -67,6 +70,8 @@ enum class Op : int {
   Blur = 4,
   Gradient = 5,
   GradientHybrid = 6,
+  NeighbourCount = 7,   // in-radius neighbour count per particle (int32)
+  NeighbourFill = 8,    // in-radius neighbour indices into CSR rows (int32)
 };
 
 struct OpPtrs {
@@ -78,6 +83,12 @@ struct OpPtrs {
   float* out0 = nullptr;      // forward output / grad_x
   float* out1 = nullptr;      // grad_s
   float* out2 = nullptr;      // grad_rho
+  int32_t* iout = nullptr;    // neighbour counts / indices
+  const int32_t* nptr = nullptr;  // CSR row offsets (B*N+1)
+  const int32_t* nidx = nullptr;  // CSR neighbour indices; non-null selects list traversal
+  const float4* xw = nullptr;     // packed positions and weights (set by the launcher)
+  const int32_t* order = nullptr; // particles by list-length class (optional, list traversal)
+  int32_t class_count[4] = {0, 0, 0, 0};
   uint32_t C = 0;
   float tol = 1e-3f;
 };
@@ -86,6 +97,11 @@ void run_forward(const Grid& g, Op op, const int32_t* bin_offsets, const OpPtrs&
 // full = false selects the dL/ds-only variant (Blur, Gradient)
 void run_backward(const Grid& g, Op op, bool full, const int32_t* bin_offsets, const OpPtrs& a,
                   hipStream_t st);
+void run_neighbour_count(const Grid& g, const float* x, const int32_t* bo, int32_t* nptr, hipStream_t st);
+// particles ordered by neighbour-list length class (group sizes 1, 4, 16, 64)
+void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, int32_t* class_counts,
+                            hipStream_t st);
+constexpr int kGroupSizes[4] = {1, 4, 16, 64};
 void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;

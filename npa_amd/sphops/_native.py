@@ -50,7 +50,23 @@ _SIGNATURES = {
                                  _i32),
     "sphops_moment_matrix_backward": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _p], _i32),
     "sphops_safe_inv_sym_mat": ([_p, _p, _i64, _i32, _f32, _p], _i32),
+    "sphops_forward": ([_p, _i32, _p, _p], _i32),
+    "sphops_backward": ([_p, _i32, _i32, _i32, _i32, _p, _p], _i32),
+    "sphops_neighbor_count": ([_p, _p, _p, _p, _p], _i32),
+    "sphops_neighbor_fill": ([_p, _p, _p, _p, _p, _p], _i32),
+    "sphops_neighbor_schedule": ([_p, _p, _p, _p, _p], _i32),
 }
+
+
+class Args(ctypes.Structure):
+    """``sphops_args`` (include/sphops_hip.h)."""
+    _fields_ = [("x", _p), ("mass", _p), ("rho", _p), ("state", _p), ("upstream", _p), ("out", _p),
+                ("grad_state", _p), ("grad_rho", _p), ("feature_dim", _u32), ("tol", _f32),
+                ("bin_offsets", _p), ("nbr_offsets", _p), ("nbr_index", _p), ("nbr_order", _p),
+                ("nbr_class_count", ctypes.c_int32 * 4)]
+
+
+OP_COUNT, OP_DENSITY, OP_DENSITY_GRADIENT, OP_MOMENT_MATRIX, OP_BLUR, OP_GRADIENT, OP_GRADIENT_HYBRID = range(7)
 
 for _name, (_args, _res) in _SIGNATURES.items():
     _fn = getattr(lib, _name)

@@ -25,6 +25,7 @@ from dataclasses import dataclass
 
 import torch
 
+from . import _native as _OP
 from . import sph_hip
 
 _MASS_CACHE = {}
@@ -66,6 +67,7 @@ class HashGridSnapshot:
     block_info: torch.Tensor
     dim: int
     total_blocks: torch.Tensor = None
+    plan: tuple = None  # cached neighbour list, see _plan()
 
 
 class HashGrid:
@@ -170,6 +172,32 @@ def unbin_particles(x_bin, s_bin, snapshot, mass_bin=None):
     return x, s, mass
 
 
+def _plan(snapshot, x_bin):
+    """Per-snapshot CSR neighbour list for positions ``x_bin``, built on first
+    use and reused while ``x_bin`` (same storage, shape and version) is
+    unchanged.  The cache keeps a detached alias of ``x_bin`` so its storage
+    cannot be recycled under the key."""
+    p = snapshot.plan
+    if p is not None and p[1] == x_bin.data_ptr() and p[2] == x_bin._version and p[3] == tuple(x_bin.shape):
+        return p[4]
+    xd = _c(x_bin.detach())
+    nbr = snapshot.grid.neighbor_list(xd, snapshot.bin_offsets)
+    snapshot.plan = (xd, x_bin.data_ptr(), x_bin._version, tuple(x_bin.shape), nbr)
+    return nbr
+
+
+def _fwd(snapshot, op, x_bin, out, mass=None, rho=None, state=None, tol=1e-3):
+    snapshot.grid.op_forward(op, x_bin, out, snapshot.bin_offsets, mass=mass, rho=rho, state=state, tol=tol,
+                             nbr=_plan(snapshot, x_bin))
+
+
+def _bwd(snapshot, op, x_bin, upstream, mass, rho=None, state=None, grad_x=None, grad_s=None, grad_rho=None,
+         dLdx=True, dLds=True, dLdrho=True):
+    snapshot.grid.op_backward(op, x_bin, _c(upstream), snapshot.bin_offsets, mass, rho=rho, state=state,
+                              grad_x=grad_x, grad_state=grad_s, grad_rho=grad_rho, dLdx=dLdx, dLds=dLds,
+                              dLdrho=dLdrho, nbr=_plan(snapshot, x_bin))
+
+
 class Count(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, snapshot):
@@ -191,7 +219,7 @@ class Density(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, mass, snapshot):
         rho = torch.empty(x_bin.shape[:-1], dtype=torch.float32, device=x_bin.device)
-        snapshot.grid.density_forward(x_bin, mass, rho, snapshot.bin_offsets, snapshot.block_info)
+        _fwd(snapshot, _OP.OP_DENSITY, x_bin, rho, mass=mass)
         ctx.save_for_backward(x_bin, mass)
         ctx.snapshot = snapshot
         ctx.dLdx = x_bin.requires_grad
@@ -202,10 +230,8 @@ class Density(torch.autograd.Function):
         if not ctx.dLdx:
             return None, None, None
         x_bin, mass = ctx.saved_tensors
-        snap = ctx.snapshot
         grad_x = torch.empty_like(x_bin)
-        snap.grid.density_backward(x_bin, mass, _c(grad_output), grad_x, snap.bin_offsets, snap.block_info,
-                                   ctx.dLdx)
+        _bwd(ctx.snapshot, _OP.OP_DENSITY, x_bin, grad_output, mass, grad_x=grad_x)
         return grad_x, None, None
 
 
@@ -218,7 +244,7 @@ class Blur(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, s_bin, rho, mass, snapshot):
         s_blur = torch.empty_like(s_bin)
-        snapshot.grid.blur_forward(x_bin, rho, mass, s_bin, s_blur, snapshot.bin_offsets, snapshot.block_info)
+        _fwd(snapshot, _OP.OP_BLUR, x_bin, s_blur, mass=mass, rho=rho, state=s_bin)
         ctx.save_for_backward(x_bin, s_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
@@ -226,15 +252,19 @@ class Blur(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        x_bin, s_bin, rho, mass = ctx.saved_tensors
-        snap = ctx.snapshot
-        grad_s = torch.empty_like(s_bin)
-        grad_x = torch.empty_like(x_bin)
-        grad_rho = torch.empty_like(rho)
-        snap.grid.blur_backward(x_bin, rho, mass, s_bin, _c(grad_output), grad_x, grad_s, grad_rho,
-                                snap.bin_offsets, snap.block_info, ctx.dLdx, ctx.dLds, ctx.dLdrho)
-        return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
-                grad_rho if ctx.dLdrho else None, None, None)
+        return _state_backward(ctx, _OP.OP_BLUR, grad_output)
+
+
+def _state_backward(ctx, op, grad_output):
+    x_bin, s_bin, rho, mass = ctx.saved_tensors
+    ds_only = ctx.dLds and not ctx.dLdx and not ctx.dLdrho
+    grad_s = torch.empty_like(s_bin)
+    grad_x = None if ds_only else torch.empty_like(x_bin)
+    grad_rho = None if ds_only else torch.empty_like(rho)
+    _bwd(ctx.snapshot, op, x_bin, grad_output, mass, rho=rho, state=s_bin, grad_x=grad_x, grad_s=grad_s,
+         grad_rho=grad_rho, dLdx=ctx.dLdx, dLds=ctx.dLds, dLdrho=ctx.dLdrho)
+    return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
+            grad_rho if ctx.dLdrho else None, None, None)
 
 
 def blur(x_bin, rho, s_bin, snapshot, mass=None):
@@ -242,23 +272,11 @@ def blur(x_bin, rho, s_bin, snapshot, mass=None):
     return Blur.apply(x_bin, s_bin, rho, mass, snapshot)
 
 
-def _gradient_backward(ctx, grad_output):
-    x_bin, s_bin, rho, mass = ctx.saved_tensors
-    snap = ctx.snapshot
-    grad_s = torch.empty_like(s_bin)
-    grad_x = torch.empty_like(x_bin)
-    grad_rho = torch.empty_like(rho)
-    snap.grid.gradient_backward(x_bin, rho, mass, s_bin, _c(grad_output), grad_x, grad_s, grad_rho,
-                                snap.bin_offsets, snap.block_info, ctx.dLdx, ctx.dLds, ctx.dLdrho)
-    return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
-            grad_rho if ctx.dLdrho else None, None, None)
-
-
 class Gradient(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, s_bin, rho, mass, snapshot):
         grad_s = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
-        snapshot.grid.gradient_forward(x_bin, rho, mass, s_bin, grad_s, snapshot.bin_offsets, snapshot.block_info)
+        _fwd(snapshot, _OP.OP_GRADIENT, x_bin, grad_s, mass=mass, rho=rho, state=s_bin)
         ctx.save_for_backward(x_bin, s_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
@@ -266,7 +284,7 @@ class Gradient(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        return _gradient_backward(ctx, grad_output)
+        return _state_backward(ctx, _OP.OP_GRADIENT, grad_output)
 
 
 def gradient(x_bin, rho, s_bin, snapshot, mass=None):
@@ -278,7 +296,7 @@ class DensityGradient(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, mass, snapshot):
         out = torch.empty(*x_bin.shape[:-1], snapshot.dim, dtype=torch.float32, device=x_bin.device)
-        snapshot.grid.density_gradient_forward(x_bin, mass, out, snapshot.bin_offsets, snapshot.block_info)
+        _fwd(snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, out, mass=mass)
         ctx.save_for_backward(x_bin, mass)
         ctx.snapshot = snapshot
         ctx.dLdx = x_bin.requires_grad
@@ -289,10 +307,8 @@ class DensityGradient(torch.autograd.Function):
         if not ctx.dLdx:
             return None, None, None
         x_bin, mass = ctx.saved_tensors
-        snap = ctx.snapshot
         grad_x = torch.empty_like(x_bin)
-        snap.grid.density_gradient_backward(x_bin, mass, _c(grad_output), grad_x, snap.bin_offsets,
-                                            snap.block_info, ctx.dLdx)
+        _bwd(ctx.snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, grad_output, mass, grad_x=grad_x)
         return grad_x, None, None
 
 
@@ -306,7 +322,7 @@ class MomentMatrix(torch.autograd.Function):
     def forward(ctx, x_bin, rho, mass, snapshot):
         D = snapshot.dim
         M = torch.empty(*x_bin.shape[:-1], D, D, dtype=torch.float32, device=x_bin.device)
-        snapshot.grid.moment_matrix_forward(x_bin, rho, mass, M, snapshot.bin_offsets, snapshot.block_info)
+        _fwd(snapshot, _OP.OP_MOMENT_MATRIX, x_bin, M, mass=mass, rho=rho)
         ctx.save_for_backward(x_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLdrho = x_bin.requires_grad, rho.requires_grad
@@ -315,11 +331,10 @@ class MomentMatrix(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output):
         x_bin, rho, mass = ctx.saved_tensors
-        snap = ctx.snapshot
         grad_x = torch.empty_like(x_bin)
         grad_rho = torch.empty_like(rho)
-        snap.grid.moment_matrix_backward(x_bin, rho, mass, _c(grad_output), grad_x, grad_rho, snap.bin_offsets,
-                                         snap.block_info, ctx.dLdx, ctx.dLdrho)
+        _bwd(ctx.snapshot, _OP.OP_MOMENT_MATRIX, x_bin, grad_output, mass, rho=rho, grad_x=grad_x,
+             grad_rho=grad_rho, dLdx=ctx.dLdx, dLdrho=ctx.dLdrho)
         return grad_x if ctx.dLdx else None, grad_rho if ctx.dLdrho else None, None, None
 
 
@@ -345,8 +360,7 @@ class GradientHybrid(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, s_bin, rho, mass, snapshot, tol):
         out = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
-        snapshot.grid.gradient_hybrid_forward(x_bin, rho, mass, s_bin, out, snapshot.bin_offsets,
-                                              snapshot.block_info, tol)
+        _fwd(snapshot, _OP.OP_GRADIENT_HYBRID, x_bin, out, mass=mass, rho=rho, state=s_bin, tol=tol)
         ctx.save_for_backward(x_bin, s_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
@@ -354,7 +368,7 @@ class GradientHybrid(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        return _gradient_backward(ctx, grad_output) + (None,)
+        return _state_backward(ctx, _OP.OP_GRADIENT_HYBRID, grad_output) + (None,)
 
 
 def gradient_hybrid(x_bin, rho, s_bin, snapshot, mass=None):

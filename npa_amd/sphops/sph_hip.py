@@ -336,6 +336,72 @@ class _HashGridNative:
             self._offsets(bin_offsets), self._blocks(block_info), 1, 1, _stream(binned_positions)))
 
 
+    # ---- generic operator interface with an optional neighbour list
+    def neighbor_list(self, x_bin, bin_offsets):
+        """In-radius neighbour list of the binned particles plus its
+        traversal schedule: ``(offsets (B*N+1,), index (pairs,), order (B*N,),
+        class_counts (4 ints, host))``.  Reads the pair total and the class
+        sizes back to the host to size ``index`` (one synchronisation)."""
+        x = self._pos(x_bin, "binned_positions")
+        bo = self._offsets(bin_offsets)
+        dev = x_bin.device
+        n = self._b * self._n
+        offs = torch.empty(n + 1, dtype=_I32, device=dev)
+        order = torch.empty(max(n, 1), dtype=_I32, device=dev)
+        small = torch.empty(5, dtype=_I32, device=dev)
+        st = _stream(x_bin)
+        _check(_lib.sphops_neighbor_count(self._h, x, bo, ctypes.c_void_p(offs.data_ptr()), st))
+        _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(offs.data_ptr()),
+                                             ctypes.c_void_p(order.data_ptr()),
+                                             ctypes.c_void_p(small.data_ptr() + 4), st))
+        small[0:1].copy_(offs[n:n + 1])
+        host = small.cpu().tolist()
+        total, counts = host[0], tuple(host[1:])
+        index = torch.empty(max(total, 1), dtype=_I32, device=dev)
+        _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(offs.data_ptr()),
+                                         ctypes.c_void_p(index.data_ptr()), st))
+        return offs, index, order, counts
+
+    def _args(self, x, bin_offsets, mass=None, rho=None, state=None, upstream=None, out=None, grad_state=None,
+              grad_rho=None, tol=1e-3, nbr=None):
+        a = _native.Args()
+        a.x = self._pos(x, "binned_positions")
+        a.bin_offsets = self._offsets(bin_offsets)
+        if mass is not None:
+            a.mass = self._bn(mass, "mass")
+        if rho is not None:
+            a.rho = self._bn(rho, "rho")
+        C = 0
+        if state is not None:
+            C = state.shape[2] if state.dim() == 3 else -1
+            a.state = self._state(state, "state_in", C)
+        a.feature_dim = max(C, 0)
+        a.tol = tol
+        for name, t in (("upstream", upstream), ("out", out), ("grad_state", grad_state), ("grad_rho", grad_rho)):
+            if t is not None:
+                if t.dtype != _F32 or not t.is_contiguous() or t.device.type != "cuda":
+                    raise TypeError(f"{name}: expected a contiguous float32 GPU tensor")
+                setattr(a, name, t.data_ptr())
+        if nbr is not None:
+            a.nbr_offsets, a.nbr_index = nbr[0].data_ptr(), nbr[1].data_ptr()
+            if len(nbr) > 2:
+                a.nbr_order = nbr[2].data_ptr()
+                for c in range(4):
+                    a.nbr_class_count[c] = nbr[3][c]
+        return a
+
+    def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None):
+        a = self._args(x, bin_offsets, mass, rho, state, out=out, tol=tol, nbr=nbr)
+        _check(_lib.sphops_forward(self._h, op, ctypes.byref(a), _stream(x)))
+
+    def op_backward(self, op, x, upstream, bin_offsets, mass, rho=None, state=None, grad_x=None, grad_state=None,
+                    grad_rho=None, dLdx=True, dLds=True, dLdrho=True, nbr=None):
+        a = self._args(x, bin_offsets, mass, rho, state, upstream=upstream, out=grad_x, grad_state=grad_state,
+                       grad_rho=grad_rho, nbr=nbr)
+        _check(_lib.sphops_backward(self._h, op, int(bool(dLdx)), int(bool(dLds)), int(bool(dLdrho)),
+                                    ctypes.byref(a), _stream(x)))
+
+
 class _Grid3DProps:
     @property
     def grid_size_z(self):

@@ -107,76 +107,52 @@ def gradient_hybrid(P, m, rho, s, cs, tol=1e-3):
 
 # ------------------------------------------------------------- CPU baseline
 
-def perception_step_cpu(x, s, h, periodic=False, box=None, row_block=None, full=True, tol=1e-3):
-    """One perception fwd+bwd step on the host in the input dtype: pass A
-    (rho, grad rho), pass B (blur, moment matrix, safe inverse, gradient_hybrid)
-    and the backward of ``sum(out * g)`` for fixed seeded upstream ``g``.
-
-    Rows are processed in blocks of ``row_block`` particles against all
-    columns (exact; per-block graphs).  Returns the number of in-radius pairs
-    (including self) so throughput can be reported per pair."""
-    B, N, D = x.shape
-    C = s.shape[-1]
-    c6, cs = poly6_coef(h, D), spiky_coef(h, D)
-    rb = row_block or N
-    gen = torch.Generator().manual_seed(7)
-    g_blur = torch.randn(B, N, C, generator=gen, dtype=x.dtype)
-    g_grad = torch.randn(B, N, C, D, generator=gen, dtype=x.dtype)
-    g_dg = torch.randn(B, N, D, generator=gen, dtype=x.dtype)
-    x = x.detach().requires_grad_(full)
-    s = s.detach().requires_grad_(True)
-    m = torch.ones(B, N, dtype=x.dtype)
-    pairs = 0
-    with torch.no_grad():
-        rho_nd = torch.empty(B, N, dtype=x.dtype)
-        for a in range(0, N, rb):
-            r = pairwise_displacement(x, periodic, box)[:, a:a + rb] if rb == N else \
-                _rows(x, a, rb, periodic, box)
-            mask = (r * r).sum(-1) < h * h
-            pairs += int(mask.sum())
-            rho_nd[:, a:a + rb] = c6 * (poly6(r, h, mask) * m.unsqueeze(1)).sum(2)
-    rho = rho_nd.clone().requires_grad_(full)
-    drho_total = torch.zeros(B, N, dtype=x.dtype)
-    for a in range(0, N, rb):
-        r = _rows(x, a, rb, periodic, box)
-        mask = (r.detach() ** 2).sum(-1) < h * h
-        P = _RowPairs(r, mask, h)
-        sl = slice(a, a + rb)
-        vj = (m / rho).unsqueeze(1)
-        Wm = poly6(P.r, h, mask)
-        blur_o = c6 * torch.einsum("bij,bjf->bif", Wm * vj, s)
-        K = spiky(P.r, h, mask)
-        dA = s.unsqueeze(1) - s[:, sl].unsqueeze(2)
-        raw = cs * (dA.unsqueeze(-1) * (K * vj.unsqueeze(-1)).unsqueeze(3)).sum(2)
-        with torch.no_grad():
-            M = cs * (P.r.unsqueeze(-1) * (K * vj.unsqueeze(-1)).unsqueeze(-2)).sum(2)
-            L = safe_inv_sym(M, tol)
-        gh = raw + (raw @ L - raw).detach()
-        dg = cs * (K * m.unsqueeze(1).unsqueeze(-1)).sum(2)
-        loss = (blur_o * g_blur[:, sl]).sum() + (gh * g_grad[:, sl]).sum()
-        if full:
-            loss = loss + (dg * g_dg[:, sl]).sum()
-        loss.backward()
-    if full and rho.grad is not None:
-        # rho -> x through the density pass (pass A backward)
-        for a in range(0, N, rb):
-            r = _rows(x, a, rb, periodic, box)
-            mask = (r.detach() ** 2).sum(-1) < h * h
-            rr = c6 * (poly6(r, h, mask) * m.unsqueeze(1)).sum(2)
-            (rr * rho.grad[:, a:a + rb]).sum().backward()
-        drho_total += rho.grad
-    return pairs
-
-
-class _RowPairs:
-    def __init__(self, r, mask, h):
-        self.r, self.mask, self.h = r, mask, h
-
-
 def _rows(x, a, rb, periodic, box):
-    xi = x[:, a:a + rb]
-    r = x.unsqueeze(1) - xi.unsqueeze(2)
+    """Displacements x_j - x_i for rows i in [a, a+rb) against all j."""
+    r = x.unsqueeze(1) - x[:, a:a + rb].unsqueeze(2)
     if periodic:
         L = torch.as_tensor(box, dtype=x.dtype)
         r = torch.remainder(r + 0.5 * L, L) - 0.5 * L
     return r
+
+
+def row_block_step(x, s, h, a, rows, periodic=False, box=None, tol=1e-3, seed=7):
+    """One row block of the perception fwd+bwd step on the host, in the
+    reference's brute-force form (``torch_sph.py:185-471``): for rows
+    ``[a, a+rows)`` against all N columns, pass A (density, density
+    gradient), pass B (blur, moment matrix, safe inverse, gradient_hybrid) and
+    the backward of ``sum(out * g)`` for seeded upstream ``g`` into x, s and
+    rho (through the density rows too).  The full step is the sum of N/rows
+    such blocks; each costs the same because every block spans all columns.
+    Returns the number of in-radius pairs of the block."""
+    B, N, D = x.shape
+    C = s.shape[-1]
+    rows = min(rows, N - a)
+    c6, cs = poly6_coef(h, D), spiky_coef(h, D)
+    gen = torch.Generator().manual_seed(seed)
+    g_blur = torch.randn(B, rows, C, generator=gen, dtype=x.dtype)
+    g_grad = torch.randn(B, rows, C, D, generator=gen, dtype=x.dtype)
+    g_dg = torch.randn(B, rows, D, generator=gen, dtype=x.dtype)
+    xr = x.detach().requires_grad_(True)
+    sr = s.detach().requires_grad_(True)
+    m = torch.ones(B, N, dtype=x.dtype)
+    rho = torch.full((B, N), float(c6 * h ** (2 * D + 2)), dtype=x.dtype, requires_grad=True)
+    r = _rows(xr, a, rows, periodic, box)
+    mask = (r.detach() ** 2).sum(-1) < h * h
+    W = poly6(r, h, mask)
+    rho_rows = c6 * (W * m.unsqueeze(1)).sum(2)
+    K = spiky(r, h, mask)
+    vj = (m / rho).unsqueeze(1)
+    blur_o = c6 * torch.einsum("bij,bjf->bif", W * vj, sr)
+    dA = sr.unsqueeze(1) - sr[:, a:a + rows].unsqueeze(2)
+    Kv = K * vj.unsqueeze(-1)
+    raw = cs * (dA.unsqueeze(-1) * Kv.unsqueeze(3)).sum(2)
+    with torch.no_grad():
+        M = cs * (r.unsqueeze(-1) * Kv.unsqueeze(-2)).sum(2)
+        L = safe_inv_sym(M, tol)
+    gh = raw + (raw @ L - raw).detach()
+    dg = cs * (K * m.unsqueeze(1).unsqueeze(-1)).sum(2)
+    loss = (blur_o * g_blur).sum() + (gh * g_grad).sum() + (dg * g_dg).sum()
+    loss.backward(retain_graph=True)
+    (rho_rows * rho.grad[:, a:a + rows]).sum().backward()
+    return int(mask.sum())

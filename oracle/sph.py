@@ -127,13 +127,19 @@ def gradient_hybrid(ctx, m, rho, s, tol=1e-3):
 
 
 # ---------------------------------------------------------------- backward
+#
+# ``mag`` of a backward output sums the absolute values of the elementary
+# products (pair x channel x component) the value is accumulated from, so it
+# bounds the fp32 rounding of sums that cancel inside a pair as well as
+# across pairs.
 
 def density_backward(ctx, m, g):
     """dL/dx for upstream ``g`` = dL/drho (``sph_cuda.cu:1160-1184``)."""
     p = ctx.p
     coef = g[p.i] * m[p.j] + g[p.j] * m[p.i]
+    acoef = np.abs(g[p.i] * m[p.j]) + np.abs(g[p.j] * m[p.i])
     t = ctx.c6 * coef[:, None] * ctx.gWb
-    return _seg_sum(t, p), _seg_sum(np.abs(t), p)
+    return _seg_sum(t, p), _seg_sum(ctx.c6 * acoef[:, None] * np.abs(ctx.gWb), p)
 
 
 def blur_backward(ctx, m, rho, s, g):
@@ -142,15 +148,18 @@ def blur_backward(ctx, m, rho, s, g):
     v = m / rho
     vi, vj = v[p.i], v[p.j]
     W = ctx.Wb
+    mr2 = m[p.i] / rho[p.i] ** 2
     t_s = ctx.c6 * (vi * W)[:, None] * g[p.j]
     B = np.sum(g[p.j] * s[p.i], axis=1)
     A = np.sum(g[p.i] * s[p.j], axis=1)
-    t_r = -ctx.c6 * (m[p.i] / rho[p.i] ** 2) * W * B
+    aB = np.sum(np.abs(g[p.j] * s[p.i]), axis=1)
+    aA = np.sum(np.abs(g[p.i] * s[p.j]), axis=1)
+    t_r = -ctx.c6 * mr2 * W * B
     t_x = ctx.c6 * (A * vj + B * vi)[:, None] * ctx.gWb
-    out = []
-    for t in (t_x, t_s, t_r):
-        out.append((_seg_sum(t, p), _seg_sum(np.abs(t), p)))
-    return out
+    m_r = ctx.c6 * mr2 * np.abs(W) * aB
+    m_x = ctx.c6 * (aA * np.abs(vj) + aB * np.abs(vi))[:, None] * np.abs(ctx.gWb)
+    return [(_seg_sum(t_x, p), _seg_sum(m_x, p)), (_seg_sum(t_s, p), _seg_sum(np.abs(t_s), p)),
+            (_seg_sum(t_r, p), _seg_sum(m_r, p))]
 
 
 def gradient_backward(ctx, m, rho, s, g):
@@ -161,21 +170,30 @@ def gradient_backward(ctx, m, rho, s, g):
     vi, vj = v[p.i], v[p.j]
     w = ctx.Kb
     gi, gj = g[p.i], g[p.j]
+    mr2 = m[p.i] / rho[p.i] ** 2
     c = gj * vi[:, None, None] + gi * vj[:, None, None]
+    ac = np.abs(gj * vi[:, None, None]) + np.abs(gi * vj[:, None, None])
     t_s = ctx.cs * np.sum(c * w[:, None, :], axis=2)
+    m_s = ctx.cs * np.sum(ac * np.abs(w)[:, None, :], axis=2)
     delta = s[p.i] - s[p.j]
-    t_r = -ctx.cs * (m[p.i] / rho[p.i] ** 2) * np.sum(gj * delta[:, :, None] * w[:, None, :], axis=(1, 2))
+    t_r = -ctx.cs * mr2 * np.sum(gj * delta[:, :, None] * w[:, None, :], axis=(1, 2))
+    m_r = ctx.cs * mr2 * np.sum(np.abs(gj * delta[:, :, None] * w[:, None, :]), axis=(1, 2))
     u = np.sum(delta[:, :, None] * c, axis=1)
+    au = np.sum(np.abs(delta)[:, :, None] * ac, axis=1)
     t_x = ctx.cs * np.einsum("pab,pb->pa", ctx.Jb, u)
-    return [(_seg_sum(t, p), _seg_sum(np.abs(t), p)) for t in (t_x, t_s, t_r)]
+    m_x = ctx.cs * np.einsum("pab,pb->pa", np.abs(ctx.Jb), au)
+    return [(_seg_sum(t_x, p), _seg_sum(m_x, p)), (_seg_sum(t_s, p), _seg_sum(m_s, p)),
+            (_seg_sum(t_r, p), _seg_sum(m_r, p))]
 
 
 def density_gradient_backward(ctx, m, g):
     """dL/dx for upstream ``g`` (B*N, D) = dL/d(grad rho) (``sph_cuda.cu:1236-1264``)."""
     p = ctx.p
     diff = g[p.j] * m[p.i][:, None] - g[p.i] * m[p.j][:, None]
+    adiff = np.abs(g[p.j] * m[p.i][:, None]) + np.abs(g[p.i] * m[p.j][:, None])
     t = ctx.cs * np.einsum("pab,pb->pa", ctx.Jb, diff)
-    return _seg_sum(t, p), _seg_sum(np.abs(t), p)
+    mt = ctx.cs * np.einsum("pab,pb->pa", np.abs(ctx.Jb), adiff)
+    return _seg_sum(t, p), _seg_sum(mt, p)
 
 
 def moment_matrix_backward(ctx, m, rho, g):
@@ -186,10 +204,15 @@ def moment_matrix_backward(ctx, m, rho, g):
     r = np.asarray(p.rb, dtype=np.float64)
     w = ctx.Kb
     gi, gj = g[p.i], g[p.j]
+    mr2 = m[p.i] / rho[p.i] ** 2
     c = gi * vj[:, None, None] + gj * vi[:, None, None]
-    t_r = -ctx.cs * (m[p.i] / rho[p.i] ** 2) * np.einsum("pab,pa,pb->p", gj, r, w)
+    ac = np.abs(gi * vj[:, None, None]) + np.abs(gj * vi[:, None, None])
+    t_r = -ctx.cs * mr2 * np.einsum("pab,pa,pb->p", gj, r, w)
+    m_r = ctx.cs * mr2 * np.einsum("pab,pa,pb->p", np.abs(gj), np.abs(r), np.abs(w))
     direct = np.einsum("pab,pb->pa", c, w)
-    gd = r[:, :, None] * c
-    via_j = np.einsum("pcb,pab->pc", ctx.Jb, gd)
+    a_direct = np.einsum("pab,pb->pa", ac, np.abs(w))
+    via_j = np.einsum("pcb,pab->pc", ctx.Jb, r[:, :, None] * c)
+    a_via = np.einsum("pcb,pab->pc", np.abs(ctx.Jb), np.abs(r)[:, :, None] * ac)
     t_x = ctx.cs * (direct + via_j)
-    return [(_seg_sum(t, p), _seg_sum(np.abs(t), p)) for t in (t_x, t_r)]
+    m_x = ctx.cs * (a_direct + a_via)
+    return [(_seg_sum(t_x, p), _seg_sum(m_x, p)), (_seg_sum(t_r, p), _seg_sum(m_r, p))]

@@ -1,10 +1,14 @@
 """Shared test utilities: case construction, oracle evaluation, tolerances.
 
 Tolerance used for every fp32 output (written once, here):
-    |gpu - ref| <= RTOL * |ref| + ATOL * mag
-with RTOL = 1e-5, ATOL = 1e-6 and ``mag`` the oracle's sum of absolute pair
+    |gpu - ref| <= RTOL * |ref| + ATOL * (mag + rms)
+with RTOL = 1e-5, ATOL = 1e-6, ``mag`` the oracle's sum of absolute pair
 terms for that element (the scale of fp32 summation error; equal to |ref|
-when no term cancels).  Integer and index outputs are compared exactly.
+when no term cancels) and ``rms`` the root-mean-square of the whole
+reference tensor (the absolute 1e-6 expressed in the tensor's own units; it
+covers elements whose only terms are pairs at |r| ~ h, where fp32 and the
+exact value differ by ~1e-14 of a typical term but mag is ~0).  Integer and
+index outputs are compared exactly.
 """
 from dataclasses import dataclass, field
 
@@ -100,19 +104,19 @@ def assert_close(name, got, ref, mag, rtol=RTOL, atol=ATOL, skip=None):
     mag = np.asarray(mag, dtype=np.float64)
     assert got.shape == ref.shape, f"{name}: shape {got.shape} vs {ref.shape}"
     err = np.abs(got - ref)
-    bound = rtol * np.abs(ref) + atol * mag
+    rms = float(np.sqrt(np.mean(ref ** 2))) if ref.size else 0.0
+    bound = rtol * np.abs(ref) + atol * (mag + rms)
     bad = err > bound
     if skip is not None:
-        bad &= ~np.broadcast_to(skip.reshape(skip.shape + (1,) * (bad.ndim - skip.ndim)), bad.shape)
+        sk = np.broadcast_to(skip.reshape(skip.shape + (1,) * (bad.ndim - skip.ndim)), bad.shape)
+        bad &= ~sk
     if bad.any():
-        ratio = np.where(bound > 0, err / np.maximum(bound, 1e-300), np.inf)
-        if skip is not None:
-            ratio = np.where(np.broadcast_to(skip.reshape(skip.shape + (1,) * (bad.ndim - skip.ndim)), bad.shape),
-                             0, ratio)
+        ratio = np.where(bad, err / np.maximum(bound, 1e-300), 0.0)
         idx = np.unravel_index(np.argmax(ratio), ratio.shape)
         raise AssertionError(
             f"{name}: {int(bad.sum())}/{bad.size} elements out of tolerance; worst at {idx}: "
-            f"got {got[idx]!r} ref {ref[idx]!r} err {err[idx]:.3e} bound {bound[idx]:.3e} mag {mag[idx]:.3e}")
+            f"got {got[idx]!r} ref {ref[idx]!r} err {err[idx]:.3e} bound {bound[idx]:.3e} "
+            f"mag {mag[idx]:.3e} rms {rms:.3e}")
     return float(np.max(err / np.maximum(bound, 1e-300))) if err.size else 0.0
 
 

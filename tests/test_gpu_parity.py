@@ -210,3 +210,69 @@ def test_backward(name):
         # the unused w lane of 3D position gradients is written as zero
         assert np.all(res["b_density"]["x"][..., 3] == 0)
         assert np.all(res["b_grad"]["x"][..., 3] == 0)
+
+
+MIRROR_CASES = [n for n in NAMES if n.startswith(("ref2d", "ref3d", "chan12", "chan33", "cfg2", "cfg5"))]
+
+
+@pytest.mark.parametrize("name", MIRROR_CASES)
+def test_stencil_methods_match_oracle(name):
+    """The reference-shaped methods (one stencil scan per call, one lane per
+    particle) against the oracle, as the list path is checked above."""
+    import npa_amd.sphops as sp
+    c, res, ora = run(name)
+    q = ora["q"]
+    grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    snap = grid.instantiate(dev(c.x))
+    hg = grid.hashgrid
+    xb, sb, mb = dev(res["xb"]), dev(res["sb"]), dev(res["mb"])
+    rho = dev(res["rho"])
+    B, N, C, D = c.B, c.N, c.C, c.dim
+    bo, bi = snap.bin_offsets, snap.block_info
+    out = torch.empty(B, N, device="cuda")
+    hg.count_forward(xb, out, bo, bi)
+    np.testing.assert_array_equal(out.cpu().numpy(), res["count"])
+    hg.density_forward(xb, mb, out, bo, bi)
+    H.assert_close(f"{name}:rho", _flat(out.cpu().numpy(), q), *ora["rho"])
+    o = torch.empty(B, N, C, device="cuda")
+    hg.blur_forward(xb, rho, mb, sb, o, bo, bi)
+    H.assert_close(f"{name}:blur", _flat(o.cpu().numpy(), q), *ora["blur"])
+    o = torch.empty(B, N, C, D, device="cuda")
+    hg.gradient_forward(xb, rho, mb, sb, o, bo, bi)
+    H.assert_close(f"{name}:grad", _flat(o.cpu().numpy(), q), *ora["grad"])
+    o = torch.empty(B, N, D, device="cuda")
+    hg.density_gradient_forward(xb, mb, o, bo, bi)
+    H.assert_close(f"{name}:dgrad", _flat(o.cpu().numpy(), q), *ora["dgrad"])
+    o = torch.empty(B, N, D, D, device="cuda")
+    hg.moment_matrix_forward(xb, rho, mb, o, bo, bi)
+    H.assert_close(f"{name}:M", _flat(o.cpu().numpy(), q), *ora["M"])
+    rng = np.random.default_rng(11)
+    g_rho = dev(rng.standard_normal((B, N)).astype(np.float32))
+    g_blur = dev(rng.standard_normal((B, N, C)).astype(np.float32))
+    g_grad = dev(rng.standard_normal((B, N, C, D)).astype(np.float32))
+    gx, gs, gr = torch.empty_like(xb), torch.empty_like(sb), torch.empty_like(rho)
+    hg.density_backward(xb, mb, g_rho, gx, bo, bi, True)
+    H.assert_close(f"{name}:density.dx", _flat(gx.cpu().numpy(), q, D), *ora["b_density"])
+    hg.blur_backward(xb, rho, mb, sb, g_blur, gx, gs, gr, bo, bi, True, True, True)
+    for got, (ref, mag), key in zip((gx, gs, gr), ora["b_blur"], ("dx", "ds", "drho")):
+        H.assert_close(f"{name}:blur.{key}", _flat(got.cpu().numpy(), q, D if key == "dx" else None), ref, mag)
+    hg.gradient_backward(xb, rho, mb, sb, g_grad, gx, gs, gr, bo, bi, True, True, True)
+    for got, (ref, mag), key in zip((gx, gs, gr), ora["b_grad"], ("dx", "ds", "drho")):
+        H.assert_close(f"{name}:grad.{key}", _flat(got.cpu().numpy(), q, D if key == "dx" else None), ref, mag)
+    hg.gradient_backward(xb, rho, mb, sb, g_grad, gx, gs, gr, bo, bi, False, True, False)
+    H.assert_close(f"{name}:grad_ds.ds", _flat(gs.cpu().numpy(), q), *ora["b_grad"][1])
+
+
+@pytest.mark.parametrize("name", ["ref2d-clamp-grid", "cfg5"])
+def test_deterministic_replay(name):
+    """Two fresh runs of the whole path give bitwise identical results."""
+    c, res, _ = run(name)
+    run.cache_clear()
+    c2, res2, _ = run(name)
+    for key in ("perm", "bo", "bi", "rho", "blur", "grad", "hyb", "dgrad", "M"):
+        np.testing.assert_array_equal(res[key], res2[key])
+    for key in ("b_density", "b_blur", "b_grad", "b_hyb", "b_moment", "b_dgrad"):
+        for k in ("x", "s", "rho"):
+            if res[key][k] is not None:
+                np.testing.assert_array_equal(res[key][k], res2[key][k])
