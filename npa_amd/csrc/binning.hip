@@ -418,12 +418,25 @@ inline dim3 blocks_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) /
 
 namespace {
 
-__device__ __forceinline__ uint32_t length_class(int32_t len) {
-  return len <= 4 ? 0u : (len <= 32 ? 1u : (len <= 128 ? 2u : 3u));
+struct ClassBounds {
+  int32_t t0, t1, t2;  // class 0: len <= t0, 1: <= t1, 2: <= t2, 3: longer
+};
+
+// Length of item idx: from CSR offsets (CSR) or a plain length array.
+template <bool CSR>
+__device__ __forceinline__ int32_t item_length(const int32_t* __restrict__ src, uint32_t idx) {
+  if constexpr (CSR) return src[idx + 1] - src[idx];
+  return src[idx];
 }
 
-__global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restrict__ nptr, uint32_t n,
-                                                          uint32_t* __restrict__ cnt, uint32_t ntiles) {
+__device__ __forceinline__ uint32_t length_class(int32_t len, ClassBounds cb) {
+  return len <= cb.t0 ? 0u : (len <= cb.t1 ? 1u : (len <= cb.t2 ? 2u : 3u));
+}
+
+template <bool CSR>
+__global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restrict__ src, uint32_t n,
+                                                          ClassBounds cb, uint32_t* __restrict__ cnt,
+                                                          uint32_t ntiles) {
   __shared__ uint32_t h[4];
   if (threadIdx.x < 4) h[threadIdx.x] = 0;
   __syncthreads();
@@ -433,7 +446,7 @@ __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restr
   for (int i = 0; i < kItems; ++i) {
     const uint32_t idx = base + i * kThreads + threadIdx.x;
     if (idx < n) {
-      const uint32_t k = length_class(nptr[idx + 1] - nptr[idx]);
+      const uint32_t k = length_class(item_length<CSR>(src, idx), cb);
 #pragma unroll
       for (int q = 0; q < 4; ++q) c[q] += (k == (uint32_t)q);
     }
@@ -451,9 +464,10 @@ __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restr
 
 // Same tile walk as the radix scatter: wave w owns items [w*1024, (w+1)*1024)
 // in index order; two ballots identify lanes of the same class.
-__global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __restrict__ nptr, uint32_t n,
-                                                            const uint32_t* __restrict__ cnt_scan, uint32_t ntiles,
-                                                            int32_t* __restrict__ order) {
+template <bool CSR>
+__global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __restrict__ src, uint32_t n,
+                                                            ClassBounds cb, const uint32_t* __restrict__ cnt_scan,
+                                                            uint32_t ntiles, int32_t* __restrict__ order) {
   __shared__ uint32_t wcnt[kThreads / 64][4];
   __shared__ uint32_t gbase[4];
   const int wave = threadIdx.x >> 6, lane = __lane_id();
@@ -467,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
   for (int t = 0; t < kItems; ++t) {
     const uint32_t idx = base + t * 64 + lane;
     const bool valid = idx < n;
-    const uint32_t k = valid ? length_class(nptr[idx + 1] - nptr[idx]) : 0u;
+    const uint32_t k = valid ? length_class(item_length<CSR>(src, idx), cb) : 0u;
     cls[t] = k;
     uint64_t peers = __ballot(valid);
     const uint64_t b0 = __ballot(k & 1u), b1 = __ballot((k >> 1) & 1u);
@@ -506,21 +520,34 @@ __global__ void k_class_totals(const uint32_t* __restrict__ cnt_scan, uint32_t n
   }
 }
 
+template <bool CSR>
+void partition_by_length(const Grid& g, const int32_t* src, ClassBounds cb, int32_t* order, int32_t* class_counts,
+                         hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  const uint32_t ntiles = (uint32_t)g.n_tiles;
+  uint32_t* cnt = g.hist;  // 4 * ntiles <= 256 * ntiles words
+  hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles);
+  SPHOPS_LAUNCHED();
+  device_exclusive_scan(cnt, cnt, 4ull * ntiles, g.scan_tmp, nullptr, st);
+  hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles, order);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL(k_class_totals, dim3(1), dim3(64), 0, st, cnt, ntiles, n, class_counts);
+  SPHOPS_LAUNCHED();
+}
+
 }  // namespace
 
 void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, int32_t* class_counts,
                             hipStream_t st) {
-  const uint32_t n = (uint32_t)g.n_keys;
-  if (n == 0) return;
-  const uint32_t ntiles = (uint32_t)g.n_tiles;
-  uint32_t* cnt = g.hist;  // 4 * ntiles <= 256 * ntiles words
-  hipLaunchKernelGGL(k_class_count, dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cnt, ntiles);
-  SPHOPS_LAUNCHED();
-  device_exclusive_scan(cnt, cnt, 4ull * ntiles, g.scan_tmp, nullptr, st);
-  hipLaunchKernelGGL(k_class_scatter, dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cnt, ntiles, order);
-  SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_class_totals, dim3(1), dim3(64), 0, st, cnt, ntiles, n, class_counts);
-  SPHOPS_LAUNCHED();
+  if (g.n_keys == 0) return;
+  partition_by_length<true>(g, nptr, ClassBounds{kListClassBounds[0], kListClassBounds[1], kListClassBounds[2]},
+                            order, class_counts, st);
+}
+
+void run_candidate_schedule(const Grid& g, const int32_t* cand, int32_t* order, int32_t* class_counts,
+                            hipStream_t st) {
+  if (g.n_keys == 0) return;
+  partition_by_length<false>(g, cand, ClassBounds{16, 64, 256}, order, class_counts, st);
 }
 
 void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* total, hipStream_t st) {

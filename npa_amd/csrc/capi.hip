@@ -60,6 +60,9 @@ void free_grid(Grid* g) {
   (void)hipFree(g->chunk_lo);
   (void)hipFree(g->flags);
   (void)hipFree(g->packed);
+  (void)hipFree(g->cand);
+  (void)hipFree(g->cand_order);
+  (void)hipFree(g->cand_classes);
   delete g;
 }
 
@@ -227,6 +230,9 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
       g->flags = dalloc<uint32_t>(BN + 1);
       g->packed = dalloc<float4>(BN);
+      g->cand = dalloc<int32_t>(BN);
+      g->cand_order = dalloc<int32_t>(BN);
+      g->cand_classes = dalloc<int32_t>(4);
     } catch (...) {
       sphops::free_grid(g);
       throw;

@@ -817,7 +817,7 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
   if (wave >= sc.wave_start[4]) return;
   int c = 0;
   while (c < 3 && wave >= sc.wave_start[c + 1]) ++c;
-  const int G = kGroupSizes[c];
+  const int G = kListGroupSizes[c];
   const int lane = __lane_id();
   const uint32_t slot = (wave - sc.wave_start[c]) * (uint32_t)(kWave / G) + (uint32_t)(lane / G);
   const int sub = lane & (G - 1);
@@ -856,6 +856,135 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
   if (active && sub == 0) op.finish(g, a, k);
 }
 
+// ------------------------------------------------- neighbour-list build
+//
+// Candidates of particle k = the concatenation of its stencil ranges.  The
+// count and fill passes serve k with a group of G lanes (G by candidate-count
+// class): lane `sub` tests candidate positions sub, sub+G, ...  The fill
+// ranks each round's in-radius hits by ballot inside the group, so the list
+// keeps stencil order.  Both kernels are persistent: the grid is fixed and
+// waves loop over work units computed from the device-side class sizes.
+
+template <int D, bool P>
+__global__ __launch_bounds__(kThreads) void k_candidates(GridParams g, const int32_t* __restrict__ bo,
+                                                         const float4* __restrict__ xw, int32_t* __restrict__ cand) {
+  const uint32_t n = g.B * g.N;
+  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
+  if (k >= n) return;
+  float xi[3];
+  unpack(xw[k], xi);
+  Walker<D, P> w;
+  w.init(g, xi, k);
+  int32_t total = 0;
+  while (w.fetch(g, bo, w.r)) {
+    ++w.r;
+    total += (int32_t)(w.jend - w.j);
+  }
+  cand[k] = total;
+}
+
+constexpr int kScanUnroll = 4;
+
+template <int D, bool P, bool FILL>
+__global__ __launch_bounds__(kThreads) void k_scan_grouped(GridParams g, const int32_t* __restrict__ bo,
+                                                           const float4* __restrict__ xw,
+                                                           const int32_t* __restrict__ cand,
+                                                           const int32_t* __restrict__ order,
+                                                           const int32_t* __restrict__ classes,
+                                                           const int32_t* __restrict__ nptr,
+                                                           int32_t* __restrict__ out) {
+  uint32_t ustart[5], pstart[4], ncls[4];
+  {
+    uint32_t run = 0, pr = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      ncls[c] = (uint32_t)classes[c];
+      const uint32_t per = (uint32_t)(kWave / kGroupSizes[c]);
+      ustart[c] = run;
+      pstart[c] = pr;
+      run += (ncls[c] + per - 1) / per;
+      pr += ncls[c];
+    }
+    ustart[4] = run;
+  }
+  const uint32_t nwaves = gridDim.x * (kThreads / kWave);
+  const int lane = __lane_id();
+  for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < ustart[4]; u += nwaves) {
+    int c = 0;
+    while (c < 3 && u >= ustart[c + 1]) ++c;
+    const int G = kGroupSizes[c];
+    const uint32_t slot = (u - ustart[c]) * (uint32_t)(kWave / G) + (uint32_t)(lane / G);
+    const int sub = lane & (G - 1);
+    const bool active = slot < ncls[c];
+    const uint32_t k = active ? (uint32_t)order[pstart[c] + slot] : 0u;
+    const uint32_t ncand = active ? (uint32_t)cand[k] : 0u;
+    float xi[3] = {0.0f, 0.0f, 0.0f};
+    Walker<D, P> w;
+    uint32_t pr = 0, ra = 0, rlen = 0;
+    if (active) {
+      unpack(xw[k], xi);
+      w.init(g, xi, k);
+      if (w.next(g, bo)) {
+        ra = w.j;
+        rlen = w.jend - w.j;
+      }
+    }
+    const uint64_t gmask = G == 64 ? ~0ull : ((1ull << G) - 1ull);
+    const int gshift = lane & ~(G - 1);
+    int32_t acc = FILL ? (active ? nptr[k] : 0) : 0;
+    const int32_t row_end = FILL ? (active ? nptr[k + 1] : 0) : 0;
+    for (uint32_t base = 0; base < ncand; base += (uint32_t)(G * kScanUnroll)) {
+      uint32_t jj[kScanUnroll];
+      bool ok[kScanUnroll];
+#pragma unroll
+      for (int q = 0; q < kScanUnroll; ++q) {
+        const uint32_t p = base + (uint32_t)(q * G + sub);
+        ok[q] = p < ncand;
+        jj[q] = 0;
+        if (ok[q]) {
+          while (p >= pr + rlen) {
+            pr += rlen;
+            w.j = w.jend;
+            if (!w.next(g, bo)) {  // stencil exhausted: candidate count and ranges disagree
+              rlen = 0xFFFFFFFFu - pr;
+              ok[q] = false;
+              break;
+            }
+            ra = w.j;
+            rlen = w.jend - w.j;
+          }
+          if (ok[q]) jj[q] = ra + (p - pr);
+        }
+      }
+      float4 pj[kScanUnroll];
+#pragma unroll
+      for (int q = 0; q < kScanUnroll; ++q) pj[q] = xw[jj[q]];
+#pragma unroll
+      for (int q = 0; q < kScanUnroll; ++q) {
+        bool in = false;
+        if (ok[q]) {
+          float xj[3], r[3];
+          unpack(pj[q], xj);
+          in = displacement<D, P>(g, xi, xj, r) < g.eps2;
+        }
+        if constexpr (FILL) {
+          const uint64_t gb = (__ballot(in) >> gshift) & gmask;
+          const int32_t pos = acc + (int32_t)__popcll(gb & ((1ull << sub) - 1ull));
+          if (in && pos < row_end) out[pos] = (int32_t)jj[q];
+          acc += (int32_t)__popcll(gb);
+        } else {
+          acc += in ? 1 : 0;
+        }
+      }
+    }
+    if constexpr (!FILL) {
+      float v = (float)acc;
+      v = grp_sum(v, G);
+      if (active && sub == 0) out[k] = (int32_t)v;
+    }
+  }
+}
+
 inline dim3 grid_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) / kThreads)); }
 
 template <int D, class OP>
@@ -865,6 +994,36 @@ void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
                      (uint32_t)g.n_keys);
   SPHOPS_LAUNCHED();
   a.xw = g.packed;
+}
+
+constexpr uint32_t kPersistentWorkgroups = 2048;
+
+// Candidate counts and their class schedule (into the grid's scratch).
+template <int D, bool P>
+void candidate_schedule(const Grid& g, const int32_t* bo, const float* x, hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, g.cand);
+  SPHOPS_LAUNCHED();
+  run_candidate_schedule(g, g.cand, g.cand_order, g.cand_classes, st);
+}
+
+template <int D, bool P>
+void neighbour_count(const Grid& g, const int32_t* bo, const float* x, int32_t* counts, hipStream_t st) {
+  candidate_schedule<D, P>(g, bo, x, st);
+  hipLaunchKernelGGL((k_scan_grouped<D, P, false>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo,
+                     g.packed, g.cand, g.cand_order, g.cand_classes, nullptr, counts);
+  SPHOPS_LAUNCHED();
+}
+
+template <int D, bool P>
+void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, const int32_t* nptr, int32_t* nidx,
+                    hipStream_t st) {
+  candidate_schedule<D, P>(g, bo, x, st);
+  hipLaunchKernelGGL((k_scan_grouped<D, P, true>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo,
+                     g.packed, g.cand, g.cand_order, g.cand_classes, nptr, nidx);
+  SPHOPS_LAUNCHED();
 }
 
 template <int D, bool P, class OP>
@@ -878,7 +1037,7 @@ void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
     for (int c = 0; c < 4; ++c) {
       sc.wave_start[c] = waves;
       sc.part_start[c] = part;
-      const uint32_t per_wave = (uint32_t)(kWave / kGroupSizes[c]);
+      const uint32_t per_wave = (uint32_t)(kWave / kListGroupSizes[c]);
       waves += ((uint32_t)a.class_count[c] + per_wave - 1) / per_wave;
       part += (uint32_t)a.class_count[c];
     }
@@ -928,16 +1087,12 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
     case Op::Blur: return launch_channels<D, P, OpBlur>(g, bo, a, st);
     case Op::Gradient: return launch_channels<D, P, OpGradient>(g, bo, a, st);
     case Op::GradientHybrid: return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
-    case Op::NeighbourCount: {
-      OpPtrs b = a;
-      b.nidx = nullptr;  // counting always scans the stencil
-      return launch_pairs<D, P, OpNeighbourCount<D, P>>(g, bo, b, st);
-    }
-    case Op::NeighbourFill: {
-      OpPtrs b = a;
-      b.nidx = nullptr;
-      return launch_pairs<D, P, OpNeighbourFill<D, P>>(g, bo, b, st);
-    }
+    case Op::NeighbourCount:
+      if (g.n_keys) neighbour_count<D, P>(g, bo, a.x, a.iout, st);
+      return;
+    case Op::NeighbourFill:
+      if (g.n_keys) neighbour_fill<D, P>(g, bo, a.x, a.nptr, a.iout, st);
+      return;
   }
   throw Error("unknown forward operator");
 }

@@ -146,13 +146,19 @@ __device__ __forceinline__ float poly6(float eps2, float d2) {
   return fmaxf(0.0f, t * t * t);
 }
 
+// Hardware square root and reciprocal (v_sqrt_f32 / v_rcp_f32, 1 ulp): the
+// pair kernels use them for |r| and 1/|r|; the in-radius decision never
+// depends on them (it compares |r|^2 with eps^2).
+__device__ __forceinline__ float fast_sqrt(float v) { return __builtin_amdgcn_sqrtf(v); }
+__device__ __forceinline__ float fast_rcp(float v) { return __builtin_amdgcn_rcpf(v); }
+
 // Spiky magnitude 3 (h - d)^2 / d for 0 < d < h, else 0; returns d too.
 __device__ __forceinline__ float spiky_mag(float eps, float d2, float* d_out) {
-  float d = sqrtf(d2);
+  const float d = fast_sqrt(d2);
   *d_out = d;
-  if (d == 0.0f || !(d < eps)) return 0.0f;
-  float t = eps - d;
-  return 3.0f * t * t / d;
+  if (d2 == 0.0f || !(d < eps)) return 0.0f;
+  const float t = eps - d;
+  return 3.0f * t * t * fast_rcp(d);
 }
 
 // grad_out += J(r) * v with J = dK/dr (utils.cuh:242-260); no-op outside (0, h).
@@ -160,10 +166,10 @@ template <int D>
 __device__ __forceinline__ void spiky_jacobian_apply(const float* r, float d2, float eps, float eps2,
                                                      const float* v, float* out) {
   if (d2 == 0.0f || !(d2 < eps2)) return;
-  float d = sqrtf(d2);
-  float di = 1.0f / d;
-  float a = 3.0f * (eps - d) * (eps - d) * di;    // diagonal part
-  float b = 3.0f * (eps2 - d2) * di * di * di;    // r r^T part
+  const float d = fast_sqrt(d2);
+  const float di = fast_rcp(d);
+  const float a = 3.0f * (eps - d) * (eps - d) * di;   // diagonal part
+  const float b = 3.0f * (eps2 - d2) * di * di * di;   // r r^T part
   float rv = 0.0f;
 #pragma unroll
   for (int e = 0; e < D; ++e) rv += r[e] * v[e];

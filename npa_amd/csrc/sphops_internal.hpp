@@ -49,6 +49,10 @@ struct Grid {
   uint32_t* chunk_lo = nullptr;   // n_chunks + 1
   uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
   float4* packed = nullptr;       // B*N (x, y, z|0, weight) read by the pair kernels
+  int32_t* cand = nullptr;        // B*N stencil candidate counts
+  int32_t* cand_order = nullptr;  // B*N particles by candidate-count class
+  int32_t* cand_classes = nullptr;  // 4 class sizes (device)
+  const void* cand_key[2] = {nullptr, nullptr};  // (positions, bin_offsets) the schedule was built for
 };
 
 // binning.hip
@@ -101,7 +105,13 @@ void run_neighbour_count(const Grid& g, const float* x, const int32_t* bo, int32
 // particles ordered by neighbour-list length class (group sizes 1, 4, 16, 64)
 void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, int32_t* class_counts,
                             hipStream_t st);
-constexpr int kGroupSizes[4] = {1, 4, 16, 64};
+// particles ordered by stencil candidate count class (group sizes 1, 4, 8, 16)
+void run_candidate_schedule(const Grid& g, const int32_t* cand, int32_t* order, int32_t* class_counts,
+                            hipStream_t st);
+constexpr int kGroupSizes[4] = {1, 4, 8, 16};       // candidate-scan groups
+constexpr int kListGroupSizes[4] = {1, 4, 16, 64};  // pair-list groups
+// list-length class bounds for the pair-list groups (<= t0, <= t1, <= t2, longer)
+constexpr int kListClassBounds[3] = {4, 32, 128};
 void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
