@@ -5,6 +5,9 @@ the reference) with the full backward (stopgrad_pos=False):
   instantiate (rebin) -> bin_particles -> density -> blur -> gradient_hybrid
   -> density_gradient -> backward of all three outputs with fixed upstream
   gradients (through density and the permutation).
+The calls are the reference's public functions; the library evaluates
+density + density_gradient and blur + gradient_hybrid as two fused passes
+once the grid has seen them called together (the warm-up step does that).
 Workload: BASELINE.json config 5 (3D stress): N = 1,048,576 particles from 8
 Gaussians, C = 16, h calibrated to 32 mean neighbours, clamped grid, inputs
 resident in HBM before timing.
@@ -36,6 +39,9 @@ def parse():
     ap.add_argument("--variant", default="full", choices=["full", "npa"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE runs that fill roofline.traffic")
+    ap.add_argument("--pmc-child", default=None, help=argparse.SUPPRESS)
     return ap.parse_args()
 
 
@@ -55,19 +61,43 @@ def per_particle_bytes(C, D, P):
         "gradient_bwd": x + m + rho + s + g_cd + P * f + C * f + f,
         "density_gradient_bwd": x + m + D * f + P * f,
         "density_bwd": x + m + f + P * f,
+        # fused passes: pass A = density + density_gradient, pass B = blur + gradient_hybrid
+        "pass_a_fwd": x + m + f + D * f,
+        "pass_b_fwd": x + m + rho + s + C * f + C * D * f,
+        "pass_a_bwd": x + m + f + D * f + P * f,
+        "pass_b_bwd": x + m + rho + s + g_s + g_cd + P * f + C * f + f,
+        "pass_b_bwd_ds": x + m + rho + g_s + g_cd + C * f,
     }
 
 
-def step_bytes(C, D, P, cells):
-    """Algorithmic bytes of one full step: the kernels above plus binning
-    (key pass, sort, permutation, bin_offsets write), bin and unbin moves."""
-    k = per_particle_bytes(C, D, P)
-    f = 4
-    binning = P * f + 4 * f + f        # read x, keys+values out, permutation out
-    move = 2 * (P * f + C * f + f) + f  # bin_particles read+write, perm read
-    unmove = 2 * (P * f + C * f + f) + f
-    per_particle = binning + move + unmove + sum(k.values())
-    return per_particle, 4 * cells
+# single pair kernels the timed step launches (with pass fusion), per variant;
+# the pass-B backward is blur's backward followed by the gradient's backward
+# (which adds into blur's outputs)
+STEP_KERNELS = {
+    "full": ("pass_a_fwd", "pass_b_fwd", "pass_a_bwd", "blur_bwd", "gradient_bwd"),
+    "npa": ("density_fwd", "pass_b_fwd", "blur_bwd", "gradient_bwd"),
+}
+
+# rocprofv3 kernel-name fragment of each timed call's pair kernel
+PAIR_KERNEL = {
+    "gradient_bwd": "OpGradientBwd<3, false, 16, true, true, false>",
+    "blur_bwd": "OpBlurBwd<3, false, 16, true, true>",
+    "pass_b_fwd": "OpBlurGradientHybrid<3, false, 16, true>",
+    "pass_a_fwd": "OpDensityPair<3, false>",
+    "pass_a_bwd": "OpDensityPairBwd<3, false>",
+}
+COPY_BYTES = 256 << 20
+
+
+def step_bytes(C, D, P, full=True):
+    """Minimal compulsory HBM bytes of one step per particle (each tensor of
+    the step read or written once per pass: hash + sort, permute, pass A,
+    pass B, their backward, permute backward) and per cell (the bin_offsets
+    write): full backward 48P + 36C + 8CD + 8D + 68, NPA default
+    (stopgrad_pos, no density gradient) 32P + 32C + 8CD + 4D + 56."""
+    if full:
+        return 48 * P + 36 * C + 8 * C * D + 8 * D + 68, 4
+    return 32 * P + 32 * C + 8 * C * D + 4 * D + 56, 4
 
 
 def main():
@@ -76,6 +106,12 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
                           "(multi-GPU sharding is a design note, not implemented)"}))
         sys.exit(2)
+    if args.pmc_child:
+        return pmc_child(args)
+    # counter runs first, in child processes, before this process touches the GPU
+    pmc = None
+    if not args.no_traffic:
+        pmc = measure_traffic(args, "gradient_bwd")
     import numpy as np
     import torch
 
@@ -141,12 +177,15 @@ def main():
     # ---- per-kernel timing (HIP events on the launch stream)
     kt = kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, args.kernel_reps)
     ppb = per_particle_bytes(C, D, P)
-    dom = max((k for k in kt if k in ppb), key=lambda k: kt[k])
+    dom = max(STEP_KERNELS[args.variant], key=lambda k: kt[k])
     dom_ms = kt[dom]
     alg = ppb[dom] * B * N
     achieved = alg / (dom_ms * 1e-3) / 1e9
-    pp, cell_bytes = step_bytes(C, D, P, cells)
-    step_alg = pp * B * N + cell_bytes
+    pp, pc = step_bytes(C, D, P, full)
+    step_alg = pp * B * N + pc * cells
+    traffic = None
+    if pmc is not None and pmc.get("kernel") == dom:
+        traffic = pmc["bytes_per_launch"]
     print("[bench] kernel ms: " + ", ".join(f"{k}={v:.3f}" for k, v in sorted(kt.items(), key=lambda t: -t[1])),
           file=sys.stderr, flush=True)
 
@@ -184,16 +223,18 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
             "alg_bytes_per_launch": alg,
             "avg_launch_ms": dom_ms,
+            "pair_kernel": PAIR_KERNEL.get(dom),
+            "pmc": pmc,
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
 
-def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps):
+def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps, only=None):
     """Average duration of each native operator call on the path the step
     takes (generic entry points with the snapshot's neighbour list), by HIP
     events on the current stream around `reps` back-to-back calls.  An
@@ -215,11 +256,13 @@ def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps):
         torch.cuda.synchronize()
         out[name] = a.elapsed_time(b) / n
 
-    timed("instantiate", lambda: grid.instantiate(x))
+    if only is None:
+        timed("instantiate", lambda: grid.instantiate(x))
     snap = grid.instantiate(x)
     xb, sb = sp.bin_particles(x, s, snap)
-    timed("bin_particles", lambda: sp.bin_particles(x, s, snap))
-    timed("neighbor_list", lambda: hg.neighbor_list(xb, snap.bin_offsets))
+    if only is None:
+        timed("bin_particles", lambda: sp.bin_particles(x, s, snap))
+        timed("neighbor_list", lambda: hg.neighbor_list(xb, snap.bin_offsets))
     nbr = _plan(snap, xb)
     rho = sp.density(xb, snap)
     m = torch.ones_like(rho)
@@ -246,9 +289,119 @@ def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps):
         calls["density_gradient_bwd"] = lambda: hg.op_backward(O.OP_DENSITY_GRADIENT, xb, g_dg, bo, m,
                                                                grad_x=bufs["gx"], nbr=nbr)
         calls["density_bwd"] = lambda: hg.op_backward(O.OP_DENSITY, xb, rho, bo, m, grad_x=bufs["gx"], nbr=nbr)
+    calls["pass_a_fwd"] = lambda: hg.op_forward(O.OP_DENSITY_PAIR, xb, bufs["rho"], bo, mass=m, nbr=nbr,
+                                                out2=bufs["dg"])
+    calls["pass_b_fwd"] = lambda: hg.op_forward(O.OP_BLUR_GRADIENT_HYBRID, xb, bufs["blur"], bo, mass=m, rho=rho,
+                                                state=sb, nbr=nbr, out2=bufs["gh"])
+    calls["pass_a_bwd"] = lambda: hg.op_backward(O.OP_DENSITY_PAIR, xb, rho, bo, m, grad_x=bufs["gx"], nbr=nbr,
+                                                 upstream2=g_dg)
+    calls["pass_b_bwd"] = lambda: hg.op_backward(O.OP_BLUR_GRADIENT_HYBRID, xb, g_blur, bo, m, rho=rho, state=sb,
+                                                 grad_x=bufs["gx"], grad_state=bufs["gs"], grad_rho=bufs["gr"],
+                                                 nbr=nbr, upstream2=g_hyb)
+    calls["pass_b_bwd_ds"] = lambda: hg.op_backward(O.OP_BLUR_GRADIENT_HYBRID, xb, g_blur, bo, m, rho=rho,
+                                                    state=sb, grad_state=bufs["gs"], dLdx=False, dLdrho=False,
+                                                    nbr=nbr, upstream2=g_hyb)
     for name, fn in calls.items():
-        timed(name, fn)
+        if only is None or name == only:
+            timed(name, fn)
     return out
+
+
+def pmc_child(args):
+    """Runs under rocprofv3 --pmc: a plain copy of COPY_BYTES (the counter
+    calibration), then three calls of one timed operator on the workload."""
+    import torch
+    import npa_amd.sphops as sp
+    from npa_amd import workloads
+    torch.cuda.set_device(0)
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    wl = workloads.make(args.config)
+    B, N, C, D = wl.B, wl.N, wl.C, wl.dim
+    dev = torch.device("cuda", 0)
+    x = torch.from_numpy(wl.x).to(dev)
+    s = torch.from_numpy(wl.s).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    g_blur = torch.randn(B, N, C, device=dev, generator=gen)
+    g_hyb = torch.randn(B, N, C, D, device=dev, generator=gen)
+    g_dg = torch.randn(B, N, D, device=dev, generator=gen)
+    grid = sp.HashGrid(dim=D, boundary="periodic" if wl.periodic else "clamped", mode="grid",
+                       grid_size=list(wl.grid_size), eps=wl.h, num_particles=N, batch_size=B,
+                       max_particles_per_block=wl.maxp)
+    kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, args.variant == "full", 3, only=args.pmc_child)
+    torch.cuda.synchronize()
+    print(f"[pmc-child] {args.pmc_child} done", flush=True)
+
+
+def _pmc_run(counter, kernel, args):
+    """One rocprofv3 --pmc run of the child; returns {kernel name: mean value
+    per dispatch} for the copy kernel and the operator's pair kernel."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        raise RuntimeError("rocprofv3 not on PATH")
+    out = tempfile.mkdtemp(prefix="npa_pmc_", dir="/tmp")
+    cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "run", "--",
+           sys.executable, os.path.abspath(__file__), "--pmc-child", kernel, "--config", args.config,
+           "--variant", args.variant]
+    env = dict(os.environ, TMPDIR="/tmp")
+    r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=240)
+    if r.returncode != 0 or b"[pmc-child]" not in r.stdout:
+        raise RuntimeError(f"rocprofv3 --pmc {counter} exited {r.returncode}: {r.stdout[-400:]!r}")
+    path = None
+    for root, _, files in os.walk(out):
+        for f in files:
+            if f.endswith("counter_collection.csv"):
+                path = os.path.join(root, f)
+    if path is None:
+        raise RuntimeError("no counter_collection.csv")
+    per_dispatch = {}
+    with open(path) as fh:
+        for row in csv.DictReader(fh):
+            if row["Counter_Name"] != counter:
+                continue
+            key = (row["Dispatch_Id"], row["Kernel_Name"])
+            per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
+    shutil.rmtree(out, ignore_errors=True)
+    copy, target = [], []
+    for (_, name), v in per_dispatch.items():
+        if "copy" in name.lower():
+            copy.append(v)
+        elif PAIR_KERNEL[kernel] in name:
+            target.append(v)
+    if not copy or not target:
+        raise RuntimeError(f"{counter}: kernels not found in the counter output")
+    # the largest copy dispatches are the calibration copies
+    copy = sorted(copy)[-3:]
+    return sum(copy) / len(copy), sum(target) / len(target)
+
+
+def measure_traffic(args, kernel):
+    """HBM bytes per launch of `kernel`'s pair kernel: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
+    for a plain copy of COPY_BYTES (which must fetch and write COPY_BYTES)."""
+    try:
+        res = {"kernel": kernel, "copy_bytes": COPY_BYTES}
+        total = 0.0
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            c, t = _pmc_run(counter, kernel, args)
+            scale = COPY_BYTES / (c * 1024.0)
+            res[counter] = {"copy_kib": c, "kernel_kib": t, "scale": scale, "kernel_bytes": t * 1024.0 * scale}
+            total += t * 1024.0 * scale
+        res["bytes_per_launch"] = total
+        print(f"[bench] traffic of {kernel}: {total / 1e6:.1f} MB per launch "
+              f"(fetch {res['FETCH_SIZE']['kernel_bytes'] / 1e6:.1f}, write {res['WRITE_SIZE']['kernel_bytes'] / 1e6:.1f})",
+              file=sys.stderr, flush=True)
+        return res
+    except Exception as e:  # the counters are a report, not part of the measurement
+        print(f"[bench] traffic not measured: {e}", file=sys.stderr, flush=True)
+        return None
 
 
 def cpu_baseline(wl, pairs_per_step):

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 1
+#define SPHOPS_ABI_VERSION 2
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -137,7 +137,15 @@ int sphops_moment_matrix_backward(const sphops_grid* grid, const float* x, const
  * its methods above traverse the cell stencil on every call.  Building the
  * list once per snapshot (sphops_neighbor_count + sphops_neighbor_fill) and
  * passing it here makes every later operator walk only in-radius pairs;
- * results are identical (same pairs, same order, same arithmetic). */
+ * the pair set is identical, only the fp32 summation order can differ.
+ *
+ * Two fused codes evaluate operators that the reference always runs over the
+ * same neighbours one after the other (models/npa.py:106-126) in one pass:
+ * DENSITY_PAIR = density (out) + density_gradient (out2), both mass-weighted;
+ * BLUR_GRADIENT_HYBRID = blur (out) + gradient_hybrid (out2), both reading
+ * x, rho, mass and state.  Their backward takes the first operator's
+ * upstream in `upstream` and the second's in `upstream2` and writes the sum
+ * of both operators' gradients. */
 
 #define SPHOPS_OP_COUNT 0
 #define SPHOPS_OP_DENSITY 1
@@ -146,6 +154,8 @@ int sphops_moment_matrix_backward(const sphops_grid* grid, const float* x, const
 #define SPHOPS_OP_BLUR 4
 #define SPHOPS_OP_GRADIENT 5
 #define SPHOPS_OP_GRADIENT_HYBRID 6
+#define SPHOPS_OP_DENSITY_PAIR 7
+#define SPHOPS_OP_BLUR_GRADIENT_HYBRID 8
 
 typedef struct sphops_args {
   const float* x;              /* binned positions (B,N,2|4) */
@@ -163,6 +173,8 @@ typedef struct sphops_args {
   const int32_t* nbr_index;    /* optional CSR indices from sphops_neighbor_fill; NULL: scan the stencil */
   const int32_t* nbr_order;    /* optional particle order by list-length class (sphops_neighbor_schedule) */
   int32_t nbr_class_count[4];  /* host copy of the class sizes written by sphops_neighbor_schedule */
+  const float* upstream2;      /* fused backward: dL/d(second output) */
+  float* out2;                 /* fused forward: the second output */
 } sphops_args;
 
 /* Forward operator `op` (SPHOPS_OP_*) on binned particles. */
@@ -170,7 +182,9 @@ int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, voi
 
 /* Backward of operator `op` (not COUNT); flags as in the per-operator
  * functions above.  For SPHOPS_OP_GRADIENT_HYBRID it is the gradient
- * operator's backward (straight-through, sphops/sph.py:482). */
+ * operator's backward (straight-through, sphops/sph.py:482); the fused codes
+ * need both upstreams (pass zeros, or better the single operator, when one
+ * output has no gradient). */
 int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLdrho, const sphops_args* args,
                     void* stream);
 

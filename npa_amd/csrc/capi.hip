@@ -296,13 +296,14 @@ static int fwd_op(const sphops_grid* grid, Op op, const int32_t* bo, OpPtrs a, v
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
     require(bo != nullptr && a.x != nullptr && a.out0 != nullptr, "null buffer");
-    if (op == Op::Blur || op == Op::Gradient || op == Op::GradientHybrid) {
+    const bool chan = op == Op::Blur || op == Op::Gradient || op == Op::GradientHybrid || op == Op::BlurGradientHybrid;
+    if (chan) {
       sphops::check_channels(a.C);
       require(a.s != nullptr, "state must not be NULL");
     }
     if (op != Op::Count) require(a.m != nullptr, "mass must not be NULL");
-    if (op == Op::Blur || op == Op::Gradient || op == Op::GradientHybrid || op == Op::MomentMatrix)
-      require(a.rho != nullptr, "rho must not be NULL");
+    if (chan || op == Op::MomentMatrix) require(a.rho != nullptr, "rho must not be NULL");
+    if (op == Op::DensityPair || op == Op::BlurGradientHybrid) require(a.out3 != nullptr, "out2 must not be NULL");
     require(grid->dim == 2 || sphops::pk::aligned16(a.x), "3D positions must be 16-byte aligned");
     sphops::forward(*grid, op, bo, a, sphops::as_stream(stream));
   });
@@ -388,7 +389,7 @@ static int bwd_op(const sphops_grid* grid, Op op, bool full, const int32_t* bo, 
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
     require(bo != nullptr && a.x != nullptr && a.m != nullptr && a.g != nullptr, "null buffer");
-    if (op == Op::Blur || op == Op::Gradient) {
+    if (op == Op::Blur || op == Op::Gradient || op == Op::BlurGradientHybrid) {
       sphops::check_channels(a.C);
       require(a.rho != nullptr && a.s != nullptr && a.out1 != nullptr, "null buffer");
       if (full) require(a.out0 != nullptr && a.out2 != nullptr, "null buffer");
@@ -493,6 +494,8 @@ static OpPtrs from_args(const sphops_args* a) {
   p.nidx = a->nbr_index;
   p.order = a->nbr_order;
   for (int c = 0; c < 4; ++c) p.class_count[c] = a->nbr_class_count[c];
+  p.g2 = a->upstream2;
+  p.out3 = a->out2;
   return p;
 }
 
@@ -507,7 +510,7 @@ int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, voi
     sphops::g_last_error = "args must not be NULL";
     return -1;
   }
-  if (op < SPHOPS_OP_COUNT || op > SPHOPS_OP_GRADIENT_HYBRID) {
+  if (op < SPHOPS_OP_COUNT || op > SPHOPS_OP_BLUR_GRADIENT_HYBRID) {
     sphops::g_last_error = "unknown operator " + std::to_string(op);
     return -1;
   }
@@ -522,7 +525,7 @@ int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLd
     sphops::g_last_error = "args must not be NULL";
     return -1;
   }
-  if (op <= SPHOPS_OP_COUNT || op > SPHOPS_OP_GRADIENT_HYBRID) {
+  if (op <= SPHOPS_OP_COUNT || op > SPHOPS_OP_BLUR_GRADIENT_HYBRID) {
     sphops::g_last_error = "operator " + std::to_string(op) + " has no backward";
     return -1;
   }
@@ -530,9 +533,14 @@ int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLd
   if (st) return st;
   const Op o = static_cast<Op>(op);
   OpPtrs a = from_args(args);
+  if (o == Op::DensityPair || o == Op::BlurGradientHybrid) {
+    st = guarded([&] { require(a.g != nullptr && a.g2 != nullptr, "fused backward needs upstream and upstream2"); });
+    if (st) return st;
+  }
   switch (o) {
     case Op::Density:
     case Op::DensityGradient:
+    case Op::DensityPair:
       if (!dLdx) return 0;
       return bwd_op(grid, o, true, args->bin_offsets, a, stream);
     case Op::MomentMatrix:

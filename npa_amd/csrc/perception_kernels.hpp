@@ -125,9 +125,9 @@ struct Walker {
 // ------------------------------------------------------------- row loads
 
 template <int N, bool VEC>
-__device__ __forceinline__ void load_row(const float* __restrict__ p, uint64_t row, float* v) {
+__device__ __forceinline__ void load_span(const float* __restrict__ p, float* v) {
   if constexpr (VEC) {
-    const float4* q = reinterpret_cast<const float4*>(p + row * N);
+    const float4* q = reinterpret_cast<const float4*>(p);
 #pragma unroll
     for (int u = 0; u < N / 4; ++u) {
       const float4 t = q[u];
@@ -138,7 +138,7 @@ __device__ __forceinline__ void load_row(const float* __restrict__ p, uint64_t r
     }
   } else {
 #pragma unroll
-    for (int u = 0; u < N; ++u) v[u] = p[row * N + u];
+    for (int u = 0; u < N; ++u) v[u] = p[u];
   }
 }
 
@@ -147,9 +147,10 @@ __device__ __forceinline__ void load_row(const float* __restrict__ p, uint64_t r
 template <int CM, bool EXACT>
 struct Chan {
   static constexpr bool kVec = EXACT && (CM % 4 == 0);
+  __device__ static __forceinline__ uint32_t stride(uint32_t C) { return EXACT ? (uint32_t)CM : C; }
   __device__ static __forceinline__ void load(const float* __restrict__ p, uint64_t row, uint32_t C, float* v) {
     if constexpr (EXACT) {
-      load_row<CM, kVec>(p, row, v);
+      load_span<CM, kVec>(p + row * CM, v);
     } else {
 #pragma unroll
       for (int f = 0; f < CM; ++f) v[f] = (f < (int)C) ? p[row * C + f] : 0.0f;
@@ -158,7 +159,7 @@ struct Chan {
   template <int D>
   __device__ static __forceinline__ void load_cd(const float* __restrict__ p, uint64_t row, uint32_t C, float* v) {
     if constexpr (EXACT) {
-      load_row<CM * D, (CM * D) % 4 == 0 && kVec>(p, row, v);
+      load_span<CM * D, (CM * D) % 4 == 0 && kVec>(p + row * CM * D, v);
     } else {
 #pragma unroll
       for (int f = 0; f < CM * D; ++f) v[f] = (f < (int)C * D) ? p[row * C * D + f] : 0.0f;
@@ -166,12 +167,33 @@ struct Chan {
   }
 };
 
-template <int D>
+// Backward outputs: store, or (ACC) add to what an earlier launch on the
+// same stream stored; each element has one owning lane.
+template <bool ACC>
+__device__ __forceinline__ void put(float* __restrict__ out, uint64_t i, float v) {
+  if constexpr (ACC) v += out[i];
+  out[i] = v;
+}
+
+template <int D, bool ACC = false>
 __device__ __forceinline__ void store_pos_grad(float* __restrict__ out, uint32_t k, const float* v, float scale) {
   if constexpr (D == 2) {
-    reinterpret_cast<float2*>(out)[k] = make_float2(v[0] * scale, v[1] * scale);
+    float2 o = make_float2(v[0] * scale, v[1] * scale);
+    if constexpr (ACC) {
+      const float2 p = reinterpret_cast<const float2*>(out)[k];
+      o.x += p.x;
+      o.y += p.y;
+    }
+    reinterpret_cast<float2*>(out)[k] = o;
   } else {
-    reinterpret_cast<float4*>(out)[k] = make_float4(v[0] * scale, v[1] * scale, v[2] * scale, 0.0f);
+    float4 o = make_float4(v[0] * scale, v[1] * scale, v[2] * scale, 0.0f);
+    if constexpr (ACC) {
+      const float4 p = reinterpret_cast<const float4*>(out)[k];
+      o.x += p.x;
+      o.y += p.y;
+      o.z += p.z;
+    }
+    reinterpret_cast<float4*>(out)[k] = o;
   }
 }
 
@@ -218,17 +240,42 @@ __device__ __forceinline__ float back_disp(const GridParams& g, const float* xi,
   }
 }
 
-// Sum over the aligned group of G lanes (G a power of two <= 64); every lane
-// of the group receives the same total (xor butterfly, fixed order).
-__device__ __forceinline__ float grp_sum(float v, int G) {
-  for (int off = 1; off < G; off <<= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+// Sum over aligned groups of G lanes (G a wave-uniform power of two <= 64),
+// delivered to each group's first lane; the other lanes keep partial sums.
+// A fixed tree: lane i adds lane i+1, then i+2, i+4, ... (DPP row_shl inside
+// 16-lane rows, with no LDS round trip; a bpermute for the 16 and 32 steps).
+// Every step shuffles all accumulators before adding, so the shuffles of one
+// step overlap.  The order is fixed, so results are deterministic.
+template <int STEP>
+__device__ __forceinline__ float grp_fetch(float v) {
+  if constexpr (STEP < 16) {
+    // DPP row_shl:STEP (0x100 + STEP), all rows and banks, 0 past the row end
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x100 + STEP, 0xF, 0xF, true));
+  } else {
+    return __shfl_down(v, STEP, kWave);
+  }
 }
 
-template <int N>
-__device__ __forceinline__ void grp_sum(float (&v)[N], int G) {
+template <int STEP>
+__device__ __forceinline__ void grp_add(float& v) { v += grp_fetch<STEP>(v); }
+
+template <int STEP, int N>
+__device__ __forceinline__ void grp_add(float (&v)[N]) {
+  float t[N];
 #pragma unroll
-  for (int q = 0; q < N; ++q) v[q] = grp_sum(v[q], G);
+  for (int q = 0; q < N; ++q) t[q] = grp_fetch<STEP>(v[q]);
+#pragma unroll
+  for (int q = 0; q < N; ++q) v[q] += t[q];
+}
+
+template <class... A>
+__device__ __forceinline__ void grp_sum(int G, A&... v) {
+  if (G > 1) (grp_add<1>(v), ...);
+  if (G > 2) (grp_add<2>(v), ...);
+  if (G > 4) (grp_add<4>(v), ...);
+  if (G > 8) (grp_add<8>(v), ...);
+  if (G > 16) (grp_add<16>(v), ...);
+  if (G > 32) (grp_add<32>(v), ...);
 }
 
 // ------------------------------------------------------------- operators
@@ -290,7 +337,7 @@ struct OpDensity {
                        float d2, uint32_t) {
     acc += poly6(g.eps2, d2) * wj;
   }
-  __device__ void reduce(int G) { acc = grp_sum(acc, G); }
+  __device__ void reduce(int G) { grp_sum(G, acc); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { a.out0[k] = acc * g.c6; }
 };
 
@@ -307,7 +354,7 @@ struct OpDensityGradient {
 #pragma unroll
     for (int e = 0; e < D; ++e) acc[e] += t * r[e];
   }
-  __device__ void reduce(int G) { grp_sum(acc, G); }
+  __device__ void reduce(int G) { grp_sum(G, acc); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
 #pragma unroll
     for (int e = 0; e < D; ++e) a.out0[(uint64_t)k * D + e] = acc[e] * g.cs;
@@ -329,7 +376,7 @@ struct OpMomentMatrix {
 #pragma unroll
       for (int q = 0; q < D; ++q) acc[p * D + q] += t * r[p] * r[q];
   }
-  __device__ void reduce(int G) { grp_sum(acc, G); }
+  __device__ void reduce(int G) { grp_sum(G, acc); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
 #pragma unroll
     for (int q = 0; q < D * D; ++q) a.out0[(uint64_t)k * D * D + q] = acc[q] * g.cs;
@@ -351,12 +398,12 @@ struct OpBlur {
 #pragma unroll
     for (int f = 0; f < CM; ++f) acc[f] += w * sj[f];
   }
-  __device__ void reduce(int G) { grp_sum(acc, G); }
+  __device__ void reduce(int G) { grp_sum(G, acc); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
 #pragma unroll
     for (int f = 0; f < CM; ++f)
-      if (f < (int)C) a.out0[(uint64_t)k * C + f] = acc[f] * g.c6;
+      if (f < (int)C) a.out0[(uint64_t)k * Ch::stride(a.C) + f] = acc[f] * g.c6;
   }
 };
 
@@ -381,12 +428,12 @@ struct OpGradient {
       for (int e = 0; e < D; ++e) acc[f * D + e] += q * r[e];
     }
   }
-  __device__ void reduce(int G) { grp_sum(acc, G); }
+  __device__ void reduce(int G) { grp_sum(G, acc); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
 #pragma unroll
     for (int f = 0; f < CM * D; ++f)
-      if (f < (int)(C * D)) a.out0[(uint64_t)k * C * D + f] = acc[f] * g.cs;
+      if (f < (int)(C * D)) a.out0[(uint64_t)k * Ch::stride(a.C) * D + f] = acc[f] * g.cs;
   }
 };
 
@@ -418,7 +465,7 @@ struct OpGradientHybrid {
       for (int e = 0; e < D; ++e) acc[f * D + e] += q * r[e];
     }
   }
-  __device__ void reduce(int G) { grp_sum(acc, G); grp_sum(M, G); }
+  __device__ void reduce(int G) { grp_sum(G, acc, M); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     float Ms[D * D], L[D * D];
 #pragma unroll
@@ -438,7 +485,94 @@ struct OpGradientHybrid {
         float o = 0.0f;
 #pragma unroll
         for (int q = 0; q < D; ++q) o += raw[q] * L[q * D + e];
-        a.out0[((uint64_t)k * C + f) * D + e] = o;
+        a.out0[(uint64_t)k * Ch::stride(a.C) * D + f * D + e] = o;
+      }
+    }
+  }
+};
+
+// ------------------------------------------------------- fused forward
+//
+// Operators that share a neighbour pass: density with density gradient
+// (both weighted by mass), blur with gradient_hybrid (both weighted by
+// volume m/rho and both reading s_j).  out0 gets the first, out3 the second.
+
+template <int D, bool P>
+struct OpDensityPair {
+  static constexpr int kWeightKind = kWMass;
+  static constexpr bool kChannels = false;
+  float rho = 0.0f;
+  float grad[D] = {};
+  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
+  __device__ void pair(const GridParams& g, const OpPtrs&, const float*, const float*, float wj, const float* r,
+                       float d2, uint32_t) {
+    rho += poly6(g.eps2, d2) * wj;
+    float d;
+    const float t = spiky_mag(g.eps, d2, &d) * wj;
+#pragma unroll
+    for (int e = 0; e < D; ++e) grad[e] += t * r[e];
+  }
+  __device__ void reduce(int G) { grp_sum(G, rho, grad); }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    a.out0[k] = rho * g.c6;
+#pragma unroll
+    for (int e = 0; e < D; ++e) a.out3[(uint64_t)k * D + e] = grad[e] * g.cs;
+  }
+};
+
+template <int D, bool P, int CM, bool EX>
+struct OpBlurGradientHybrid {
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr bool kChannels = true;
+  using Ch = Chan<CM, EX>;
+  float si[CM];
+  float blur[CM] = {};
+  float acc[CM * D] = {};
+  float M[D * D] = {};
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) { Ch::load(a.s, k, a.C, si); }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float*, const float*, float wj, const float* r,
+                       float d2, uint32_t j) {
+    const float w = poly6(g.eps2, d2) * wj;
+    float d;
+    const float t = spiky_mag(g.eps, d2, &d) * wj;
+#pragma unroll
+    for (int p = 0; p < D; ++p)
+#pragma unroll
+      for (int q = p; q < D; ++q) M[p * D + q] += t * r[p] * r[q];
+    float sj[CM];
+    Ch::load(a.s, j, a.C, sj);
+#pragma unroll
+    for (int f = 0; f < CM; ++f) {
+      blur[f] += w * sj[f];
+      const float q = t * (sj[f] - si[f]);
+#pragma unroll
+      for (int e = 0; e < D; ++e) acc[f * D + e] += q * r[e];
+    }
+  }
+  __device__ void reduce(int G) { grp_sum(G, blur, acc, M); }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    const uint32_t C = EX ? CM : a.C;
+#pragma unroll
+    for (int f = 0; f < CM; ++f)
+      if (f < (int)C) a.out0[(uint64_t)k * Ch::stride(a.C) + f] = blur[f] * g.c6;
+    float Ms[D * D], L[D * D];
+#pragma unroll
+    for (int p = 0; p < D; ++p)
+#pragma unroll
+      for (int q = 0; q < D; ++q) Ms[p * D + q] = (q >= p ? M[p * D + q] : M[q * D + p]) * g.cs;
+    safe_inv_sym<D>(Ms, a.tol, L);
+#pragma unroll
+    for (int f = 0; f < CM; ++f) {
+      if (f >= (int)C) continue;
+      float raw[D];
+#pragma unroll
+      for (int e = 0; e < D; ++e) raw[e] = acc[f * D + e] * g.cs;
+#pragma unroll
+      for (int e = 0; e < D; ++e) {
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < D; ++q) o += raw[q] * L[q * D + e];
+        a.out3[(uint64_t)k * Ch::stride(a.C) * D + f * D + e] = o;
       }
     }
   }
@@ -467,7 +601,7 @@ struct OpDensityBwd {
 #pragma unroll
     for (int e = 0; e < D; ++e) dx[e] += mag * rb[e];
   }
-  __device__ void reduce(int G) { grp_sum(dx, G); }
+  __device__ void reduce(int G) { grp_sum(G, dx); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { store_pos_grad<D>(a.out0, k, dx, g.c6); }
 };
 
@@ -491,7 +625,7 @@ struct OpDensityGradientBwd {
     for (int e = 0; e < D; ++e) diff[e] = a.g[(uint64_t)j * D + e] * mi - gi[e] * wj;
     spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, diff, dx);
   }
-  __device__ void reduce(int G) { grp_sum(dx, G); }
+  __device__ void reduce(int G) { grp_sum(G, dx); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) { store_pos_grad<D>(a.out0, k, dx, g.cs); }
 };
 
@@ -533,7 +667,7 @@ struct OpMomentMatrixBwd {
 #pragma unroll
     for (int p = 0; p < D; ++p) spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, &gd[p * D], dx);
   }
-  __device__ void reduce(int G) { grp_sum(dx, G); drho = grp_sum(drho, G); }
+  __device__ void reduce(int G) { grp_sum(G, dx, drho); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     store_pos_grad<D>(a.out0, k, dx, g.cs);
     a.out2[k] = -drho * mr2 * g.cs;
@@ -586,13 +720,13 @@ struct OpBlurBwd {
       }
     }
   }
-  __device__ void reduce(int G) { grp_sum(ds, G); grp_sum(dx, G); drho = grp_sum(drho, G); }
+  __device__ void reduce(int G) { grp_sum(G, ds, dx, drho); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
     const float sc = vi * g.c6;
 #pragma unroll
     for (int f = 0; f < CM; ++f)
-      if (f < (int)C) a.out1[(uint64_t)k * C + f] = ds[f] * sc;
+      if (f < (int)C) a.out1[(uint64_t)k * Ch::stride(a.C) + f] = ds[f] * sc;
     if constexpr (FULL) {
       a.out2[k] = -drho * mr2 * g.c6;
       store_pos_grad<D>(a.out0, k, dx, g.c6);
@@ -600,7 +734,7 @@ struct OpBlurBwd {
   }
 };
 
-template <int D, bool P, int CM, bool EX, bool FULL>
+template <int D, bool P, int CM, bool EX, bool FULL, bool ACC = false>
 struct OpGradientBwd {
   static constexpr int kWeightKind = kWVolume;
   static constexpr bool kChannels = true;
@@ -666,7 +800,7 @@ struct OpGradientBwd {
       spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, u, dx);
     }
   }
-  __device__ void reduce(int G) { grp_sum(ds, G); grp_sum(wsum, G); grp_sum(dx, G); drho = grp_sum(drho, G); }
+  __device__ void reduce(int G) { grp_sum(G, ds, wsum, dx, drho); }
   __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
     const uint32_t C = EX ? CM : a.C;
 #pragma unroll
@@ -675,12 +809,53 @@ struct OpGradientBwd {
       float t = vi * ds[f];
 #pragma unroll
       for (int e = 0; e < D; ++e) t += gi[f * D + e] * wsum[e];
-      a.out1[(uint64_t)k * C + f] = t * g.cs;
+      put<ACC>(a.out1, (uint64_t)k * Ch::stride(a.C) + f, t * g.cs);
     }
     if constexpr (FULL) {
-      a.out2[k] = -drho * mr2 * g.cs;
-      store_pos_grad<D>(a.out0, k, dx, g.cs);
+      put<ACC>(a.out2, k, -drho * mr2 * g.cs);
+      store_pos_grad<D, ACC>(a.out0, k, dx, g.cs);
     }
+  }
+};
+
+// ------------------------------------------------------ fused backward
+//
+// Backward of the fused pairs: upstream a.g for the first operator, a.g2
+// for the second; the gradients of both are summed into one set of outputs.
+
+template <int D, bool P>
+struct OpDensityPairBwd {
+  static constexpr int kWeightKind = kWMass;
+  static constexpr bool kChannels = false;
+  float gi = 0.0f, gdi[D], mi = 0.0f;
+  float dx_w[D] = {}, dx_k[D] = {};
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) {
+    gi = a.g[k];
+#pragma unroll
+    for (int e = 0; e < D; ++e) gdi[e] = a.g2[(uint64_t)k * D + e];
+    mi = a.m[k];
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float wj,
+                       const float* r, float d2, uint32_t j) {
+    float rb[3];
+    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
+    if (db != 0.0f && db < g.eps2) {
+      const float t = g.eps2 - db;
+      const float mag = -(gi * wj + a.g[j] * mi) * 6.0f * t * t;
+#pragma unroll
+      for (int e = 0; e < D; ++e) dx_w[e] += mag * rb[e];
+    }
+    float diff[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) diff[e] = a.g2[(uint64_t)j * D + e] * mi - gdi[e] * wj;
+    spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, diff, dx_k);
+  }
+  __device__ void reduce(int G) { grp_sum(G, dx_w, dx_k); }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k) {
+    float dx[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) dx[e] = dx_w[e] * g.c6 + dx_k[e] * g.cs;
+    store_pos_grad<D>(a.out0, k, dx, 1.0f);
   }
 };
 
@@ -979,7 +1154,7 @@ __global__ __launch_bounds__(kThreads) void k_scan_grouped(GridParams g, const i
     }
     if constexpr (!FILL) {
       float v = (float)acc;
-      v = grp_sum(v, G);
+      grp_sum(G, v);
       if (active && sub == 0) out[k] = (int32_t)v;
     }
   }
@@ -1062,7 +1237,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 template <int D, bool P, template <int, bool, int, bool> class OPT>
 void launch_channels(const Grid& g, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
   const uint32_t C = a.C;
-  const bool al = aligned16(a.s) && aligned16(a.g);
+  const bool al = aligned16(a.s) && aligned16(a.g) && aligned16(a.g2);
   if (al && C == 16) return launch_pairs<D, P, OPT<D, P, 16, true>>(g, bo, a, st);
   if (al && C == 12) return launch_pairs<D, P, OPT<D, P, 12, true>>(g, bo, a, st);
   if (al && C == 32) return launch_pairs<D, P, OPT<D, P, 32, true>>(g, bo, a, st);
@@ -1076,6 +1251,8 @@ template <int D, bool P, int CM, bool EX> using BlurBwdFull = OpBlurBwd<D, P, CM
 template <int D, bool P, int CM, bool EX> using BlurBwdDs = OpBlurBwd<D, P, CM, EX, false>;
 template <int D, bool P, int CM, bool EX> using GradientBwdFull = OpGradientBwd<D, P, CM, EX, true>;
 template <int D, bool P, int CM, bool EX> using GradientBwdDs = OpGradientBwd<D, P, CM, EX, false>;
+template <int D, bool P, int CM, bool EX> using GradientBwdFullAcc = OpGradientBwd<D, P, CM, EX, true, true>;
+template <int D, bool P, int CM, bool EX> using GradientBwdDsAcc = OpGradientBwd<D, P, CM, EX, false, true>;
 
 template <int D, bool P>
 void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
@@ -1087,6 +1264,8 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
     case Op::Blur: return launch_channels<D, P, OpBlur>(g, bo, a, st);
     case Op::Gradient: return launch_channels<D, P, OpGradient>(g, bo, a, st);
     case Op::GradientHybrid: return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
+    case Op::DensityPair: return launch_pairs<D, P, OpDensityPair<D, P>>(g, bo, a, st);
+    case Op::BlurGradientHybrid: return launch_channels<D, P, OpBlurGradientHybrid>(g, bo, a, st);
     case Op::NeighbourCount:
       if (g.n_keys) neighbour_count<D, P>(g, bo, a.x, a.iout, st);
       return;
@@ -1110,6 +1289,16 @@ void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const
     case Op::GradientHybrid:
       if (full) return launch_channels<D, P, GradientBwdFull>(g, bo, a, st);
       return launch_channels<D, P, GradientBwdDs>(g, bo, a, st);
+    case Op::DensityPair: return launch_pairs<D, P, OpDensityPairBwd<D, P>>(g, bo, a, st);
+    case Op::BlurGradientHybrid: {
+      // blur's backward stores, the gradient's backward (upstream2) adds
+      OpPtrs b = a;
+      b.g2 = nullptr;
+      backward_dispatch<D, P>(g, Op::Blur, full, bo, b, st);
+      b.g = a.g2;
+      if (full) return launch_channels<D, P, GradientBwdFullAcc>(g, bo, b, st);
+      return launch_channels<D, P, GradientBwdDsAcc>(g, bo, b, st);
+    }
     default:
       break;
   }

@@ -74,8 +74,10 @@ enum class Op : int {
   Blur = 4,
   Gradient = 5,
   GradientHybrid = 6,
-  NeighbourCount = 7,   // in-radius neighbour count per particle (int32)
-  NeighbourFill = 8,    // in-radius neighbour indices into CSR rows (int32)
+  DensityPair = 7,      // density + density gradient in one pass
+  BlurGradientHybrid = 8,  // blur + gradient_hybrid in one pass
+  NeighbourCount = 9,   // in-radius neighbour count per particle (int32)
+  NeighbourFill = 10,   // in-radius neighbour indices into CSR rows (int32)
 };
 
 struct OpPtrs {
@@ -84,9 +86,11 @@ struct OpPtrs {
   const float* rho = nullptr;
   const float* s = nullptr;
   const float* g = nullptr;   // upstream gradient (backward)
+  const float* g2 = nullptr;  // second upstream gradient (fused backward)
   float* out0 = nullptr;      // forward output / grad_x
   float* out1 = nullptr;      // grad_s
   float* out2 = nullptr;      // grad_rho
+  float* out3 = nullptr;      // second forward output (fused forward)
   int32_t* iout = nullptr;    // neighbour counts / indices
   const int32_t* nptr = nullptr;  // CSR row offsets (B*N+1)
   const int32_t* nidx = nullptr;  // CSR neighbour indices; non-null selects list traversal

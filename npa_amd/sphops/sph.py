@@ -18,9 +18,15 @@ Differences, all compatible with callers of the reference:
 * ``gradient_hybrid`` runs as one fused kernel (same forward value
   ``raw @ safe_inv(M)``, same straight-through backward);
 * ``Count.backward`` returns a zero gradient instead of failing;
-* the default unit mass tensor is cached per shape instead of re-allocated.
+* the default unit mass tensor is cached per shape instead of re-allocated;
+* operator pairs that read the same neighbours with the same inputs
+  (density + density_gradient, blur + gradient_hybrid, as the reference's
+  NPA.perceive calls them, ``models/npa.py:106-126``) are evaluated by one
+  fused kernel once a grid has seen the pair (see ``_PassFusion``).
 """
 import math
+import os
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -192,10 +198,10 @@ def _fwd(snapshot, op, x_bin, out, mass=None, rho=None, state=None, tol=1e-3):
 
 
 def _bwd(snapshot, op, x_bin, upstream, mass, rho=None, state=None, grad_x=None, grad_s=None, grad_rho=None,
-         dLdx=True, dLds=True, dLdrho=True):
+         dLdx=True, dLds=True, dLdrho=True, upstream2=None):
     snapshot.grid.op_backward(op, x_bin, _c(upstream), snapshot.bin_offsets, mass, rho=rho, state=state,
                               grad_x=grad_x, grad_state=grad_s, grad_rho=grad_rho, dLdx=dLdx, dLds=dLds,
-                              dLdrho=dLdrho, nbr=_plan(snapshot, x_bin))
+                              dLdrho=dLdrho, nbr=_plan(snapshot, x_bin), upstream2=upstream2)
 
 
 class Count(torch.autograd.Function):
@@ -237,7 +243,7 @@ class Density(torch.autograd.Function):
 
 def density(x_bin, snapshot, mass=None):
     mass = _default_mass(x_bin, mass)
-    return Density.apply(x_bin, mass, snapshot)
+    return _PASS_A.run(snapshot, 0, (x_bin, mass), lambda: Density.apply(x_bin, mass, snapshot))
 
 
 class Blur(torch.autograd.Function):
@@ -255,21 +261,22 @@ class Blur(torch.autograd.Function):
         return _state_backward(ctx, _OP.OP_BLUR, grad_output)
 
 
-def _state_backward(ctx, op, grad_output):
+def _state_backward(ctx, op, grad_output, grad_output2=None):
     x_bin, s_bin, rho, mass = ctx.saved_tensors
     ds_only = ctx.dLds and not ctx.dLdx and not ctx.dLdrho
     grad_s = torch.empty_like(s_bin)
     grad_x = None if ds_only else torch.empty_like(x_bin)
     grad_rho = None if ds_only else torch.empty_like(rho)
     _bwd(ctx.snapshot, op, x_bin, grad_output, mass, rho=rho, state=s_bin, grad_x=grad_x, grad_s=grad_s,
-         grad_rho=grad_rho, dLdx=ctx.dLdx, dLds=ctx.dLds, dLdrho=ctx.dLdrho)
+         grad_rho=grad_rho, dLdx=ctx.dLdx, dLds=ctx.dLds, dLdrho=ctx.dLdrho,
+         upstream2=None if grad_output2 is None else _c(grad_output2))
     return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
             grad_rho if ctx.dLdrho else None, None, None)
 
 
 def blur(x_bin, rho, s_bin, snapshot, mass=None):
     mass = _default_mass(x_bin, mass)
-    return Blur.apply(x_bin, s_bin, rho, mass, snapshot)
+    return _PASS_B.run(snapshot, 0, (x_bin, s_bin, rho, mass), lambda: Blur.apply(x_bin, s_bin, rho, mass, snapshot))
 
 
 class Gradient(torch.autograd.Function):
@@ -314,7 +321,7 @@ class DensityGradient(torch.autograd.Function):
 
 def density_gradient(x_bin, snapshot, mass=None):
     mass = _default_mass(x_bin, mass)
-    return DensityGradient.apply(x_bin, mass, snapshot)
+    return _PASS_A.run(snapshot, 1, (x_bin, mass), lambda: DensityGradient.apply(x_bin, mass, snapshot))
 
 
 class MomentMatrix(torch.autograd.Function):
@@ -382,4 +389,143 @@ def gradient_hybrid(x_bin, rho, s_bin, snapshot, mass=None):
         raw = gradient(x_bin, rho, s_bin, snapshot, mass=mass)
         return raw + (raw @ L - raw).detach()
     mass = _default_mass(x_bin, mass)
-    return GradientHybrid.apply(x_bin, s_bin, rho, mass, snapshot, 1e-3)
+    return _PASS_B.run(snapshot, 1, (x_bin, s_bin, rho, mass),
+                       lambda: GradientHybrid.apply(x_bin, s_bin, rho, mass, snapshot, 1e-3))
+
+
+# ------------------------------------------------------------ pass fusion
+
+class DensityPair(torch.autograd.Function):
+    """Density and density gradient of the same (x_bin, mass) in one neighbour
+    pass; the backward runs the fused kernel when both outputs carry a
+    gradient and the single operator's kernel when only one does."""
+
+    @staticmethod
+    def forward(ctx, x_bin, mass, snapshot):
+        ctx.set_materialize_grads(False)
+        rho = torch.empty(x_bin.shape[:-1], dtype=torch.float32, device=x_bin.device)
+        grad_rho = torch.empty(*x_bin.shape[:-1], snapshot.dim, dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.op_forward(_OP.OP_DENSITY_PAIR, x_bin, rho, snapshot.bin_offsets, mass=mass,
+                                 nbr=_plan(snapshot, x_bin), out2=grad_rho)
+        ctx.save_for_backward(x_bin, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx = x_bin.requires_grad
+        return rho, grad_rho
+
+    @staticmethod
+    def backward(ctx, g_rho, g_grad_rho):
+        if not ctx.dLdx or (g_rho is None and g_grad_rho is None):
+            return None, None, None
+        x_bin, mass = ctx.saved_tensors
+        grad_x = torch.empty_like(x_bin)
+        if g_grad_rho is None:
+            _bwd(ctx.snapshot, _OP.OP_DENSITY, x_bin, g_rho, mass, grad_x=grad_x)
+        elif g_rho is None:
+            _bwd(ctx.snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, g_grad_rho, mass, grad_x=grad_x)
+        else:
+            ctx.snapshot.grid.op_backward(_OP.OP_DENSITY_PAIR, x_bin, _c(g_rho), ctx.snapshot.bin_offsets, mass,
+                                          grad_x=grad_x, nbr=_plan(ctx.snapshot, x_bin), upstream2=_c(g_grad_rho))
+        return grad_x, None, None
+
+
+class BlurGradientHybrid(torch.autograd.Function):
+    """Blur and gradient_hybrid of the same (x_bin, s_bin, rho, mass) in one
+    neighbour pass; backward as for ``DensityPair`` (the gradient_hybrid
+    part is the straight-through gradient backward)."""
+
+    @staticmethod
+    def forward(ctx, x_bin, s_bin, rho, mass, snapshot, tol):
+        ctx.set_materialize_grads(False)
+        s_blur = torch.empty_like(s_bin)
+        hyb = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
+        snapshot.grid.op_forward(_OP.OP_BLUR_GRADIENT_HYBRID, x_bin, s_blur, snapshot.bin_offsets, mass=mass,
+                                 rho=rho, state=s_bin, tol=tol, nbr=_plan(snapshot, x_bin), out2=hyb)
+        ctx.save_for_backward(x_bin, s_bin, rho, mass)
+        ctx.snapshot = snapshot
+        ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
+        return s_blur, hyb
+
+    @staticmethod
+    def backward(ctx, g_blur, g_hyb):
+        if g_blur is None and g_hyb is None:
+            return None, None, None, None, None, None
+        if g_hyb is None:
+            return _state_backward(ctx, _OP.OP_BLUR, g_blur) + (None,)
+        if g_blur is None:
+            return _state_backward(ctx, _OP.OP_GRADIENT, g_hyb) + (None,)
+        return _state_backward(ctx, _OP.OP_BLUR_GRADIENT_HYBRID, g_blur, g_hyb) + (None,)
+
+
+class _PassFusion:
+    """Evaluates two operators that read the same neighbours with the same
+    inputs in one fused kernel.
+
+    The reference's NPA.perceive (``models/npa.py:106-126``) calls density and
+    density_gradient on the same ``(x_bin, mass)``, and blur and
+    gradient_hybrid on the same ``(x_bin, s_bin, rho, mass)``, once per
+    snapshot.  A grid learns that pattern: when both operators of a pair run
+    on one snapshot with the very same input tensors, the grid is marked, and
+    from then on the first call of either operator on a snapshot runs the
+    fused kernel and keeps the partner output.  The partner call receives it
+    only if it passes the same snapshot and input objects, at the same
+    versions, with the same requires_grad flags and grad mode, and only once;
+    any other call runs the single operator.  If a fused partner output is
+    never collected, the grid drops the mark and the output.  One record per
+    pass and grid is kept (inputs and snapshot by weak reference), so nothing
+    outlives the next call.  Values agree with the single operators to fp32
+    rounding (same pairs, same per-pair arithmetic).  ``NPA_SPHOPS_FUSE=0`` in
+    the environment switches fusion off.
+    """
+
+    def __init__(self, name, fused_apply):
+        self.name = name
+        self.fused_apply = fused_apply
+        self.enabled = os.environ.get("NPA_SPHOPS_FUSE", "1") != "0"
+
+    @staticmethod
+    def _record(kind, snapshot, inputs, **extra):
+        key = (tuple(t._version for t in inputs), tuple(t.requires_grad for t in inputs), torch.is_grad_enabled())
+        return dict(kind=kind, snap=weakref.ref(snapshot), refs=[weakref.ref(t) for t in inputs], key=key, **extra)
+
+    @staticmethod
+    def _matches(rec, snapshot, inputs):
+        if rec is None or rec["snap"]() is not snapshot:
+            return False
+        if any(r() is not t for r, t in zip(rec["refs"], inputs)):
+            return False
+        key = (tuple(t._version for t in inputs), tuple(t.requires_grad for t in inputs), torch.is_grad_enabled())
+        return rec["key"] == key
+
+    def run(self, snapshot, which, inputs, single):
+        if not self.enabled:
+            return single()
+        states = snapshot.grid.__dict__.setdefault("_pass_fusion", {})
+        st = states.setdefault(self.name, {"hint": False, "rec": None})
+        rec = st["rec"]
+        same = self._matches(rec, snapshot, inputs)
+        if same and rec["kind"] == "fused" and rec["outputs"] is not None and not rec["taken"][which]:
+            out = rec["outputs"][which]
+            if out._version == rec["versions"][which]:
+                rec["taken"][which] = True
+                rec["outputs"] = None
+                return out
+        repeat = same and rec["kind"] == "fused"   # this pass was already fused for these inputs
+        if st["hint"] and not repeat:
+            if rec is not None and rec["kind"] == "fused" and not all(rec["taken"]):
+                st["hint"], st["rec"] = False, None   # the last fused partner output was never used
+            else:
+                outputs = self.fused_apply(snapshot, inputs)
+                st["rec"] = self._record("fused", snapshot, inputs, outputs=outputs,
+                                         versions=[o._version for o in outputs], taken=[which == 0, which == 1])
+                return outputs[which]
+        out = single()
+        if same and rec["kind"] == "single" and rec["which"] != which:
+            st["hint"], st["rec"] = True, None
+        elif not repeat:
+            st["rec"] = self._record("single", snapshot, inputs, which=which)
+        return out
+
+
+_PASS_A = _PassFusion("density_pair", lambda snap, t: DensityPair.apply(t[0], t[1], snap))
+_PASS_B = _PassFusion("blur_gradient_hybrid",
+                      lambda snap, t: BlurGradientHybrid.apply(t[0], t[1], t[2], t[3], snap, 1e-3))

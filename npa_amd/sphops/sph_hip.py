@@ -362,8 +362,26 @@ class _HashGridNative:
                                          ctypes.c_void_p(index.data_ptr()), st))
         return offs, index, order, counts
 
-    def _args(self, x, bin_offsets, mass=None, rho=None, state=None, upstream=None, out=None, grad_state=None,
-              grad_rho=None, tol=1e-3, nbr=None):
+    # Per operator: trailing dims of (first output, second output) after (B, N);
+    # "C" stands for the channel count, "D" for the spatial dimension.
+    _OUT_DIMS = {
+        _native.OP_COUNT: ((), None), _native.OP_DENSITY: ((), None), _native.OP_DENSITY_GRADIENT: (("D",), None),
+        _native.OP_MOMENT_MATRIX: (("D", "D"), None), _native.OP_BLUR: (("C",), None),
+        _native.OP_GRADIENT: (("C", "D"), None), _native.OP_GRADIENT_HYBRID: (("C", "D"), None),
+        _native.OP_DENSITY_PAIR: ((), ("D",)), _native.OP_BLUR_GRADIENT_HYBRID: (("C",), ("C", "D")),
+    }
+
+    def _numel(self, dims, C):
+        n = self.batch_size * self.particle_count
+        for d in dims:
+            n *= C if d == "C" else self._dim
+        return n
+
+    def _args(self, op, x, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, **buffers):
+        """Build ``sphops_args``; every buffer is checked for dtype, device,
+        contiguity and element count against ``op``'s output shapes."""
+        if op not in self._OUT_DIMS:
+            raise RuntimeError(f"unknown operator {op}")
         a = _native.Args()
         a.x = self._pos(x, "binned_positions")
         a.bin_offsets = self._offsets(bin_offsets)
@@ -377,11 +395,20 @@ class _HashGridNative:
             a.state = self._state(state, "state_in", C)
         a.feature_dim = max(C, 0)
         a.tol = tol
-        for name, t in (("upstream", upstream), ("out", out), ("grad_state", grad_state), ("grad_rho", grad_rho)):
-            if t is not None:
-                if t.dtype != _F32 or not t.is_contiguous() or t.device.type != "cuda":
-                    raise TypeError(f"{name}: expected a contiguous float32 GPU tensor")
-                setattr(a, name, t.data_ptr())
+        first, second = self._OUT_DIMS[op]
+        BN = self.batch_size * self.particle_count
+        sizes = {"upstream": self._numel(first, C), "out": self._numel(first, C),
+                 "upstream2": self._numel(second, C) if second else None,
+                 "out2": self._numel(second, C) if second else None,
+                 "grad_x": BN * self._pw, "grad_state": BN * C, "grad_rho": BN}
+        for name, t in buffers.items():
+            if t is None:
+                continue
+            if t.dtype != _F32 or not t.is_contiguous() or t.device.type != "cuda":
+                raise TypeError(f"{name}: expected a contiguous float32 GPU tensor")
+            if sizes[name] is None or t.numel() != sizes[name]:
+                raise RuntimeError(f"{name}: expected {sizes[name]} elements, got {t.numel()}")
+            setattr(a, "out" if name == "grad_x" else name, t.data_ptr())
         if nbr is not None:
             a.nbr_offsets, a.nbr_index = nbr[0].data_ptr(), nbr[1].data_ptr()
             if len(nbr) > 2:
@@ -390,14 +417,18 @@ class _HashGridNative:
                     a.nbr_class_count[c] = nbr[3][c]
         return a
 
-    def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None):
-        a = self._args(x, bin_offsets, mass, rho, state, out=out, tol=tol, nbr=nbr)
+    def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None):
+        """Forward of operator ``op`` (``_native.OP_*``) into ``out`` (and
+        ``out2`` for the fused codes), optionally over a neighbour list."""
+        a = self._args(op, x, bin_offsets, mass, rho, state, tol=tol, nbr=nbr, out=out, out2=out2)
         _check(_lib.sphops_forward(self._h, op, ctypes.byref(a), _stream(x)))
 
     def op_backward(self, op, x, upstream, bin_offsets, mass, rho=None, state=None, grad_x=None, grad_state=None,
-                    grad_rho=None, dLdx=True, dLds=True, dLdrho=True, nbr=None):
-        a = self._args(x, bin_offsets, mass, rho, state, upstream=upstream, out=grad_x, grad_state=grad_state,
-                       grad_rho=grad_rho, nbr=nbr)
+                    grad_rho=None, dLdx=True, dLds=True, dLdrho=True, nbr=None, upstream2=None):
+        """Backward of operator ``op``: gradients w.r.t. x, state and rho
+        written into the given buffers according to the flags."""
+        a = self._args(op, x, bin_offsets, mass, rho, state, nbr=nbr, upstream=upstream, upstream2=upstream2,
+                       grad_x=grad_x, grad_state=grad_state, grad_rho=grad_rho)
         _check(_lib.sphops_backward(self._h, op, int(bool(dLdx)), int(bool(dLds)), int(bool(dLdrho)),
                                     ctypes.byref(a), _stream(x)))
 

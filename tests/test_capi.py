@@ -34,7 +34,9 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_channel():
     from npa_amd.sphops import _native
-    assert _native.lib.sphops_abi_version() == 1
+    hdr = open(HEADER).read()
+    version = int(re.search(r"#define SPHOPS_ABI_VERSION (\d+)", hdr).group(1))
+    assert _native.lib.sphops_abi_version() == version == _native.ABI_VERSION
     # a failing call without touching the GPU: invalid dimension
     h = ctypes.c_void_p()
     gs = (ctypes.c_int32 * 2)(4, 4)
@@ -50,3 +52,13 @@ def test_abi_version_and_error_channel():
     assert st != 0 and b"Morton" in _native.lib.sphops_last_error()
     st = _native.lib.sphops_safe_inv_sym_mat(None, None, 4, 4, ctypes.c_float(1e-3), None)
     assert st != 0 and b"2x2 or 3x3" in _native.lib.sphops_last_error()
+
+
+def test_args_struct_matches_header():
+    """The ctypes mirror of sphops_args lists the header's fields in order."""
+    from npa_amd.sphops import _native
+    hdr = open(HEADER).read()
+    body = re.search(r"typedef struct sphops_args \{(.*?)\} sphops_args;", hdr, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = [re.sub(r"\[.*\]", "", decl.split()[-1].lstrip("*")) for decl in body.split(";") if decl.strip()]
+    assert names == [f[0] for f in _native.Args._fields_]

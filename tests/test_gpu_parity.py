@@ -105,6 +105,28 @@ def run(name):
     res["b_grad"] = grads(lambda X, S, R: sp.gradient(X, R, S, snap, mb), g_grad)
     res["b_grad_ds"] = grads(lambda X, S, R: sp.gradient(X, R, S, snap, mb), g_grad, ("s",))
     res["b_hyb"] = grads(lambda X, S, R: sp.gradient_hybrid(X, R, S, snap, mb), g_grad)
+
+    # fused passes: density + density_gradient, blur + gradient_hybrid
+    from npa_amd.sphops.sph import BlurGradientHybrid, DensityPair
+    with torch.no_grad():
+        f = DensityPair.apply(xb, mb, snap)
+        res["f_rho"], res["f_dgrad"] = (t.cpu().numpy() for t in f)
+        f = BlurGradientHybrid.apply(xb, sb, rho, mb, snap, 1e-3)
+        res["f_blur"], res["f_hyb"] = (t.cpu().numpy() for t in f)
+
+    def fused_grads(fn, upstreams, need=("x", "s", "rho")):
+        xr = xb.detach().clone().requires_grad_("x" in need)
+        sr = sb.detach().clone().requires_grad_("s" in need)
+        rr = rho.detach().clone().requires_grad_("rho" in need)
+        torch.autograd.backward(fn(xr, sr, rr), [dev(u) for u in upstreams])
+        return {k: (t.grad.cpu().numpy() if t.grad is not None else None) for k, t in
+                (("x", xr), ("s", sr), ("rho", rr))}
+
+    res["b_pair_a"] = fused_grads(lambda X, S, R: DensityPair.apply(X, mb, snap), (g_rho, g_dg), ("x",))
+    res["b_pair_b"] = fused_grads(lambda X, S, R: BlurGradientHybrid.apply(X, S, R, mb, snap, 1e-3),
+                                  (g_blur, g_grad))
+    res["b_pair_b_ds"] = fused_grads(lambda X, S, R: BlurGradientHybrid.apply(X, S, R, mb, snap, 1e-3),
+                                     (g_blur, g_grad), ("s",))
     torch.cuda.synchronize()
 
     # ---- oracle on the same binned inputs
@@ -210,6 +232,71 @@ def test_backward(name):
         # the unused w lane of 3D position gradients is written as zero
         assert np.all(res["b_density"]["x"][..., 3] == 0)
         assert np.all(res["b_grad"]["x"][..., 3] == 0)
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_fused_passes(name):
+    """One-pass density + density_gradient and blur + gradient_hybrid, forward
+    and backward (the backward is the sum of both operators' gradients)."""
+    c, res, ora = run(name)
+    q = ora["q"]
+    D = c.dim
+    for key, ref in (("f_rho", "rho"), ("f_dgrad", "dgrad"), ("f_blur", "blur")):
+        H.assert_close(f"{name}:{key}", _flat(res[key], q), *ora[ref])
+    out, raw, raw_mag, M, M_mag, L, det = ora["hyb"]
+    amb = np.abs(np.abs(det) - 1e-3) < 1e-6
+    H.assert_close(f"{name}:f_hyb", _flat(res["f_hyb"], q), out, H.hybrid_bound(raw, raw_mag, M_mag, L), skip=amb)
+    (ax, axm), (bx, bxm) = ora["b_density"], ora["b_dgrad"]
+    H.assert_close(f"{name}:pair_a.dx", _flat(res["b_pair_a"]["x"], q, D), ax + bx, axm + bxm)
+    for i, k in enumerate(("x", "s", "rho")):
+        (ra, ma), (rb, mb_) = ora["b_blur"][i], ora["b_grad"][i]
+        H.assert_close(f"{name}:pair_b.d{k}", _flat(res["b_pair_b"][k], q, D if k == "x" else None), ra + rb,
+                       ma + mb_)
+    (ra, ma), (rb, mb_) = ora["b_blur"][1], ora["b_grad"][1]
+    H.assert_close(f"{name}:pair_b_ds.ds", _flat(res["b_pair_b_ds"]["s"], q), ra + rb, ma + mb_)
+    assert res["b_pair_b_ds"]["x"] is None and res["b_pair_b_ds"]["rho"] is None
+
+
+@pytest.mark.parametrize("name", ["ref2d-per-grid", "ref3d-clamp-grid", "cfg5"])
+def test_perceive_fusion(name):
+    """NPA.perceive's call sequence (models/npa.py:87-126) twice on one grid:
+    the first step runs single operators, the grid then fuses both passes;
+    values and gradients of the two steps agree to fp32 rounding."""
+    import npa_amd.sphops as sp
+    c = CASES[name]
+    print(f"[case] perceive-fusion {name}", flush=True)
+    grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    rng = np.random.default_rng(5)
+    ups = [dev(rng.standard_normal(shape).astype(np.float32)) for shape in
+           ((c.B, c.N, c.C), (c.B, c.N, c.C, c.dim), (c.B, c.N, c.dim))]
+    steps = []
+    for step in range(2):
+        x = dev(c.x).requires_grad_(True)
+        s = dev(c.s).requires_grad_(True)
+        snap = grid.instantiate(x.detach())
+        xb, sb = sp.bin_particles(x, s, snap)
+        rho = sp.density(xb, snap)
+        bl = sp.blur(xb, rho, sb, snap)
+        gh = sp.gradient_hybrid(xb, rho, sb, snap)
+        dg = sp.density_gradient(xb, snap)
+        state = grid.hashgrid._pass_fusion
+        kinds = (state["density_pair"]["rec"], state["blur_gradient_hybrid"]["rec"])
+        loss = (bl * ups[0]).sum() + (gh * ups[1]).sum() + (dg * ups[2]).sum()
+        loss.backward()
+        steps.append({k: v.detach().cpu().numpy() for k, v in
+                      (("rho", rho), ("blur", bl), ("hyb", gh), ("dg", dg), ("gx", x.grad), ("gs", s.grad))})
+        if step == 0:
+            assert kinds == (None, None)  # both pairs seen: marks set, records cleared
+        else:
+            assert kinds[0]["kind"] == "fused" and all(kinds[0]["taken"])
+            assert kinds[1]["kind"] == "fused" and all(kinds[1]["taken"])
+    a, b = steps
+    for k in a:
+        rms = np.sqrt(np.mean(a[k].astype(np.float64) ** 2)) + 1e-30
+        err = np.abs(a[k].astype(np.float64) - b[k])
+        bound = 1e-5 * (np.abs(a[k]) + np.abs(b[k])) + 1e-5 * rms
+        assert np.all(err <= bound), f"{name}:{k} max err {err.max():.3e}"
 
 
 MIRROR_CASES = [n for n in NAMES if n.startswith(("ref2d", "ref3d", "chan12", "chan33", "cfg2", "cfg5"))]
