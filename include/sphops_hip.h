@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 2
+#define SPHOPS_ABI_VERSION 3
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -171,8 +171,9 @@ typedef struct sphops_args {
   const int32_t* bin_offsets;  /* (B*G+1) from sphops_initialize */
   const int32_t* nbr_offsets;  /* optional (B*N+1) CSR offsets from sphops_neighbor_count */
   const int32_t* nbr_index;    /* optional CSR indices from sphops_neighbor_fill; NULL: scan the stencil */
-  const int32_t* nbr_order;    /* optional particle order by list-length class (sphops_neighbor_schedule) */
-  int32_t nbr_class_count[4];  /* host copy of the class sizes written by sphops_neighbor_schedule */
+  const int32_t* nbr_order;    /* optional schedule from sphops_neighbor_schedule: particle order ... */
+  const uint32_t* nbr_waves;   /* ... its wave descriptors (2 words per wave) ... */
+  int32_t nbr_wave_count;      /* ... and the host copy of its wave count */
   const float* upstream2;      /* fused backward: dL/d(second output) */
   float* out2;                 /* fused forward: the second output */
 } sphops_args;
@@ -200,12 +201,19 @@ int sphops_neighbor_count(const sphops_grid* grid, const float* x, const int32_t
 int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
                          const int32_t* nbr_offsets, int32_t* nbr_index, void* stream);
 
-/* Schedule for list traversal: a stable partition of the binned particles by
- * list length into four classes (<=4, <=32, <=128, >128 neighbours), served by
- * groups of 1, 4, 16 and 64 lanes per particle.  nbr_order (B*N) receives the
- * particles class by class; class_counts (4 device int32) the class sizes. */
+/* Schedule for list traversal.  The binned particles are cut into tiles of
+ * 4096; within a tile they are partitioned (stably) by list length into four
+ * classes (<=4, <=32, <=128, >128 neighbours), served by groups of 1, 4, 16
+ * and 64 lanes per particle; tiles stay in order, so each region of space is
+ * processed in one stretch.  nbr_order (B*N) receives the particles in that
+ * order, nbr_waves (2 words per wave, capacity sphops_neighbor_wave_capacity)
+ * one descriptor per 64-lane wave {first slot in nbr_order, class << 8 |
+ * particles in the wave}, wave_count (one device int32) the number of waves. */
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_offsets, int32_t* nbr_order,
-                             int32_t* class_counts, void* stream);
+                             uint32_t* nbr_waves, int32_t* wave_count, void* stream);
+
+/* Number of wave descriptors nbr_waves must hold for this grid (B*N + 4 per tile). */
+int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid);
 
 /* Module function safe_inv_sym_mat (sph_cuda.cu:3181-3226): `count` symmetric
  * dim x dim matrices (dim 2 or 3), identity where |det| < tol. */

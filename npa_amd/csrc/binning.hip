@@ -414,7 +414,11 @@ inline dim3 blocks_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) /
 //
 // Stable partition of the binned particles into four classes by neighbour
 // list length (<=4, <=32, <=128, more), which the pair kernels serve with
-// groups of 1, 4, 16 and 64 lanes per particle.
+// groups of 1, 4, 16 and 64 lanes per particle.  The partition is done per
+// tile of 4096 binned particles; the candidate schedule concatenates the
+// tiles class by class (class-major), the list schedule keeps them tile by
+// tile (tile-major: every class of a region of space is processed together,
+// so neighbour rows shared between classes are reused from the same L2).
 
 namespace {
 
@@ -433,7 +437,13 @@ __device__ __forceinline__ uint32_t length_class(int32_t len, ClassBounds cb) {
   return len <= cb.t0 ? 0u : (len <= cb.t1 ? 1u : (len <= cb.t2 ? 2u : 3u));
 }
 
-template <bool CSR>
+// Segment (tile, class) of the count / offset tables in either layout.
+template <bool TM>
+__device__ __forceinline__ uint32_t seg_index(uint32_t tile, uint32_t q, uint32_t ntiles) {
+  return TM ? tile * 4u + q : q * ntiles + tile;
+}
+
+template <bool CSR, bool TM>
 __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restrict__ src, uint32_t n,
                                                           ClassBounds cb, uint32_t* __restrict__ cnt,
                                                           uint32_t ntiles) {
@@ -459,12 +469,12 @@ __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restr
     if (__lane_id() == 0) atomicAdd(&h[q], v);
   }
   __syncthreads();
-  if (threadIdx.x < 4) cnt[threadIdx.x * ntiles + blockIdx.x] = h[threadIdx.x];
+  if (threadIdx.x < 4) cnt[seg_index<TM>(blockIdx.x, threadIdx.x, ntiles)] = h[threadIdx.x];
 }
 
 // Same tile walk as the radix scatter: wave w owns items [w*1024, (w+1)*1024)
 // in index order; two ballots identify lanes of the same class.
-template <bool CSR>
+template <bool CSR, bool TM>
 __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __restrict__ src, uint32_t n,
                                                             ClassBounds cb, const uint32_t* __restrict__ cnt_scan,
                                                             uint32_t ntiles, int32_t* __restrict__ order) {
@@ -472,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
   __shared__ uint32_t gbase[4];
   const int wave = threadIdx.x >> 6, lane = __lane_id();
   if (threadIdx.x < (kThreads / 64) * 4) (&wcnt[0][0])[threadIdx.x] = 0;
-  if (threadIdx.x < 4) gbase[threadIdx.x] = cnt_scan[threadIdx.x * ntiles + blockIdx.x];
+  if (threadIdx.x < 4) gbase[threadIdx.x] = cnt_scan[seg_index<TM>(blockIdx.x, threadIdx.x, ntiles)];
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
   const uint64_t below_mask = lanemask_lt();
@@ -520,28 +530,76 @@ __global__ void k_class_totals(const uint32_t* __restrict__ cnt_scan, uint32_t n
   }
 }
 
+// Class-major partition: order holds class 0 of every tile, then class 1, ...
 template <bool CSR>
 void partition_by_length(const Grid& g, const int32_t* src, ClassBounds cb, int32_t* order, int32_t* class_counts,
                          hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
   uint32_t* cnt = g.hist;  // 4 * ntiles <= 256 * ntiles words
-  hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles);
+  hipLaunchKernelGGL((k_class_count<CSR, false>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles);
   SPHOPS_LAUNCHED();
   device_exclusive_scan(cnt, cnt, 4ull * ntiles, g.scan_tmp, nullptr, st);
-  hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles, order);
+  hipLaunchKernelGGL((k_class_scatter<CSR, false>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles,
+                     order);
   SPHOPS_LAUNCHED();
   hipLaunchKernelGGL(k_class_totals, dim3(1), dim3(64), 0, st, cnt, ntiles, n, class_counts);
   SPHOPS_LAUNCHED();
 }
 
+// Waves needed by segment s = (tile, class): particles / (64 / group size), rounded up.
+__global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, uint32_t n,
+                              uint32_t* __restrict__ wcnt) {
+  const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= nseg) return;
+  const uint32_t lo = seg[s], hi = s + 1 < nseg ? seg[s + 1] : n;
+  const uint32_t per = (uint32_t)(kWave / kListGroupSizes[s & 3u]);
+  wcnt[s] = (hi - lo + per - 1) / per;
+}
+
+// One workgroup per tile writes the wave descriptors of its four segments:
+// {first slot in order, class << 8 | particles in the wave}.
+__global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restrict__ seg,
+                                                        const uint32_t* __restrict__ wstart, uint32_t ntiles,
+                                                        uint32_t n, uint2* __restrict__ waves) {
+  const uint32_t t = blockIdx.x;
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q) {
+    const uint32_t s = t * 4u + q;
+    const uint32_t lo = seg[s], hi = s + 1 < 4u * ntiles ? seg[s + 1] : n;
+    const uint32_t per = (uint32_t)(kWave / kListGroupSizes[q]);
+    const uint32_t nw = (hi - lo + per - 1) / per;
+    for (uint32_t u = threadIdx.x; u < nw; u += blockDim.x) {
+      const uint32_t first = lo + u * per;
+      waves[wstart[s] + u] = make_uint2(first, (q << 8) | min(per, hi - first));
+    }
+  }
+}
+
 }  // namespace
 
-void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, int32_t* class_counts,
+uint64_t neighbour_wave_capacity(const Grid& g) { return g.n_keys + 4 * g.n_tiles; }
+
+void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st) {
-  if (g.n_keys == 0) return;
-  partition_by_length<true>(g, nptr, ClassBounds{kListClassBounds[0], kListClassBounds[1], kListClassBounds[2]},
-                            order, class_counts, st);
+  const uint32_t n = (uint32_t)g.n_keys;
+  const uint32_t ntiles = (uint32_t)g.n_tiles;
+  const uint32_t nseg = 4u * ntiles;
+  uint32_t* seg = g.hist;            // 4 * ntiles particle offsets
+  uint32_t* wcnt = g.hist + nseg;    // 4 * ntiles wave offsets (hist holds 256 * ntiles words)
+  const ClassBounds cb{kListClassBounds[0], kListClassBounds[1], kListClassBounds[2]};
+  hipLaunchKernelGGL((k_class_count<true, true>), dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cb, seg, ntiles);
+  SPHOPS_LAUNCHED();
+  device_exclusive_scan(seg, seg, nseg, g.scan_tmp, nullptr, st);
+  hipLaunchKernelGGL((k_class_scatter<true, true>), dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cb, seg, ntiles,
+                     order);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, n,
+                     wcnt);
+  SPHOPS_LAUNCHED();
+  device_exclusive_scan(wcnt, wcnt, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total), st);
+  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt, ntiles, n, waves);
+  SPHOPS_LAUNCHED();
 }
 
 void run_candidate_schedule(const Grid& g, const int32_t* cand, int32_t* order, int32_t* class_counts,

@@ -493,7 +493,8 @@ static OpPtrs from_args(const sphops_args* a) {
   p.nptr = a->nbr_offsets;
   p.nidx = a->nbr_index;
   p.order = a->nbr_order;
-  for (int c = 0; c < 4; ++c) p.class_count[c] = a->nbr_class_count[c];
+  p.waves = reinterpret_cast<const uint2*>(a->nbr_waves);
+  p.nwaves = (uint32_t)std::max(a->nbr_wave_count, 0);
   p.g2 = a->upstream2;
   p.out3 = a->out2;
   return p;
@@ -502,7 +503,9 @@ static OpPtrs from_args(const sphops_args* a) {
 static void check_list(const sphops_args* a) {
   require(a->nbr_index == nullptr || a->nbr_offsets != nullptr, "nbr_index needs nbr_offsets");
   require(a->nbr_order == nullptr || a->nbr_index != nullptr, "nbr_order needs nbr_index");
-  for (int c = 0; c < 4; ++c) require(a->nbr_class_count[c] >= 0, "negative class count");
+  require(a->nbr_waves == nullptr || a->nbr_order != nullptr, "nbr_waves needs nbr_order");
+  require(a->nbr_order == nullptr || a->nbr_waves != nullptr, "nbr_order needs nbr_waves");
+  require(a->nbr_wave_count >= 0, "negative wave count");
 }
 
 int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream) {
@@ -591,18 +594,28 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
 }
 
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_offsets, int32_t* nbr_order,
-                             int32_t* class_counts, void* stream) {
+                             uint32_t* nbr_waves, int32_t* wave_count, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(nbr_offsets != nullptr && class_counts != nullptr && (nbr_order != nullptr || grid->n_keys == 0),
+    require(nbr_offsets != nullptr && wave_count != nullptr &&
+                ((nbr_order != nullptr && nbr_waves != nullptr) || grid->n_keys == 0),
             "null buffer");
     const hipStream_t st = sphops::as_stream(stream);
     if (grid->n_keys == 0) {
-      SPHOPS_HIP(hipMemsetAsync(class_counts, 0, 4 * sizeof(int32_t), st));
+      SPHOPS_HIP(hipMemsetAsync(wave_count, 0, sizeof(int32_t), st));
       return;
     }
-    sphops::run_neighbour_schedule(*grid, nbr_offsets, nbr_order, class_counts, st);
+    sphops::run_neighbour_schedule(*grid, nbr_offsets, nbr_order, reinterpret_cast<uint2*>(nbr_waves), wave_count,
+                                   st);
   });
+}
+
+int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid) {
+  if (grid == nullptr) {
+    sphops::g_last_error = "grid must not be NULL";
+    return -1;
+  }
+  return (int64_t)sphops::neighbour_wave_capacity(*grid);
 }
 
 int sphops_safe_inv_sym_mat(const float* in, float* out, int64_t count, int dim, float tol, void* stream) {

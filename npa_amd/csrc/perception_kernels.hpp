@@ -977,27 +977,23 @@ __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t*
   if (active) op.finish(g, a, k);
 }
 
-// List traversal with a group of G lanes per particle, G by list-length class
-// (particles ordered by class in a.order): lane `sub` of the group takes pairs
-// sub, sub+G, ... of the particle's list, so consecutive lanes read
-// consecutive neighbours; the group then sums its partials.
-struct GroupSched {
-  uint32_t wave_start[5];  // first wave of each class; wave_start[4] = total waves
-  uint32_t part_start[4];  // first slot of each class in a.order
-};
-
+// List traversal with a group of G lanes per particle, G by list-length class:
+// wave w serves the particles a.order[first .. first + n) of its descriptor
+// a.waves[w] = {first, class << 8 | n}; lane `sub` of a group takes pairs sub,
+// sub+G, ... of the particle's list, so consecutive lanes read consecutive
+// neighbours; the group then sums its partials.
 template <int D, bool P, class OP>
-__global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs a, GroupSched sc) {
+__global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs a) {
   const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (wave >= sc.wave_start[4]) return;
-  int c = 0;
-  while (c < 3 && wave >= sc.wave_start[c + 1]) ++c;
+  if (wave >= a.nwaves) return;
+  const uint2 wd = a.waves[wave];
+  const int c = (int)(wd.y >> 8);
   const int G = kListGroupSizes[c];
   const int lane = __lane_id();
-  const uint32_t slot = (wave - sc.wave_start[c]) * (uint32_t)(kWave / G) + (uint32_t)(lane / G);
+  const uint32_t slot = (uint32_t)(lane / G);
   const int sub = lane & (G - 1);
-  const bool active = slot < (uint32_t)a.class_count[c];
-  const uint32_t k = active ? (uint32_t)a.order[sc.part_start[c] + slot] : 0u;
+  const bool active = slot < (wd.y & 0xFFu);
+  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
   const float4* __restrict__ xw = a.xw;
   OP op;
   float xi[3] = {0.0f, 0.0f, 0.0f};
@@ -1206,21 +1202,10 @@ void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
   const uint64_t n = g.n_keys;
   if (n == 0) return;
   pack_for<D, OP>(g, a, st);
-  if (a.nidx != nullptr && a.order != nullptr) {
-    GroupSched sc{};
-    uint32_t waves = 0, part = 0;
-    for (int c = 0; c < 4; ++c) {
-      sc.wave_start[c] = waves;
-      sc.part_start[c] = part;
-      const uint32_t per_wave = (uint32_t)(kWave / kListGroupSizes[c]);
-      waves += ((uint32_t)a.class_count[c] + per_wave - 1) / per_wave;
-      part += (uint32_t)a.class_count[c];
-    }
-    sc.wave_start[4] = waves;
-    if (part != n) throw Error("neighbour schedule class counts do not add up to the particle count");
-    const uint32_t wgs = (waves + (kThreads / kWave) - 1) / (kThreads / kWave);
+  if (a.nidx != nullptr && a.waves != nullptr) {
+    const uint32_t wgs = (a.nwaves + (kThreads / kWave) - 1) / (kThreads / kWave);
     if (wgs == 0) return;
-    hipLaunchKernelGGL((k_pairs_grouped<D, P, OP>), dim3(wgs), dim3(kThreads), 0, st, g.p, a, sc);
+    hipLaunchKernelGGL((k_pairs_grouped<D, P, OP>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else if (a.nidx != nullptr) {
     hipLaunchKernelGGL((k_pairs<D, P, kList, OP>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, a);
   } else if (OP::kChannels) {

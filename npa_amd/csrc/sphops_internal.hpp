@@ -95,8 +95,9 @@ struct OpPtrs {
   const int32_t* nptr = nullptr;  // CSR row offsets (B*N+1)
   const int32_t* nidx = nullptr;  // CSR neighbour indices; non-null selects list traversal
   const float4* xw = nullptr;     // packed positions and weights (set by the launcher)
-  const int32_t* order = nullptr; // particles by list-length class (optional, list traversal)
-  int32_t class_count[4] = {0, 0, 0, 0};
+  const int32_t* order = nullptr; // particles in schedule order (optional, list traversal)
+  const uint2* waves = nullptr;   // per-wave descriptors {first slot in order, class << 8 | particles}
+  uint32_t nwaves = 0;
   uint32_t C = 0;
   float tol = 1e-3f;
 };
@@ -106,9 +107,13 @@ void run_forward(const Grid& g, Op op, const int32_t* bin_offsets, const OpPtrs&
 void run_backward(const Grid& g, Op op, bool full, const int32_t* bin_offsets, const OpPtrs& a,
                   hipStream_t st);
 void run_neighbour_count(const Grid& g, const float* x, const int32_t* bo, int32_t* nptr, hipStream_t st);
-// particles ordered by neighbour-list length class (group sizes 1, 4, 16, 64)
-void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, int32_t* class_counts,
+// Pair-kernel schedule: per tile of 4096 binned particles, a stable partition
+// by neighbour-list length class (group sizes 1, 4, 16, 64), tiles in order;
+// one descriptor per wave {first slot in order, class << 8 | particles}.
+void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st);
+// upper bound of the number of waves a schedule can hold
+uint64_t neighbour_wave_capacity(const Grid& g);
 // particles ordered by stencil candidate count class (group sizes 1, 4, 8, 16)
 void run_candidate_schedule(const Grid& g, const int32_t* cand, int32_t* order, int32_t* class_counts,
                             hipStream_t st);

@@ -339,28 +339,30 @@ class _HashGridNative:
     # ---- generic operator interface with an optional neighbour list
     def neighbor_list(self, x_bin, bin_offsets):
         """In-radius neighbour list of the binned particles plus its
-        traversal schedule: ``(offsets (B*N+1,), index (pairs,), order (B*N,),
-        class_counts (4 ints, host))``.  Reads the pair total and the class
-        sizes back to the host to size ``index`` (one synchronisation)."""
+        traversal schedule: ``(offsets (B*N+1,), index (pairs,), order
+        (B*N,), waves (2 words per wave), wave_count (host int))``.  Reads the
+        pair total and the wave count back to the host to size ``index`` and
+        the later launches (one synchronisation)."""
         x = self._pos(x_bin, "binned_positions")
         bo = self._offsets(bin_offsets)
         dev = x_bin.device
         n = self._b * self._n
         offs = torch.empty(n + 1, dtype=_I32, device=dev)
         order = torch.empty(max(n, 1), dtype=_I32, device=dev)
-        small = torch.empty(5, dtype=_I32, device=dev)
+        cap = int(_lib.sphops_neighbor_wave_capacity(self._h))
+        waves = torch.empty(2 * max(cap, 1), dtype=_I32, device=dev)
+        small = torch.empty(2, dtype=_I32, device=dev)
         st = _stream(x_bin)
         _check(_lib.sphops_neighbor_count(self._h, x, bo, ctypes.c_void_p(offs.data_ptr()), st))
         _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(offs.data_ptr()),
-                                             ctypes.c_void_p(order.data_ptr()),
+                                             ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
                                              ctypes.c_void_p(small.data_ptr() + 4), st))
         small[0:1].copy_(offs[n:n + 1])
-        host = small.cpu().tolist()
-        total, counts = host[0], tuple(host[1:])
+        total, nwaves = small.cpu().tolist()
         index = torch.empty(max(total, 1), dtype=_I32, device=dev)
         _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(offs.data_ptr()),
                                          ctypes.c_void_p(index.data_ptr()), st))
-        return offs, index, order, counts
+        return offs, index, order, waves, nwaves
 
     # Per operator: trailing dims of (first output, second output) after (B, N);
     # "C" stands for the channel count, "D" for the spatial dimension.
@@ -412,9 +414,7 @@ class _HashGridNative:
         if nbr is not None:
             a.nbr_offsets, a.nbr_index = nbr[0].data_ptr(), nbr[1].data_ptr()
             if len(nbr) > 2:
-                a.nbr_order = nbr[2].data_ptr()
-                for c in range(4):
-                    a.nbr_class_count[c] = nbr[3][c]
+                a.nbr_order, a.nbr_waves, a.nbr_wave_count = nbr[2].data_ptr(), nbr[3].data_ptr(), nbr[4]
         return a
 
     def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None):
