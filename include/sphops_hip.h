@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 3
+#define SPHOPS_ABI_VERSION 4
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -135,9 +135,10 @@ int sphops_moment_matrix_backward(const sphops_grid* grid, const float* x, const
  * One entry point per direction for every perception operator, with an
  * optional per-snapshot neighbour list.  The reference has no counterpart:
  * its methods above traverse the cell stencil on every call.  Building the
- * list once per snapshot (sphops_neighbor_count + sphops_neighbor_fill) and
- * passing it here makes every later operator walk only in-radius pairs;
- * the pair set is identical, only the fp32 summation order can differ.
+ * list once per snapshot (sphops_neighbor_candidates, sphops_neighbor_fill,
+ * sphops_neighbor_schedule) and passing it here makes every later operator
+ * walk only in-radius pairs; the pair set is identical, only the fp32
+ * summation order can differ.
  *
  * Two fused codes evaluate operators that the reference always runs over the
  * same neighbours one after the other (models/npa.py:106-126) in one pass:
@@ -169,8 +170,9 @@ typedef struct sphops_args {
   uint32_t feature_dim;        /* C */
   float tol;                   /* gradient_hybrid: safe-inverse threshold */
   const int32_t* bin_offsets;  /* (B*G+1) from sphops_initialize */
-  const int32_t* nbr_offsets;  /* optional (B*N+1) CSR offsets from sphops_neighbor_count */
-  const int32_t* nbr_index;    /* optional CSR indices from sphops_neighbor_fill; NULL: scan the stencil */
+  const int32_t* nbr_start;    /* optional list row start per particle: cand_offsets of sphops_neighbor_fill */
+  const int32_t* nbr_count;    /* optional list length per particle from sphops_neighbor_fill */
+  const int32_t* nbr_index;    /* optional list entries from sphops_neighbor_fill; NULL: scan the stencil */
   const int32_t* nbr_order;    /* optional schedule from sphops_neighbor_schedule: particle order ... */
   const uint32_t* nbr_waves;   /* ... its wave descriptors (2 words per wave) ... */
   int32_t nbr_wave_count;      /* ... and the host copy of its wave count */
@@ -189,27 +191,32 @@ int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, voi
 int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLdrho, const sphops_args* args,
                     void* stream);
 
-/* In-radius neighbour count of every binned particle (pairs |r| < eps incl.
- * self, the reference's `count` as integers) written to nbr_offsets[0..B*N),
- * then scanned in place: nbr_offsets becomes the exclusive prefix sum with the
- * total number of pairs in nbr_offsets[B*N]. */
-int sphops_neighbor_count(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
-                          int32_t* nbr_offsets, void* stream);
+/* Row offsets of the neighbour list: for every binned particle the number of
+ * particles in its 3^D cell stencil (the cells the reference traverses, an
+ * upper bound of its in-radius count), exclusive-scanned into cand_offsets
+ * (B*N+1); cand_offsets[B*N] is the total. */
+int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
+                               int32_t* cand_offsets, void* stream);
 
-/* Fill nbr_index[nbr_offsets[i] .. nbr_offsets[i+1]) with the binned indices
- * of i's in-radius neighbours in stencil order. */
+/* In-radius neighbours (pairs |r| < eps incl. self) of every binned particle,
+ * in stencil order: the binned indices go to nbr_index[cand_offsets[i] ..),
+ * their number (the reference's `count`) to nbr_count[i] (B*N).  Entries at
+ * or past index_capacity are not written: a caller that sized nbr_index below
+ * cand_offsets[B*N] checks that total afterwards and fills again. */
 int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
-                         const int32_t* nbr_offsets, int32_t* nbr_index, void* stream);
+                         const int32_t* cand_offsets, int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count,
+                         void* stream);
 
 /* Schedule for list traversal.  The binned particles are cut into tiles of
  * 4096; within a tile they are partitioned (stably) by list length into four
  * classes (<=4, <=32, <=128, >128 neighbours), served by groups of 1, 4, 16
  * and 64 lanes per particle; tiles stay in order, so each region of space is
- * processed in one stretch.  nbr_order (B*N) receives the particles in that
+ * processed in one stretch.  From the list lengths nbr_count (B*N),
+ * nbr_order (B*N) receives the particles in that
  * order, nbr_waves (2 words per wave, capacity sphops_neighbor_wave_capacity)
  * one descriptor per 64-lane wave {first slot in nbr_order, class << 8 |
  * particles in the wave}, wave_count (one device int32) the number of waves. */
-int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_offsets, int32_t* nbr_order,
+int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,
                              uint32_t* nbr_waves, int32_t* wave_count, void* stream);
 
 /* Number of wave descriptors nbr_waves must hold for this grid (B*N + 4 per tile). */

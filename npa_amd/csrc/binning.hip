@@ -519,41 +519,17 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
   }
 }
 
-__global__ void k_class_totals(const uint32_t* __restrict__ cnt_scan, uint32_t ntiles, uint32_t n,
-                               int32_t* __restrict__ out) {
-  // class q holds [cnt_scan[q*ntiles], cnt_scan[(q+1)*ntiles]) of the order
-  const int q = threadIdx.x;
-  if (q < 4) {
-    const uint32_t lo = cnt_scan[q * ntiles];
-    const uint32_t hi = q < 3 ? cnt_scan[(q + 1) * ntiles] : n;
-    out[q] = (int32_t)(hi - lo);
-  }
-}
-
-// Class-major partition: order holds class 0 of every tile, then class 1, ...
-template <bool CSR>
-void partition_by_length(const Grid& g, const int32_t* src, ClassBounds cb, int32_t* order, int32_t* class_counts,
-                         hipStream_t st) {
-  const uint32_t n = (uint32_t)g.n_keys;
-  const uint32_t ntiles = (uint32_t)g.n_tiles;
-  uint32_t* cnt = g.hist;  // 4 * ntiles <= 256 * ntiles words
-  hipLaunchKernelGGL((k_class_count<CSR, false>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles);
-  SPHOPS_LAUNCHED();
-  device_exclusive_scan(cnt, cnt, 4ull * ntiles, g.scan_tmp, nullptr, st);
-  hipLaunchKernelGGL((k_class_scatter<CSR, false>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, ntiles,
-                     order);
-  SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_class_totals, dim3(1), dim3(64), 0, st, cnt, ntiles, n, class_counts);
-  SPHOPS_LAUNCHED();
-}
+struct GroupSizes {
+  int32_t g[4];  // lanes per particle of each class
+};
 
 // Waves needed by segment s = (tile, class): particles / (64 / group size), rounded up.
-__global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, uint32_t n,
+__global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, uint32_t n, GroupSizes gs,
                               uint32_t* __restrict__ wcnt) {
   const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= nseg) return;
   const uint32_t lo = seg[s], hi = s + 1 < nseg ? seg[s + 1] : n;
-  const uint32_t per = (uint32_t)(kWave / kListGroupSizes[s & 3u]);
+  const uint32_t per = (uint32_t)(kWave / gs.g[s & 3u]);
   wcnt[s] = (hi - lo + per - 1) / per;
 }
 
@@ -561,13 +537,13 @@ __global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, u
 // {first slot in order, class << 8 | particles in the wave}.
 __global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restrict__ seg,
                                                         const uint32_t* __restrict__ wstart, uint32_t ntiles,
-                                                        uint32_t n, uint2* __restrict__ waves) {
+                                                        uint32_t n, GroupSizes gs, uint2* __restrict__ waves) {
   const uint32_t t = blockIdx.x;
 #pragma unroll
   for (uint32_t q = 0; q < 4; ++q) {
     const uint32_t s = t * 4u + q;
     const uint32_t lo = seg[s], hi = s + 1 < 4u * ntiles ? seg[s + 1] : n;
-    const uint32_t per = (uint32_t)(kWave / kListGroupSizes[q]);
+    const uint32_t per = (uint32_t)(kWave / gs.g[q]);
     const uint32_t nw = (hi - lo + per - 1) / per;
     for (uint32_t u = threadIdx.x; u < nw; u += blockDim.x) {
       const uint32_t first = lo + u * per;
@@ -576,36 +552,46 @@ __global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restri
   }
 }
 
-}  // namespace
-
-uint64_t neighbour_wave_capacity(const Grid& g) { return g.n_keys + 4 * g.n_tiles; }
-
-void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, uint2* waves, int32_t* wave_total,
-                            hipStream_t st) {
+// Tile-major schedule: per tile of 4096 binned particles a stable partition
+// by length class, tiles in order, plus one descriptor per 64-lane wave.
+template <bool CSR>
+void tiled_schedule(const Grid& g, const int32_t* src, ClassBounds cb, GroupSizes gs, int32_t* order, uint2* waves,
+                    int32_t* wave_total, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
   const uint32_t nseg = 4u * ntiles;
   uint32_t* seg = g.hist;            // 4 * ntiles particle offsets
   uint32_t* wcnt = g.hist + nseg;    // 4 * ntiles wave offsets (hist holds 256 * ntiles words)
-  const ClassBounds cb{kListClassBounds[0], kListClassBounds[1], kListClassBounds[2]};
-  hipLaunchKernelGGL((k_class_count<true, true>), dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cb, seg, ntiles);
+  hipLaunchKernelGGL((k_class_count<CSR, true>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg, ntiles);
   SPHOPS_LAUNCHED();
   device_exclusive_scan(seg, seg, nseg, g.scan_tmp, nullptr, st);
-  hipLaunchKernelGGL((k_class_scatter<true, true>), dim3(ntiles), dim3(kThreads), 0, st, nptr, n, cb, seg, ntiles,
+  hipLaunchKernelGGL((k_class_scatter<CSR, true>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg, ntiles,
                      order);
   SPHOPS_LAUNCHED();
   hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, n,
-                     wcnt);
+                     gs, wcnt);
   SPHOPS_LAUNCHED();
   device_exclusive_scan(wcnt, wcnt, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total), st);
-  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt, ntiles, n, waves);
+  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt, ntiles, n, gs, waves);
   SPHOPS_LAUNCHED();
 }
 
-void run_candidate_schedule(const Grid& g, const int32_t* cand, int32_t* order, int32_t* class_counts,
+}  // namespace
+
+uint64_t neighbour_wave_capacity(const Grid& g) { return g.n_keys + 4 * g.n_tiles; }
+
+void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st) {
-  if (g.n_keys == 0) return;
-  partition_by_length<false>(g, cand, ClassBounds{16, 64, 256}, order, class_counts, st);
+  tiled_schedule<false>(g, ncnt, ClassBounds{kListClassBounds[0], kListClassBounds[1], kListClassBounds[2]},
+                       GroupSizes{{kListGroupSizes[0], kListGroupSizes[1], kListGroupSizes[2], kListGroupSizes[3]}},
+                       order, waves, wave_total, st);
+}
+
+void run_candidate_schedule(const Grid& g, const int32_t* coff, int32_t* order, uint2* waves, int32_t* wave_total,
+                            hipStream_t st) {
+  tiled_schedule<true>(g, coff, ClassBounds{kScanClassBounds[0], kScanClassBounds[1], kScanClassBounds[2]},
+                        GroupSizes{{kGroupSizes[0], kGroupSizes[1], kGroupSizes[2], kGroupSizes[3]}}, order, waves,
+                        wave_total, st);
 }
 
 void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* total, hipStream_t st) {

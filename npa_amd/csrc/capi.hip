@@ -60,9 +60,9 @@ void free_grid(Grid* g) {
   (void)hipFree(g->chunk_lo);
   (void)hipFree(g->flags);
   (void)hipFree(g->packed);
-  (void)hipFree(g->cand);
   (void)hipFree(g->cand_order);
-  (void)hipFree(g->cand_classes);
+  (void)hipFree(g->cand_waves);
+  (void)hipFree(g->cand_wave_total);
   delete g;
 }
 
@@ -230,9 +230,9 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
       g->flags = dalloc<uint32_t>(BN + 1);
       g->packed = dalloc<float4>(BN);
-      g->cand = dalloc<int32_t>(BN);
       g->cand_order = dalloc<int32_t>(BN);
-      g->cand_classes = dalloc<int32_t>(4);
+      g->cand_waves = dalloc<uint2>(sphops::neighbour_wave_capacity(*g));
+      g->cand_wave_total = dalloc<int32_t>(1);
     } catch (...) {
       sphops::free_grid(g);
       throw;
@@ -490,7 +490,8 @@ static OpPtrs from_args(const sphops_args* a) {
   p.out2 = a->grad_rho;
   p.C = a->feature_dim;
   p.tol = a->tol;
-  p.nptr = a->nbr_offsets;
+  p.nptr = a->nbr_start;
+  p.ncnt = a->nbr_count;
   p.nidx = a->nbr_index;
   p.order = a->nbr_order;
   p.waves = reinterpret_cast<const uint2*>(a->nbr_waves);
@@ -501,7 +502,8 @@ static OpPtrs from_args(const sphops_args* a) {
 }
 
 static void check_list(const sphops_args* a) {
-  require(a->nbr_index == nullptr || a->nbr_offsets != nullptr, "nbr_index needs nbr_offsets");
+  require(a->nbr_index == nullptr || (a->nbr_start != nullptr && a->nbr_count != nullptr),
+          "nbr_index needs nbr_start and nbr_count");
   require(a->nbr_order == nullptr || a->nbr_index != nullptr, "nbr_order needs nbr_index");
   require(a->nbr_waves == nullptr || a->nbr_order != nullptr, "nbr_waves needs nbr_order");
   require(a->nbr_order == nullptr || a->nbr_waves != nullptr, "nbr_order needs nbr_waves");
@@ -557,47 +559,48 @@ int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLd
   }
 }
 
-int sphops_neighbor_count(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* nbr_offsets,
-                          void* stream) {
+int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* cand_offsets,
+                               void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(bo != nullptr && nbr_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
+    require(bo != nullptr && cand_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
     require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
     const hipStream_t st = sphops::as_stream(stream);
     if (grid->n_keys == 0) {
-      SPHOPS_HIP(hipMemsetAsync(nbr_offsets, 0, sizeof(int32_t), st));
+      SPHOPS_HIP(hipMemsetAsync(cand_offsets, 0, sizeof(int32_t), st));
       return;
     }
     OpPtrs a;
     a.x = x;
-    a.iout = nbr_offsets;
-    sphops::forward(*grid, Op::NeighbourCount, bo, a, st);
-    sphops::exclusive_scan_u32(*grid, reinterpret_cast<uint32_t*>(nbr_offsets), grid->n_keys,
-                               reinterpret_cast<uint32_t*>(nbr_offsets) + grid->n_keys, st);
+    a.iout = cand_offsets;
+    sphops::forward(*grid, Op::NeighbourCandidates, bo, a, st);
   });
 }
 
-int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, const int32_t* nbr_offsets,
-                         int32_t* nbr_index, void* stream) {
+int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, const int32_t* cand_offsets,
+                         int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(bo != nullptr && nbr_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
+    require(bo != nullptr && cand_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
     require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
+    require(index_capacity >= 0, "negative index capacity");
     if (grid->n_keys == 0) return;
-    require(nbr_index != nullptr, "nbr_index must not be NULL");
+    require(nbr_count != nullptr && (nbr_index != nullptr || index_capacity == 0), "null buffer");
     OpPtrs a;
     a.x = x;
-    a.nptr = nbr_offsets;
+    a.nptr = cand_offsets;
     a.iout = nbr_index;
+    a.iout2 = nbr_count;
+    a.cap = index_capacity;
     sphops::forward(*grid, Op::NeighbourFill, bo, a, sphops::as_stream(stream));
   });
 }
 
-int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_offsets, int32_t* nbr_order,
+int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,
                              uint32_t* nbr_waves, int32_t* wave_count, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(nbr_offsets != nullptr && wave_count != nullptr &&
+    require(nbr_count != nullptr && wave_count != nullptr &&
                 ((nbr_order != nullptr && nbr_waves != nullptr) || grid->n_keys == 0),
             "null buffer");
     const hipStream_t st = sphops::as_stream(stream);
@@ -605,7 +608,7 @@ int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_offsets
       SPHOPS_HIP(hipMemsetAsync(wave_count, 0, sizeof(int32_t), st));
       return;
     }
-    sphops::run_neighbour_schedule(*grid, nbr_offsets, nbr_order, reinterpret_cast<uint2*>(nbr_waves), wave_count,
+    sphops::run_neighbour_schedule(*grid, nbr_count, nbr_order, reinterpret_cast<uint2*>(nbr_waves), wave_count,
                                    st);
   });
 }

@@ -6,9 +6,9 @@
 // operator, so one 16-byte load gives a neighbour's position and weight.
 //
 // Three traversals of i's neighbours:
-//  * kList     — walk i's precomputed in-radius list (CSR, built once per
-//                snapshot by the count/fill operators below); no distance
-//                tests, no divergence beyond list length.
+//  * kList     — walk i's precomputed in-radius list (row nptr[i], ncnt[i]
+//                entries, built once per snapshot by the fill kernel below);
+//                no distance tests, no divergence beyond list length.
 //  * kStencil  — test every candidate of the 3^D cell stencil, four loads in
 //                flight per lane, and call the operator for in-radius pairs.
 //  * kStencil2 — the same scan, but in-radius neighbours are first appended to
@@ -284,34 +284,6 @@ __device__ __forceinline__ void grp_sum(int G, A&... v) {
 // for every in-radius neighbour j (r = x_j - x_i wrapped, d2 = |r|^2 in fp32,
 // wj = the packed weight of j), finish(g, a, k).  kWeightKind selects what the
 // packed float4 carries in .w.
-
-template <int D, bool P>
-struct OpNeighbourCount {
-  static constexpr int kWeightKind = kWNone;
-  static constexpr bool kChannels = false;
-  int32_t n = 0;
-  __device__ void init(const GridParams&, const OpPtrs&, uint32_t) {}
-  __device__ void pair(const GridParams&, const OpPtrs&, const float*, const float*, float, const float*, float,
-                       uint32_t) {
-    ++n;
-  }
-  __device__ void reduce(int G) { (void)G; }
-  __device__ void finish(const GridParams&, const OpPtrs& a, uint32_t k) { a.iout[k] = n; }
-};
-
-template <int D, bool P>
-struct OpNeighbourFill {
-  static constexpr int kWeightKind = kWNone;
-  static constexpr bool kChannels = false;
-  int32_t pos = 0;
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k) { pos = a.nptr[k]; }
-  __device__ void pair(const GridParams&, const OpPtrs& a, const float*, const float*, float, const float*, float,
-                       uint32_t j) {
-    a.iout[pos++] = (int32_t)j;
-  }
-  __device__ void reduce(int G) { (void)G; }
-  __device__ void finish(const GridParams&, const OpPtrs&, uint32_t) {}
-};
 
 template <int D, bool P>
 struct OpCount {
@@ -898,7 +870,7 @@ __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t*
     if (active) {
       const int32_t* __restrict__ nidx = a.nidx;
       int t = a.nptr[k];
-      const int end = a.nptr[k + 1];
+      const int end = t + a.ncnt[k];
       for (; t + 1 < end; t += 2) {
         const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + 1];
         const float4 p0 = xw[j0], p1 = xw[j1];
@@ -1001,8 +973,9 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
     unpack(xw[k], xi);
     op.init(g, a, k);
     const int32_t* __restrict__ nidx = a.nidx;
-    const int end = a.nptr[k + 1];
-    int t = a.nptr[k] + sub;
+    const int start = a.nptr[k];
+    const int end = start + a.ncnt[k];
+    int t = start + sub;
     for (; t + G < end; t += 2 * G) {
       const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + G];
       const float4 p0 = xw[j0], p1 = xw[j1];
@@ -1056,39 +1029,31 @@ __global__ __launch_bounds__(kThreads) void k_candidates(GridParams g, const int
 
 constexpr int kScanUnroll = 4;
 
-template <int D, bool P, bool FILL>
-__global__ __launch_bounds__(kThreads) void k_scan_grouped(GridParams g, const int32_t* __restrict__ bo,
-                                                           const float4* __restrict__ xw,
-                                                           const int32_t* __restrict__ cand,
-                                                           const int32_t* __restrict__ order,
-                                                           const int32_t* __restrict__ classes,
-                                                           const int32_t* __restrict__ nptr,
-                                                           int32_t* __restrict__ out) {
-  uint32_t ustart[5], pstart[4], ncls[4];
-  {
-    uint32_t run = 0, pr = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      ncls[c] = (uint32_t)classes[c];
-      const uint32_t per = (uint32_t)(kWave / kGroupSizes[c]);
-      ustart[c] = run;
-      pstart[c] = pr;
-      run += (ncls[c] + per - 1) / per;
-      pr += ncls[c];
-    }
-    ustart[4] = run;
-  }
+// Neighbour-list fill: particle k's in-radius neighbours (stencil order) go
+// to nidx[coff[k] ..), coff = exclusive scan of the stencil candidate counts;
+// their number goes to ncnt[k].  Writes past `cap` entries are dropped (the
+// caller sized nidx from an earlier total and checks coff[n] afterwards).
+template <int D, bool P>
+__global__ __launch_bounds__(kThreads) void k_scan_fill(GridParams g, const int32_t* __restrict__ bo,
+                                                        const float4* __restrict__ xw,
+                                                        const int32_t* __restrict__ coff,
+                                                        const int32_t* __restrict__ order,
+                                                        const uint2* __restrict__ waves,
+                                                        const int32_t* __restrict__ wave_total,
+                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ ncnt,
+                                                        int64_t cap) {
+  const uint32_t total = (uint32_t)*wave_total;
   const uint32_t nwaves = gridDim.x * (kThreads / kWave);
   const int lane = __lane_id();
-  for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < ustart[4]; u += nwaves) {
-    int c = 0;
-    while (c < 3 && u >= ustart[c + 1]) ++c;
-    const int G = kGroupSizes[c];
-    const uint32_t slot = (u - ustart[c]) * (uint32_t)(kWave / G) + (uint32_t)(lane / G);
+  for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < total; u += nwaves) {
+    const uint2 wd = waves[u];
+    const int G = kGroupSizes[wd.y >> 8];
+    const uint32_t slot = (uint32_t)(lane / G);
     const int sub = lane & (G - 1);
-    const bool active = slot < ncls[c];
-    const uint32_t k = active ? (uint32_t)order[pstart[c] + slot] : 0u;
-    const uint32_t ncand = active ? (uint32_t)cand[k] : 0u;
+    const bool active = slot < (wd.y & 0xFFu);
+    const uint32_t k = active ? (uint32_t)order[wd.x + slot] : 0u;
+    const int32_t row = active ? coff[k] : 0;
+    const uint32_t ncand = active ? (uint32_t)(coff[k + 1] - row) : 0u;
     float xi[3] = {0.0f, 0.0f, 0.0f};
     Walker<D, P> w;
     uint32_t pr = 0, ra = 0, rlen = 0;
@@ -1102,8 +1067,8 @@ __global__ __launch_bounds__(kThreads) void k_scan_grouped(GridParams g, const i
     }
     const uint64_t gmask = G == 64 ? ~0ull : ((1ull << G) - 1ull);
     const int gshift = lane & ~(G - 1);
-    int32_t acc = FILL ? (active ? nptr[k] : 0) : 0;
-    const int32_t row_end = FILL ? (active ? nptr[k + 1] : 0) : 0;
+    int32_t acc = 0;
+    const int64_t row_end = min((int64_t)row + (int64_t)ncand, cap);
     for (uint32_t base = 0; base < ncand; base += (uint32_t)(G * kScanUnroll)) {
       uint32_t jj[kScanUnroll];
       bool ok[kScanUnroll];
@@ -1138,21 +1103,13 @@ __global__ __launch_bounds__(kThreads) void k_scan_grouped(GridParams g, const i
           unpack(pj[q], xj);
           in = displacement<D, P>(g, xi, xj, r) < g.eps2;
         }
-        if constexpr (FILL) {
-          const uint64_t gb = (__ballot(in) >> gshift) & gmask;
-          const int32_t pos = acc + (int32_t)__popcll(gb & ((1ull << sub) - 1ull));
-          if (in && pos < row_end) out[pos] = (int32_t)jj[q];
-          acc += (int32_t)__popcll(gb);
-        } else {
-          acc += in ? 1 : 0;
-        }
+        const uint64_t gb = (__ballot(in) >> gshift) & gmask;
+        const int64_t pos = (int64_t)row + acc + (int64_t)__popcll(gb & ((1ull << sub) - 1ull));
+        if (in && pos < row_end) nidx[pos] = (int32_t)jj[q];
+        acc += (int32_t)__popcll(gb);
       }
     }
-    if constexpr (!FILL) {
-      float v = (float)acc;
-      grp_sum(G, v);
-      if (active && sub == 0) out[k] = (int32_t)v;
-    }
+    if (active && sub == 0) ncnt[k] = acc;
   }
 }
 
@@ -1169,31 +1126,28 @@ void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
 
 constexpr uint32_t kPersistentWorkgroups = 2048;
 
-// Candidate counts and their class schedule (into the grid's scratch).
+// Stencil candidate counts of every binned particle, exclusive-scanned into
+// coff (B*N+1, total in coff[B*N]).
 template <int D, bool P>
-void candidate_schedule(const Grid& g, const int32_t* bo, const float* x, hipStream_t st) {
+void neighbour_candidates(const Grid& g, const int32_t* bo, const float* x, int32_t* coff, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, g.cand);
+  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, coff);
   SPHOPS_LAUNCHED();
-  run_candidate_schedule(g, g.cand, g.cand_order, g.cand_classes, st);
+  exclusive_scan_u32(g, reinterpret_cast<uint32_t*>(coff), n, reinterpret_cast<uint32_t*>(coff) + n, st);
 }
 
+// Fill the rows at coff: candidate-count schedule, then the grouped scan.
 template <int D, bool P>
-void neighbour_count(const Grid& g, const int32_t* bo, const float* x, int32_t* counts, hipStream_t st) {
-  candidate_schedule<D, P>(g, bo, x, st);
-  hipLaunchKernelGGL((k_scan_grouped<D, P, false>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo,
-                     g.packed, g.cand, g.cand_order, g.cand_classes, nullptr, counts);
+void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, const int32_t* coff, int32_t* nidx,
+                    int32_t* ncnt, int64_t cap, hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-}
-
-template <int D, bool P>
-void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, const int32_t* nptr, int32_t* nidx,
-                    hipStream_t st) {
-  candidate_schedule<D, P>(g, bo, x, st);
-  hipLaunchKernelGGL((k_scan_grouped<D, P, true>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo,
-                     g.packed, g.cand, g.cand_order, g.cand_classes, nptr, nidx);
+  run_candidate_schedule(g, coff, g.cand_order, g.cand_waves, g.cand_wave_total, st);
+  hipLaunchKernelGGL((k_scan_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo, g.packed,
+                     coff, g.cand_order, g.cand_waves, g.cand_wave_total, nidx, ncnt, cap);
   SPHOPS_LAUNCHED();
 }
 
@@ -1251,11 +1205,11 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
     case Op::GradientHybrid: return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
     case Op::DensityPair: return launch_pairs<D, P, OpDensityPair<D, P>>(g, bo, a, st);
     case Op::BlurGradientHybrid: return launch_channels<D, P, OpBlurGradientHybrid>(g, bo, a, st);
-    case Op::NeighbourCount:
-      if (g.n_keys) neighbour_count<D, P>(g, bo, a.x, a.iout, st);
+    case Op::NeighbourCandidates:
+      if (g.n_keys) neighbour_candidates<D, P>(g, bo, a.x, a.iout, st);
       return;
     case Op::NeighbourFill:
-      if (g.n_keys) neighbour_fill<D, P>(g, bo, a.x, a.nptr, a.iout, st);
+      if (g.n_keys) neighbour_fill<D, P>(g, bo, a.x, a.nptr, a.iout, a.iout2, a.cap, st);
       return;
   }
   throw Error("unknown forward operator");

@@ -49,9 +49,9 @@ struct Grid {
   uint32_t* chunk_lo = nullptr;   // n_chunks + 1
   uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
   float4* packed = nullptr;       // B*N (x, y, z|0, weight) read by the pair kernels
-  int32_t* cand = nullptr;        // B*N stencil candidate counts
-  int32_t* cand_order = nullptr;  // B*N particles by candidate-count class
-  int32_t* cand_classes = nullptr;  // 4 class sizes (device)
+  int32_t* cand_order = nullptr;  // B*N particles in candidate-scan schedule order
+  uint2* cand_waves = nullptr;    // candidate-scan wave descriptors (neighbour_wave_capacity)
+  int32_t* cand_wave_total = nullptr;  // number of candidate-scan waves (device)
   const void* cand_key[2] = {nullptr, nullptr};  // (positions, bin_offsets) the schedule was built for
 };
 
@@ -76,8 +76,8 @@ enum class Op : int {
   GradientHybrid = 6,
   DensityPair = 7,      // density + density gradient in one pass
   BlurGradientHybrid = 8,  // blur + gradient_hybrid in one pass
-  NeighbourCount = 9,   // in-radius neighbour count per particle (int32)
-  NeighbourFill = 10,   // in-radius neighbour indices into CSR rows (int32)
+  NeighbourCandidates = 9,  // scanned stencil candidate counts (int32, the list's row offsets)
+  NeighbourFill = 10,       // in-radius neighbour indices and counts (int32)
 };
 
 struct OpPtrs {
@@ -91,9 +91,12 @@ struct OpPtrs {
   float* out1 = nullptr;      // grad_s
   float* out2 = nullptr;      // grad_rho
   float* out3 = nullptr;      // second forward output (fused forward)
-  int32_t* iout = nullptr;    // neighbour counts / indices
-  const int32_t* nptr = nullptr;  // CSR row offsets (B*N+1)
-  const int32_t* nidx = nullptr;  // CSR neighbour indices; non-null selects list traversal
+  int32_t* iout = nullptr;    // candidate offsets / neighbour indices (list build)
+  int32_t* iout2 = nullptr;   // neighbour counts (list build)
+  int64_t cap = 0;            // capacity of iout for the fill
+  const int32_t* nptr = nullptr;  // list row start per particle (B*N)
+  const int32_t* ncnt = nullptr;  // list length per particle (B*N)
+  const int32_t* nidx = nullptr;  // neighbour indices; non-null selects list traversal
   const float4* xw = nullptr;     // packed positions and weights (set by the launcher)
   const int32_t* order = nullptr; // particles in schedule order (optional, list traversal)
   const uint2* waves = nullptr;   // per-wave descriptors {first slot in order, class << 8 | particles}
@@ -106,18 +109,19 @@ void run_forward(const Grid& g, Op op, const int32_t* bin_offsets, const OpPtrs&
 // full = false selects the dL/ds-only variant (Blur, Gradient)
 void run_backward(const Grid& g, Op op, bool full, const int32_t* bin_offsets, const OpPtrs& a,
                   hipStream_t st);
-void run_neighbour_count(const Grid& g, const float* x, const int32_t* bo, int32_t* nptr, hipStream_t st);
 // Pair-kernel schedule: per tile of 4096 binned particles, a stable partition
 // by neighbour-list length class (group sizes 1, 4, 16, 64), tiles in order;
 // one descriptor per wave {first slot in order, class << 8 | particles}.
-void run_neighbour_schedule(const Grid& g, const int32_t* nptr, int32_t* order, uint2* waves, int32_t* wave_total,
+void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st);
 // upper bound of the number of waves a schedule can hold
 uint64_t neighbour_wave_capacity(const Grid& g);
-// particles ordered by stencil candidate count class (group sizes 1, 4, 8, 16)
-void run_candidate_schedule(const Grid& g, const int32_t* cand, int32_t* order, int32_t* class_counts,
+// Candidate-scan schedule: as the pair-kernel schedule, classes by stencil
+// candidate count (from the scanned offsets coff; group sizes 1, 4, 8, 16).
+void run_candidate_schedule(const Grid& g, const int32_t* coff, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st);
 constexpr int kGroupSizes[4] = {1, 4, 8, 16};       // candidate-scan groups
+constexpr int kScanClassBounds[3] = {16, 64, 256};  // candidate-count class bounds for those groups
 constexpr int kListGroupSizes[4] = {1, 4, 16, 64};  // pair-list groups
 // list-length class bounds for the pair-list groups (<= t0, <= t1, <= t2, longer)
 constexpr int kListClassBounds[3] = {4, 32, 128};

@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -52,8 +52,8 @@ _SIGNATURES = {
     "sphops_safe_inv_sym_mat": ([_p, _p, _i64, _i32, _f32, _p], _i32),
     "sphops_forward": ([_p, _i32, _p, _p], _i32),
     "sphops_backward": ([_p, _i32, _i32, _i32, _i32, _p, _p], _i32),
-    "sphops_neighbor_count": ([_p, _p, _p, _p, _p], _i32),
-    "sphops_neighbor_fill": ([_p, _p, _p, _p, _p, _p], _i32),
+    "sphops_neighbor_candidates": ([_p, _p, _p, _p, _p], _i32),
+    "sphops_neighbor_fill": ([_p, _p, _p, _p, _p, _i64, _p, _p], _i32),
     "sphops_neighbor_schedule": ([_p, _p, _p, _p, _p, _p], _i32),
     "sphops_neighbor_wave_capacity": ([_p], _i64),
 }
@@ -63,7 +63,7 @@ class Args(ctypes.Structure):
     """``sphops_args`` (include/sphops_hip.h)."""
     _fields_ = [("x", _p), ("mass", _p), ("rho", _p), ("state", _p), ("upstream", _p), ("out", _p),
                 ("grad_state", _p), ("grad_rho", _p), ("feature_dim", _u32), ("tol", _f32),
-                ("bin_offsets", _p), ("nbr_offsets", _p), ("nbr_index", _p), ("nbr_order", _p),
+                ("bin_offsets", _p), ("nbr_start", _p), ("nbr_count", _p), ("nbr_index", _p), ("nbr_order", _p),
                 ("nbr_waves", _p), ("nbr_wave_count", ctypes.c_int32), ("upstream2", _p), ("out2", _p)]
 
 

@@ -339,30 +339,46 @@ class _HashGridNative:
     # ---- generic operator interface with an optional neighbour list
     def neighbor_list(self, x_bin, bin_offsets):
         """In-radius neighbour list of the binned particles plus its
-        traversal schedule: ``(offsets (B*N+1,), index (pairs,), order
-        (B*N,), waves (2 words per wave), wave_count (host int))``.  Reads the
-        pair total and the wave count back to the host to size ``index`` and
-        the later launches (one synchronisation)."""
+        traversal schedule: ``(start (B*N+1,), count (B*N,), index, order
+        (B*N,), waves (2 words per wave), wave_count (host int))``.  Row i is
+        ``index[start[i] : start[i] + count[i]]``; rows start at the scanned
+        stencil candidate counts, so ``index`` needs ``start[B*N]`` entries.
+        The index buffer is sized from the previous call's total and the
+        total is read back with the wave count (one synchronisation); the
+        fill is repeated in the rare case that the buffer was too small."""
         x = self._pos(x_bin, "binned_positions")
         bo = self._offsets(bin_offsets)
         dev = x_bin.device
         n = self._b * self._n
-        offs = torch.empty(n + 1, dtype=_I32, device=dev)
-        order = torch.empty(max(n, 1), dtype=_I32, device=dev)
-        cap = int(_lib.sphops_neighbor_wave_capacity(self._h))
-        waves = torch.empty(2 * max(cap, 1), dtype=_I32, device=dev)
-        small = torch.empty(2, dtype=_I32, device=dev)
         st = _stream(x_bin)
-        _check(_lib.sphops_neighbor_count(self._h, x, bo, ctypes.c_void_p(offs.data_ptr()), st))
-        _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(offs.data_ptr()),
+        start = torch.empty(n + 1, dtype=_I32, device=dev)
+        count = torch.empty(max(n, 1), dtype=_I32, device=dev)
+        order = torch.empty(max(n, 1), dtype=_I32, device=dev)
+        waves = torch.empty(2 * max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 1), dtype=_I32, device=dev)
+        small = torch.empty(2, dtype=_I32, device=dev)
+        _check(_lib.sphops_neighbor_candidates(self._h, x, bo, ctypes.c_void_p(start.data_ptr()), st))
+        prev = getattr(self, "_index_capacity", 0)
+        cap = prev if prev else int(start[n].item())
+        index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
+
+        def fill(buf, capacity):
+            _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
+                                             ctypes.c_void_p(buf.data_ptr()), capacity,
+                                             ctypes.c_void_p(count.data_ptr()), st))
+
+        fill(index, cap)
+        _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
                                              ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
                                              ctypes.c_void_p(small.data_ptr() + 4), st))
-        small[0:1].copy_(offs[n:n + 1])
+        small[0:1].copy_(start[n:n + 1])
         total, nwaves = small.cpu().tolist()
-        index = torch.empty(max(total, 1), dtype=_I32, device=dev)
-        _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(offs.data_ptr()),
-                                         ctypes.c_void_p(index.data_ptr()), st))
-        return offs, index, order, waves, nwaves
+        if total > cap:
+            cap = total
+            index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
+            fill(index, cap)
+        if total > prev:  # ~12% headroom, so that the next snapshot of a moving cloud fits
+            self._index_capacity = total + total // 8
+        return start, count, index, order, waves, nwaves
 
     # Per operator: trailing dims of (first output, second output) after (B, N);
     # "C" stands for the channel count, "D" for the spatial dimension.
@@ -412,9 +428,9 @@ class _HashGridNative:
                 raise RuntimeError(f"{name}: expected {sizes[name]} elements, got {t.numel()}")
             setattr(a, "out" if name == "grad_x" else name, t.data_ptr())
         if nbr is not None:
-            a.nbr_offsets, a.nbr_index = nbr[0].data_ptr(), nbr[1].data_ptr()
-            if len(nbr) > 2:
-                a.nbr_order, a.nbr_waves, a.nbr_wave_count = nbr[2].data_ptr(), nbr[3].data_ptr(), nbr[4]
+            a.nbr_start, a.nbr_count, a.nbr_index = nbr[0].data_ptr(), nbr[1].data_ptr(), nbr[2].data_ptr()
+            if len(nbr) > 3:
+                a.nbr_order, a.nbr_waves, a.nbr_wave_count = nbr[3].data_ptr(), nbr[4].data_ptr(), nbr[5]
         return a
 
     def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None):

@@ -235,6 +235,40 @@ def test_backward(name):
 
 
 @pytest.mark.parametrize("name", NAMES)
+def test_neighbor_list(name):
+    """The per-snapshot list holds exactly the oracle's in-radius pairs of
+    every particle (as sets; the row order is the stencil traversal order),
+    also when the index buffer was sized too small and the fill is redone."""
+    import npa_amd.sphops as sp
+    c, res, ora = run(name)
+    grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    hg = grid.hashgrid
+    xb, bo = dev(res["xb"]), dev(res["bo"])
+    p = ora["ctx"].p
+    q = p.queries
+    ref = np.lexsort((p.j, p.q))
+    ref_q, ref_j = p.q[ref], p.j[ref]
+
+    def check(nbr, label):
+        start, count, index = (t.cpu().numpy() for t in nbr[:3])
+        np.testing.assert_array_equal(count[q], np.bincount(p.q, minlength=len(q)), err_msg=label)
+        gq = np.repeat(np.arange(len(q)), count[q])
+        gj = np.concatenate([index[start[k]:start[k] + count[k]] for k in q]) if len(q) else np.zeros(0)
+        o = np.lexsort((gj, gq))
+        np.testing.assert_array_equal(gq[o], ref_q, err_msg=label)
+        np.testing.assert_array_equal(gj[o], ref_j, err_msg=label)
+        assert np.all(start[1:] >= start[:-1] + count), label   # rows do not overlap
+        assert nbr[5] > 0 or c.B * c.N == 0
+
+    check(hg.neighbor_list(xb, bo), f"{name}:first")
+    hg._index_capacity = 7            # force the too-small buffer and the second fill
+    nbr = hg.neighbor_list(xb, bo)
+    check(nbr, f"{name}:refill")
+    assert hg._index_capacity >= int(nbr[0][-1].item())
+
+
+@pytest.mark.parametrize("name", NAMES)
 def test_fused_passes(name):
     """One-pass density + density_gradient and blur + gradient_hybrid, forward
     and backward (the backward is the sum of both operators' gradients)."""
