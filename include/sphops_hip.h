@@ -208,18 +208,18 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
                          void* stream);
 
 /* Schedule for list traversal.  The binned particles are cut into tiles of
- * 4096; within a tile they are partitioned (stably) by list length into four
- * classes (<=4, <=32, <=128, >128 neighbours), served by groups of 1, 4, 16
- * and 64 lanes per particle; tiles stay in order, so each region of space is
- * processed in one stretch.  From the list lengths nbr_count (B*N),
- * nbr_order (B*N) receives the particles in that
- * order, nbr_waves (2 words per wave, capacity sphops_neighbor_wave_capacity)
- * one descriptor per 64-lane wave {first slot in nbr_order, class << 8 |
- * particles in the wave}, wave_count (one device int32) the number of waves. */
+ * 4096; within a tile they are partitioned (stably) by list length into eight
+ * classes (<=6, <=12, <=24, ..., <=384, >384 neighbours), served by groups of
+ * 1, 1, 2, 4, ..., 64 lanes per particle; tiles stay in order, so each region
+ * of space is processed in one stretch.  From the list lengths nbr_count
+ * (B*N), nbr_order (B*N) receives the particles in that order, nbr_waves
+ * (2 words per wave, capacity sphops_neighbor_wave_capacity) one descriptor
+ * per 64-lane wave {first slot in nbr_order, group size << 8 | particles in
+ * the wave}, wave_count (one device int32) the number of waves. */
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,
                              uint32_t* nbr_waves, int32_t* wave_count, void* stream);
 
-/* Number of wave descriptors nbr_waves must hold for this grid (B*N + 4 per tile). */
+/* Number of wave descriptors nbr_waves must hold for this grid (B*N + 8 per tile of 4096). */
 int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid);
 
 /* Module function safe_inv_sym_mat (sph_cuda.cu:3181-3226): `count` symmetric

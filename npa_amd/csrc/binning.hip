@@ -256,61 +256,69 @@ __global__ __launch_bounds__(kThreads) void k_chunk_counts(const uint32_t* __res
   if (i < nch) cnt[i] = cend[i] - cfirst[i];
 }
 
-// bin_offsets[c] = number of sorted keys < c, for the 1024 cells of one chunk.
+// bin_offsets[c] = number of sorted keys < c, for the 1024 cells of a chunk.
 // Run heads inside the chunk mark their cell; empty cells take the next run
-// head (suffix minimum), the chunk end being the sentinel.
+// head (suffix minimum), the chunk end being the sentinel.  A workgroup
+// handles kChunksPerBlock consecutive chunks (most of them empty at large
+// cell counts, where the kernel is a 16-byte-per-lane store stream).
+constexpr int kChunksPerBlock = 8;
+
 __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint32_t* __restrict__ keys,
-                                                          const uint32_t* __restrict__ chunk_lo,
+                                                          const uint32_t* __restrict__ chunk_lo, uint32_t nch,
                                                           int32_t* __restrict__ bo, uint64_t ncells_p1) {
   __shared__ uint32_t first[kChunk];
   __shared__ uint32_t wmin[kThreads / 64];
-  const uint32_t ch = blockIdx.x;
-  const uint32_t lo = chunk_lo[ch], hi = chunk_lo[ch + 1];
-  const uint64_t c0 = (uint64_t)ch << kChunkLog2;
   const int t = threadIdx.x;
-  uint32_t s[4];
-  if (lo == hi) {
+  for (int i = 0; i < kChunksPerBlock; ++i) {
+    const uint32_t ch = blockIdx.x * kChunksPerBlock + (uint32_t)i;
+    if (ch >= nch) break;  // uniform over the workgroup
+    const uint32_t lo = chunk_lo[ch], hi = chunk_lo[ch + 1];
+    const uint64_t c0 = (uint64_t)ch << kChunkLog2;
+    uint32_t s[4];
+    if (lo == hi) {  // uniform over the workgroup
 #pragma unroll
-    for (int q = 0; q < 4; ++q) s[q] = lo;
-  } else {
+      for (int q = 0; q < 4; ++q) s[q] = lo;
+    } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) first[t * 4 + q] = hi;
-    __syncthreads();
-    for (uint32_t p = lo + t; p < hi; p += kThreads) {
-      const uint32_t key = keys[p];
-      if (p == lo || keys[p - 1] != key) first[key - (uint32_t)c0] = p;
+      for (int q = 0; q < 4; ++q) first[t * 4 + q] = hi;
+      __syncthreads();
+      for (uint32_t p = lo + t; p < hi; p += kThreads) {
+        const uint32_t key = keys[p];
+        if (p == lo || keys[p - 1] != key) first[key - (uint32_t)c0] = p;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s[q] = first[t * 4 + q];
+      s[2] = min(s[2], s[3]);
+      s[1] = min(s[1], s[2]);
+      s[0] = min(s[0], s[1]);
+      // exclusive suffix minimum over threads
+      const int lane = __lane_id(), wave = t >> 6;
+      uint32_t incl = s[0];
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_down(incl, off, 64);
+        if (lane + off < 64) incl = min(incl, y);
+      }
+      if (lane == 0) wmin[wave] = incl;
+      __syncthreads();
+      uint32_t after = hi;
+      for (int w = wave + 1; w < kThreads / 64; ++w) after = min(after, wmin[w]);
+      uint32_t nxt = __shfl_down(incl, 1, 64);
+      if (lane == 63) nxt = hi;
+      after = min(after, nxt);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s[q] = min(s[q], after);
+      __syncthreads();  // `first` and `wmin` are reused by the next chunk
     }
-    __syncthreads();
+    const uint64_t c = c0 + (uint64_t)t * 4;
+    if (c + 3 < ncells_p1) {
+      *reinterpret_cast<int4*>(bo + c) = make_int4((int)s[0], (int)s[1], (int)s[2], (int)s[3]);
+    } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) s[q] = first[t * 4 + q];
-    s[2] = min(s[2], s[3]);
-    s[1] = min(s[1], s[2]);
-    s[0] = min(s[0], s[1]);
-    // exclusive suffix minimum over threads
-    const int lane = __lane_id(), wave = t >> 6;
-    uint32_t incl = s[0];
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t y = __shfl_down(incl, off, 64);
-      if (lane + off < 64) incl = min(incl, y);
+      for (int q = 0; q < 4; ++q)
+        if (c + q < ncells_p1) bo[c + q] = (int)s[q];
     }
-    if (lane == 0) wmin[wave] = incl;
-    __syncthreads();
-    uint32_t after = hi;
-    for (int w = wave + 1; w < kThreads / 64; ++w) after = min(after, wmin[w]);
-    uint32_t nxt = __shfl_down(incl, 1, 64);
-    if (lane == 63) nxt = hi;
-    after = min(after, nxt);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) s[q] = min(s[q], after);
-  }
-  const uint64_t c = c0 + (uint64_t)t * 4;
-  if (c + 3 < ncells_p1) {
-    *reinterpret_cast<int4*>(bo + c) = make_int4((int)s[0], (int)s[1], (int)s[2], (int)s[3]);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (c + q < ncells_p1) bo[c + q] = (int)s[q];
   }
 }
 
@@ -422,9 +430,13 @@ inline dim3 blocks_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) /
 
 namespace {
 
-struct ClassBounds {
-  int32_t t0, t1, t2;  // class 0: len <= t0, 1: <= t1, 2: <= t2, 3: longer
-};
+// Class of a list (or candidate) length: the number of bounds it exceeds.
+__device__ __forceinline__ uint32_t length_class(int32_t len, const ClassBounds& cb) {
+  uint32_t q = 0;
+#pragma unroll
+  for (int i = 0; i < kNumClasses - 1; ++i) q += (len > cb.t[i]) ? 1u : 0u;
+  return q;
+}
 
 // Length of item idx: from CSR offsets (CSR) or a plain length array.
 template <bool CSR>
@@ -433,56 +445,49 @@ __device__ __forceinline__ int32_t item_length(const int32_t* __restrict__ src, 
   return src[idx];
 }
 
-__device__ __forceinline__ uint32_t length_class(int32_t len, ClassBounds cb) {
-  return len <= cb.t0 ? 0u : (len <= cb.t1 ? 1u : (len <= cb.t2 ? 2u : 3u));
-}
-
-// Segment (tile, class) of the count / offset tables in either layout.
-template <bool TM>
-__device__ __forceinline__ uint32_t seg_index(uint32_t tile, uint32_t q, uint32_t ntiles) {
-  return TM ? tile * 4u + q : q * ntiles + tile;
-}
-
-template <bool CSR, bool TM>
+// Per tile of kTile items: the number of items of each class, written to
+// cnt[tile * kNumClasses + class].
+template <bool CSR>
 __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restrict__ src, uint32_t n,
-                                                          ClassBounds cb, uint32_t* __restrict__ cnt,
-                                                          uint32_t ntiles) {
-  __shared__ uint32_t h[4];
-  if (threadIdx.x < 4) h[threadIdx.x] = 0;
+                                                          ClassBounds cb, uint32_t* __restrict__ cnt) {
+  __shared__ uint32_t h[kNumClasses];
+  if (threadIdx.x < kNumClasses) h[threadIdx.x] = 0;
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile;
-  uint32_t c[4] = {0, 0, 0, 0};
+  uint32_t c[kNumClasses] = {};
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const uint32_t idx = base + i * kThreads + threadIdx.x;
     if (idx < n) {
       const uint32_t k = length_class(item_length<CSR>(src, idx), cb);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) c[q] += (k == (uint32_t)q);
+      for (int q = 0; q < kNumClasses; ++q) c[q] += (k == (uint32_t)q);
     }
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < kNumClasses; ++q) {
     uint32_t v = c[q];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
     if (__lane_id() == 0) atomicAdd(&h[q], v);
   }
   __syncthreads();
-  if (threadIdx.x < 4) cnt[seg_index<TM>(blockIdx.x, threadIdx.x, ntiles)] = h[threadIdx.x];
+  if (threadIdx.x < kNumClasses) cnt[blockIdx.x * kNumClasses + threadIdx.x] = h[threadIdx.x];
 }
 
-// Same tile walk as the radix scatter: wave w owns items [w*1024, (w+1)*1024)
-// in index order; two ballots identify lanes of the same class.
-template <bool CSR, bool TM>
+// Stable scatter of a tile's items into order, class by class, at the
+// scanned segment offsets.  Same tile walk as the radix scatter: wave w owns
+// items [w*1024, (w+1)*1024) in index order; three ballots identify lanes of
+// the same class.
+template <bool CSR>
 __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __restrict__ src, uint32_t n,
                                                             ClassBounds cb, const uint32_t* __restrict__ cnt_scan,
-                                                            uint32_t ntiles, int32_t* __restrict__ order) {
-  __shared__ uint32_t wcnt[kThreads / 64][4];
-  __shared__ uint32_t gbase[4];
+                                                            int32_t* __restrict__ order) {
+  __shared__ uint32_t wcnt[kThreads / 64][kNumClasses];
+  __shared__ uint32_t gbase[kNumClasses];
   const int wave = threadIdx.x >> 6, lane = __lane_id();
-  if (threadIdx.x < (kThreads / 64) * 4) (&wcnt[0][0])[threadIdx.x] = 0;
-  if (threadIdx.x < 4) gbase[threadIdx.x] = cnt_scan[seg_index<TM>(blockIdx.x, threadIdx.x, ntiles)];
+  if (threadIdx.x < (kThreads / 64) * kNumClasses) (&wcnt[0][0])[threadIdx.x] = 0;
+  if (threadIdx.x < kNumClasses) gbase[threadIdx.x] = cnt_scan[blockIdx.x * kNumClasses + threadIdx.x];
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
   const uint64_t below_mask = lanemask_lt();
@@ -494,16 +499,18 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
     const uint32_t k = valid ? length_class(item_length<CSR>(src, idx), cb) : 0u;
     cls[t] = k;
     uint64_t peers = __ballot(valid);
-    const uint64_t b0 = __ballot(k & 1u), b1 = __ballot((k >> 1) & 1u);
-    peers &= (k & 1u) ? b0 : ~b0;
-    peers &= (k & 2u) ? b1 : ~b1;
+#pragma unroll
+    for (int bit = 0; bit < 3; ++bit) {
+      const uint64_t bb = __ballot((k >> bit) & 1u);
+      peers &= ((k >> bit) & 1u) ? bb : ~bb;
+    }
     const uint32_t before = (uint32_t)__popcll(peers & below_mask);
     const uint32_t prior = wcnt[wave][k];
     if (valid && before == 0) wcnt[wave][k] = prior + (uint32_t)__popcll(peers);
     rank[t] = prior + before;
   }
   __syncthreads();
-  if (threadIdx.x < 4) {
+  if (threadIdx.x < kNumClasses) {
     uint32_t run = 0;
     for (int w = 0; w < kThreads / 64; ++w) {
       const uint32_t c = wcnt[w][threadIdx.x];
@@ -519,35 +526,32 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
   }
 }
 
-struct GroupSizes {
-  int32_t g[4];  // lanes per particle of each class
-};
-
-// Waves needed by segment s = (tile, class): particles / (64 / group size), rounded up.
+// Waves needed by segment s = (tile, class): items / (64 / group size), rounded up.
 __global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, uint32_t n, GroupSizes gs,
                               uint32_t* __restrict__ wcnt) {
   const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= nseg) return;
   const uint32_t lo = seg[s], hi = s + 1 < nseg ? seg[s + 1] : n;
-  const uint32_t per = (uint32_t)(kWave / gs.g[s & 3u]);
+  const uint32_t per = (uint32_t)(kWave / gs.g[s % kNumClasses]);
   wcnt[s] = (hi - lo + per - 1) / per;
 }
 
-// One workgroup per tile writes the wave descriptors of its four segments:
-// {first slot in order, class << 8 | particles in the wave}.
+// One workgroup per tile writes the wave descriptors of its segments:
+// {first slot in order, group size << 8 | items in the wave}.
 __global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restrict__ seg,
                                                         const uint32_t* __restrict__ wstart, uint32_t ntiles,
                                                         uint32_t n, GroupSizes gs, uint2* __restrict__ waves) {
   const uint32_t t = blockIdx.x;
+  const uint32_t nseg = (uint32_t)kNumClasses * ntiles;
 #pragma unroll
-  for (uint32_t q = 0; q < 4; ++q) {
-    const uint32_t s = t * 4u + q;
-    const uint32_t lo = seg[s], hi = s + 1 < 4u * ntiles ? seg[s + 1] : n;
+  for (uint32_t q = 0; q < (uint32_t)kNumClasses; ++q) {
+    const uint32_t s = t * kNumClasses + q;
+    const uint32_t lo = seg[s], hi = s + 1 < nseg ? seg[s + 1] : n;
     const uint32_t per = (uint32_t)(kWave / gs.g[q]);
     const uint32_t nw = (hi - lo + per - 1) / per;
     for (uint32_t u = threadIdx.x; u < nw; u += blockDim.x) {
       const uint32_t first = lo + u * per;
-      waves[wstart[s] + u] = make_uint2(first, (q << 8) | min(per, hi - first));
+      waves[wstart[s] + u] = make_uint2(first, ((uint32_t)gs.g[q] << 8) | min(per, hi - first));
     }
   }
 }
@@ -555,18 +559,17 @@ __global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restri
 // Tile-major schedule: per tile of 4096 binned particles a stable partition
 // by length class, tiles in order, plus one descriptor per 64-lane wave.
 template <bool CSR>
-void tiled_schedule(const Grid& g, const int32_t* src, ClassBounds cb, GroupSizes gs, int32_t* order, uint2* waves,
-                    int32_t* wave_total, hipStream_t st) {
+void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, const GroupSizes& gs, int32_t* order,
+                    uint2* waves, int32_t* wave_total, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
-  const uint32_t nseg = 4u * ntiles;
-  uint32_t* seg = g.hist;            // 4 * ntiles particle offsets
-  uint32_t* wcnt = g.hist + nseg;    // 4 * ntiles wave offsets (hist holds 256 * ntiles words)
-  hipLaunchKernelGGL((k_class_count<CSR, true>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg, ntiles);
+  const uint32_t nseg = (uint32_t)kNumClasses * ntiles;
+  uint32_t* seg = g.hist;            // item offsets per segment
+  uint32_t* wcnt = g.hist + nseg;    // wave offsets per segment (hist holds 256 * ntiles words)
+  hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg);
   SPHOPS_LAUNCHED();
   device_exclusive_scan(seg, seg, nseg, g.scan_tmp, nullptr, st);
-  hipLaunchKernelGGL((k_class_scatter<CSR, true>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg, ntiles,
-                     order);
+  hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg, order);
   SPHOPS_LAUNCHED();
   hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, n,
                      gs, wcnt);
@@ -578,20 +581,16 @@ void tiled_schedule(const Grid& g, const int32_t* src, ClassBounds cb, GroupSize
 
 }  // namespace
 
-uint64_t neighbour_wave_capacity(const Grid& g) { return g.n_keys + 4 * g.n_tiles; }
+uint64_t neighbour_wave_capacity(const Grid& g) { return g.n_keys + (uint64_t)kNumClasses * g.n_tiles; }
 
 void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st) {
-  tiled_schedule<false>(g, ncnt, ClassBounds{kListClassBounds[0], kListClassBounds[1], kListClassBounds[2]},
-                       GroupSizes{{kListGroupSizes[0], kListGroupSizes[1], kListGroupSizes[2], kListGroupSizes[3]}},
-                       order, waves, wave_total, st);
+  tiled_schedule<false>(g, ncnt, kListClasses, kListGroups, order, waves, wave_total, st);
 }
 
 void run_candidate_schedule(const Grid& g, const int32_t* coff, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st) {
-  tiled_schedule<true>(g, coff, ClassBounds{kScanClassBounds[0], kScanClassBounds[1], kScanClassBounds[2]},
-                        GroupSizes{{kGroupSizes[0], kGroupSizes[1], kGroupSizes[2], kGroupSizes[3]}}, order, waves,
-                        wave_total, st);
+  tiled_schedule<true>(g, coff, kScanClasses, kScanGroups, order, waves, wave_total, st);
 }
 
 void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* total, hipStream_t st) {
@@ -649,7 +648,8 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
                      g.chunk_lo, nch);
   SPHOPS_LAUNCHED();
   device_exclusive_scan(g.chunk_lo, g.chunk_lo, nch, g.scan_tmp, g.chunk_lo + nch, st);
-  hipLaunchKernelGGL(k_bin_offsets, dim3(nch), dim3(kThreads), 0, st, skeys, g.chunk_lo, bo, ncp1);
+  hipLaunchKernelGGL(k_bin_offsets, dim3((nch + kChunksPerBlock - 1) / kChunksPerBlock), dim3(kThreads), 0, st,
+                     skeys, g.chunk_lo, nch, bo, ncp1);
   SPHOPS_LAUNCHED();
 
   // 4. permutation (destination slot of each input particle)

@@ -951,7 +951,7 @@ __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t*
 
 // List traversal with a group of G lanes per particle, G by list-length class:
 // wave w serves the particles a.order[first .. first + n) of its descriptor
-// a.waves[w] = {first, class << 8 | n}; lane `sub` of a group takes pairs sub,
+// a.waves[w] = {first, G << 8 | n}; lane `sub` of a group takes pairs sub,
 // sub+G, ... of the particle's list, so consecutive lanes read consecutive
 // neighbours; the group then sums its partials.
 template <int D, bool P, class OP>
@@ -959,8 +959,7 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
   const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
   if (wave >= a.nwaves) return;
   const uint2 wd = a.waves[wave];
-  const int c = (int)(wd.y >> 8);
-  const int G = kListGroupSizes[c];
+  const int G = (int)(wd.y >> 8);
   const int lane = __lane_id();
   const uint32_t slot = (uint32_t)(lane / G);
   const int sub = lane & (G - 1);
@@ -1047,7 +1046,7 @@ __global__ __launch_bounds__(kThreads) void k_scan_fill(GridParams g, const int3
   const int lane = __lane_id();
   for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < total; u += nwaves) {
     const uint2 wd = waves[u];
-    const int G = kGroupSizes[wd.y >> 8];
+    const int G = (int)(wd.y >> 8);
     const uint32_t slot = (uint32_t)(lane / G);
     const int sub = lane & (G - 1);
     const bool active = slot < (wd.y & 0xFFu);

@@ -99,7 +99,7 @@ struct OpPtrs {
   const int32_t* nidx = nullptr;  // neighbour indices; non-null selects list traversal
   const float4* xw = nullptr;     // packed positions and weights (set by the launcher)
   const int32_t* order = nullptr; // particles in schedule order (optional, list traversal)
-  const uint2* waves = nullptr;   // per-wave descriptors {first slot in order, class << 8 | particles}
+  const uint2* waves = nullptr;   // per-wave descriptors {first slot in order, group size << 8 | particles}
   uint32_t nwaves = 0;
   uint32_t C = 0;
   float tol = 1e-3f;
@@ -110,21 +110,35 @@ void run_forward(const Grid& g, Op op, const int32_t* bin_offsets, const OpPtrs&
 void run_backward(const Grid& g, Op op, bool full, const int32_t* bin_offsets, const OpPtrs& a,
                   hipStream_t st);
 // Pair-kernel schedule: per tile of 4096 binned particles, a stable partition
-// by neighbour-list length class (group sizes 1, 4, 16, 64), tiles in order;
-// one descriptor per wave {first slot in order, class << 8 | particles}.
+// by neighbour-list length class (kListClasses / kListGroups), tiles in
+// order; one descriptor per wave {first slot in order, group size << 8 | particles}.
 void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st);
 // upper bound of the number of waves a schedule can hold
 uint64_t neighbour_wave_capacity(const Grid& g);
 // Candidate-scan schedule: as the pair-kernel schedule, classes by stencil
-// candidate count (from the scanned offsets coff; group sizes 1, 4, 8, 16).
+// candidate count (from the scanned offsets coff; kScanClasses / kScanGroups).
 void run_candidate_schedule(const Grid& g, const int32_t* coff, int32_t* order, uint2* waves, int32_t* wave_total,
                             hipStream_t st);
-constexpr int kGroupSizes[4] = {1, 4, 8, 16};       // candidate-scan groups
-constexpr int kScanClassBounds[3] = {16, 64, 256};  // candidate-count class bounds for those groups
-constexpr int kListGroupSizes[4] = {1, 4, 16, 64};  // pair-list groups
-// list-length class bounds for the pair-list groups (<= t0, <= t1, <= t2, longer)
-constexpr int kListClassBounds[3] = {4, 32, 128};
+// Work classes of the list traversal and the candidate scan: class q holds
+// the items whose length is <= t[q] (and above the previous bound), the last
+// class the rest; each class is served by groups of g[q] lanes per particle
+// (a power of two <= 64).  Bounds double from class to class, and so do the
+// group sizes up to their cap, so a class spans a factor of two in items per
+// lane.  The tables were chosen by timing the cfg5 workload on an MI355X.
+constexpr int kNumClasses = 8;
+struct ClassBounds {
+  int32_t t[kNumClasses - 1];
+};
+struct GroupSizes {
+  int32_t g[kNumClasses];
+};
+// pair lists: about 6-12 pairs per lane
+constexpr ClassBounds kListClasses{{6, 12, 24, 48, 96, 192, 384}};
+constexpr GroupSizes kListGroups{{1, 1, 2, 4, 8, 16, 32, 64}};
+// stencil candidates: 32-64 candidates per lane, at most 16 lanes per particle
+constexpr ClassBounds kScanClasses{{64, 128, 256, 512, 1024, 2048, 4096}};
+constexpr GroupSizes kScanGroups{{1, 1, 2, 4, 8, 16, 16, 16}};
 void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
