@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 4
+#define SPHOPS_ABI_VERSION 5
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -176,6 +176,8 @@ typedef struct sphops_args {
   const int32_t* nbr_order;    /* optional schedule from sphops_neighbor_schedule: particle order ... */
   const uint32_t* nbr_waves;   /* ... its wave descriptors (2 words per wave) ... */
   int32_t nbr_wave_count;      /* ... and the host copy of its wave count */
+  const uint32_t* nbr_waves_split;  /* optional second descriptor table of the schedule ... */
+  int32_t nbr_wave_count_split;     /* ... and its wave count (lane-split channel kernels) */
   const float* upstream2;      /* fused backward: dL/d(second output) */
   float* out2;                 /* fused forward: the second output */
 } sphops_args;
@@ -215,9 +217,14 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
  * (B*N), nbr_order (B*N) receives the particles in that order, nbr_waves
  * (2 words per wave, capacity sphops_neighbor_wave_capacity) one descriptor
  * per 64-lane wave {first slot in nbr_order, group size << 8 | particles in
- * the wave}, wave_count (one device int32) the number of waves. */
+ * the wave}, wave_count (one device int32) the number of waves.  Optionally
+ * (both non-NULL) nbr_waves_split / wave_count_split receive a second table
+ * over the same order with 4, 4, 4, 8, 16, 32, 64, 64 lanes per particle,
+ * used by the kernels that split 16 or 32 channels over four lanes (the
+ * fused blur + gradient_hybrid pass). */
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,
-                             uint32_t* nbr_waves, int32_t* wave_count, void* stream);
+                             uint32_t* nbr_waves, int32_t* wave_count, uint32_t* nbr_waves_split,
+                             int32_t* wave_count_split, void* stream);
 
 /* Number of wave descriptors nbr_waves must hold for this grid (B*N + 8 per tile of 4096). */
 int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid);

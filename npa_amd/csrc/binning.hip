@@ -560,7 +560,8 @@ __global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restri
 // by length class, tiles in order, plus one descriptor per 64-lane wave.
 template <bool CSR>
 void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, const GroupSizes& gs, int32_t* order,
-                    uint2* waves, int32_t* wave_total, hipStream_t st) {
+                    uint2* waves, int32_t* wave_total, hipStream_t st, const GroupSizes* gs2 = nullptr,
+                    uint2* waves2 = nullptr, int32_t* wave_total2 = nullptr) {
   const uint32_t n = (uint32_t)g.n_keys;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
   const uint32_t nseg = (uint32_t)kNumClasses * ntiles;
@@ -577,6 +578,15 @@ void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, co
   device_exclusive_scan(wcnt, wcnt, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total), st);
   hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt, ntiles, n, gs, waves);
   SPHOPS_LAUNCHED();
+  if (waves2 != nullptr) {  // a second descriptor table over the same order, other group sizes
+    uint32_t* wcnt2 = g.hist + 2 * nseg;
+    hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, n,
+                       *gs2, wcnt2);
+    SPHOPS_LAUNCHED();
+    device_exclusive_scan(wcnt2, wcnt2, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total2), st);
+    hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt2, ntiles, n, *gs2, waves2);
+    SPHOPS_LAUNCHED();
+  }
 }
 
 }  // namespace
@@ -584,8 +594,9 @@ void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, co
 uint64_t neighbour_wave_capacity(const Grid& g) { return g.n_keys + (uint64_t)kNumClasses * g.n_tiles; }
 
 void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
-                            hipStream_t st) {
-  tiled_schedule<false>(g, ncnt, kListClasses, kListGroups, order, waves, wave_total, st);
+                            uint2* waves2, int32_t* wave_total2, hipStream_t st) {
+  tiled_schedule<false>(g, ncnt, kListClasses, kListGroups, order, waves, wave_total, st, &kSplitGroups, waves2,
+                        wave_total2);
 }
 
 void run_candidate_schedule(const Grid& g, const int32_t* coff, int32_t* order, uint2* waves, int32_t* wave_total,

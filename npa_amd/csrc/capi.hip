@@ -496,6 +496,8 @@ static OpPtrs from_args(const sphops_args* a) {
   p.order = a->nbr_order;
   p.waves = reinterpret_cast<const uint2*>(a->nbr_waves);
   p.nwaves = (uint32_t)std::max(a->nbr_wave_count, 0);
+  p.waves2 = reinterpret_cast<const uint2*>(a->nbr_waves_split);
+  p.nwaves2 = (uint32_t)std::max(a->nbr_wave_count_split, 0);
   p.g2 = a->upstream2;
   p.out3 = a->out2;
   return p;
@@ -507,7 +509,8 @@ static void check_list(const sphops_args* a) {
   require(a->nbr_order == nullptr || a->nbr_index != nullptr, "nbr_order needs nbr_index");
   require(a->nbr_waves == nullptr || a->nbr_order != nullptr, "nbr_waves needs nbr_order");
   require(a->nbr_order == nullptr || a->nbr_waves != nullptr, "nbr_order needs nbr_waves");
-  require(a->nbr_wave_count >= 0, "negative wave count");
+  require(a->nbr_wave_count >= 0 && a->nbr_wave_count_split >= 0, "negative wave count");
+  require(a->nbr_waves_split == nullptr || a->nbr_waves != nullptr, "nbr_waves_split needs nbr_waves");
 }
 
 int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream) {
@@ -597,19 +600,23 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
 }
 
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,
-                             uint32_t* nbr_waves, int32_t* wave_count, void* stream) {
+                             uint32_t* nbr_waves, int32_t* wave_count, uint32_t* nbr_waves_split,
+                             int32_t* wave_count_split, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
     require(nbr_count != nullptr && wave_count != nullptr &&
                 ((nbr_order != nullptr && nbr_waves != nullptr) || grid->n_keys == 0),
             "null buffer");
     const hipStream_t st = sphops::as_stream(stream);
+    require((nbr_waves_split == nullptr) == (wave_count_split == nullptr),
+            "nbr_waves_split and wave_count_split go together");
     if (grid->n_keys == 0) {
       SPHOPS_HIP(hipMemsetAsync(wave_count, 0, sizeof(int32_t), st));
+      if (wave_count_split) SPHOPS_HIP(hipMemsetAsync(wave_count_split, 0, sizeof(int32_t), st));
       return;
     }
     sphops::run_neighbour_schedule(*grid, nbr_count, nbr_order, reinterpret_cast<uint2*>(nbr_waves), wave_count,
-                                   st);
+                                   reinterpret_cast<uint2*>(nbr_waves_split), wave_count_split, st);
   });
 }
 

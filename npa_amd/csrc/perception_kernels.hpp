@@ -999,6 +999,192 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
   if (active && sub == 0) op.finish(g, a, k);
 }
 
+// ------------------------------------------------ lane-split channel kernels
+//
+// A group of G >= 4 lanes serves one particle as G/4 pair streams x 4 channel
+// slices: lane sub = 4 * stream + slice walks pairs stream, stream + G/4, ...
+// of the particle's list and handles channels [slice*CW, (slice+1)*CW) of
+// C = 4*CW.  The four lanes of a stream read adjacent pieces of each
+// neighbour's rows, so a wave's row loads are contiguous per neighbour, and a
+// lane holds a quarter of the channel state.  The per-pair geometry is
+// evaluated by all four slices.  Channel sums are reduced over the streams
+// (into the group's first four lanes, one per slice); sums over channels
+// (dL/dx, dL/drho) are then reduced over the slices into the first lane.
+
+template <class... A>
+__device__ __forceinline__ void grp_sum_streams(int G, A&... v) {
+  if (G > 4) (grp_add<4>(v), ...);
+  if (G > 8) (grp_add<8>(v), ...);
+  if (G > 16) (grp_add<16>(v), ...);
+  if (G > 32) (grp_add<32>(v), ...);
+}
+
+template <class... A>
+__device__ __forceinline__ void grp_sum_slices(A&... v) {
+  (grp_add<1>(v), ...);
+  (grp_add<2>(v), ...);
+}
+
+// Backward of blur (upstream a.g) + gradient_hybrid (upstream a.g2, the
+// straight-through gradient backward) in one pass: dL/ds of both, and with
+// FULL dL/drho and dL/dx summed over both operators.
+template <int D, bool P, int CW, bool FULL>
+struct OpSplitBlurHybridBwd {
+  static constexpr int kWeightKind = kWVolume;
+  static constexpr int C = 4 * CW;
+  static constexpr int kMinWaves = CW == 4 ? 4 : 2;  // C = 16: 128 VGPRs, four waves per SIMD
+  uint32_t c0 = 0;
+  float vi = 0.0f, mr2 = 0.0f;
+  float si[FULL ? CW : 1], gbi[FULL ? CW : 1];
+  float ggi[CW * D];
+  float dsb[CW] = {}, dsg[CW] = {};
+  float wsum[D] = {};
+  float dxb[D] = {}, dxg[D] = {};
+  float drb = 0.0f, drg = 0.0f;
+  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, int slice) {
+    c0 = (uint32_t)slice * CW;
+    const float mi = a.m[k], ri = a.rho[k];
+    vi = mi / ri;
+    mr2 = mi / (ri * ri);
+    load_span<CW * D, true>(a.g2 + ((uint64_t)k * C + c0) * D, ggi);
+    if constexpr (FULL) {
+      load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
+      load_span<CW, true>(a.g + (uint64_t)k * C + c0, gbi);
+    }
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float vj,
+                       const float* r, float d2, uint32_t j) {
+    float rb[3];
+    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
+    const float W = poly6(g.eps2, db);
+    float d;
+    const float mag = spiky_mag(g.eps, db, &d);
+    float w[D];
+#pragma unroll
+    for (int e = 0; e < D; ++e) {
+      w[e] = mag * rb[e];
+      wsum[e] += vj * w[e];
+    }
+    float gbj[CW], ggj[CW * D];
+    load_span<CW, true>(a.g + (uint64_t)j * C + c0, gbj);
+    load_span<CW * D, true>(a.g2 + ((uint64_t)j * C + c0) * D, ggj);
+    if constexpr (!FULL) {
+#pragma unroll
+      for (int f = 0; f < CW; ++f) {
+        dsb[f] += W * gbj[f];
+        float pf = 0.0f;
+#pragma unroll
+        for (int e = 0; e < D; ++e) pf += ggj[f * D + e] * w[e];
+        dsg[f] += pf;
+      }
+    } else {
+      float sj[CW];
+      load_span<CW, true>(a.s + (uint64_t)j * C + c0, sj);
+      float A = 0.0f, Bv = 0.0f;
+      float u1[D] = {}, u2[D] = {};
+#pragma unroll
+      for (int f = 0; f < CW; ++f) {
+        dsb[f] += W * gbj[f];
+        A += gbi[f] * sj[f];
+        Bv += gbj[f] * si[f];
+        float pf = 0.0f;
+        const float df = si[f] - sj[f];
+#pragma unroll
+        for (int e = 0; e < D; ++e) {
+          pf += ggj[f * D + e] * w[e];
+          u1[e] += df * ggj[f * D + e];
+          u2[e] += df * ggi[f * D + e];
+        }
+        dsg[f] += pf;
+      }
+      drb += W * Bv;
+      if (db != 0.0f && db < g.eps2) {
+        const float t = g.eps2 - db;
+        const float m6 = -6.0f * t * t * (A * vj + Bv * vi);
+#pragma unroll
+        for (int e = 0; e < D; ++e) dxb[e] += m6 * rb[e];
+      }
+      float u[D], uw = 0.0f;
+#pragma unroll
+      for (int e = 0; e < D; ++e) {
+        uw += u1[e] * w[e];
+        u[e] = vi * u1[e] + vj * u2[e];
+      }
+      drg += uw;
+      spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, u, dxg);
+    }
+  }
+  __device__ void reduce(int G) {
+    grp_sum_streams(G, dsb, dsg, wsum, dxb, dxg, drb, drg);
+    if constexpr (FULL) grp_sum_slices(dxb, dxg, drb, drg);
+  }
+  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k, int slice) {
+    const float sb = vi * g.c6;
+#pragma unroll
+    for (int f = 0; f < CW; ++f) {
+      float t = vi * dsg[f];
+#pragma unroll
+      for (int e = 0; e < D; ++e) t += ggi[f * D + e] * wsum[e];
+      a.out1[(uint64_t)k * C + c0 + f] = dsb[f] * sb + t * g.cs;
+    }
+    if constexpr (FULL) {
+      if (slice == 0) {
+        a.out2[k] = -mr2 * (drb * g.c6 + drg * g.cs);
+        float dx[D];
+#pragma unroll
+        for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6 + dxg[e] * g.cs;
+        store_pos_grad<D>(a.out0, k, dx, 1.0f);
+      }
+    }
+  }
+};
+
+template <int D, bool P, class OP>
+__global__ __launch_bounds__(kThreads, OP::kMinWaves) void k_pairs_split(GridParams g, OpPtrs a) {
+  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (wave >= a.nwaves2) return;
+  const uint2 wd = a.waves2[wave];
+  const int G = (int)(wd.y >> 8);
+  const int lane = __lane_id();
+  const uint32_t slot = (uint32_t)(lane / G);
+  const int sub = lane & (G - 1);
+  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
+  const bool active = slot < (wd.y & 0xFFu);
+  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
+  const float4* __restrict__ xw = a.xw;
+  OP op;
+  float xi[3] = {0.0f, 0.0f, 0.0f};
+  if (active) {
+    unpack(xw[k], xi);
+    op.init(g, a, k, slice);
+    const int32_t* __restrict__ nidx = a.nidx;
+    const int start = a.nptr[k];
+    const int end = start + a.ncnt[k];
+    int t = start + stream;
+    for (; t + S < end; t += 2 * S) {
+      const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + S];
+      const float4 p0 = xw[j0], p1 = xw[j1];
+      float x0[3], x1[3], r0[3], r1[3];
+      unpack(p0, x0);
+      unpack(p1, x1);
+      const float d0 = displacement<D, P>(g, xi, x0, r0);
+      const float d1 = displacement<D, P>(g, xi, x1, r1);
+      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+      op.pair(g, a, xi, x1, p1.w, r1, d1, j1);
+    }
+    if (t < end) {
+      const uint32_t j0 = (uint32_t)nidx[t];
+      const float4 p0 = xw[j0];
+      float x0[3], r0[3];
+      unpack(p0, x0);
+      const float d0 = displacement<D, P>(g, xi, x0, r0);
+      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+    }
+  }
+  op.reduce(G);
+  if (active && stream == 0) op.finish(g, a, k, slice);
+}
+
 // ------------------------------------------------- neighbour-list build
 //
 // Candidates of particle k = the concatenation of its stencil ranges.  The
@@ -1171,6 +1357,33 @@ void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Lane-split kernels serve rows of 16 or 32 channels read as 16-byte vectors.
+// Only the pass-B backward uses them: its per-channel work is heavy enough to
+// pay for evaluating the pair geometry in all four slices; the forward is
+// faster with one lane per pair stream.
+inline bool split_ok(const OpPtrs& a) {
+  return a.nidx != nullptr && a.waves2 != nullptr && (a.C == 16 || a.C == 32) && aligned16(a.s) &&
+         aligned16(a.g) && aligned16(a.g2);
+}
+
+template <int D, bool P, template <int, bool, int> class OPT>
+void launch_split(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
+  (void)bo;
+  if (g.n_keys == 0) return;
+  const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
+  if (a.C == 16) {
+    pack_for<D, OPT<D, P, 4>>(g, a, st);
+    if (wgs) hipLaunchKernelGGL((k_pairs_split<D, P, OPT<D, P, 4>>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+  } else {
+    pack_for<D, OPT<D, P, 8>>(g, a, st);
+    if (wgs) hipLaunchKernelGGL((k_pairs_split<D, P, OPT<D, P, 8>>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+  }
+  SPHOPS_LAUNCHED();
+}
+
+template <int D, bool P, int CW> using SplitBwdFull = OpSplitBlurHybridBwd<D, P, CW, true>;
+template <int D, bool P, int CW> using SplitBwdDs = OpSplitBlurHybridBwd<D, P, CW, false>;
+
 // Pick the register-channel configuration for C.
 template <int D, bool P, template <int, bool, int, bool> class OPT>
 void launch_channels(const Grid& g, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
@@ -1229,6 +1442,10 @@ void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const
       return launch_channels<D, P, GradientBwdDs>(g, bo, a, st);
     case Op::DensityPair: return launch_pairs<D, P, OpDensityPairBwd<D, P>>(g, bo, a, st);
     case Op::BlurGradientHybrid: {
+      if (split_ok(a)) {
+        if (full) return launch_split<D, P, SplitBwdFull>(g, bo, a, st);
+        return launch_split<D, P, SplitBwdDs>(g, bo, a, st);
+      }
       // blur's backward stores, the gradient's backward (upstream2) adds
       OpPtrs b = a;
       b.g2 = nullptr;

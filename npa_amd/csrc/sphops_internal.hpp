@@ -101,6 +101,8 @@ struct OpPtrs {
   const int32_t* order = nullptr; // particles in schedule order (optional, list traversal)
   const uint2* waves = nullptr;   // per-wave descriptors {first slot in order, group size << 8 | particles}
   uint32_t nwaves = 0;
+  const uint2* waves2 = nullptr;  // descriptors for lane-split channel kernels (group sizes kSplitGroups)
+  uint32_t nwaves2 = 0;
   uint32_t C = 0;
   float tol = 1e-3f;
 };
@@ -113,7 +115,7 @@ void run_backward(const Grid& g, Op op, bool full, const int32_t* bin_offsets, c
 // by neighbour-list length class (kListClasses / kListGroups), tiles in
 // order; one descriptor per wave {first slot in order, group size << 8 | particles}.
 void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
-                            hipStream_t st);
+                            uint2* waves2, int32_t* wave_total2, hipStream_t st);
 // upper bound of the number of waves a schedule can hold
 uint64_t neighbour_wave_capacity(const Grid& g);
 // Candidate-scan schedule: as the pair-kernel schedule, classes by stencil
@@ -136,6 +138,9 @@ struct GroupSizes {
 // pair lists: about 6-12 pairs per lane
 constexpr ClassBounds kListClasses{{6, 12, 24, 48, 96, 192, 384}};
 constexpr GroupSizes kListGroups{{1, 1, 2, 4, 8, 16, 32, 64}};
+// lane-split channel kernels: four lanes (channel slices) per pair stream,
+// 1, 1, 1, 2, 4, 8, 16, 16 streams per particle (about 12-24 pairs each)
+constexpr GroupSizes kSplitGroups{{4, 4, 4, 8, 16, 32, 64, 64}};
 // stencil candidates: 32-64 candidates per lane, at most 16 lanes per particle
 constexpr ClassBounds kScanClasses{{64, 128, 256, 512, 1024, 2048, 4096}};
 constexpr GroupSizes kScanGroups{{1, 1, 2, 4, 8, 16, 16, 16}};

@@ -340,7 +340,8 @@ class _HashGridNative:
     def neighbor_list(self, x_bin, bin_offsets):
         """In-radius neighbour list of the binned particles plus its
         traversal schedule: ``(start (B*N+1,), count (B*N,), index, order
-        (B*N,), waves (2 words per wave), wave_count (host int))``.  Row i is
+        (B*N,), waves (2 words per wave), wave_count (host int), waves_split,
+        wave_count_split)``.  Row i is
         ``index[start[i] : start[i] + count[i]]``; rows start at the scanned
         stencil candidate counts, so ``index`` needs ``start[B*N]`` entries.
         The index buffer is sized from the previous call's total and the
@@ -354,8 +355,10 @@ class _HashGridNative:
         start = torch.empty(n + 1, dtype=_I32, device=dev)
         count = torch.empty(max(n, 1), dtype=_I32, device=dev)
         order = torch.empty(max(n, 1), dtype=_I32, device=dev)
-        waves = torch.empty(2 * max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 1), dtype=_I32, device=dev)
-        small = torch.empty(2, dtype=_I32, device=dev)
+        wcap = 2 * max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 1)
+        waves = torch.empty(wcap, dtype=_I32, device=dev)
+        waves2 = torch.empty(wcap, dtype=_I32, device=dev)
+        small = torch.empty(3, dtype=_I32, device=dev)
         _check(_lib.sphops_neighbor_candidates(self._h, x, bo, ctypes.c_void_p(start.data_ptr()), st))
         prev = getattr(self, "_index_capacity", 0)
         cap = prev if prev else int(start[n].item())
@@ -369,16 +372,17 @@ class _HashGridNative:
         fill(index, cap)
         _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
                                              ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
-                                             ctypes.c_void_p(small.data_ptr() + 4), st))
+                                             ctypes.c_void_p(small.data_ptr() + 4), ctypes.c_void_p(waves2.data_ptr()),
+                                             ctypes.c_void_p(small.data_ptr() + 8), st))
         small[0:1].copy_(start[n:n + 1])
-        total, nwaves = small.cpu().tolist()
+        total, nwaves, nwaves2 = small.cpu().tolist()
         if total > cap:
             cap = total
             index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
             fill(index, cap)
         if total > prev:  # ~12% headroom, so that the next snapshot of a moving cloud fits
             self._index_capacity = total + total // 8
-        return start, count, index, order, waves, nwaves
+        return start, count, index, order, waves, nwaves, waves2, nwaves2
 
     # Per operator: trailing dims of (first output, second output) after (B, N);
     # "C" stands for the channel count, "D" for the spatial dimension.
@@ -431,6 +435,8 @@ class _HashGridNative:
             a.nbr_start, a.nbr_count, a.nbr_index = nbr[0].data_ptr(), nbr[1].data_ptr(), nbr[2].data_ptr()
             if len(nbr) > 3:
                 a.nbr_order, a.nbr_waves, a.nbr_wave_count = nbr[3].data_ptr(), nbr[4].data_ptr(), nbr[5]
+            if len(nbr) > 6:
+                a.nbr_waves_split, a.nbr_wave_count_split = nbr[6].data_ptr(), nbr[7]
         return a
 
     def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None):
