@@ -70,21 +70,23 @@ def per_particle_bytes(C, D, P):
     }
 
 
-# single pair kernels the timed step launches (with pass fusion), per variant;
-# the pass-B backward is blur's backward followed by the gradient's backward
-# (which adds into blur's outputs)
+# pair kernels the timed step launches (with pass fusion), one launch each,
+# per variant
 STEP_KERNELS = {
-    "full": ("pass_a_fwd", "pass_b_fwd", "pass_a_bwd", "blur_bwd", "gradient_bwd"),
-    "npa": ("density_fwd", "pass_b_fwd", "blur_bwd", "gradient_bwd"),
+    "full": ("pass_a_fwd", "pass_b_fwd", "pass_a_bwd", "pass_b_bwd"),
+    "npa": ("density_fwd", "pass_b_fwd", "pass_b_bwd_ds"),
 }
+DOMINANT = {"full": "pass_b_bwd", "npa": "pass_b_bwd_ds"}
 
-# rocprofv3 kernel-name fragment of each timed call's pair kernel
+# rocprofv3 kernel-name fragment of each timed call's pair kernel (cfg5: 3D, clamped, C = 16)
 PAIR_KERNEL = {
     "gradient_bwd": "OpGradientBwd<3, false, 16, true, true, false>",
     "blur_bwd": "OpBlurBwd<3, false, 16, true, true>",
     "pass_b_fwd": "OpBlurGradientHybrid<3, false, 16, true>",
     "pass_a_fwd": "OpDensityPair<3, false>",
     "pass_a_bwd": "OpDensityPairBwd<3, false>",
+    "pass_b_bwd": "OpSplitBlurHybridBwd<3, false, 4, true>",
+    "pass_b_bwd_ds": "OpSplitBlurHybridBwd<3, false, 4, false>",
 }
 COPY_BYTES = 256 << 20
 
@@ -111,7 +113,7 @@ def main():
     # counter runs first, in child processes, before this process touches the GPU
     pmc = None
     if not args.no_traffic:
-        pmc = measure_traffic(args, "gradient_bwd")
+        pmc = measure_traffic(args, DOMINANT[args.variant])
     import numpy as np
     import torch
 

@@ -32,6 +32,13 @@ def _cases():
         cs.append(H.random_case(f"chan{C}", 2, 300, C, 2, 12, 0.15, False, "grid", maxp=16, sigma=0.9))
     cs.append(H.random_case("chan32-3d", 1, 500, 32, 3, 10, 0.2, True, "grid"))
     cs.append(H.random_case("randn-2d", 2, 512, 16, 2, 16, 0.1, False, "grid", uniform=False, sigma=0.4))
+    # clusters with cells of several hundred particles (the per-cell list fill)
+    cs.append(H.random_case("dense3d", 1, 1200, 4, 3, 8, 0.25, False, "grid", uniform=False, sigma=0.07))
+    cs.append(H.random_case("dense3d-particle", 1, 1200, 4, 3, 8, 0.25, False, "particle", uniform=False,
+                            sigma=0.07))
+    d = H.random_case("dense2d-per", 1, 1000, 16, 2, 8, 0.125, True, "grid", uniform=False, sigma=0.05)
+    d.x[..., :2] += 0.5  # the cluster straddles the periodic boundary
+    cs.append(d)
     return cs
 
 
