@@ -85,8 +85,8 @@ PAIR_KERNEL = {
     "pass_b_fwd": "OpBlurGradientHybrid<3, false, 16, true>",
     "pass_a_fwd": "OpDensityPair<3, false>",
     "pass_a_bwd": "OpDensityPairBwd<3, false>",
-    "pass_b_bwd": "OpSplitBlurHybridBwd<3, false, 4, true>",
-    "pass_b_bwd_ds": "OpSplitBlurHybridBwd<3, false, 4, false>",
+    "pass_b_bwd": "k_blur_hybrid_bwd_quad<3, false, 4, true>",
+    "pass_b_bwd_ds": "k_blur_hybrid_bwd_quad<3, false, 4, false>",
 }
 COPY_BYTES = 256 << 20
 

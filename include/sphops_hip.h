@@ -219,7 +219,7 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
  * per 64-lane wave {first slot in nbr_order, group size << 8 | particles in
  * the wave}, wave_count (one device int32) the number of waves.  Optionally
  * (both non-NULL) nbr_waves_split / wave_count_split receive a second table
- * over the same order with 4, 4, 4, 8, 16, 32, 64, 64 lanes per particle,
+ * over the same order with 4, 4, 4, 4, 16, 32, 64, 64 lanes per particle,
  * used by the kernels that split 16 or 32 channels over four lanes (the
  * fused blur + gradient_hybrid pass). */
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,

@@ -1002,14 +1002,17 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
 // ------------------------------------------------ lane-split channel kernels
 //
 // A group of G >= 4 lanes serves one particle as G/4 pair streams x 4 channel
-// slices: lane sub = 4 * stream + slice walks pairs stream, stream + G/4, ...
-// of the particle's list and handles channels [slice*CW, (slice+1)*CW) of
-// C = 4*CW.  The four lanes of a stream read adjacent pieces of each
-// neighbour's rows, so a wave's row loads are contiguous per neighbour, and a
-// lane holds a quarter of the channel state.  The per-pair geometry is
-// evaluated by all four slices.  Channel sums are reduced over the streams
-// (into the group's first four lanes, one per slice); sums over channels
-// (dL/dx, dL/drho) are then reduced over the slices into the first lane.
+// slices: lane sub = 4 * stream + slice walks the stream's pairs and handles
+// channels [slice*CW, (slice+1)*CW) of C = 4*CW.  The four lanes of a stream
+// read adjacent pieces of each neighbour's rows, so a wave's row loads are
+// contiguous per neighbour, and a lane holds a quarter of the channel state.
+// Channel sums are reduced over the streams (into the group's first four
+// lanes, one per slice); sums over channels (dL/dx, dL/drho) over the whole
+// group into its first lane.
+
+struct VolumeWeights {  // packing of (x, m / rho) for the kernels below
+  static constexpr int kWeightKind = kWVolume;
+};
 
 template <class... A>
 __device__ __forceinline__ void grp_sum_streams(int G, A&... v) {
@@ -1019,30 +1022,49 @@ __device__ __forceinline__ void grp_sum_streams(int G, A&... v) {
   if (G > 32) (grp_add<32>(v), ...);
 }
 
-template <class... A>
-__device__ __forceinline__ void grp_sum_slices(A&... v) {
-  (grp_add<1>(v), ...);
-  (grp_add<2>(v), ...);
+// Pass-B backward (blur with upstream a.g + gradient_hybrid with upstream
+// a.g2, the straight-through gradient backward) in one pass on the lane-split
+// layout; with FULL also dL/drho and dL/dx, summed over both operators.  The
+// four slice lanes of a stream take the stream's pairs four at a time: lane q evaluates the geometry of the q-th pair (index, weight, W,
+// grad W, the Jacobian coefficients) and the quad exchanges it by DPP
+// quad_perm broadcasts, so each pair's geometry is evaluated once instead of
+// in all four slices.  Terms summed over channels (dL/dx, dL/drho) stay
+// per-lane partial sums over the lane's slice, reduced at the end; sum_j v_j
+// grad W is accumulated by the owning lane only.
+template <int Q>
+__device__ __forceinline__ float quad_get(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), Q * 0x55, 0xF, 0xF, false));
+}
+template <int Q>
+__device__ __forceinline__ uint32_t quad_get(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, Q * 0x55, 0xF, 0xF, false);
 }
 
-// Backward of blur (upstream a.g) + gradient_hybrid (upstream a.g2, the
-// straight-through gradient backward) in one pass: dL/ds of both, and with
-// FULL dL/drho and dL/dx summed over both operators.
 template <int D, bool P, int CW, bool FULL>
-struct OpSplitBlurHybridBwd {
-  static constexpr int kWeightKind = kWVolume;
-  static constexpr int C = 4 * CW;
-  static constexpr int kMinWaves = CW == 4 ? 4 : 2;  // C = 16: 128 VGPRs, four waves per SIMD
-  uint32_t c0 = 0;
+__global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_quad(GridParams g, OpPtrs a) {
+  constexpr int C = 4 * CW;
+  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (wave >= a.nwaves2) return;
+  const uint2 wd = a.waves2[wave];
+  const int G = (int)(wd.y >> 8);
+  const int lane = __lane_id();
+  const uint32_t slot = (uint32_t)(lane / G);
+  const int sub = lane & (G - 1);
+  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
+  const bool active = slot < (wd.y & 0xFFu);
+  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
+  const uint32_t c0 = (uint32_t)slice * CW;
+  const float4* __restrict__ xw = a.xw;
+  float xi[3] = {0.0f, 0.0f, 0.0f};
   float vi = 0.0f, mr2 = 0.0f;
-  float si[FULL ? CW : 1], gbi[FULL ? CW : 1];
-  float ggi[CW * D];
+  float si[FULL ? CW : 1] = {}, gbi[FULL ? CW : 1] = {};
+  float ggi[CW * D] = {};
   float dsb[CW] = {}, dsg[CW] = {};
   float wsum[D] = {};
   float dxb[D] = {}, dxg[D] = {};
   float drb = 0.0f, drg = 0.0f;
-  __device__ void init(const GridParams&, const OpPtrs& a, uint32_t k, int slice) {
-    c0 = (uint32_t)slice * CW;
+  if (active) {
+    unpack(xw[k], xi);
     const float mi = a.m[k], ri = a.rho[k];
     vi = mi / ri;
     mr2 = mi / (ri * ri);
@@ -1051,74 +1073,115 @@ struct OpSplitBlurHybridBwd {
       load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
       load_span<CW, true>(a.g + (uint64_t)k * C + c0, gbi);
     }
-  }
-  __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float vj,
-                       const float* r, float d2, uint32_t j) {
-    float rb[3];
-    const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
-    const float W = poly6(g.eps2, db);
-    float d;
-    const float mag = spiky_mag(g.eps, db, &d);
-    float w[D];
-#pragma unroll
-    for (int e = 0; e < D; ++e) {
-      w[e] = mag * rb[e];
-      wsum[e] += vj * w[e];
-    }
-    float gbj[CW], ggj[CW * D];
-    load_span<CW, true>(a.g + (uint64_t)j * C + c0, gbj);
-    load_span<CW * D, true>(a.g2 + ((uint64_t)j * C + c0) * D, ggj);
-    if constexpr (!FULL) {
-#pragma unroll
-      for (int f = 0; f < CW; ++f) {
-        dsb[f] += W * gbj[f];
-        float pf = 0.0f;
-#pragma unroll
-        for (int e = 0; e < D; ++e) pf += ggj[f * D + e] * w[e];
-        dsg[f] += pf;
-      }
-    } else {
-      float sj[CW];
-      load_span<CW, true>(a.s + (uint64_t)j * C + c0, sj);
-      float A = 0.0f, Bv = 0.0f;
-      float u1[D] = {}, u2[D] = {};
-#pragma unroll
-      for (int f = 0; f < CW; ++f) {
-        dsb[f] += W * gbj[f];
-        A += gbi[f] * sj[f];
-        Bv += gbj[f] * si[f];
-        float pf = 0.0f;
-        const float df = si[f] - sj[f];
+    const int32_t* __restrict__ nidx = a.nidx;
+    const int start = a.nptr[k];
+    const int end = start + a.ncnt[k];
+    for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
+      // geometry of the pair this lane owns
+      const int to = t0 + slice * S;
+      uint32_t jo = 0u;
+      float vo = 0.0f, Wo = 0.0f, t2o = 0.0f, jao = 0.0f, jbo = 0.0f;
+      float rbo[3] = {0.0f, 0.0f, 0.0f}, wo[3] = {0.0f, 0.0f, 0.0f};
+      if (to < end) {
+        jo = (uint32_t)nidx[to];
+        const float4 pj = xw[jo];
+        float xj[3], r[3];
+        unpack(pj, xj);
+        vo = pj.w;
+        const float d2 = displacement<D, P>(g, xi, xj, r);
+        const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
+        Wo = poly6(g.eps2, db);
+        float d;
+        const float mag = spiky_mag(g.eps, db, &d);
 #pragma unroll
         for (int e = 0; e < D; ++e) {
-          pf += ggj[f * D + e] * w[e];
-          u1[e] += df * ggj[f * D + e];
-          u2[e] += df * ggi[f * D + e];
+          wo[e] = mag * rbo[e];
+          wsum[e] += vo * wo[e];
         }
-        dsg[f] += pf;
+        if (db != 0.0f && db < g.eps2) {
+          const float tt = g.eps2 - db;
+          t2o = tt * tt;
+          const float di = fast_rcp(d);
+          jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
+          jbo = 3.0f * (g.eps2 - db) * di * di * di;
+        }
       }
-      drb += W * Bv;
-      if (db != 0.0f && db < g.eps2) {
-        const float t = g.eps2 - db;
-        const float m6 = -6.0f * t * t * (A * vj + Bv * vi);
 #pragma unroll
-        for (int e = 0; e < D; ++e) dxb[e] += m6 * rb[e];
-      }
-      float u[D], uw = 0.0f;
+      for (int q = 0; q < 4; ++q) {
+        if (t0 + q * S >= end) break;  // uniform over the quad
+        uint32_t j;
+        float vj, W, t2, ja, jb, rb[3], w[3];
+#define SPHOPS_QUAD_FETCH(QQ)                                                   \
+  j = quad_get<QQ>(jo);                                                         \
+  vj = quad_get<QQ>(vo);                                                        \
+  W = quad_get<QQ>(Wo);                                                         \
+  t2 = quad_get<QQ>(t2o);                                                       \
+  ja = quad_get<QQ>(jao);                                                       \
+  jb = quad_get<QQ>(jbo);                                                       \
+  for (int e = 0; e < D; ++e) {                                                 \
+    rb[e] = quad_get<QQ>(rbo[e]);                                               \
+    w[e] = quad_get<QQ>(wo[e]);                                                 \
+  }
+        if (q == 0) { SPHOPS_QUAD_FETCH(0) }
+        else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
+        else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
+        else { SPHOPS_QUAD_FETCH(3) }
+#undef SPHOPS_QUAD_FETCH
+        float gbj[CW], ggj[CW * D];
+        load_span<CW, true>(a.g + (uint64_t)j * C + c0, gbj);
+        load_span<CW * D, true>(a.g2 + ((uint64_t)j * C + c0) * D, ggj);
+        if constexpr (!FULL) {
 #pragma unroll
-      for (int e = 0; e < D; ++e) {
-        uw += u1[e] * w[e];
-        u[e] = vi * u1[e] + vj * u2[e];
+          for (int f = 0; f < CW; ++f) {
+            dsb[f] += W * gbj[f];
+            float pf = 0.0f;
+#pragma unroll
+            for (int e = 0; e < D; ++e) pf += ggj[f * D + e] * w[e];
+            dsg[f] += pf;
+          }
+        } else {
+          float sj[CW];
+          load_span<CW, true>(a.s + (uint64_t)j * C + c0, sj);
+          float A = 0.0f, Bv = 0.0f;
+          float u1[D] = {}, u2[D] = {};
+#pragma unroll
+          for (int f = 0; f < CW; ++f) {
+            dsb[f] += W * gbj[f];
+            A += gbi[f] * sj[f];
+            Bv += gbj[f] * si[f];
+            float pf = 0.0f;
+            const float df = si[f] - sj[f];
+#pragma unroll
+            for (int e = 0; e < D; ++e) {
+              pf += ggj[f * D + e] * w[e];
+              u1[e] += df * ggj[f * D + e];
+              u2[e] += df * ggi[f * D + e];
+            }
+            dsg[f] += pf;
+          }
+          drb += W * Bv;
+          const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
+          float u[D], uw = 0.0f, rv = 0.0f;
+#pragma unroll
+          for (int e = 0; e < D; ++e) {
+            dxb[e] += m6 * rb[e];
+            uw += u1[e] * w[e];
+            u[e] = vi * u1[e] + vj * u2[e];
+            rv += rb[e] * u[e];
+          }
+          drg += uw;
+#pragma unroll
+          for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
+        }
       }
-      drg += uw;
-      spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, u, dxg);
     }
   }
-  __device__ void reduce(int G) {
-    grp_sum_streams(G, dsb, dsg, wsum, dxb, dxg, drb, drg);
-    if constexpr (FULL) grp_sum_slices(dxb, dxg, drb, drg);
-  }
-  __device__ void finish(const GridParams& g, const OpPtrs& a, uint32_t k, int slice) {
+  grp_sum_streams(G, dsb, dsg);
+  grp_sum(G, wsum);
+  if constexpr (FULL) grp_sum(G, dxb, dxg, drb, drg);
+#pragma unroll
+  for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
+  if (active && stream == 0) {
     const float sb = vi * g.c6;
 #pragma unroll
     for (int f = 0; f < CW; ++f) {
@@ -1137,52 +1200,6 @@ struct OpSplitBlurHybridBwd {
       }
     }
   }
-};
-
-template <int D, bool P, class OP>
-__global__ __launch_bounds__(kThreads, OP::kMinWaves) void k_pairs_split(GridParams g, OpPtrs a) {
-  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (wave >= a.nwaves2) return;
-  const uint2 wd = a.waves2[wave];
-  const int G = (int)(wd.y >> 8);
-  const int lane = __lane_id();
-  const uint32_t slot = (uint32_t)(lane / G);
-  const int sub = lane & (G - 1);
-  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
-  const bool active = slot < (wd.y & 0xFFu);
-  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
-  const float4* __restrict__ xw = a.xw;
-  OP op;
-  float xi[3] = {0.0f, 0.0f, 0.0f};
-  if (active) {
-    unpack(xw[k], xi);
-    op.init(g, a, k, slice);
-    const int32_t* __restrict__ nidx = a.nidx;
-    const int start = a.nptr[k];
-    const int end = start + a.ncnt[k];
-    int t = start + stream;
-    for (; t + S < end; t += 2 * S) {
-      const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + S];
-      const float4 p0 = xw[j0], p1 = xw[j1];
-      float x0[3], x1[3], r0[3], r1[3];
-      unpack(p0, x0);
-      unpack(p1, x1);
-      const float d0 = displacement<D, P>(g, xi, x0, r0);
-      const float d1 = displacement<D, P>(g, xi, x1, r1);
-      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
-      op.pair(g, a, xi, x1, p1.w, r1, d1, j1);
-    }
-    if (t < end) {
-      const uint32_t j0 = (uint32_t)nidx[t];
-      const float4 p0 = xw[j0];
-      float x0[3], r0[3];
-      unpack(p0, x0);
-      const float d0 = displacement<D, P>(g, xi, x0, r0);
-      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
-    }
-  }
-  op.reduce(G);
-  if (active && stream == 0) op.finish(g, a, k, slice);
 }
 
 // ------------------------------------------------- neighbour-list build
@@ -1358,31 +1375,26 @@ void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Lane-split kernels serve rows of 16 or 32 channels read as 16-byte vectors.
-// Only the pass-B backward uses them: its per-channel work is heavy enough to
-// pay for evaluating the pair geometry in all four slices; the forward is
-// faster with one lane per pair stream.
+// Only the pass-B backward uses them; the forward is faster with one lane per
+// pair stream.
 inline bool split_ok(const OpPtrs& a) {
   return a.nidx != nullptr && a.waves2 != nullptr && (a.C == 16 || a.C == 32) && aligned16(a.s) &&
          aligned16(a.g) && aligned16(a.g2);
 }
 
-template <int D, bool P, template <int, bool, int> class OPT>
-void launch_split(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
-  (void)bo;
+template <int D, bool P, bool FULL>
+void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
   const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
+  pack_for<D, VolumeWeights>(g, a, st);
+  if (wgs == 0) return;
   if (a.C == 16) {
-    pack_for<D, OPT<D, P, 4>>(g, a, st);
-    if (wgs) hipLaunchKernelGGL((k_pairs_split<D, P, OPT<D, P, 4>>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 4, FULL>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else {
-    pack_for<D, OPT<D, P, 8>>(g, a, st);
-    if (wgs) hipLaunchKernelGGL((k_pairs_split<D, P, OPT<D, P, 8>>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   }
   SPHOPS_LAUNCHED();
 }
-
-template <int D, bool P, int CW> using SplitBwdFull = OpSplitBlurHybridBwd<D, P, CW, true>;
-template <int D, bool P, int CW> using SplitBwdDs = OpSplitBlurHybridBwd<D, P, CW, false>;
 
 // Pick the register-channel configuration for C.
 template <int D, bool P, template <int, bool, int, bool> class OPT>
@@ -1443,8 +1455,8 @@ void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const
     case Op::DensityPair: return launch_pairs<D, P, OpDensityPairBwd<D, P>>(g, bo, a, st);
     case Op::BlurGradientHybrid: {
       if (split_ok(a)) {
-        if (full) return launch_split<D, P, SplitBwdFull>(g, bo, a, st);
-        return launch_split<D, P, SplitBwdDs>(g, bo, a, st);
+        if (full) return launch_blur_hybrid_bwd_quad<D, P, true>(g, a, st);
+        return launch_blur_hybrid_bwd_quad<D, P, false>(g, a, st);
       }
       // blur's backward stores, the gradient's backward (upstream2) adds
       OpPtrs b = a;

@@ -139,8 +139,8 @@ struct GroupSizes {
 constexpr ClassBounds kListClasses{{6, 12, 24, 48, 96, 192, 384}};
 constexpr GroupSizes kListGroups{{1, 1, 2, 4, 8, 16, 32, 64}};
 // lane-split channel kernels: four lanes (channel slices) per pair stream,
-// 1, 1, 1, 2, 4, 8, 16, 16 streams per particle (about 12-24 pairs each)
-constexpr GroupSizes kSplitGroups{{4, 4, 4, 8, 16, 32, 64, 64}};
+// 1, 1, 1, 1, 4, 8, 16, 16 streams per particle (about 12-48 pairs each)
+constexpr GroupSizes kSplitGroups{{4, 4, 4, 4, 16, 32, 64, 64}};
 // stencil candidates: 32-64 candidates per lane, at most 16 lanes per particle
 constexpr ClassBounds kScanClasses{{64, 128, 256, 512, 1024, 2048, 4096}};
 constexpr GroupSizes kScanGroups{{1, 1, 2, 4, 8, 16, 16, 16}};
