@@ -1202,6 +1202,112 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
   }
 }
 
+// Pass-B forward (blur + gradient_hybrid) on the lane-split layout with the
+// pair geometry shared per quad, as k_blur_hybrid_bwd_quad: lane q of a quad
+// evaluates the q-th of four pairs (index, volume-weighted W and spiky
+// magnitude, r), the quad exchanges them by DPP, and every lane accumulates
+// its channel slice.  The moment matrix is accumulated by the owning lane,
+// reduced over the group and handed to the four slice lanes.
+template <int D, bool P, int CW>
+__global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
+  constexpr int C = 4 * CW;
+  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (wave >= a.nwaves2) return;
+  const uint2 wd = a.waves2[wave];
+  const int G = (int)(wd.y >> 8);
+  const int lane = __lane_id();
+  const uint32_t slot = (uint32_t)(lane / G);
+  const int sub = lane & (G - 1);
+  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
+  const bool active = slot < (wd.y & 0xFFu);
+  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
+  const uint32_t c0 = (uint32_t)slice * CW;
+  const float4* __restrict__ xw = a.xw;
+  float xi[3] = {0.0f, 0.0f, 0.0f};
+  float si[CW] = {};
+  float blur[CW] = {};
+  float acc[CW * D] = {};
+  float M[D * D] = {};
+  if (active) {
+    unpack(xw[k], xi);
+    load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
+    const int32_t* __restrict__ nidx = a.nidx;
+    const int start = a.nptr[k];
+    const int end = start + a.ncnt[k];
+    for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
+      const int to = t0 + slice * S;
+      uint32_t jo = 0u;
+      float wo = 0.0f, to_ = 0.0f, ro[3] = {0.0f, 0.0f, 0.0f};
+      if (to < end) {
+        jo = (uint32_t)nidx[to];
+        const float4 pj = xw[jo];
+        float xj[3];
+        unpack(pj, xj);
+        const float d2 = displacement<D, P>(g, xi, xj, ro);
+        wo = poly6(g.eps2, d2) * pj.w;
+        float d;
+        to_ = spiky_mag(g.eps, d2, &d) * pj.w;
+#pragma unroll
+        for (int p = 0; p < D; ++p)
+#pragma unroll
+          for (int q = p; q < D; ++q) M[p * D + q] += to_ * ro[p] * ro[q];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (t0 + q * S >= end) break;  // uniform over the quad
+        uint32_t j;
+        float w, t, r[3];
+#define SPHOPS_QUAD_FETCH(QQ)             \
+  j = quad_get<QQ>(jo);                   \
+  w = quad_get<QQ>(wo);                   \
+  t = quad_get<QQ>(to_);                  \
+  for (int e = 0; e < D; ++e) r[e] = quad_get<QQ>(ro[e]);
+        if (q == 0) { SPHOPS_QUAD_FETCH(0) }
+        else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
+        else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
+        else { SPHOPS_QUAD_FETCH(3) }
+#undef SPHOPS_QUAD_FETCH
+        float sj[CW];
+        load_span<CW, true>(a.s + (uint64_t)j * C + c0, sj);
+#pragma unroll
+        for (int f = 0; f < CW; ++f) {
+          blur[f] += w * sj[f];
+          const float qf = t * (sj[f] - si[f]);
+#pragma unroll
+          for (int e = 0; e < D; ++e) acc[f * D + e] += qf * r[e];
+        }
+      }
+    }
+  }
+  grp_sum_streams(G, blur, acc);
+  grp_sum(G, M);
+#pragma unroll
+  for (int q = 0; q < D * D; ++q) M[q] = quad_get<0>(M[q]);  // the group total, to the four slice lanes
+  if (active && stream == 0) {
+#pragma unroll
+    for (int f = 0; f < CW; ++f) a.out0[(uint64_t)k * C + c0 + f] = blur[f] * g.c6;
+    float Ms[D * D], L[D * D];
+#pragma unroll
+    for (int p = 0; p < D; ++p)
+#pragma unroll
+      for (int q = 0; q < D; ++q) Ms[p * D + q] = (q >= p ? M[p * D + q] : M[q * D + p]) * g.cs;
+    safe_inv_sym<D>(Ms, a.tol, L);
+#pragma unroll
+    for (int f = 0; f < CW; ++f) {
+      float raw[D];
+#pragma unroll
+      for (int e = 0; e < D; ++e) raw[e] = acc[f * D + e] * g.cs;
+#pragma unroll
+      for (int e = 0; e < D; ++e) {
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < D; ++q) o += raw[q] * L[q * D + e];
+        a.out3[((uint64_t)k * C + c0 + f) * D + e] = o;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------- neighbour-list build
 //
 // Candidates of particle k = the concatenation of its stencil ranges.  The
@@ -1374,12 +1480,25 @@ void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Lane-split kernels serve rows of 16 or 32 channels read as 16-byte vectors.
-// Only the pass-B backward uses them; the forward is faster with one lane per
-// pair stream.
+// Lane-split kernels serve rows of 16 or 32 channels read as 16-byte vectors
+// (the fused pass B, forward and backward).
 inline bool split_ok(const OpPtrs& a) {
   return a.nidx != nullptr && a.waves2 != nullptr && (a.C == 16 || a.C == 32) && aligned16(a.s) &&
          aligned16(a.g) && aligned16(a.g2);
+}
+
+template <int D, bool P>
+void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
+  if (g.n_keys == 0) return;
+  const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
+  pack_for<D, VolumeWeights>(g, a, st);
+  if (wgs == 0) return;
+  if (a.C == 16) {
+    hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 4>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+  } else {
+    hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 8>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+  }
+  SPHOPS_LAUNCHED();
 }
 
 template <int D, bool P, bool FULL>
@@ -1428,7 +1547,9 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
     case Op::Gradient: return launch_channels<D, P, OpGradient>(g, bo, a, st);
     case Op::GradientHybrid: return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
     case Op::DensityPair: return launch_pairs<D, P, OpDensityPair<D, P>>(g, bo, a, st);
-    case Op::BlurGradientHybrid: return launch_channels<D, P, OpBlurGradientHybrid>(g, bo, a, st);
+    case Op::BlurGradientHybrid:
+      if (split_ok(a)) return launch_blur_hybrid_fwd_quad<D, P>(g, a, st);
+      return launch_channels<D, P, OpBlurGradientHybrid>(g, bo, a, st);
     case Op::NeighbourCandidates:
       if (g.n_keys) neighbour_candidates<D, P>(g, bo, a.x, a.iout, st);
       return;

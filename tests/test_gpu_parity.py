@@ -302,7 +302,8 @@ def test_fused_passes(name):
 def test_perceive_fusion(name):
     """NPA.perceive's call sequence (models/npa.py:87-126) twice on one grid:
     the first step runs single operators, the grid then fuses both passes;
-    values and gradients of the two steps agree to fp32 rounding."""
+    values and gradients of the two steps agree to fp32 rounding, and
+    gradient_hybrid of both steps matches the oracle."""
     import npa_amd.sphops as sp
     c = CASES[name]
     print(f"[case] perceive-fusion {name}", flush=True)
@@ -334,10 +335,25 @@ def test_perceive_fusion(name):
             assert kinds[1]["kind"] == "fused" and all(kinds[1]["taken"])
     a, b = steps
     for k in a:
+        if k == "hyb":
+            continue  # ill-conditioned where M is near-singular: checked against the oracle below
         rms = np.sqrt(np.mean(a[k].astype(np.float64) ** 2)) + 1e-30
         err = np.abs(a[k].astype(np.float64) - b[k])
         bound = 1e-5 * (np.abs(a[k]) + np.abs(b[k])) + 1e-5 * rms
         assert np.all(err <= bound), f"{name}:{k} max err {err.max():.3e}"
+    # gradient_hybrid of both steps (unit masses here) against the oracle, with
+    # the first-order error bound through the safe inverse
+    _, res, ora = run(name)
+    ctx, q = ora["ctx"], ora["q"]
+    D = c.dim
+    mf = np.ones(c.B * c.N)
+    for step, st in enumerate(steps):
+        rf = st["rho"].reshape(-1).astype(np.float64)
+        out, raw, raw_mag, M, M_mag, L, det = sph.gradient_hybrid(ctx, mf, rf, res["sb"].reshape(-1, c.C).astype(
+            np.float64), 1e-3)
+        amb = np.abs(np.abs(det) - 1e-3) < 1e-6
+        H.assert_close(f"{name}:step{step}:hyb", _flat(st["hyb"], q), out, H.hybrid_bound(raw, raw_mag, M_mag, L),
+                       skip=amb)
 
 
 MIRROR_CASES = [n for n in NAMES if n.startswith(("ref2d", "ref3d", "chan12", "chan33", "cfg2", "cfg5"))]
