@@ -447,6 +447,7 @@ __device__ __forceinline__ int32_t item_length(const int32_t* __restrict__ src, 
 
 // Per tile of kTile items: the number of items of each class, written to
 // cnt[tile * kNumClasses + class].
+// Items of negative length are skipped: they get no class and no slot.
 template <bool CSR>
 __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restrict__ src, uint32_t n,
                                                           ClassBounds cb, uint32_t* __restrict__ cnt) {
@@ -458,8 +459,9 @@ __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restr
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const uint32_t idx = base + i * kThreads + threadIdx.x;
-    if (idx < n) {
-      const uint32_t k = length_class(item_length<CSR>(src, idx), cb);
+    const int32_t len = idx < n ? item_length<CSR>(src, idx) : -1;
+    if (len >= 0) {
+      const uint32_t k = length_class(len, cb);
 #pragma unroll
       for (int q = 0; q < kNumClasses; ++q) c[q] += (k == (uint32_t)q);
     }
@@ -495,8 +497,9 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
 #pragma unroll
   for (int t = 0; t < kItems; ++t) {
     const uint32_t idx = base + t * 64 + lane;
-    const bool valid = idx < n;
-    const uint32_t k = valid ? length_class(item_length<CSR>(src, idx), cb) : 0u;
+    const int32_t len = idx < n ? item_length<CSR>(src, idx) : -1;
+    const bool valid = len >= 0;
+    const uint32_t k = valid ? length_class(len, cb) : 0u;
     cls[t] = k;
     uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -522,16 +525,17 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
 #pragma unroll
   for (int t = 0; t < kItems; ++t) {
     const uint32_t idx = base + t * 64 + lane;
-    if (idx < n) order[gbase[cls[t]] + wcnt[wave][cls[t]] + rank[t]] = (int32_t)idx;
+    if (idx < n && item_length<CSR>(src, idx) >= 0) order[gbase[cls[t]] + wcnt[wave][cls[t]] + rank[t]] = (int32_t)idx;
   }
 }
 
-// Waves needed by segment s = (tile, class): items / (64 / group size), rounded up.
-__global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, uint32_t n, GroupSizes gs,
+// Waves needed by segment s = (tile, class): items / (64 / group size),
+// rounded up.  seg holds nseg + 1 offsets (the last one is the item total).
+__global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, GroupSizes gs,
                               uint32_t* __restrict__ wcnt) {
   const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= nseg) return;
-  const uint32_t lo = seg[s], hi = s + 1 < nseg ? seg[s + 1] : n;
+  const uint32_t lo = seg[s], hi = seg[s + 1];
   const uint32_t per = (uint32_t)(kWave / gs.g[s % kNumClasses]);
   wcnt[s] = (hi - lo + per - 1) / per;
 }
@@ -539,14 +543,13 @@ __global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, u
 // One workgroup per tile writes the wave descriptors of its segments:
 // {first slot in order, group size << 8 | items in the wave}.
 __global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restrict__ seg,
-                                                        const uint32_t* __restrict__ wstart, uint32_t ntiles,
-                                                        uint32_t n, GroupSizes gs, uint2* __restrict__ waves) {
+                                                        const uint32_t* __restrict__ wstart, GroupSizes gs,
+                                                        uint2* __restrict__ waves) {
   const uint32_t t = blockIdx.x;
-  const uint32_t nseg = (uint32_t)kNumClasses * ntiles;
 #pragma unroll
   for (uint32_t q = 0; q < (uint32_t)kNumClasses; ++q) {
     const uint32_t s = t * kNumClasses + q;
-    const uint32_t lo = seg[s], hi = s + 1 < nseg ? seg[s + 1] : n;
+    const uint32_t lo = seg[s], hi = seg[s + 1];
     const uint32_t per = (uint32_t)(kWave / gs.g[q]);
     const uint32_t nw = (hi - lo + per - 1) / per;
     for (uint32_t u = threadIdx.x; u < nw; u += blockDim.x) {
@@ -565,26 +568,28 @@ void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, co
   const uint32_t n = (uint32_t)g.n_keys;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
   const uint32_t nseg = (uint32_t)kNumClasses * ntiles;
-  uint32_t* seg = g.hist;            // item offsets per segment
-  uint32_t* wcnt = g.hist + nseg;    // wave offsets per segment (hist holds 256 * ntiles words)
+  // hist holds 256 * ntiles words: item offsets per segment (nseg + 1, the
+  // last is the number of scheduled items), then wave offsets per segment
+  uint32_t* seg = g.hist;
+  uint32_t* wcnt = g.hist + nseg + 1;
   hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg);
   SPHOPS_LAUNCHED();
-  device_exclusive_scan(seg, seg, nseg, g.scan_tmp, nullptr, st);
+  device_exclusive_scan(seg, seg, nseg, g.scan_tmp, seg + nseg, st);
   hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg, order);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, n,
-                     gs, wcnt);
+  hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, gs,
+                     wcnt);
   SPHOPS_LAUNCHED();
   device_exclusive_scan(wcnt, wcnt, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total), st);
-  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt, ntiles, n, gs, waves);
+  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt, gs, waves);
   SPHOPS_LAUNCHED();
   if (waves2 != nullptr) {  // a second descriptor table over the same order, other group sizes
-    uint32_t* wcnt2 = g.hist + 2 * nseg;
-    hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, n,
+    uint32_t* wcnt2 = wcnt + nseg;
+    hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg,
                        *gs2, wcnt2);
     SPHOPS_LAUNCHED();
     device_exclusive_scan(wcnt2, wcnt2, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total2), st);
-    hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt2, ntiles, n, *gs2, waves2);
+    hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt2, *gs2, waves2);
     SPHOPS_LAUNCHED();
   }
 }
@@ -599,9 +604,28 @@ void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, 
                         wave_total2);
 }
 
-void run_candidate_schedule(const Grid& g, const int32_t* coff, int32_t* order, uint2* waves, int32_t* wave_total,
-                            hipStream_t st) {
-  tiled_schedule<true>(g, coff, kScanClasses, kScanGroups, order, waves, wave_total, st);
+void run_candidate_schedule(const Grid& g, const int32_t* sparse_len, int32_t* order, uint2* waves,
+                            int32_t* wave_total, hipStream_t st) {
+  tiled_schedule<false>(g, sparse_len, kScanClasses, kScanGroups, order, waves, wave_total, st);
+}
+
+namespace {
+__global__ __launch_bounds__(kThreads) void k_unit_write(const int32_t* __restrict__ unit_len,
+                                                         const uint32_t* __restrict__ slot, uint32_t n,
+                                                         uint2* __restrict__ units) {
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= n) return;
+  const int32_t len = unit_len[k];
+  if (len > 0) units[slot[k]] = make_uint2(k, (uint32_t)len);
+}
+}  // namespace
+
+void run_unit_schedule(const Grid& g, hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, reinterpret_cast<uint32_t*>(g.unit_total), st);
+  hipLaunchKernelGGL(k_unit_write, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, st, g.unit_len, g.flags,
+                     n, g.units);
+  SPHOPS_LAUNCHED();
 }
 
 void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* total, hipStream_t st) {

@@ -63,6 +63,10 @@ void free_grid(Grid* g) {
   (void)hipFree(g->cand_order);
   (void)hipFree(g->cand_waves);
   (void)hipFree(g->cand_wave_total);
+  (void)hipFree(g->sparse_len);
+  (void)hipFree(g->unit_len);
+  (void)hipFree(g->units);
+  (void)hipFree(g->unit_total);
   delete g;
 }
 
@@ -233,6 +237,10 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->cand_order = dalloc<int32_t>(BN);
       g->cand_waves = dalloc<uint2>(sphops::neighbour_wave_capacity(*g));
       g->cand_wave_total = dalloc<int32_t>(1);
+      g->sparse_len = dalloc<int32_t>(BN);
+      g->unit_len = dalloc<int32_t>(BN);
+      g->units = dalloc<uint2>(BN);
+      g->unit_total = dalloc<int32_t>(1);
     } catch (...) {
       sphops::free_grid(g);
       throw;

@@ -1202,6 +1202,216 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
   }
 }
 
+// Broadcast lane q's value to its quad (q a compile-time constant after
+// unrolling).
+template <class T>
+__device__ __forceinline__ T quad_bcast(T v, int q) {
+  if (q == 0) return quad_get<0>(v);
+  if (q == 1) return quad_get<1>(v);
+  if (q == 2) return quad_get<2>(v);
+  return quad_get<3>(v);
+}
+
+// N floats at a 16-byte aligned byte offset `off` from a uniform base: global
+// loads with a scalar base and a 32-bit vector offset (the launcher checks
+// that every offset fits in 32 bits).
+template <int N>
+__device__ __forceinline__ void load_off(const float* __restrict__ base, uint32_t off, float* v) {
+  const char* p = reinterpret_cast<const char*>(base) + off;
+#pragma unroll
+  for (int u = 0; u < N / 4; ++u) {
+    const float4 t = *reinterpret_cast<const float4*>(p + 16 * u);
+    v[4 * u + 0] = t.x;
+    v[4 * u + 1] = t.y;
+    v[4 * u + 2] = t.z;
+    v[4 * u + 3] = t.w;
+  }
+}
+
+// One neighbour's channel slice for the pass-B backward: blur upstream,
+// gradient upstream and (FULL) state.
+template <int D, int CW, bool FULL>
+struct PassBRows {
+  float gb[CW];
+  float gg[CW * D];
+  float s[FULL ? CW : 1];
+  __device__ __forceinline__ void load(const OpPtrs& a, uint32_t j, uint32_t off_s, uint32_t off_g) {
+    constexpr uint32_t RS = 16u * CW, RG = 16u * CW * D;  // bytes per row of s / g and of g2
+    load_off<CW>(a.g, j * RS + off_s, gb);
+    load_off<CW * D>(a.g2, j * RG + off_g, gg);
+    if constexpr (FULL) load_off<CW>(a.s, j * RS + off_s, s);
+  }
+};
+
+// Pass-B backward, software-pipelined form of k_blur_hybrid_bwd_quad (same
+// layout and formulas): the index and packed position of the next quad
+// iteration's owned pair are loaded one iteration ahead, and the rows of pair
+// q + 1 while pair q is computed (two row buffers).  Pairs past the end of a
+// stream are computed against the particle itself with all weights zero, so
+// the four pair blocks of an iteration have no branches.  dL/drho of blur is
+// taken from the slice's dL/ds sum at the end (sum_j W_j g_j . s_i =
+// s_i . sum_j W_j g_j).
+template <int D, bool P, int CW, bool FULL, int WAVES>
+__global__ __launch_bounds__(kThreads, WAVES) void k_blur_hybrid_bwd_pipe(GridParams g, OpPtrs a) {
+  constexpr int C = 4 * CW;
+  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (wave >= a.nwaves2) return;
+  const uint2 wd = a.waves2[wave];
+  const int G = (int)(wd.y >> 8);
+  const int lane = __lane_id();
+  const uint32_t slot = (uint32_t)(lane / G);
+  const int sub = lane & (G - 1);
+  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
+  const bool active = slot < (wd.y & 0xFFu);
+  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
+  const uint32_t c0 = (uint32_t)slice * CW;
+  const uint32_t off_s = c0 * 4u, off_g = c0 * 4u * D;
+  const float4* __restrict__ xw = a.xw;
+  float xi[3] = {0.0f, 0.0f, 0.0f};
+  float vi = 0.0f, mr2 = 0.0f;
+  float si[FULL ? CW : 1] = {}, gbi[FULL ? CW : 1] = {};
+  float ggi[CW * D] = {};
+  float dsb[CW] = {}, dsg[CW] = {};
+  float wsum[D] = {};
+  float dxb[D] = {}, dxg[D] = {};
+  float drb = 0.0f, drg = 0.0f;
+  if (active) {
+    unpack(xw[k], xi);
+    const float mi = a.m[k], ri = a.rho[k];
+    vi = mi / ri;
+    mr2 = mi / (ri * ri);
+    load_off<CW * D>(a.g2, k * (16u * CW * D) + off_g, ggi);
+    if constexpr (FULL) {
+      load_off<CW>(a.s, k * (16u * CW) + off_s, si);
+      load_off<CW>(a.g, k * (16u * CW) + off_s, gbi);
+    }
+    const int32_t* __restrict__ nidx = a.nidx;
+    const int start = a.nptr[k];
+    const int end = start + a.ncnt[k];
+    const int step = 4 * S;
+    int to = start + stream + slice * S;  // position of the pair this lane owns in the current iteration
+    uint32_t jn = to < end ? (uint32_t)nidx[to] : k;
+    float4 pn = xw[jn];
+    uint32_t jn2 = to + step < end ? (uint32_t)nidx[to + step] : k;
+    PassBRows<D, CW, FULL> rb_[2];
+    rb_[0].load(a, quad_get<0>(jn), off_s, off_g);
+    for (int t0 = start + stream; t0 < end; t0 += step, to += step) {
+      const uint32_t jo = jn;
+      const float4 pj = pn;
+      const bool own = to < end;
+      jn = jn2;
+      pn = xw[jn];
+      jn2 = to + 2 * step < end ? (uint32_t)nidx[to + 2 * step] : k;
+      // geometry of the pair this lane owns (all zero past the end)
+      float vo = 0.0f, Wo = 0.0f, t2o = 0.0f, jao = 0.0f, jbo = 0.0f;
+      float rbo[3] = {0.0f, 0.0f, 0.0f}, wo[3] = {0.0f, 0.0f, 0.0f};
+      if (own) {
+        float xj[3], r[3];
+        unpack(pj, xj);
+        vo = pj.w;
+        const float d2 = displacement<D, P>(g, xi, xj, r);
+        const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
+        Wo = poly6(g.eps2, db);
+        float d;
+        const float mag = spiky_mag(g.eps, db, &d);
+#pragma unroll
+        for (int e = 0; e < D; ++e) {
+          wo[e] = mag * rbo[e];
+          wsum[e] += vo * wo[e];
+        }
+        if constexpr (FULL) {
+          if (db != 0.0f && db < g.eps2) {
+            const float tt = g.eps2 - db;
+            t2o = -6.0f * tt * tt;
+            const float di = fast_rcp(d);
+            jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
+            jbo = 3.0f * (g.eps2 - db) * di * di * di;
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q < 3) rb_[(q + 1) & 1].load(a, quad_bcast(jo, q + 1), off_s, off_g);
+        else rb_[0].load(a, quad_get<0>(jn), off_s, off_g);
+        const PassBRows<D, CW, FULL>& R = rb_[q & 1];
+        const float W = quad_bcast(Wo, q);
+        float w[3];
+#pragma unroll
+        for (int e = 0; e < D; ++e) w[e] = quad_bcast(wo[e], q);
+        if constexpr (!FULL) {
+#pragma unroll
+          for (int f = 0; f < CW; ++f) {
+            dsb[f] += W * R.gb[f];
+#pragma unroll
+            for (int e = 0; e < D; ++e) dsg[f] += R.gg[f * D + e] * w[e];
+          }
+        } else {
+          const float vj = quad_bcast(vo, q), t2 = quad_bcast(t2o, q);
+          const float ja = quad_bcast(jao, q), jb = quad_bcast(jbo, q);
+          float rb[3];
+#pragma unroll
+          for (int e = 0; e < D; ++e) rb[e] = quad_bcast(rbo[e], q);
+          float A = 0.0f, Bv = 0.0f;
+          float u1[D] = {}, u2[D] = {};
+#pragma unroll
+          for (int f = 0; f < CW; ++f) {
+            dsb[f] += W * R.gb[f];
+            A += gbi[f] * R.s[f];
+            Bv += R.gb[f] * si[f];
+            const float df = si[f] - R.s[f];
+#pragma unroll
+            for (int e = 0; e < D; ++e) {
+              dsg[f] += R.gg[f * D + e] * w[e];
+              u1[e] += df * R.gg[f * D + e];
+              u2[e] += df * ggi[f * D + e];
+            }
+          }
+          const float m6 = t2 * (A * vj + Bv * vi);  // t2 = -6 (h^2 - r^2)^2, 0 outside (0, h)
+          float u[D], uw = 0.0f, rv = 0.0f;
+#pragma unroll
+          for (int e = 0; e < D; ++e) {
+            dxb[e] += m6 * rb[e];
+            uw += u1[e] * w[e];
+            u[e] = vi * u1[e] + vj * u2[e];
+            rv += rb[e] * u[e];
+          }
+          drg += uw;
+#pragma unroll
+          for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
+        }
+      }
+    }
+    if constexpr (FULL) {
+#pragma unroll
+      for (int f = 0; f < CW; ++f) drb += si[f] * dsb[f];
+    }
+  }
+  grp_sum_streams(G, dsb, dsg);
+  grp_sum(G, wsum);
+  if constexpr (FULL) grp_sum(G, dxb, dxg, drb, drg);
+#pragma unroll
+  for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
+  if (active && stream == 0) {
+    const float sb = vi * g.c6;
+#pragma unroll
+    for (int f = 0; f < CW; ++f) {
+      float t = vi * dsg[f];
+#pragma unroll
+      for (int e = 0; e < D; ++e) t += ggi[f * D + e] * wsum[e];
+      a.out1[(uint64_t)k * C + c0 + f] = dsb[f] * sb + t * g.cs;
+    }
+    if constexpr (FULL) {
+      if (slice == 0) {
+        a.out2[k] = -mr2 * (drb * g.c6 + drg * g.cs);
+        float dx[D];
+#pragma unroll
+        for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6 + dxg[e] * g.cs;
+        store_pos_grad<D>(a.out0, k, dx, 1.0f);
+      }
+    }
+  }
+}
+
 // Pass-B forward (blur + gradient_hybrid) on the lane-split layout with the
 // pair geometry shared per quad, as k_blur_hybrid_bwd_quad: lane q of a quad
 // evaluates the q-th of four pairs (index, volume-weighted W and spiky
@@ -1335,6 +1545,106 @@ __global__ __launch_bounds__(kThreads) void k_candidates(GridParams g, const int
   cand[k] = total;
 }
 
+// Work split of the list fill, recomputed by every fill from its own
+// arguments: particles of cells with at least kDenseCell particles are filled
+// cell-major (sparse_len = -1; unit_len and flags mark the first particle of
+// every run of kUnitParticles particles of the cell), the others by the
+// grouped scan (sparse_len = stencil candidate count, from coff).
+template <int D, bool P>
+__global__ __launch_bounds__(kThreads) void k_fill_split(GridParams g, const int32_t* __restrict__ bo,
+                                                         const float4* __restrict__ xw,
+                                                         const int32_t* __restrict__ coff,
+                                                         int32_t* __restrict__ sparse_len,
+                                                         int32_t* __restrict__ unit_len, uint32_t* __restrict__ flags) {
+  const uint32_t n = g.B * g.N;
+  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
+  if (k >= n) return;
+  float xi[3];
+  unpack(xw[k], xi);
+  int c[3] = {0, 0, 0};
+  pos2cell<D, P>(g, xi, c);
+  const uint32_t h = (k / g.N) * g.G + cell_hash<D>(g, c);
+  const int32_t cs = bo[h], ce = bo[h + 1];
+  const bool dense = ce - cs >= kDenseCell;
+  const int32_t off = (int32_t)k - cs;
+  const int32_t ul = (dense && off % kUnitParticles == 0) ? min(kUnitParticles, ce - (int32_t)k) : 0;
+  sparse_len[k] = dense ? -1 : coff[k + 1] - coff[k];
+  unit_len[k] = ul;
+  flags[k] = ul > 0 ? 1u : 0u;
+}
+
+// Lane t's value of v (t wave-uniform).
+__device__ __forceinline__ float lane_float(float v, uint32_t t) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)t));
+}
+
+// Cell-major neighbour-list fill of the dense cells: one wave per unit (up
+// to kUnitParticles consecutive particles of one cell, which share the
+// cell's stencil).  The wave walks the stencil ranges 64 candidates at a
+// time, lane l taking the l-th candidate, and tests each candidate against
+// every particle of the unit (positions wave-uniform by readlane); a ballot
+// ranks the in-radius candidates, so each particle's row keeps stencil order
+// and holds the same entries as the per-particle scan writes.  Lane t keeps
+// particle t's next write position (row start + entries so far).
+template <int D, bool P>
+__global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const int32_t* __restrict__ bo,
+                                                        const float4* __restrict__ xw,
+                                                        const int32_t* __restrict__ coff,
+                                                        const uint2* __restrict__ units,
+                                                        const int32_t* __restrict__ unit_total,
+                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ ncnt,
+                                                        int64_t cap) {
+  const uint32_t total = (uint32_t)*unit_total;
+  const uint32_t nwaves = gridDim.x * (kThreads / kWave);
+  const uint32_t lane = (uint32_t)__lane_id();
+  const uint32_t cap32 = (uint32_t)min<int64_t>(cap, (int64_t)0x7FFFFFFF);
+  for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < total; u += nwaves) {
+    const uint2 ud = units[u];
+    const uint32_t i0 = __builtin_amdgcn_readfirstlane(ud.x);
+    const uint32_t ni = __builtin_amdgcn_readfirstlane(ud.y);
+    const uint32_t it = i0 + min(lane, ni - 1u);
+    const float4 pt = xw[it];
+    const int32_t row0 = coff[it];
+    const int32_t ncand = __builtin_amdgcn_readfirstlane(coff[i0 + 1] - coff[i0]);
+    int32_t wpos = row0;  // lane t < ni: particle i0 + t's next list slot
+    float x0[3] = {lane_float(pt.x, 0), lane_float(pt.y, 0), lane_float(pt.z, 0)};
+    Walker<D, P> w;
+    w.init(g, x0, i0);
+    bool more = w.next(g, bo);
+    for (int32_t base = 0; base < ncand; base += kWave) {
+      // candidate of this lane: position base + lane of the concatenated ranges
+      uint32_t j = i0;
+      bool valid = false;
+      uint32_t covered = 0;
+      while (covered < (uint32_t)kWave && more) {
+        const uint32_t take = min(w.jend - w.j, (uint32_t)kWave - covered);
+        if (lane >= covered && lane < covered + take) {
+          j = w.j + (lane - covered);
+          valid = true;
+        }
+        covered += take;
+        w.j += take;
+        if (w.j >= w.jend) more = w.next(g, bo);
+      }
+      float xj[3];
+      unpack(xw[j], xj);
+      if (!valid) xj[0] = __int_as_float(0x7FC00000);  // NaN: never in radius
+      for (uint32_t t = 0; t < ni; ++t) {
+        const float xi[3] = {lane_float(pt.x, t), lane_float(pt.y, t), lane_float(pt.z, t)};
+        float r[3];
+        const bool in = displacement<D, P>(g, xi, xj, r) < g.eps2;
+        const uint64_t m = __ballot(in);
+        const uint32_t at = (uint32_t)__builtin_amdgcn_readlane(wpos, (int)t);
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        const uint32_t pos = at + rank;
+        if (in && pos < cap32) nidx[pos] = (int32_t)j;
+        if (lane == t) wpos = (int32_t)(at + (uint32_t)__popcll(m));
+      }
+    }
+    if (lane < ni) ncnt[i0 + lane] = wpos - row0;
+  }
+}
+
 constexpr int kScanUnroll = 4;
 
 // Neighbour-list fill: particle k's in-radius neighbours (stencil order) go
@@ -1446,14 +1756,22 @@ void neighbour_candidates(const Grid& g, const int32_t* bo, const float* x, int3
   exclusive_scan_u32(g, reinterpret_cast<uint32_t*>(coff), n, reinterpret_cast<uint32_t*>(coff) + n, st);
 }
 
-// Fill the rows at coff: candidate-count schedule, then the grouped scan.
+// Fill the rows at coff: the dense cells' units cell-major, then the other
+// particles by the grouped scan over their candidate-count schedule.
 template <int D, bool P>
 void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, const int32_t* coff, int32_t* nidx,
                     int32_t* ncnt, int64_t cap, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-  run_candidate_schedule(g, coff, g.cand_order, g.cand_waves, g.cand_wave_total, st);
+  hipLaunchKernelGGL((k_fill_split<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, coff,
+                     g.sparse_len, g.unit_len, g.flags);
+  SPHOPS_LAUNCHED();
+  run_unit_schedule(g, st);
+  hipLaunchKernelGGL((k_unit_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo, g.packed,
+                     coff, g.units, g.unit_total, nidx, ncnt, cap);
+  SPHOPS_LAUNCHED();
+  run_candidate_schedule(g, g.sparse_len, g.cand_order, g.cand_waves, g.cand_wave_total, st);
   hipLaunchKernelGGL((k_scan_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo, g.packed,
                      coff, g.cand_order, g.cand_waves, g.cand_wave_total, nidx, ncnt, cap);
   SPHOPS_LAUNCHED();
@@ -1507,7 +1825,21 @@ void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
   pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
-  if (a.C == 16) {
+  const char* ev = getenv("SPHOPS_EXP_BWD");
+  const int var = ev ? atoi(ev) : 0;
+  if (var == 1) {
+    if (a.C == 16) {
+      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 4, FULL, 3>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    } else {
+      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 8, FULL, 2>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    }
+  } else if (var == 2) {
+    if (a.C == 16) {
+      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 4, FULL, 4>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    } else {
+      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 8, FULL, 2>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    }
+  } else if (a.C == 16) {
     hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 4, FULL>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else {
     hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);

@@ -52,6 +52,11 @@ struct Grid {
   int32_t* cand_order = nullptr;  // B*N particles in candidate-scan schedule order
   uint2* cand_waves = nullptr;    // candidate-scan wave descriptors (neighbour_wave_capacity)
   int32_t* cand_wave_total = nullptr;  // number of candidate-scan waves (device)
+  // cell-major list fill of dense cells (at least kDenseCell particles):
+  int32_t* sparse_len = nullptr;  // B*N: stencil candidate count of particles in sparse cells, -1 in dense ones
+  int32_t* unit_len = nullptr;    // B*N: particles of the unit starting at this particle, 0 if none starts here
+  uint2* units = nullptr;         // B*N: unit descriptors {first particle, particles}
+  int32_t* unit_total = nullptr;  // number of units (device)
   const void* cand_key[2] = {nullptr, nullptr};  // (positions, bin_offsets) the schedule was built for
 };
 
@@ -120,8 +125,18 @@ void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, 
 uint64_t neighbour_wave_capacity(const Grid& g);
 // Candidate-scan schedule: as the pair-kernel schedule, classes by stencil
 // candidate count (from the scanned offsets coff; kScanClasses / kScanGroups).
-void run_candidate_schedule(const Grid& g, const int32_t* coff, int32_t* order, uint2* waves, int32_t* wave_total,
-                            hipStream_t st);
+// Only particles with sparse_len >= 0 are scheduled.
+void run_candidate_schedule(const Grid& g, const int32_t* sparse_len, int32_t* order, uint2* waves,
+                            int32_t* wave_total, hipStream_t st);
+// Units of the cell-major fill: units[u] = {first particle, count} for every
+// particle k with unit_len[k] > 0 (flags[k] = 1 there, 0 elsewhere), in
+// particle order; their number goes to unit_total.  Scans flags in place.
+void run_unit_schedule(const Grid& g, hipStream_t st);
+// Cells holding at least kDenseCell particles have their neighbour lists
+// filled cell-major, in units of at most kUnitParticles particles of one
+// cell served by one wave; the other particles by the grouped candidate scan.
+constexpr int32_t kDenseCell = 8;
+constexpr int32_t kUnitParticles = 16;
 // Work classes of the list traversal and the candidate scan: class q holds
 // the items whose length is <= t[q] (and above the previous bound), the last
 // class the rest; each class is served by groups of g[q] lanes per particle
