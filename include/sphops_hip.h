@@ -196,7 +196,9 @@ int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLd
 /* Row offsets of the neighbour list: for every binned particle the number of
  * particles in its 3^D cell stencil (the cells the reference traverses, an
  * upper bound of its in-radius count), exclusive-scanned into cand_offsets
- * (B*N+1); cand_offsets[B*N] is the total. */
+ * (B*N+1); cand_offsets[B*N] is the total.  Also leaves in the grid's
+ * scratch what sphops_neighbor_fill reads: the stencil ranges and the split
+ * of the particles between the cell-major and the per-particle fill. */
 int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
                                int32_t* cand_offsets, void* stream);
 
@@ -204,7 +206,11 @@ int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const in
  * in stencil order: the binned indices go to nbr_index[cand_offsets[i] ..),
  * their number (the reference's `count`) to nbr_count[i] (B*N).  Entries at
  * or past index_capacity are not written: a caller that sized nbr_index below
- * cand_offsets[B*N] checks that total afterwards and fills again. */
+ * cand_offsets[B*N] checks that total afterwards and fills again;
+ * index_capacity is at most 2^30.  Must follow
+ * sphops_neighbor_candidates on the same grid with the same x and bin_offsets
+ * (checked by pointer; their contents must not change in between), with no
+ * other candidates call on that grid in between. */
 int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
                          const int32_t* cand_offsets, int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count,
                          void* stream);

@@ -420,13 +420,12 @@ inline dim3 blocks_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) /
 
 // ------------------------------------------------ neighbour-list schedule
 //
-// Stable partition of the binned particles into four classes by neighbour
-// list length (<=4, <=32, <=128, more), which the pair kernels serve with
-// groups of 1, 4, 16 and 64 lanes per particle.  The partition is done per
-// tile of 4096 binned particles; the candidate schedule concatenates the
-// tiles class by class (class-major), the list schedule keeps them tile by
-// tile (tile-major: every class of a region of space is processed together,
-// so neighbour rows shared between classes are reused from the same L2).
+// Stable partition of the binned particles into kNumClasses classes by
+// neighbour-list length (kListClasses), which the pair kernels serve with
+// groups of kListGroups (or kSplitGroups) lanes per particle.  The partition
+// is done per tile of 4096 binned particles and the tiles stay in order
+// (tile-major: every class of a region of space is processed together, so
+// neighbour rows shared between classes are reused from the same L2).
 
 namespace {
 
@@ -602,11 +601,6 @@ void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, 
                             uint2* waves2, int32_t* wave_total2, hipStream_t st) {
   tiled_schedule<false>(g, ncnt, kListClasses, kListGroups, order, waves, wave_total, st, &kSplitGroups, waves2,
                         wave_total2);
-}
-
-void run_candidate_schedule(const Grid& g, const int32_t* sparse_len, int32_t* order, uint2* waves,
-                            int32_t* wave_total, hipStream_t st) {
-  tiled_schedule<false>(g, sparse_len, kScanClasses, kScanGroups, order, waves, wave_total, st);
 }
 
 namespace {

@@ -60,13 +60,11 @@ void free_grid(Grid* g) {
   (void)hipFree(g->chunk_lo);
   (void)hipFree(g->flags);
   (void)hipFree(g->packed);
-  (void)hipFree(g->cand_order);
-  (void)hipFree(g->cand_waves);
-  (void)hipFree(g->cand_wave_total);
   (void)hipFree(g->sparse_len);
   (void)hipFree(g->unit_len);
   (void)hipFree(g->units);
   (void)hipFree(g->unit_total);
+  (void)hipFree(g->ranges);
   delete g;
 }
 
@@ -234,13 +232,12 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
       g->flags = dalloc<uint32_t>(BN + 1);
       g->packed = dalloc<float4>(BN);
-      g->cand_order = dalloc<int32_t>(BN);
-      g->cand_waves = dalloc<uint2>(sphops::neighbour_wave_capacity(*g));
-      g->cand_wave_total = dalloc<int32_t>(1);
       g->sparse_len = dalloc<int32_t>(BN);
       g->unit_len = dalloc<int32_t>(BN);
       g->units = dalloc<uint2>(BN);
       g->unit_total = dalloc<int32_t>(1);
+      g->n_ranges = g->particle_mode ? (dim == 2 ? 9 : 27) : (dim == 2 ? 3 : 9) * (g->periodic ? 2 : 1);
+      g->ranges = dalloc<uint2>(BN * (uint64_t)g->n_ranges);
     } catch (...) {
       sphops::free_grid(g);
       throw;
@@ -585,6 +582,8 @@ int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const in
     a.x = x;
     a.iout = cand_offsets;
     sphops::forward(*grid, Op::NeighbourCandidates, bo, a, st);
+    grid->split_key[0] = x;
+    grid->split_key[1] = bo;
   });
 }
 
@@ -595,8 +594,13 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
     require(bo != nullptr && cand_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
     require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
     require(index_capacity >= 0, "negative index capacity");
+    require(index_capacity <= sphops::kMaxListEntries,
+            "neighbour list too large: at most 2^30 index entries (stencil candidates) per grid");
     if (grid->n_keys == 0) return;
     require(nbr_count != nullptr && (nbr_index != nullptr || index_capacity == 0), "null buffer");
+    require(grid->split_key[0] == x && grid->split_key[1] == bo,
+            "sphops_neighbor_fill must follow sphops_neighbor_candidates on the same grid with the same "
+            "positions and bin_offsets");
     OpPtrs a;
     a.x = x;
     a.nptr = cand_offsets;

@@ -1527,50 +1527,123 @@ __global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g,
 // keeps stencil order.  Both kernels are persistent: the grid is fixed and
 // waves loop over work units computed from the device-side class sizes.
 
-template <int D, bool P>
-__global__ __launch_bounds__(kThreads) void k_candidates(GridParams g, const int32_t* __restrict__ bo,
-                                                         const float4* __restrict__ xw, int32_t* __restrict__ cand) {
-  const uint32_t n = g.B * g.N;
-  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
-  if (k >= n) return;
-  float xi[3];
-  unpack(xw[k], xi);
-  Walker<D, P> w;
-  w.init(g, xi, k);
-  int32_t total = 0;
-  while (w.fetch(g, bo, w.r)) {
-    ++w.r;
-    total += (int32_t)(w.jend - w.j);
+// Stencil ranges of a particle's cell, all fetched before any is used so
+// that their loads overlap; range r is the one Walker::fetch(r) visits.
+template <int D, bool P, int R>
+__device__ __forceinline__ uint32_t fetch_ranges(const GridParams& g, const int32_t* __restrict__ bo,
+                                                 Walker<D, P>& w, uint2 (&rg)[R]) {
+  uint32_t total = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    w.fetch(g, bo, r);
+    rg[r] = make_uint2(w.j, w.jend);
+    total += w.jend - w.j;
   }
-  cand[k] = total;
+  return total;
 }
 
-// Work split of the list fill, recomputed by every fill from its own
-// arguments: particles of cells with at least kDenseCell particles are filled
-// cell-major (sparse_len = -1; unit_len and flags mark the first particle of
-// every run of kUnitParticles particles of the cell), the others by the
-// grouped scan (sparse_len = stencil candidate count, from coff).
+// Candidate count of every binned particle and the work split of the list
+// fill.  Cells with at least two particles, and lone particles with at least
+// kLaneMaxCand candidates, are filled cell-major by k_unit_fill (unit_len and
+// flags mark the first particle of every run of kUnitParticles particles of
+// the cell); the other lone particles by k_lane_fill (lane_len = candidate
+// count, -1 elsewhere).  The first particle of every unit, and every lone
+// particle, stores its cell's stencil ranges (ranges[k * R + r]).
+template <int D, bool P, int R>
+__device__ __forceinline__ void candidates_of(const GridParams& g, const int32_t* __restrict__ bo, uint32_t k,
+                                              const float* xi, int32_t* __restrict__ cand,
+                                              int32_t* __restrict__ lane_len, int32_t* __restrict__ unit_len,
+                                              uint32_t* __restrict__ flags, uint2* __restrict__ ranges) {
+  Walker<D, P> w;
+  w.init(g, xi, k);
+  uint2 rg[R];
+  const int32_t total = (int32_t)fetch_ranges<D, P, R>(g, bo, w, rg);
+  const uint32_t h = w.base + cell_hash<D>(g, w.c);
+  const int32_t cs = bo[h], ce = bo[h + 1];
+  const bool unit = ce - cs >= 2 || total >= kLaneMaxCand;
+  const int32_t off = (int32_t)k - cs;
+  const bool first = off % kUnitParticles == 0;
+  const int32_t ul = (unit && first) ? min(kUnitParticles, ce - (int32_t)k) : 0;
+  cand[k] = total;
+  lane_len[k] = unit ? -1 : total;
+  unit_len[k] = ul;
+  flags[k] = ul > 0 ? 1u : 0u;
+  if (first) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) ranges[(uint64_t)k * R + r] = rg[r];
+  }
+}
+
 template <int D, bool P>
-__global__ __launch_bounds__(kThreads) void k_fill_split(GridParams g, const int32_t* __restrict__ bo,
-                                                         const float4* __restrict__ xw,
-                                                         const int32_t* __restrict__ coff,
-                                                         int32_t* __restrict__ sparse_len,
-                                                         int32_t* __restrict__ unit_len, uint32_t* __restrict__ flags) {
+__global__ __launch_bounds__(kThreads) void k_candidates(GridParams g, const int32_t* __restrict__ bo,
+                                                         const float4* __restrict__ xw, int32_t* __restrict__ cand,
+                                                         int32_t* __restrict__ lane_len,
+                                                         int32_t* __restrict__ unit_len, uint32_t* __restrict__ flags,
+                                                         uint2* __restrict__ ranges) {
   const uint32_t n = g.B * g.N;
   const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
   if (k >= n) return;
   float xi[3];
   unpack(xw[k], xi);
-  int c[3] = {0, 0, 0};
-  pos2cell<D, P>(g, xi, c);
-  const uint32_t h = (k / g.N) * g.G + cell_hash<D>(g, c);
-  const int32_t cs = bo[h], ce = bo[h + 1];
-  const bool dense = ce - cs >= kDenseCell;
-  const int32_t off = (int32_t)k - cs;
-  const int32_t ul = (dense && off % kUnitParticles == 0) ? min(kUnitParticles, ce - (int32_t)k) : 0;
-  sparse_len[k] = dense ? -1 : coff[k + 1] - coff[k];
-  unit_len[k] = ul;
-  flags[k] = ul > 0 ? 1u : 0u;
+  if (g.morton) {
+    candidates_of<D, P, Walker<D, P>::kCellRanges>(g, bo, k, xi, cand, lane_len, unit_len, flags, ranges);
+  } else {
+    candidates_of<D, P, Walker<D, P>::kRowRanges>(g, bo, k, xi, cand, lane_len, unit_len, flags, ranges);
+  }
+}
+
+// Stencil ranges per particle in the grid's range table.
+template <int D, bool P>
+__host__ __device__ constexpr int ranges_per_particle(bool morton) {
+  return morton ? Walker<D, P>::kCellRanges : Walker<D, P>::kRowRanges;
+}
+
+// List fill of lone particles with few candidates: one lane per particle,
+// walking its stored stencil ranges in turn (the row keeps stencil order).
+template <int D, bool P, int R>
+__device__ __forceinline__ int32_t lane_fill_ranges(const GridParams& g, const float4* __restrict__ xw,
+                                                    const uint2* __restrict__ rp, const float* xi, int64_t pos,
+                                                    int64_t cap, int32_t* __restrict__ nidx) {
+  uint2 rg[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rg[r] = rp[r];
+  int32_t cnt = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    for (uint32_t j = rg[r].x; j < rg[r].y; ++j) {
+      float xj[3], rr[3];
+      unpack(xw[j], xj);
+      if (displacement<D, P>(g, xi, xj, rr) < g.eps2) {
+        if (pos < cap) nidx[pos] = (int32_t)j;
+        ++pos;
+        ++cnt;
+      }
+    }
+  }
+  return cnt;
+}
+
+template <int D, bool P>
+__global__ __launch_bounds__(kThreads) void k_lane_fill(GridParams g, const float4* __restrict__ xw,
+                                                        const int32_t* __restrict__ coff,
+                                                        const int32_t* __restrict__ lane_len,
+                                                        const uint2* __restrict__ ranges,
+                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ ncnt,
+                                                        int64_t cap) {
+  const uint32_t n = g.B * g.N;
+  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
+  if (k >= n || lane_len[k] < 0) return;
+  float xi[3];
+  unpack(xw[k], xi);
+  int32_t cnt;
+  if (g.morton) {
+    constexpr int R = Walker<D, P>::kCellRanges;
+    cnt = lane_fill_ranges<D, P, R>(g, xw, ranges + (uint64_t)k * R, xi, coff[k], cap, nidx);
+  } else {
+    constexpr int R = Walker<D, P>::kRowRanges;
+    cnt = lane_fill_ranges<D, P, R>(g, xw, ranges + (uint64_t)k * R, xi, coff[k], cap, nidx);
+  }
+  ncnt[k] = cnt;
 }
 
 // Lane t's value of v (t wave-uniform).
@@ -1578,18 +1651,17 @@ __device__ __forceinline__ float lane_float(float v, uint32_t t) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)t));
 }
 
-// Cell-major neighbour-list fill of the dense cells: one wave per unit (up
-// to kUnitParticles consecutive particles of one cell, which share the
-// cell's stencil).  The wave walks the stencil ranges 64 candidates at a
-// time, lane l taking the l-th candidate, and tests each candidate against
-// every particle of the unit (positions wave-uniform by readlane); a ballot
-// ranks the in-radius candidates, so each particle's row keeps stencil order
-// and holds the same entries as the per-particle scan writes.  Lane t keeps
-// particle t's next write position (row start + entries so far).
+// Cell-major neighbour-list fill: one wave per unit (up to kUnitParticles
+// consecutive particles of one cell, which share the cell's stencil).  The
+// wave walks the stencil ranges (stored by the unit's first particle) 64
+// candidates at a time, lane l taking the l-th candidate, and tests each
+// candidate against every particle of the unit, whose positions and next
+// list slots are wave-uniform values; a ballot ranks the in-radius
+// candidates, so each particle's row keeps stencil order.
 template <int D, bool P>
-__global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const int32_t* __restrict__ bo,
-                                                        const float4* __restrict__ xw,
+__global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const float4* __restrict__ xw,
                                                         const int32_t* __restrict__ coff,
+                                                        const uint2* __restrict__ ranges,
                                                         const uint2* __restrict__ units,
                                                         const int32_t* __restrict__ unit_total,
                                                         int32_t* __restrict__ nidx, int32_t* __restrict__ ncnt,
@@ -1597,7 +1669,7 @@ __global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const int3
   const uint32_t total = (uint32_t)*unit_total;
   const uint32_t nwaves = gridDim.x * (kThreads / kWave);
   const uint32_t lane = (uint32_t)__lane_id();
-  const uint32_t cap32 = (uint32_t)min<int64_t>(cap, (int64_t)0x7FFFFFFF);
+  const uint32_t cap32 = (uint32_t)min<int64_t>(cap, kMaxListEntries);  // byte offsets fit in 32 bits
   for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < total; u += nwaves) {
     const uint2 ud = units[u];
     const uint32_t i0 = __builtin_amdgcn_readfirstlane(ud.x);
@@ -1606,128 +1678,71 @@ __global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const int3
     const float4 pt = xw[it];
     const int32_t row0 = coff[it];
     const int32_t ncand = __builtin_amdgcn_readfirstlane(coff[i0 + 1] - coff[i0]);
-    int32_t wpos = row0;  // lane t < ni: particle i0 + t's next list slot
-    float x0[3] = {lane_float(pt.x, 0), lane_float(pt.y, 0), lane_float(pt.z, 0)};
-    Walker<D, P> w;
-    w.init(g, x0, i0);
-    bool more = w.next(g, bo);
+    // wave-uniform copies: positions and next list slots of the unit's particles
+    float xs[kUnitParticles][3];
+    uint32_t at[kUnitParticles];
+#pragma unroll
+    for (int t = 0; t < kUnitParticles; ++t) {
+      xs[t][0] = lane_float(pt.x, t);
+      xs[t][1] = lane_float(pt.y, t);
+      xs[t][2] = lane_float(pt.z, t);
+      at[t] = (uint32_t)__builtin_amdgcn_readlane(row0, t);
+    }
+    // the stencil ranges of the unit's cell (stored by its first particle), lane r holding range r
+    const int R = ranges_per_particle<D, P>(g.morton != 0);
+    uint32_t rlo = 0, rhi = 0;
+    if ((int)lane < R) {
+      const uint2 rr = ranges[(uint64_t)i0 * R + lane];
+      rlo = rr.x;
+      rhi = rr.y;
+    }
+    // wave-uniform cursor over the ranges: position cj of range r, which ends at cend
+    int r = 0;
+    uint32_t cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, 0), cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, 0);
+    while (cj >= cend && ++r < R) {
+      cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
+      cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
+    }
     for (int32_t base = 0; base < ncand; base += kWave) {
       // candidate of this lane: position base + lane of the concatenated ranges
       uint32_t j = i0;
       bool valid = false;
       uint32_t covered = 0;
-      while (covered < (uint32_t)kWave && more) {
-        const uint32_t take = min(w.jend - w.j, (uint32_t)kWave - covered);
+      while (covered < (uint32_t)kWave && r < R) {
+        const uint32_t take = min(cend - cj, (uint32_t)kWave - covered);
         if (lane >= covered && lane < covered + take) {
-          j = w.j + (lane - covered);
+          j = cj + (lane - covered);
           valid = true;
         }
         covered += take;
-        w.j += take;
-        if (w.j >= w.jend) more = w.next(g, bo);
+        cj += take;
+        while (cj >= cend && ++r < R) {
+          cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
+          cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
+        }
       }
       float xj[3];
       unpack(xw[j], xj);
       if (!valid) xj[0] = __int_as_float(0x7FC00000);  // NaN: never in radius
-      for (uint32_t t = 0; t < ni; ++t) {
-        const float xi[3] = {lane_float(pt.x, t), lane_float(pt.y, t), lane_float(pt.z, t)};
-        float r[3];
-        const bool in = displacement<D, P>(g, xi, xj, r) < g.eps2;
-        const uint64_t m = __ballot(in);
-        const uint32_t at = (uint32_t)__builtin_amdgcn_readlane(wpos, (int)t);
-        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-        const uint32_t pos = at + rank;
-        if (in && pos < cap32) nidx[pos] = (int32_t)j;
-        if (lane == t) wpos = (int32_t)(at + (uint32_t)__popcll(m));
-      }
-    }
-    if (lane < ni) ncnt[i0 + lane] = wpos - row0;
-  }
-}
-
-constexpr int kScanUnroll = 4;
-
-// Neighbour-list fill: particle k's in-radius neighbours (stencil order) go
-// to nidx[coff[k] ..), coff = exclusive scan of the stencil candidate counts;
-// their number goes to ncnt[k].  Writes past `cap` entries are dropped (the
-// caller sized nidx from an earlier total and checks coff[n] afterwards).
-template <int D, bool P>
-__global__ __launch_bounds__(kThreads) void k_scan_fill(GridParams g, const int32_t* __restrict__ bo,
-                                                        const float4* __restrict__ xw,
-                                                        const int32_t* __restrict__ coff,
-                                                        const int32_t* __restrict__ order,
-                                                        const uint2* __restrict__ waves,
-                                                        const int32_t* __restrict__ wave_total,
-                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ ncnt,
-                                                        int64_t cap) {
-  const uint32_t total = (uint32_t)*wave_total;
-  const uint32_t nwaves = gridDim.x * (kThreads / kWave);
-  const int lane = __lane_id();
-  for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < total; u += nwaves) {
-    const uint2 wd = waves[u];
-    const int G = (int)(wd.y >> 8);
-    const uint32_t slot = (uint32_t)(lane / G);
-    const int sub = lane & (G - 1);
-    const bool active = slot < (wd.y & 0xFFu);
-    const uint32_t k = active ? (uint32_t)order[wd.x + slot] : 0u;
-    const int32_t row = active ? coff[k] : 0;
-    const uint32_t ncand = active ? (uint32_t)(coff[k + 1] - row) : 0u;
-    float xi[3] = {0.0f, 0.0f, 0.0f};
-    Walker<D, P> w;
-    uint32_t pr = 0, ra = 0, rlen = 0;
-    if (active) {
-      unpack(xw[k], xi);
-      w.init(g, xi, k);
-      if (w.next(g, bo)) {
-        ra = w.j;
-        rlen = w.jend - w.j;
-      }
-    }
-    const uint64_t gmask = G == 64 ? ~0ull : ((1ull << G) - 1ull);
-    const int gshift = lane & ~(G - 1);
-    int32_t acc = 0;
-    const int64_t row_end = min((int64_t)row + (int64_t)ncand, cap);
-    for (uint32_t base = 0; base < ncand; base += (uint32_t)(G * kScanUnroll)) {
-      uint32_t jj[kScanUnroll];
-      bool ok[kScanUnroll];
 #pragma unroll
-      for (int q = 0; q < kScanUnroll; ++q) {
-        const uint32_t p = base + (uint32_t)(q * G + sub);
-        ok[q] = p < ncand;
-        jj[q] = 0;
-        if (ok[q]) {
-          while (p >= pr + rlen) {
-            pr += rlen;
-            w.j = w.jend;
-            if (!w.next(g, bo)) {  // stencil exhausted: candidate count and ranges disagree
-              rlen = 0xFFFFFFFFu - pr;
-              ok[q] = false;
-              break;
-            }
-            ra = w.j;
-            rlen = w.jend - w.j;
-          }
-          if (ok[q]) jj[q] = ra + (p - pr);
+      for (int t = 0; t < kUnitParticles; ++t) {
+        if (t < (int)ni) {
+          float r[3];
+          const bool in = displacement<D, P>(g, xs[t], xj, r) < g.eps2;
+          const uint64_t m = __ballot(in);
+          const uint32_t rank =
+              __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          const uint32_t pos = at[t] + rank;
+          if (in && pos < cap32) *reinterpret_cast<int32_t*>(reinterpret_cast<char*>(nidx) + pos * 4u) = (int32_t)j;
+          at[t] += (uint32_t)__popcll(m);
         }
       }
-      float4 pj[kScanUnroll];
-#pragma unroll
-      for (int q = 0; q < kScanUnroll; ++q) pj[q] = xw[jj[q]];
-#pragma unroll
-      for (int q = 0; q < kScanUnroll; ++q) {
-        bool in = false;
-        if (ok[q]) {
-          float xj[3], r[3];
-          unpack(pj[q], xj);
-          in = displacement<D, P>(g, xi, xj, r) < g.eps2;
-        }
-        const uint64_t gb = (__ballot(in) >> gshift) & gmask;
-        const int64_t pos = (int64_t)row + acc + (int64_t)__popcll(gb & ((1ull << sub) - 1ull));
-        if (in && pos < row_end) nidx[pos] = (int32_t)jj[q];
-        acc += (int32_t)__popcll(gb);
-      }
     }
-    if (active && sub == 0) ncnt[k] = acc;
+    int32_t mine = 0;
+#pragma unroll
+    for (int t = 0; t < kUnitParticles; ++t)
+      if ((int)lane == t) mine = (int32_t)at[t];
+    if (lane < ni) ncnt[i0 + lane] = mine - row0;
   }
 }
 
@@ -1745,35 +1760,34 @@ void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
 constexpr uint32_t kPersistentWorkgroups = 2048;
 
 // Stencil candidate counts of every binned particle, exclusive-scanned into
-// coff (B*N+1, total in coff[B*N]).
+// coff (B*N+1, total in coff[B*N]), and the fill's work split, unit table
+// and stencil ranges in the grid's scratch (read by neighbour_fill).
 template <int D, bool P>
 void neighbour_candidates(const Grid& g, const int32_t* bo, const float* x, int32_t* coff, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, coff);
+  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, coff,
+                     g.sparse_len, g.unit_len, g.flags, g.ranges);
   SPHOPS_LAUNCHED();
   exclusive_scan_u32(g, reinterpret_cast<uint32_t*>(coff), n, reinterpret_cast<uint32_t*>(coff) + n, st);
+  run_unit_schedule(g, st);
 }
 
-// Fill the rows at coff: the dense cells' units cell-major, then the other
-// particles by the grouped scan over their candidate-count schedule.
+// Fill the rows at coff: cells with several particles (and lone particles
+// with many candidates) cell-major, the other lone particles a lane each,
+// with the work split and ranges neighbour_candidates left in the grid.
 template <int D, bool P>
 void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, const int32_t* coff, int32_t* nidx,
                     int32_t* ncnt, int64_t cap, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_fill_split<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, coff,
-                     g.sparse_len, g.unit_len, g.flags);
+  hipLaunchKernelGGL((k_unit_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, coff,
+                     g.ranges, g.units, g.unit_total, nidx, ncnt, cap);
   SPHOPS_LAUNCHED();
-  run_unit_schedule(g, st);
-  hipLaunchKernelGGL((k_unit_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo, g.packed,
-                     coff, g.units, g.unit_total, nidx, ncnt, cap);
-  SPHOPS_LAUNCHED();
-  run_candidate_schedule(g, g.sparse_len, g.cand_order, g.cand_waves, g.cand_wave_total, st);
-  hipLaunchKernelGGL((k_scan_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, bo, g.packed,
-                     coff, g.cand_order, g.cand_waves, g.cand_wave_total, nidx, ncnt, cap);
+  hipLaunchKernelGGL((k_lane_fill<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, g.packed, coff, g.sparse_len,
+                     g.ranges, nidx, ncnt, cap);
   SPHOPS_LAUNCHED();
 }
 

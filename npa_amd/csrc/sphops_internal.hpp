@@ -49,15 +49,16 @@ struct Grid {
   uint32_t* chunk_lo = nullptr;   // n_chunks + 1
   uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
   float4* packed = nullptr;       // B*N (x, y, z|0, weight) read by the pair kernels
-  int32_t* cand_order = nullptr;  // B*N particles in candidate-scan schedule order
-  uint2* cand_waves = nullptr;    // candidate-scan wave descriptors (neighbour_wave_capacity)
-  int32_t* cand_wave_total = nullptr;  // number of candidate-scan waves (device)
-  // cell-major list fill of dense cells (at least kDenseCell particles):
-  int32_t* sparse_len = nullptr;  // B*N: stencil candidate count of particles in sparse cells, -1 in dense ones
+  // work split of the neighbour-list fill:
+  int32_t* sparse_len = nullptr;  // B*N: candidate count of particles filled a lane each, -1 for the others
   int32_t* unit_len = nullptr;    // B*N: particles of the unit starting at this particle, 0 if none starts here
   uint2* units = nullptr;         // B*N: unit descriptors {first particle, particles}
   int32_t* unit_total = nullptr;  // number of units (device)
-  const void* cand_key[2] = {nullptr, nullptr};  // (positions, bin_offsets) the schedule was built for
+  int n_ranges = 0;               // stencil ranges per particle (rows in grid mode, cells in particle mode)
+  uint2* ranges = nullptr;        // B*N*n_ranges: stencil ranges, stored by unit-first and lone particles
+  // (positions, bin_offsets) of the last neighbour_candidates call: the fill
+  // reads the work split and ranges that call left and must get the same
+  mutable const void* split_key[2] = {nullptr, nullptr};
 };
 
 // binning.hip
@@ -123,21 +124,19 @@ void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, 
                             uint2* waves2, int32_t* wave_total2, hipStream_t st);
 // upper bound of the number of waves a schedule can hold
 uint64_t neighbour_wave_capacity(const Grid& g);
-// Candidate-scan schedule: as the pair-kernel schedule, classes by stencil
-// candidate count (from the scanned offsets coff; kScanClasses / kScanGroups).
-// Only particles with sparse_len >= 0 are scheduled.
-void run_candidate_schedule(const Grid& g, const int32_t* sparse_len, int32_t* order, uint2* waves,
-                            int32_t* wave_total, hipStream_t st);
 // Units of the cell-major fill: units[u] = {first particle, count} for every
 // particle k with unit_len[k] > 0 (flags[k] = 1 there, 0 elsewhere), in
 // particle order; their number goes to unit_total.  Scans flags in place.
 void run_unit_schedule(const Grid& g, hipStream_t st);
-// Cells holding at least kDenseCell particles have their neighbour lists
-// filled cell-major, in units of at most kUnitParticles particles of one
-// cell served by one wave; the other particles by the grouped candidate scan.
-constexpr int32_t kDenseCell = 8;
-constexpr int32_t kUnitParticles = 16;
-// Work classes of the list traversal and the candidate scan: class q holds
+// Neighbour-list fill: cells of two or more particles, and lone particles
+// with at least kLaneMaxCand stencil candidates, are filled cell-major in
+// units of at most kUnitParticles particles of one cell, one wave per unit;
+// the other lone particles one lane each.
+constexpr int32_t kLaneMaxCand = 64;
+// Largest neighbour-list index buffer (entries): byte offsets into it fit in 32 bits.
+constexpr int64_t kMaxListEntries = (int64_t)1 << 30;
+constexpr int32_t kUnitParticles = 8;
+// Work classes of the list traversal: class q holds
 // the items whose length is <= t[q] (and above the previous bound), the last
 // class the rest; each class is served by groups of g[q] lanes per particle
 // (a power of two <= 64).  Bounds double from class to class, and so do the
@@ -156,9 +155,6 @@ constexpr GroupSizes kListGroups{{1, 1, 2, 4, 8, 16, 32, 64}};
 // lane-split channel kernels: four lanes (channel slices) per pair stream,
 // 1, 1, 1, 1, 4, 8, 16, 16 streams per particle (about 12-48 pairs each)
 constexpr GroupSizes kSplitGroups{{4, 4, 4, 4, 16, 32, 64, 64}};
-// stencil candidates: 32-64 candidates per lane, at most 16 lanes per particle
-constexpr ClassBounds kScanClasses{{64, 128, 256, 512, 1024, 2048, 4096}};
-constexpr GroupSizes kScanGroups{{1, 1, 2, 4, 8, 16, 16, 16}};
 void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
