@@ -117,6 +117,39 @@ __global__ __launch_bounds__(kThreads) void k_scan_apply(const uint32_t* in, uin
   if (total_out && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *total_out = off + tot;
 }
 
+// Scan one tile with its offset computed in place: the sum of partials[0 ..
+// tile), reduced by the workgroup (no separate scan of the partials).
+__global__ __launch_bounds__(kThreads) void k_scan_apply_flat(const uint32_t* in, uint32_t* out, uint64_t n,
+                                                              const uint32_t* __restrict__ partials,
+                                                              uint32_t* total_out) {
+  __shared__ uint32_t sm[kThreads / 64];
+  const uint32_t tile = blockIdx.x;
+  uint32_t pre = 0;
+  for (uint32_t i = threadIdx.x; i < tile; i += kThreads) pre += partials[i];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) pre += __shfl_down(pre, off, 64);
+  if (lane == 0) sm[wave] = pre;
+  __syncthreads();
+  uint32_t off = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) off += sm[w];
+  __syncthreads();
+  const uint64_t base = (uint64_t)tile * kTile + (uint64_t)threadIdx.x * kItems;
+  uint32_t v[kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) v[i] = (base + i < n) ? in[base + i] : 0u;
+  const uint32_t tot = block_exclusive_scan(v, sm);
+#pragma unroll
+  for (int i = 0; i < kItems; ++i)
+    if (base + i < n) out[base + i] = v[i] + off;
+  if (total_out && tile == gridDim.x - 1 && threadIdx.x == 0) *total_out = off + tot;
+}
+
+// Tile counts up to this take the two-launch scan (partial sums, then each
+// tile reduces the partials before it); larger ones recurse.
+constexpr uint64_t kFlatScanTiles = 8192;
+
 }  // namespace
 
 uint64_t scan_tmp_elems(uint64_t n) {
@@ -145,6 +178,11 @@ void device_exclusive_scan(const uint32_t* in, uint32_t* out, uint64_t n, uint32
   uint32_t* partials = tmp;
   hipLaunchKernelGGL(k_scan_reduce, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, n, partials);
   SPHOPS_LAUNCHED();
+  if (tiles <= kFlatScanTiles) {
+    hipLaunchKernelGGL(k_scan_apply_flat, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n, partials, total);
+    SPHOPS_LAUNCHED();
+    return;
+  }
   device_exclusive_scan(partials, partials, tiles, tmp + tiles + kTile, nullptr, st);
   hipLaunchKernelGGL(k_scan_apply, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n, partials, total);
   SPHOPS_LAUNCHED();
