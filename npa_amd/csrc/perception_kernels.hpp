@@ -1040,7 +1040,18 @@ __device__ __forceinline__ uint32_t quad_get(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, Q * 0x55, 0xF, 0xF, false);
 }
 
-template <int D, bool P, int CW, bool FULL>
+// Start of the channel slice [c0, c0 + CW) of row j of a (rows, stride)
+// float array: with OFF32 a 32-bit byte offset from the (uniform) base, so
+// the load takes a scalar base and one vector offset register; the launcher
+// selects OFF32 only when every byte offset of the array fits in 32 bits.
+template <bool OFF32>
+__device__ __forceinline__ const float* row_slice(const float* __restrict__ base, uint32_t j, uint32_t stride,
+                                                  uint32_t c0) {
+  if constexpr (OFF32) return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + (j * stride + c0) * 4u);
+  return base + (uint64_t)j * stride + c0;
+}
+
+template <int D, bool P, int CW, bool FULL, bool OFF32>
 __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
   const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
@@ -1128,20 +1139,18 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
         else { SPHOPS_QUAD_FETCH(3) }
 #undef SPHOPS_QUAD_FETCH
         float gbj[CW], ggj[CW * D];
-        load_span<CW, true>(a.g + (uint64_t)j * C + c0, gbj);
-        load_span<CW * D, true>(a.g2 + ((uint64_t)j * C + c0) * D, ggj);
+        load_span<CW, true>(row_slice<OFF32>(a.g, j, C, c0), gbj);
+        load_span<CW * D, true>(row_slice<OFF32>(a.g2, j, C * D, c0 * D), ggj);
         if constexpr (!FULL) {
 #pragma unroll
           for (int f = 0; f < CW; ++f) {
             dsb[f] += W * gbj[f];
-            float pf = 0.0f;
 #pragma unroll
-            for (int e = 0; e < D; ++e) pf += ggj[f * D + e] * w[e];
-            dsg[f] += pf;
+            for (int e = 0; e < D; ++e) dsg[f] += ggj[f * D + e] * w[e];
           }
         } else {
           float sj[CW];
-          load_span<CW, true>(a.s + (uint64_t)j * C + c0, sj);
+          load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
           float A = 0.0f, Bv = 0.0f;
           float u1[D] = {}, u2[D] = {};
 #pragma unroll
@@ -1149,17 +1158,14 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
             dsb[f] += W * gbj[f];
             A += gbi[f] * sj[f];
             Bv += gbj[f] * si[f];
-            float pf = 0.0f;
             const float df = si[f] - sj[f];
 #pragma unroll
             for (int e = 0; e < D; ++e) {
-              pf += ggj[f * D + e] * w[e];
+              dsg[f] += ggj[f * D + e] * w[e];
               u1[e] += df * ggj[f * D + e];
               u2[e] += df * ggi[f * D + e];
             }
-            dsg[f] += pf;
           }
-          drb += W * Bv;
           const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
           float u[D], uw = 0.0f, rv = 0.0f;
 #pragma unroll
@@ -1175,213 +1181,7 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
         }
       }
     }
-  }
-  grp_sum_streams(G, dsb, dsg);
-  grp_sum(G, wsum);
-  if constexpr (FULL) grp_sum(G, dxb, dxg, drb, drg);
-#pragma unroll
-  for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
-  if (active && stream == 0) {
-    const float sb = vi * g.c6;
-#pragma unroll
-    for (int f = 0; f < CW; ++f) {
-      float t = vi * dsg[f];
-#pragma unroll
-      for (int e = 0; e < D; ++e) t += ggi[f * D + e] * wsum[e];
-      a.out1[(uint64_t)k * C + c0 + f] = dsb[f] * sb + t * g.cs;
-    }
-    if constexpr (FULL) {
-      if (slice == 0) {
-        a.out2[k] = -mr2 * (drb * g.c6 + drg * g.cs);
-        float dx[D];
-#pragma unroll
-        for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6 + dxg[e] * g.cs;
-        store_pos_grad<D>(a.out0, k, dx, 1.0f);
-      }
-    }
-  }
-}
-
-// Broadcast lane q's value to its quad (q a compile-time constant after
-// unrolling).
-template <class T>
-__device__ __forceinline__ T quad_bcast(T v, int q) {
-  if (q == 0) return quad_get<0>(v);
-  if (q == 1) return quad_get<1>(v);
-  if (q == 2) return quad_get<2>(v);
-  return quad_get<3>(v);
-}
-
-// N floats at a 16-byte aligned byte offset `off` from a uniform base: global
-// loads with a scalar base and a 32-bit vector offset (the launcher checks
-// that every offset fits in 32 bits).
-template <int N>
-__device__ __forceinline__ void load_off(const float* __restrict__ base, uint32_t off, float* v) {
-  const char* p = reinterpret_cast<const char*>(base) + off;
-#pragma unroll
-  for (int u = 0; u < N / 4; ++u) {
-    const float4 t = *reinterpret_cast<const float4*>(p + 16 * u);
-    v[4 * u + 0] = t.x;
-    v[4 * u + 1] = t.y;
-    v[4 * u + 2] = t.z;
-    v[4 * u + 3] = t.w;
-  }
-}
-
-// One neighbour's channel slice for the pass-B backward: blur upstream,
-// gradient upstream and (FULL) state.
-template <int D, int CW, bool FULL>
-struct PassBRows {
-  float gb[CW];
-  float gg[CW * D];
-  float s[FULL ? CW : 1];
-  __device__ __forceinline__ void load(const OpPtrs& a, uint32_t j, uint32_t off_s, uint32_t off_g) {
-    constexpr uint32_t RS = 16u * CW, RG = 16u * CW * D;  // bytes per row of s / g and of g2
-    load_off<CW>(a.g, j * RS + off_s, gb);
-    load_off<CW * D>(a.g2, j * RG + off_g, gg);
-    if constexpr (FULL) load_off<CW>(a.s, j * RS + off_s, s);
-  }
-};
-
-// Pass-B backward, software-pipelined form of k_blur_hybrid_bwd_quad (same
-// layout and formulas): the index and packed position of the next quad
-// iteration's owned pair are loaded one iteration ahead, and the rows of pair
-// q + 1 while pair q is computed (two row buffers).  Pairs past the end of a
-// stream are computed against the particle itself with all weights zero, so
-// the four pair blocks of an iteration have no branches.  dL/drho of blur is
-// taken from the slice's dL/ds sum at the end (sum_j W_j g_j . s_i =
-// s_i . sum_j W_j g_j).
-template <int D, bool P, int CW, bool FULL, int WAVES>
-__global__ __launch_bounds__(kThreads, WAVES) void k_blur_hybrid_bwd_pipe(GridParams g, OpPtrs a) {
-  constexpr int C = 4 * CW;
-  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (wave >= a.nwaves2) return;
-  const uint2 wd = a.waves2[wave];
-  const int G = (int)(wd.y >> 8);
-  const int lane = __lane_id();
-  const uint32_t slot = (uint32_t)(lane / G);
-  const int sub = lane & (G - 1);
-  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
-  const bool active = slot < (wd.y & 0xFFu);
-  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
-  const uint32_t c0 = (uint32_t)slice * CW;
-  const uint32_t off_s = c0 * 4u, off_g = c0 * 4u * D;
-  const float4* __restrict__ xw = a.xw;
-  float xi[3] = {0.0f, 0.0f, 0.0f};
-  float vi = 0.0f, mr2 = 0.0f;
-  float si[FULL ? CW : 1] = {}, gbi[FULL ? CW : 1] = {};
-  float ggi[CW * D] = {};
-  float dsb[CW] = {}, dsg[CW] = {};
-  float wsum[D] = {};
-  float dxb[D] = {}, dxg[D] = {};
-  float drb = 0.0f, drg = 0.0f;
-  if (active) {
-    unpack(xw[k], xi);
-    const float mi = a.m[k], ri = a.rho[k];
-    vi = mi / ri;
-    mr2 = mi / (ri * ri);
-    load_off<CW * D>(a.g2, k * (16u * CW * D) + off_g, ggi);
-    if constexpr (FULL) {
-      load_off<CW>(a.s, k * (16u * CW) + off_s, si);
-      load_off<CW>(a.g, k * (16u * CW) + off_s, gbi);
-    }
-    const int32_t* __restrict__ nidx = a.nidx;
-    const int start = a.nptr[k];
-    const int end = start + a.ncnt[k];
-    const int step = 4 * S;
-    int to = start + stream + slice * S;  // position of the pair this lane owns in the current iteration
-    uint32_t jn = to < end ? (uint32_t)nidx[to] : k;
-    float4 pn = xw[jn];
-    uint32_t jn2 = to + step < end ? (uint32_t)nidx[to + step] : k;
-    PassBRows<D, CW, FULL> rb_[2];
-    rb_[0].load(a, quad_get<0>(jn), off_s, off_g);
-    for (int t0 = start + stream; t0 < end; t0 += step, to += step) {
-      const uint32_t jo = jn;
-      const float4 pj = pn;
-      const bool own = to < end;
-      jn = jn2;
-      pn = xw[jn];
-      jn2 = to + 2 * step < end ? (uint32_t)nidx[to + 2 * step] : k;
-      // geometry of the pair this lane owns (all zero past the end)
-      float vo = 0.0f, Wo = 0.0f, t2o = 0.0f, jao = 0.0f, jbo = 0.0f;
-      float rbo[3] = {0.0f, 0.0f, 0.0f}, wo[3] = {0.0f, 0.0f, 0.0f};
-      if (own) {
-        float xj[3], r[3];
-        unpack(pj, xj);
-        vo = pj.w;
-        const float d2 = displacement<D, P>(g, xi, xj, r);
-        const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
-        Wo = poly6(g.eps2, db);
-        float d;
-        const float mag = spiky_mag(g.eps, db, &d);
-#pragma unroll
-        for (int e = 0; e < D; ++e) {
-          wo[e] = mag * rbo[e];
-          wsum[e] += vo * wo[e];
-        }
-        if constexpr (FULL) {
-          if (db != 0.0f && db < g.eps2) {
-            const float tt = g.eps2 - db;
-            t2o = -6.0f * tt * tt;
-            const float di = fast_rcp(d);
-            jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
-            jbo = 3.0f * (g.eps2 - db) * di * di * di;
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q < 3) rb_[(q + 1) & 1].load(a, quad_bcast(jo, q + 1), off_s, off_g);
-        else rb_[0].load(a, quad_get<0>(jn), off_s, off_g);
-        const PassBRows<D, CW, FULL>& R = rb_[q & 1];
-        const float W = quad_bcast(Wo, q);
-        float w[3];
-#pragma unroll
-        for (int e = 0; e < D; ++e) w[e] = quad_bcast(wo[e], q);
-        if constexpr (!FULL) {
-#pragma unroll
-          for (int f = 0; f < CW; ++f) {
-            dsb[f] += W * R.gb[f];
-#pragma unroll
-            for (int e = 0; e < D; ++e) dsg[f] += R.gg[f * D + e] * w[e];
-          }
-        } else {
-          const float vj = quad_bcast(vo, q), t2 = quad_bcast(t2o, q);
-          const float ja = quad_bcast(jao, q), jb = quad_bcast(jbo, q);
-          float rb[3];
-#pragma unroll
-          for (int e = 0; e < D; ++e) rb[e] = quad_bcast(rbo[e], q);
-          float A = 0.0f, Bv = 0.0f;
-          float u1[D] = {}, u2[D] = {};
-#pragma unroll
-          for (int f = 0; f < CW; ++f) {
-            dsb[f] += W * R.gb[f];
-            A += gbi[f] * R.s[f];
-            Bv += R.gb[f] * si[f];
-            const float df = si[f] - R.s[f];
-#pragma unroll
-            for (int e = 0; e < D; ++e) {
-              dsg[f] += R.gg[f * D + e] * w[e];
-              u1[e] += df * R.gg[f * D + e];
-              u2[e] += df * ggi[f * D + e];
-            }
-          }
-          const float m6 = t2 * (A * vj + Bv * vi);  // t2 = -6 (h^2 - r^2)^2, 0 outside (0, h)
-          float u[D], uw = 0.0f, rv = 0.0f;
-#pragma unroll
-          for (int e = 0; e < D; ++e) {
-            dxb[e] += m6 * rb[e];
-            uw += u1[e] * w[e];
-            u[e] = vi * u1[e] + vj * u2[e];
-            rv += rb[e] * u[e];
-          }
-          drg += uw;
-#pragma unroll
-          for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
-        }
-      }
-    }
-    if constexpr (FULL) {
+    if constexpr (FULL) {  // blur's dL/drho: sum_j W_j g_j . s_i = s_i . sum_j W_j g_j
 #pragma unroll
       for (int f = 0; f < CW; ++f) drb += si[f] * dsb[f];
     }
@@ -1418,7 +1218,7 @@ __global__ __launch_bounds__(kThreads, WAVES) void k_blur_hybrid_bwd_pipe(GridPa
 // magnitude, r), the quad exchanges them by DPP, and every lane accumulates
 // its channel slice.  The moment matrix is accumulated by the owning lane,
 // reduced over the group and handed to the four slice lanes.
-template <int D, bool P, int CW>
+template <int D, bool P, int CW, bool OFF32>
 __global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
   const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
@@ -1478,7 +1278,7 @@ __global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g,
         else { SPHOPS_QUAD_FETCH(3) }
 #undef SPHOPS_QUAD_FETCH
         float sj[CW];
-        load_span<CW, true>(a.s + (uint64_t)j * C + c0, sj);
+        load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
 #pragma unroll
         for (int f = 0; f < CW; ++f) {
           blur[f] += w * sj[f];
@@ -1819,16 +1619,24 @@ inline bool split_ok(const OpPtrs& a) {
          aligned16(a.g) && aligned16(a.g2);
 }
 
+// Byte offsets into the (B*N, C*D) gradient rows fit in 32 bits.
+inline bool row_offsets_fit_32(const Grid& g, uint32_t C) {
+  return g.n_keys * (uint64_t)C * 3u * 4u <= 0xFFFFFFFFull;
+}
+
 template <int D, bool P>
 void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
   const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
   pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
+  const bool off32 = row_offsets_fit_32(g, a.C);
   if (a.C == 16) {
-    hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 4>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    if (off32) hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 4, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    else hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 4, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else {
-    hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 8>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    if (off32) hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 8, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    else hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 8, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   }
   SPHOPS_LAUNCHED();
 }
@@ -1839,24 +1647,13 @@ void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
   pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
-  const char* ev = getenv("SPHOPS_EXP_BWD");
-  const int var = ev ? atoi(ev) : 0;
-  if (var == 1) {
-    if (a.C == 16) {
-      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 4, FULL, 3>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    } else {
-      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 8, FULL, 2>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    }
-  } else if (var == 2) {
-    if (a.C == 16) {
-      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 4, FULL, 4>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    } else {
-      hipLaunchKernelGGL((k_blur_hybrid_bwd_pipe<D, P, 8, FULL, 2>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    }
-  } else if (a.C == 16) {
-    hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 4, FULL>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+  const bool off32 = row_offsets_fit_32(g, a.C);
+  if (a.C == 16) {
+    if (off32) hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 4, FULL, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    else hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 4, FULL, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else {
-    hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    if (off32) hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    else hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   }
   SPHOPS_LAUNCHED();
 }
