@@ -78,16 +78,21 @@ STEP_KERNELS = {
 }
 DOMINANT = {"full": "pass_b_bwd", "npa": "pass_b_bwd_ds"}
 
-# rocprofv3 kernel-name fragment of each timed call's pair kernel (cfg5: 3D, clamped, C = 16)
-PAIR_KERNEL = {
-    "gradient_bwd": "OpGradientBwd<3, false, 16, true, true, false>",
-    "blur_bwd": "OpBlurBwd<3, false, 16, true, true>",
-    "pass_b_fwd": "OpBlurGradientHybrid<3, false, 16, true>",
-    "pass_a_fwd": "OpDensityPair<3, false>",
-    "pass_a_bwd": "OpDensityPairBwd<3, false>",
-    "pass_b_bwd": "k_blur_hybrid_bwd_quad<3, false, 4, true>",
-    "pass_b_bwd_ds": "k_blur_hybrid_bwd_quad<3, false, 4, false>",
-}
+def pair_kernel(name, D, periodic, C):
+    """rocprofv3 kernel-name fragment of the pair kernel an operator call of
+    the step launches (the call also launches a packing kernel), or None."""
+    p = "true" if periodic else "false"
+    split = C in (16, 32)  # blur + gradient_hybrid on the lane-split kernels
+    names = {
+        "pass_a_fwd": f"OpDensityPair<{D}, {p}>",
+        "pass_a_bwd": f"OpDensityPairBwd<{D}, {p}>",
+        "pass_b_fwd": f"k_blur_hybrid_fwd_quad<{D}, {p}, {C // 4}," if split else None,
+        "pass_b_bwd": f"k_blur_hybrid_bwd_quad<{D}, {p}, {C // 4}, true," if split else None,
+        "pass_b_bwd_ds": f"k_blur_hybrid_bwd_quad<{D}, {p}, {C // 4}, false," if split else None,
+    }
+    return names.get(name)
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -207,10 +212,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"{wl.name}: 3D stress, B={B} N={N} particles from 8 Gaussians (log sigma U[0.01,0.2]), "
-                        f"C={C} fp32, h={wl.h:.6g} (32 mean neighbours), clamped grid "
-                        f"{'x'.join(map(str, wl.grid_size))}, rebin every step, "
-                        f"{'full backward' if full else 'NPA-default backward (stopgrad_pos)'}",
+            "workload": f"{wl.name}: {workloads.DESCRIPTIONS[wl.name]}; B={B} N={N} C={C} fp32, h={wl.h:.6g} "
+                        f"({workloads.TARGETS[wl.name]:g} mean neighbours), "
+                        f"{'periodic' if wl.periodic else 'clamped'} grid {'x'.join(map(str, wl.grid_size))}, "
+                        f"rebin every step, {'full backward' if full else 'NPA-default backward (stopgrad_pos)'}",
             "particles_per_step": B * N,
             "pairs_per_step": pairs,
             "particles_per_s": B * N / (ms * 1e-3),
@@ -228,7 +233,7 @@ def main():
             "traffic": traffic,
             "alg_bytes_per_launch": alg,
             "avg_launch_ms": dom_ms,
-            "pair_kernel": PAIR_KERNEL.get(dom),
+            "pair_kernel": pair_kernel(dom, D, wl.periodic, C),
             "pmc": pmc,
         },
         "cpu_baseline": cpu,
@@ -338,7 +343,7 @@ def pmc_child(args):
     print(f"[pmc-child] {args.pmc_child} done", flush=True)
 
 
-def _pmc_run(counter, kernel, args):
+def _pmc_run(counter, kernel, frag, args):
     """One rocprofv3 --pmc run of the child; returns {kernel name: mean value
     per dispatch} for the copy kernel and the operator's pair kernel."""
     import csv
@@ -375,7 +380,7 @@ def _pmc_run(counter, kernel, args):
     for (_, name), v in per_dispatch.items():
         if "copy" in name.lower():
             copy.append(v)
-        elif PAIR_KERNEL[kernel] in name:
+        elif frag in name:
             target.append(v)
     if not copy or not target:
         raise RuntimeError(f"{counter}: kernels not found in the counter output")
@@ -389,10 +394,15 @@ def measure_traffic(args, kernel):
     WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
     for a plain copy of COPY_BYTES (which must fetch and write COPY_BYTES)."""
     try:
+        from npa_amd import workloads
+        wl = workloads.make(args.config)
+        frag = pair_kernel(kernel, wl.dim, wl.periodic, wl.C)
+        if frag is None:
+            raise RuntimeError(f"no single pair kernel for {kernel} at C = {wl.C}")
         res = {"kernel": kernel, "copy_bytes": COPY_BYTES}
         total = 0.0
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            c, t = _pmc_run(counter, kernel, args)
+            c, t = _pmc_run(counter, kernel, frag, args)
             scale = COPY_BYTES / (c * 1024.0)
             res[counter] = {"copy_kib": c, "kernel_kib": t, "scale": scale, "kernel_bytes": t * 1024.0 * scale}
             total += t * 1024.0 * scale

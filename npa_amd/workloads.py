@@ -60,6 +60,15 @@ class Workload:
 
 TARGETS = {"cfg1": 20.0, "cfg2": 24.0, "cfg3": 16.0, "cfg4": 30.0, "cfg5": 32.0}
 
+# One-line description of each configuration's cloud generator.
+DESCRIPTIONS = {
+    "cfg1": "2D growing morphology, positions uniform in the unit disk",
+    "cfg2": "2D texture, positions uniform in the periodic unit box",
+    "cfg3": "2D point-cloud classification, points on 3-6 random segments with N(0, 0.02^2) jitter",
+    "cfg4": "3D Gaussian-splat growth, mixture of 4 isotropic Gaussians (sigma U[0.05, 0.2])",
+    "cfg5": "3D stress, mixture of 8 Gaussians (log sigma U[log 0.01, log 0.2])",
+}
+
 # Mean-neighbour-calibrated radii for the seeded full-size clouds.
 CALIBRATED_H = {
     "cfg1": 0.06921905279159546,
