@@ -350,10 +350,8 @@ __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint32_t* __rest
       __syncthreads();  // `first` and `wmin` are reused by the next chunk
     }
     const uint64_t c = c0 + (uint64_t)t * 4;
-    if (c + 3 < ncells_p1) {  // streaming store: the table is far larger than the caches
-      typedef int v4i __attribute__((ext_vector_type(4)));
-      const v4i v = {(int)s[0], (int)s[1], (int)s[2], (int)s[3]};
-      __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(bo + c));
+    if (c + 3 < ncells_p1) {
+      *reinterpret_cast<int4*>(bo + c) = make_int4((int)s[0], (int)s[1], (int)s[2], (int)s[3]);
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
