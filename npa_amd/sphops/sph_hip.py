@@ -98,6 +98,8 @@ class _HashGridNative:
         _check(_lib.sphops_grid_create(self._dim, self._boundary, self._mode, gs, ctypes.c_float(self._eps),
                                        self._n, self._b, self._maxp, ctypes.byref(handle)))
         self._h = handle
+        # kept on the instance: at interpreter exit module globals may already be gone
+        self._destroy = _lib.sphops_grid_destroy
         self._device = torch.device("cuda", torch.cuda.current_device())
         self._pw = 2 if self._dim == 2 else 4
         self._cells = 1
@@ -109,8 +111,9 @@ class _HashGridNative:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h:
-            _lib.sphops_grid_destroy(h)
+        destroy = getattr(self, "_destroy", None)
+        if h and destroy is not None:
+            destroy(h)
             self._h = None
 
     # ---- properties (sph_cuda.cu:3229-3237)
