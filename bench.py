@@ -37,6 +37,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg5")
     ap.add_argument("--variant", default="full", choices=["full", "npa"])
+    ap.add_argument("--mode", default="grid", choices=["grid", "particle"],
+                    help="the reference's HashGrid mode (particle: Morton order, cubic power-of-two grid)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-traffic", action="store_true",
@@ -127,7 +129,7 @@ def main():
 
     torch.cuda.set_device(0)
     t0 = time.time()
-    wl = workloads.make(args.config)
+    wl = workloads.make(args.config, mode=args.mode)
     B, N, C, D = wl.B, wl.N, wl.C, wl.dim
     P = wl.x.shape[-1]
     cells = int(np.prod(wl.grid_size)) * B
@@ -141,7 +143,7 @@ def main():
     g_blur = torch.randn(B, N, C, device=dev, generator=gen)
     g_hyb = torch.randn(B, N, C, D, device=dev, generator=gen)
     g_dg = torch.randn(B, N, D, device=dev, generator=gen)
-    grid = sp.HashGrid(dim=D, boundary="periodic" if wl.periodic else "clamped", mode="grid",
+    grid = sp.HashGrid(dim=D, boundary="periodic" if wl.periodic else "clamped", mode=wl.mode,
                        grid_size=list(wl.grid_size), eps=wl.h, num_particles=N, batch_size=B,
                        max_particles_per_block=wl.maxp)
     full = args.variant == "full"
@@ -214,7 +216,8 @@ def main():
         "config": {
             "workload": f"{wl.name}: {workloads.DESCRIPTIONS[wl.name]}; B={B} N={N} C={C} fp32, h={wl.h:.6g} "
                         f"({workloads.TARGETS[wl.name]:g} mean neighbours), "
-                        f"{'periodic' if wl.periodic else 'clamped'} grid {'x'.join(map(str, wl.grid_size))}, "
+                        f"{'periodic' if wl.periodic else 'clamped'} {wl.mode}-mode grid "
+                        f"{'x'.join(map(str, wl.grid_size))}, "
                         f"rebin every step, {'full backward' if full else 'NPA-default backward (stopgrad_pos)'}",
             "particles_per_step": B * N,
             "pairs_per_step": pairs,
@@ -326,7 +329,7 @@ def pmc_child(args):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    wl = workloads.make(args.config)
+    wl = workloads.make(args.config, mode=args.mode)
     B, N, C, D = wl.B, wl.N, wl.C, wl.dim
     dev = torch.device("cuda", 0)
     x = torch.from_numpy(wl.x).to(dev)
@@ -335,7 +338,7 @@ def pmc_child(args):
     g_blur = torch.randn(B, N, C, device=dev, generator=gen)
     g_hyb = torch.randn(B, N, C, D, device=dev, generator=gen)
     g_dg = torch.randn(B, N, D, device=dev, generator=gen)
-    grid = sp.HashGrid(dim=D, boundary="periodic" if wl.periodic else "clamped", mode="grid",
+    grid = sp.HashGrid(dim=D, boundary="periodic" if wl.periodic else "clamped", mode=wl.mode,
                        grid_size=list(wl.grid_size), eps=wl.h, num_particles=N, batch_size=B,
                        max_particles_per_block=wl.maxp)
     kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, args.variant == "full", 3, only=args.pmc_child)
@@ -356,7 +359,7 @@ def _pmc_run(counter, kernel, frag, args):
     out = tempfile.mkdtemp(prefix="npa_pmc_", dir="/tmp")
     cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "run", "--",
            sys.executable, os.path.abspath(__file__), "--pmc-child", kernel, "--config", args.config,
-           "--variant", args.variant]
+           "--variant", args.variant, "--mode", args.mode]
     env = dict(os.environ, TMPDIR="/tmp")
     r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=240)
     if r.returncode != 0 or b"[pmc-child]" not in r.stdout:
@@ -395,7 +398,7 @@ def measure_traffic(args, kernel):
     for a plain copy of COPY_BYTES (which must fetch and write COPY_BYTES)."""
     try:
         from npa_amd import workloads
-        wl = workloads.make(args.config)
+        wl = workloads.make(args.config, mode=args.mode)
         frag = pair_kernel(kernel, wl.dim, wl.periodic, wl.C)
         if frag is None:
             raise RuntimeError(f"no single pair kernel for {kernel} at C = {wl.C}")

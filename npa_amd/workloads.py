@@ -188,9 +188,13 @@ def calibrate(name, scale=1.0, iters=40):
     return float(np.float32(hi))
 
 
-def make(name, scale=1.0, seed=SEED, h=None):
+def make(name, scale=1.0, seed=SEED, h=None, mode="grid"):
     """Build a :class:`Workload`.  ``h`` defaults to the calibrated radius for
-    full-size clouds; reduced clouds get h scaled to keep the neighbour count."""
+    full-size clouds; reduced clouds get h scaled to keep the neighbour count.
+    ``mode="particle"`` gives the reference's particle (Morton) mode, whose
+    grid must be cubic with a power-of-two side of at most 1024 cells
+    (sphops/sph.py:69-71): the grid-mode extent rounded up (clamped clouds
+    only; a periodic box fixes its side)."""
     x, s = raw_points(name, scale, seed)
     D = x.shape[-1]
     if h is None:
@@ -204,7 +208,18 @@ def make(name, scale=1.0, seed=SEED, h=None):
     periodic = name == "cfg2"
     gs = grid_for(x, h, 1.0 if periodic else None)
     maxp = 32 if name in ("cfg1", "cfg2") else 64
-    return Workload(name, _pack(x), s.astype(np.float32), h, gs, periodic, maxp)
+    if mode == "particle":
+        if periodic:
+            raise ValueError(f"{name}: particle mode needs a power-of-two periodic box; not generated")
+        side = 1
+        while side < max(gs):
+            side *= 2
+        if side > 1024:
+            raise ValueError(f"{name}: particle mode needs at most 1024 cells per axis, the cloud needs {max(gs)}")
+        gs = (side,) * D
+    elif mode != "grid":
+        raise ValueError(f"unknown mode {mode!r}")
+    return Workload(name, _pack(x), s.astype(np.float32), h, gs, periodic, maxp, mode)
 
 
 if __name__ == "__main__":
