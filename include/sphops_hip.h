@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 5
+#define SPHOPS_ABI_VERSION 6
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -239,6 +239,36 @@ int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid);
  * dim x dim matrices (dim 2 or 3), identity where |det| < tol. */
 int sphops_safe_inv_sym_mat(const float* in_matrix, float* out_matrix, int64_t count, int dim, float tol,
                             void* stream);
+
+/* Perception features of NPA.perceive (models/npa.py:87-137; no counterpart
+ * in the reference's native module: the reference builds them with torch
+ * elementwise ops and torch.cat).  For `particles` rows of C channels in D =
+ * dim dimensions, z (particles, W) receives, in order:
+ *   s (C), blur (C),
+ *   if STATE_GRAD: grad_s * coef_s (C x D, row-major), log-normalised per
+ *     channel over D when LOG_NORM_GRAD,
+ *   if DENSITY_GRAD: grad_rho * coef_rho / total_mass (D), log-normalised when
+ *     LOG_NORM_DENSITY_GRAD,
+ * so W = 2C + (STATE_GRAD ? C*D : 0) + (DENSITY_GRAD ? D : 0).  The
+ * log-normalisation is log(1 + |v|) * v / max(|v|, 1e-12)
+ * (models/npa.py:83-85).  grad_s / grad_rho may be NULL when their flag is
+ * off. */
+#define SPHOPS_GLUE_STATE_GRAD 1
+#define SPHOPS_GLUE_LOG_NORM_GRAD 2
+#define SPHOPS_GLUE_DENSITY_GRAD 4
+#define SPHOPS_GLUE_LOG_NORM_DENSITY_GRAD 8
+int sphops_perception_features_forward(int dim, const float* s, const float* blur, const float* grad_s,
+                                       const float* grad_rho, float* z, int64_t particles, uint32_t C, float coef_s,
+                                       float coef_rho, float total_mass, int flags, void* stream);
+
+/* Backward of sphops_perception_features_forward: from dL/dz (particles, W)
+ * and the forward's grad_s / grad_rho, writes dL/ds, dL/dblur (particles, C),
+ * dL/dgrad_s (particles, C, D) and dL/dgrad_rho (particles, D); any output may
+ * be NULL (not computed). */
+int sphops_perception_features_backward(int dim, const float* dz, const float* grad_s, const float* grad_rho,
+                                        float* d_s, float* d_blur, float* d_grad_s, float* d_grad_rho,
+                                        int64_t particles, uint32_t C, float coef_s, float coef_rho,
+                                        float total_mass, int flags, void* stream);
 
 #ifdef __cplusplus
 }

@@ -649,4 +649,37 @@ int sphops_safe_inv_sym_mat(const float* in, float* out, int64_t count, int dim,
   });
 }
 
+int sphops_perception_features_forward(int dim, const float* s, const float* blur, const float* grad_s,
+                                       const float* grad_rho, float* z, int64_t particles, uint32_t C, float coef_s,
+                                       float coef_rho, float total_mass, int flags, void* stream) {
+  return guarded([&] {
+    require(dim == 2 || dim == 3, "dim must be 2 or 3");
+    require(particles >= 0, "particles must be >= 0");
+    sphops::check_channels(C);
+    require(particles == 0 || (s && blur && z), "null buffer");
+    require(particles == 0 || !(flags & SPHOPS_GLUE_STATE_GRAD) || grad_s, "grad_s must not be NULL");
+    require(particles == 0 || !(flags & SPHOPS_GLUE_DENSITY_GRAD) || grad_rho, "grad_rho must not be NULL");
+    sphops::run_glue_forward(dim, s, blur, grad_s, grad_rho, z, (uint64_t)particles, C, coef_s, coef_rho,
+                             total_mass, flags, sphops::as_stream(stream));
+  });
+}
+
+int sphops_perception_features_backward(int dim, const float* dz, const float* grad_s, const float* grad_rho,
+                                        float* d_s, float* d_blur, float* d_grad_s, float* d_grad_rho,
+                                        int64_t particles, uint32_t C, float coef_s, float coef_rho,
+                                        float total_mass, int flags, void* stream) {
+  return guarded([&] {
+    require(dim == 2 || dim == 3, "dim must be 2 or 3");
+    require(particles >= 0, "particles must be >= 0");
+    sphops::check_channels(C);
+    require(particles == 0 || dz, "null buffer");
+    require(particles == 0 || !d_grad_s || !(flags & SPHOPS_GLUE_LOG_NORM_GRAD) || grad_s,
+            "grad_s must not be NULL");
+    require(particles == 0 || !d_grad_rho || !(flags & SPHOPS_GLUE_LOG_NORM_DENSITY_GRAD) || grad_rho,
+            "grad_rho must not be NULL");
+    sphops::run_glue_backward(dim, dz, grad_s, grad_rho, d_s, d_blur, d_grad_s, d_grad_rho, (uint64_t)particles, C,
+                              coef_s, coef_rho, total_mass, flags, sphops::as_stream(stream));
+  });
+}
+
 }  // extern "C"

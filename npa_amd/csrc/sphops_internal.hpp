@@ -7,6 +7,7 @@
 #include <string>
 
 #include "sphops_device.hpp"
+#include "sphops_hip.h"
 
 namespace sphops {
 
@@ -156,6 +157,13 @@ constexpr GroupSizes kListGroups{{1, 1, 2, 4, 8, 16, 32, 64}};
 // 1, 1, 1, 1, 4, 8, 16, 16 streams per particle (about 12-48 pairs each)
 constexpr GroupSizes kSplitGroups{{4, 4, 4, 4, 16, 32, 64, 64}};
 void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
+// perceive_glue.hip: perception features of NPA.perceive (include/sphops_hip.h)
+void run_glue_forward(int dim, const float* s, const float* blur, const float* grad_s, const float* grad_rho,
+                      float* z, uint64_t n, uint32_t C, float coef_s, float coef_rho, float total_mass, int flags,
+                      hipStream_t st);
+void run_glue_backward(int dim, const float* dz, const float* grad_s, const float* grad_rho, float* d_s,
+                       float* d_blur, float* d_grad_s, float* d_grad_rho, uint64_t n, uint32_t C, float coef_s,
+                       float coef_rho, float total_mass, int flags, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
 

@@ -21,6 +21,8 @@ sph          float64 SPH operators (forward and explicit gather-form backward)
 bruteforce   dense all-pairs float64/float32 torch restatement of
              ``sphops/torch_sph.py`` with autograd backward; pins ``sph`` and is
              the timed CPU baseline ("port").
+perceive     torch restatement of NPA.perceive's feature assembly (scaling,
+             log-normalisation, concatenation; ``models/npa.py:83-137``).
 
 Pinning status (what checks each function; see tests/test_oracle_*.py)
 ---------------------------------------------------------------------
@@ -34,6 +36,9 @@ Pinning status (what checks each function; see tests/test_oracle_*.py)
 * sph backward: equality with torch.autograd of ``bruteforce`` in float64 and
   ``torch.autograd.gradcheck``.
 * safe inverse: product with the input is the identity; identity below tol.
+* perceive: the log-normalisation's closed form (length log(1 + |v|), direction
+  of v, zero at zero), torch.autograd.gradcheck in float64, and an independent
+  closed-form Jacobian (tests/test_perceive_glue.py).
 No function is left "parity unpinned".  The reference holds no golden vectors
 for this path (it draws random data at run time, ``sphops/test.py:107-154``).
 """

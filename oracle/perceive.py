@@ -1,0 +1,38 @@
+"""NPA.perceive's feature assembly, restated in torch (TEST INFRASTRUCTURE ONLY).
+
+Follows ``models/npa.py:83-85`` (``_log_normalize_grad``) and
+``models/npa.py:106-135`` (the scaling of the state gradient by eps/eps0, of the
+density gradient by (eps/eps0)^(1+D)/N, the optional log-normalisations and the
+concatenation [s, blur, grad_s.view(B, N, C*D), grad_rho]).  Works in any
+dtype; the tests run it in float64 on the CPU as the checker of the fused HIP
+kernels.
+"""
+import torch
+
+
+def log_normalize(v):
+    """log(1 + |v|) * v / max(|v|, 1e-12) over the last axis (models/npa.py:83-85)."""
+    n = v.norm(dim=-1, keepdim=True)
+    return torch.log(1.0 + n) * torch.nn.functional.normalize(v, dim=-1)
+
+
+def features(s, blur, grad_s, grad_rho, eps, eps0, log_norm_grad=True, log_norm_density_grad=True):
+    """z of NPA.perceive from the operator outputs; grad_s / grad_rho may be
+    None (state_grad / density_grad off).  eps0 as the model's float32 buffer."""
+    B, N, C = s.shape
+    coef = torch.tensor([eps], dtype=torch.float32) / torch.tensor([eps0], dtype=torch.float32)
+    coef = coef.to(device=s.device, dtype=s.dtype)
+    z = [s, blur]
+    if grad_s is not None:
+        g = grad_s * coef
+        if log_norm_grad:
+            g = log_normalize(g)
+        z.append(g.reshape(B, N, -1))
+    if grad_rho is not None:
+        D = grad_rho.shape[-1]
+        gr = grad_rho * (coef ** (1 + D))
+        gr = gr / N
+        if log_norm_density_grad:
+            gr = log_normalize(gr)
+        z.append(gr)
+    return torch.cat(z, dim=-1)
