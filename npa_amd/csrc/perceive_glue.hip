@@ -7,9 +7,8 @@
 // (models/npa.py:83-85), density_gradient * coef^(1+D) / N and its
 // log-normalisation, then torch.cat([s, blur, grad_s.view(B, N, C*D),
 // grad_rho], -1).  Here one kernel writes z from the four operator outputs
-// and one kernel maps dL/dz back to them.  One thread serves one (particle,
-// channel): it moves channel c of s and blur and the D components of
-// grad_s[c]; channel 0 also serves the density gradient.
+// and one kernel maps dL/dz back to them.  Both are bound by HBM: z and the
+// operator outputs are read or written once each, through an LDS tile.
 #include "sphops_internal.hpp"
 
 namespace sphops {
@@ -56,38 +55,138 @@ __device__ __forceinline__ void log_normalize_backward(const float* v, float* w)
   for (int e = 0; e < D; ++e) w[e] = a * w[e] + b * vw * v[e];
 }
 
+// Particles per workgroup: a tile of T rows of z (W floats each) lives in LDS,
+// so every global access is a contiguous, coalesced run: the tile's slices of
+// s, blur, grad_s, grad_rho (and of d_s ... on the way back) and its rows of z.
+constexpr uint32_t kTileFloats = 5120;  // 20 KiB; W <= 5 * 64 + 3 for C <= 64
+
+__host__ __device__ inline uint32_t feature_width(uint32_t C, int D, int flags) {
+  return 2u * C + ((flags & SPHOPS_GLUE_STATE_GRAD) ? C * (uint32_t)D : 0u) +
+         ((flags & SPHOPS_GLUE_DENSITY_GRAD) ? (uint32_t)D : 0u);
+}
+
+inline uint32_t tile_particles(uint32_t W) { return std::min<uint32_t>(64u, kTileFloats / W); }
+
+// i / d and i % d for i < 2^24: a float quotient, then one correction step
+__device__ __forceinline__ uint32_t div_small(uint32_t i, uint32_t d, float inv_d, uint32_t& r) {
+  uint32_t q = (uint32_t)(((float)i + 0.5f) * inv_d);
+  int32_t rr = (int32_t)i - (int32_t)(q * d);
+  if (rr < 0) {
+    --q;
+    rr += (int32_t)d;
+  } else if (rr >= (int32_t)d) {
+    ++q;
+    rr -= (int32_t)d;
+  }
+  r = (uint32_t)rr;
+  return q;
+}
+
+// A tile's rows of z and its slices of s, blur, grad_s, grad_rho hold the same
+// number of floats, t * W.  Index i of that range maps to one source (or
+// destination) float and one element of the LDS tile: seg_of() gives both.
+// Each thread moves the indices tid + kThreads * m, all loads issued before
+// the LDS writes, so a wave keeps kSlots loads in flight.
+constexpr int kSlots = (int)(kTileFloats / kThreads);
+static_assert(kSlots * kThreads == (int)kTileFloats, "tile must split evenly over the threads");
+
+struct TileMap {
+  uint32_t C, CD, D, W, o, tC, tCD;  // o: offset of the density gradient in a row of z
+  float invC, invCD;
+  // segment of index i (0 s, 1 blur, 2 grad_s, 3 grad_rho), its offset j in
+  // that segment's slice, and the matching element of the tile
+  __device__ __forceinline__ int seg_of(uint32_t i, uint32_t& j, uint32_t& e) const {
+    uint32_t r;
+    if (i < 2u * tC) {
+      const int sgm = i < tC ? 0 : 1;
+      j = sgm ? i - tC : i;
+      const uint32_t p = div_small(j, C, invC, r);
+      e = p * W + (sgm ? C : 0u) + r;
+      return sgm;
+    }
+    if (i < 2u * tC + tCD) {
+      j = i - 2u * tC;
+      const uint32_t p = div_small(j, CD, invCD, r);
+      e = p * W + 2u * C + r;
+      return 2;
+    }
+    j = i - 2u * tC - tCD;
+    const uint32_t p = j / D;
+    e = p * W + o + (j - p * D);
+    return 3;
+  }
+};
+
+template <int D>
+__device__ __forceinline__ TileMap tile_map(uint32_t C, uint32_t t, int flags) {
+  const bool sg = flags & SPHOPS_GLUE_STATE_GRAD;
+  TileMap m;
+  m.C = C;
+  m.CD = C * D;
+  m.D = D;
+  m.W = feature_width(C, D, flags);
+  m.o = 2u * C + (sg ? m.CD : 0u);
+  m.tC = t * C;
+  m.tCD = sg ? t * m.CD : 0u;
+  m.invC = 1.0f / (float)C;
+  m.invCD = 1.0f / (float)m.CD;
+  return m;
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_glue_forward(const float* __restrict__ s, const float* __restrict__ blur,
                                                            const float* __restrict__ grad_s,
                                                            const float* __restrict__ grad_rho, float* __restrict__ z,
-                                                           uint64_t n, uint32_t C, float coef_s, float coef_rho,
-                                                           float total_mass, int flags) {
-  const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (t >= n * C) return;
-  const uint64_t k = t / C;
-  const uint32_t c = (uint32_t)(t - k * C);
-  const bool sg = flags & SPHOPS_GLUE_STATE_GRAD, lng = flags & SPHOPS_GLUE_LOG_NORM_GRAD;
-  const bool dg = flags & SPHOPS_GLUE_DENSITY_GRAD, lnd = flags & SPHOPS_GLUE_LOG_NORM_DENSITY_GRAD;
-  const uint64_t W = 2u * C + (sg ? (uint64_t)C * D : 0u) + (dg ? D : 0u);
-  float* zr = z + k * W;
-  zr[c] = s[k * C + c];
-  zr[C + c] = blur[k * C + c];
-  if (sg) {
-    float v[D];
+                                                           uint64_t n, uint32_t C, uint32_t T, float coef_s,
+                                                           float coef_rho, float total_mass, int flags) {
+  __shared__ float tile[kTileFloats];
+  const bool lng = flags & SPHOPS_GLUE_LOG_NORM_GRAD, lnd = flags & SPHOPS_GLUE_LOG_NORM_DENSITY_GRAD;
+  const uint64_t k0 = (uint64_t)blockIdx.x * T;
+  const uint32_t t = (uint32_t)min<uint64_t>(T, n - k0);
+  const TileMap mp = tile_map<D>(C, t, flags);
+  const uint32_t tW = t * mp.W, tid = threadIdx.x;
+  const float f_rho = coef_rho / total_mass;
+  s += k0 * C;
+  blur += k0 * C;
+  grad_s += k0 * mp.CD;
+  grad_rho += k0 * D;
+  float val[kSlots];
 #pragma unroll
-    for (int e = 0; e < D; ++e) v[e] = grad_s[(k * C + c) * D + e] * coef_s;
-    if (lng) log_normalize<D>(v);
-#pragma unroll
-    for (int e = 0; e < D; ++e) zr[2u * C + c * D + e] = v[e];
+  for (int m = 0; m < kSlots; ++m) {
+    const uint32_t i = tid + kThreads * m;
+    if (i < tW) {
+      uint32_t j, e;
+      const int g = mp.seg_of(i, j, e);
+      const float* src = g == 0 ? s : g == 1 ? blur : g == 2 ? grad_s : grad_rho;
+      val[m] = src[j];
+    }
   }
-  if (dg && c == 0) {
-    float v[D];
 #pragma unroll
-    for (int e = 0; e < D; ++e) v[e] = grad_rho[k * D + e] * coef_rho / total_mass;
-    if (lnd) log_normalize<D>(v);
-    const uint64_t o = 2u * C + (sg ? (uint64_t)C * D : 0u);
+  for (int m = 0; m < kSlots; ++m) {
+    const uint32_t i = tid + kThreads * m;
+    if (i < tW) {
+      uint32_t j, e;
+      const int g = mp.seg_of(i, j, e);
+      tile[e] = val[m] * (g < 2 ? 1.0f : g == 2 ? coef_s : f_rho);
+    }
+  }
+  __syncthreads();
+  if (mp.tCD && lng) {
+    for (uint32_t v = tid; v < mp.tC; v += kThreads) {
+      uint32_t c;
+      const uint32_t p = div_small(v, C, mp.invC, c);
+      log_normalize<D>(&tile[p * mp.W + 2u * C + c * D]);
+    }
+  }
+  if ((flags & SPHOPS_GLUE_DENSITY_GRAD) && lnd) {
+    for (uint32_t p = tid; p < t; p += kThreads) log_normalize<D>(&tile[p * mp.W + mp.o]);
+  }
+  __syncthreads();
+  float* zt = z + k0 * mp.W;
 #pragma unroll
-    for (int e = 0; e < D; ++e) zr[o + e] = v[e];
+  for (int m = 0; m < kSlots; ++m) {
+    const uint32_t i = tid + kThreads * m;
+    if (i < tW) zt[i] = tile[i];
   }
 }
 
@@ -98,48 +197,65 @@ __global__ __launch_bounds__(kThreads) void k_glue_backward(const float* __restr
                                                             float* __restrict__ d_s, float* __restrict__ d_blur,
                                                             float* __restrict__ d_grad_s,
                                                             float* __restrict__ d_grad_rho, uint64_t n, uint32_t C,
-                                                            float coef_s, float coef_rho, float total_mass,
-                                                            int flags) {
-  const uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (t >= n * C) return;
-  const uint64_t k = t / C;
-  const uint32_t c = (uint32_t)(t - k * C);
-  const bool sg = flags & SPHOPS_GLUE_STATE_GRAD, lng = flags & SPHOPS_GLUE_LOG_NORM_GRAD;
-  const bool dg = flags & SPHOPS_GLUE_DENSITY_GRAD, lnd = flags & SPHOPS_GLUE_LOG_NORM_DENSITY_GRAD;
-  const uint64_t W = 2u * C + (sg ? (uint64_t)C * D : 0u) + (dg ? D : 0u);
-  const float* dr = dz + k * W;
-  if (d_s) d_s[k * C + c] = dr[c];
-  if (d_blur) d_blur[k * C + c] = dr[C + c];
-  if (sg && d_grad_s) {
-    float w[D];
+                                                            uint32_t T, float coef_s, float coef_rho,
+                                                            float total_mass, int flags) {
+  __shared__ float tile[kTileFloats];
+  const bool lng = flags & SPHOPS_GLUE_LOG_NORM_GRAD, lnd = flags & SPHOPS_GLUE_LOG_NORM_DENSITY_GRAD;
+  const uint64_t k0 = (uint64_t)blockIdx.x * T;
+  const uint32_t t = (uint32_t)min<uint64_t>(T, n - k0);
+  const TileMap mp = tile_map<D>(C, t, flags);
+  const uint32_t tW = t * mp.W, tid = threadIdx.x;
+  const float* dzt = dz + k0 * mp.W;
+  {
+    float val[kSlots];
 #pragma unroll
-    for (int e = 0; e < D; ++e) w[e] = dr[2u * C + c * D + e];
-    if (lng) {
-      float v[D];
-#pragma unroll
-      for (int e = 0; e < D; ++e) v[e] = grad_s[(k * C + c) * D + e] * coef_s;
-      log_normalize_backward<D>(v, w);
+    for (int m = 0; m < kSlots; ++m) {
+      const uint32_t i = tid + kThreads * m;
+      if (i < tW) val[m] = dzt[i];
     }
 #pragma unroll
-    for (int e = 0; e < D; ++e) d_grad_s[(k * C + c) * D + e] = w[e] * coef_s;
+    for (int m = 0; m < kSlots; ++m) {
+      const uint32_t i = tid + kThreads * m;
+      if (i < tW) tile[i] = val[m];
+    }
   }
-  if (dg && d_grad_rho && c == 0) {
-    const uint64_t o = 2u * C + (sg ? (uint64_t)C * D : 0u);
-    float w[D];
+  __syncthreads();
+  // J^T of the log-normalisations, in place; the scale factors fold in below
+  if (mp.tCD && lng && d_grad_s) {
+    for (uint32_t v = tid; v < mp.tC; v += kThreads) {
+      uint32_t c;
+      const uint32_t p = div_small(v, C, mp.invC, c);
+      float g[D];
 #pragma unroll
-    for (int e = 0; e < D; ++e) w[e] = dr[o + e];
-    if (lnd) {
-      float v[D];
-#pragma unroll
-      for (int e = 0; e < D; ++e) v[e] = grad_rho[k * D + e] * coef_rho / total_mass;
-      log_normalize_backward<D>(v, w);
+      for (int e = 0; e < D; ++e) g[e] = grad_s[(k0 * C + v) * D + e] * coef_s;
+      log_normalize_backward<D>(g, &tile[p * mp.W + 2u * C + c * D]);
     }
+  }
+  if ((flags & SPHOPS_GLUE_DENSITY_GRAD) && lnd && d_grad_rho) {
+    for (uint32_t p = tid; p < t; p += kThreads) {
+      float g[D];
 #pragma unroll
-    for (int e = 0; e < D; ++e) d_grad_rho[k * D + e] = w[e] * coef_rho / total_mass;
+      for (int e = 0; e < D; ++e) g[e] = grad_rho[(k0 + p) * D + e] * coef_rho / total_mass;
+      log_normalize_backward<D>(g, &tile[p * mp.W + mp.o]);
+    }
+  }
+  __syncthreads();
+  const float f_rho = coef_rho / total_mass;
+  float* dst0 = d_s ? d_s + k0 * C : nullptr;
+  float* dst1 = d_blur ? d_blur + k0 * C : nullptr;
+  float* dst2 = d_grad_s ? d_grad_s + k0 * mp.CD : nullptr;
+  float* dst3 = d_grad_rho ? d_grad_rho + k0 * D : nullptr;
+#pragma unroll
+  for (int m = 0; m < kSlots; ++m) {
+    const uint32_t i = tid + kThreads * m;
+    if (i < tW) {
+      uint32_t j, e;
+      const int g = mp.seg_of(i, j, e);
+      float* dst = g == 0 ? dst0 : g == 1 ? dst1 : g == 2 ? dst2 : dst3;
+      if (dst) dst[j] = tile[e] * (g < 2 ? 1.0f : g == 2 ? coef_s : f_rho);
+    }
   }
 }
-
-inline dim3 blocks(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) / kThreads)); }
 
 }  // namespace
 
@@ -147,12 +263,14 @@ void run_glue_forward(int dim, const float* s, const float* blur, const float* g
                       float* z, uint64_t n, uint32_t C, float coef_s, float coef_rho, float total_mass, int flags,
                       hipStream_t st) {
   if (n == 0) return;
+  const uint32_t T = tile_particles(feature_width(C, dim, flags));
+  const dim3 grid((uint32_t)((n + T - 1) / T));
   if (dim == 2) {
-    hipLaunchKernelGGL(k_glue_forward<2>, blocks(n * C), dim3(kThreads), 0, st, s, blur, grad_s, grad_rho, z, n, C,
-                       coef_s, coef_rho, total_mass, flags);
+    hipLaunchKernelGGL(k_glue_forward<2>, grid, dim3(kThreads), 0, st, s, blur, grad_s, grad_rho, z, n, C, T, coef_s,
+                       coef_rho, total_mass, flags);
   } else {
-    hipLaunchKernelGGL(k_glue_forward<3>, blocks(n * C), dim3(kThreads), 0, st, s, blur, grad_s, grad_rho, z, n, C,
-                       coef_s, coef_rho, total_mass, flags);
+    hipLaunchKernelGGL(k_glue_forward<3>, grid, dim3(kThreads), 0, st, s, blur, grad_s, grad_rho, z, n, C, T, coef_s,
+                       coef_rho, total_mass, flags);
   }
   SPHOPS_LAUNCHED();
 }
@@ -161,12 +279,14 @@ void run_glue_backward(int dim, const float* dz, const float* grad_s, const floa
                        float* d_blur, float* d_grad_s, float* d_grad_rho, uint64_t n, uint32_t C, float coef_s,
                        float coef_rho, float total_mass, int flags, hipStream_t st) {
   if (n == 0) return;
+  const uint32_t T = tile_particles(feature_width(C, dim, flags));
+  const dim3 grid((uint32_t)((n + T - 1) / T));
   if (dim == 2) {
-    hipLaunchKernelGGL(k_glue_backward<2>, blocks(n * C), dim3(kThreads), 0, st, dz, grad_s, grad_rho, d_s, d_blur,
-                       d_grad_s, d_grad_rho, n, C, coef_s, coef_rho, total_mass, flags);
+    hipLaunchKernelGGL(k_glue_backward<2>, grid, dim3(kThreads), 0, st, dz, grad_s, grad_rho, d_s, d_blur, d_grad_s,
+                       d_grad_rho, n, C, T, coef_s, coef_rho, total_mass, flags);
   } else {
-    hipLaunchKernelGGL(k_glue_backward<3>, blocks(n * C), dim3(kThreads), 0, st, dz, grad_s, grad_rho, d_s, d_blur,
-                       d_grad_s, d_grad_rho, n, C, coef_s, coef_rho, total_mass, flags);
+    hipLaunchKernelGGL(k_glue_backward<3>, grid, dim3(kThreads), 0, st, dz, grad_s, grad_rho, d_s, d_blur, d_grad_s,
+                       d_grad_rho, n, C, T, coef_s, coef_rho, total_mass, flags);
   }
   SPHOPS_LAUNCHED();
 }

@@ -45,11 +45,13 @@ def _ops(dim, C, seed):
 
 @pytest.mark.parametrize("dim", [2, 3])
 @pytest.mark.parametrize("fi", range(len(FLAGS)))
-def test_features_match_oracle(dim, fi):
+@pytest.mark.parametrize("C", [5, 16, 64])
+def test_features_match_oracle(dim, fi, C):
+    """C = 5 and 16 give tiles whose particle count does not divide N; C = 64
+    is the widest row (the fewest particles per tile)."""
     from npa_amd import perceive as PF
     f = dict(state_grad=True, density_grad=True, log_norm_grad=True, log_norm_density_grad=True)
     f.update(FLAGS[fi])
-    C = 16
     grid, _, _, sb, bl, gs, gr = _ops(dim, C, 100 + fi)
     eps, eps0 = grid.eps, 0.1
     coef = np.float32(np.float32(eps) / np.float32(eps0))
