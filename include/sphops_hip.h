@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 6
+#define SPHOPS_ABI_VERSION 7
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -269,6 +269,29 @@ int sphops_perception_features_backward(int dim, const float* dz, const float* g
                                         float* d_s, float* d_blur, float* d_grad_s, float* d_grad_rho,
                                         int64_t particles, uint32_t C, float coef_s, float coef_rho,
                                         float total_mass, int flags, void* stream);
+
+/* Euler update of step_euler (models/npa.py:154-204, with the position-step
+ * scaling of NPA.forward, models/npa.py:125-133; no counterpart in the
+ * reference's native module).  y (particles, dim + C) is the MLP output
+ * [a, ds]; x_bin (particles, P) with P = dim (2D) or 4 (3D, lane 3 padding);
+ * s_bin (particles, C); mask (particles) or NULL (all ones); noise
+ * (particles, P) standard normals or NULL.  Writes
+ *   dx = alpha * a * eps / (1 + |a|),
+ *   x_out = x_bin + dt * [dx, 0] * mask (+ noise * noise_std * sqrt_dt * mask),
+ *   s_out = s_bin + dt * ds * mask,
+ *   dx_norm = |dx| (particles), unless NULL. */
+int sphops_euler_update_forward(int dim, int P, const float* y, const float* x_bin, const float* s_bin,
+                                const float* mask, const float* noise, float* x_out, float* s_out, float* dx_norm,
+                                int64_t particles, uint32_t C, float alpha, float eps, float dt, float noise_std,
+                                float sqrt_dt, void* stream);
+
+/* Backward of sphops_euler_update_forward with respect to y: from dL/dx_out
+ * (particles, P), dL/ds_out (particles, C) and dL/d dx_norm (particles), any
+ * of them NULL (zero), writes dL/dy (particles, dim + C).  The gradients with
+ * respect to x_bin and s_bin are dL/dx_out and dL/ds_out themselves. */
+int sphops_euler_update_backward(int dim, int P, const float* y, const float* mask, const float* d_x_out,
+                                 const float* d_s_out, const float* d_dx_norm, float* d_y, int64_t particles,
+                                 uint32_t C, float alpha, float eps, float dt, void* stream);
 
 #ifdef __cplusplus
 }

@@ -682,4 +682,33 @@ int sphops_perception_features_backward(int dim, const float* dz, const float* g
   });
 }
 
+int sphops_euler_update_forward(int dim, int P, const float* y, const float* x_bin, const float* s_bin,
+                                const float* mask, const float* noise, float* x_out, float* s_out, float* dx_norm,
+                                int64_t particles, uint32_t C, float alpha, float eps, float dt, float noise_std,
+                                float sqrt_dt, void* stream) {
+  return guarded([&] {
+    require(dim == 2 || dim == 3, "dim must be 2 or 3");
+    require(P == (dim == 2 ? 2 : 4), "P must be 2 in 2D and 4 in 3D");
+    require(particles >= 0, "particles must be >= 0");
+    sphops::check_channels(C);
+    require(particles == 0 || (y && x_bin && s_bin && x_out && s_out), "null buffer");
+    sphops::run_euler_forward(dim, y, x_bin, s_bin, mask, noise, x_out, s_out, dx_norm, (uint64_t)particles, C,
+                              (uint32_t)P, alpha, eps, dt, noise_std, sqrt_dt, sphops::as_stream(stream));
+  });
+}
+
+int sphops_euler_update_backward(int dim, int P, const float* y, const float* mask, const float* d_x_out,
+                                 const float* d_s_out, const float* d_dx_norm, float* d_y, int64_t particles,
+                                 uint32_t C, float alpha, float eps, float dt, void* stream) {
+  return guarded([&] {
+    require(dim == 2 || dim == 3, "dim must be 2 or 3");
+    require(P == (dim == 2 ? 2 : 4), "P must be 2 in 2D and 4 in 3D");
+    require(particles >= 0, "particles must be >= 0");
+    sphops::check_channels(C);
+    require(particles == 0 || (y && d_y), "null buffer");
+    sphops::run_euler_backward(dim, y, mask, d_x_out, d_s_out, d_dx_norm, d_y, (uint64_t)particles, C, (uint32_t)P,
+                               alpha, eps, dt, sphops::as_stream(stream));
+  });
+}
+
 }  // extern "C"

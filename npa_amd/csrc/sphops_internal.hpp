@@ -164,6 +164,12 @@ void run_glue_forward(int dim, const float* s, const float* blur, const float* g
 void run_glue_backward(int dim, const float* dz, const float* grad_s, const float* grad_rho, float* d_s,
                        float* d_blur, float* d_grad_s, float* d_grad_rho, uint64_t n, uint32_t C, float coef_s,
                        float coef_rho, float total_mass, int flags, hipStream_t st);
+void run_euler_forward(int dim, const float* y, const float* x_bin, const float* s_bin, const float* mask,
+                       const float* noise, float* x_out, float* s_out, float* dx_norm, uint64_t n, uint32_t C,
+                       uint32_t P, float alpha, float eps, float dt, float noise_std, float sqrt_dt, hipStream_t st);
+void run_euler_backward(int dim, const float* y, const float* mask, const float* d_x_out, const float* d_s_out,
+                        const float* d_dx_norm, float* d_y, uint64_t n, uint32_t C, uint32_t P, float alpha,
+                        float eps, float dt, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
 

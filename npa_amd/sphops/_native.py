@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -54,6 +54,9 @@ _SIGNATURES = {
                                            _i32),
     "sphops_perception_features_backward": ([_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _u32, _f32, _f32, _f32, _i32,
                                              _p], _i32),
+    "sphops_euler_update_forward": ([_i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _u32, _f32, _f32, _f32,
+                                     _f32, _f32, _p], _i32),
+    "sphops_euler_update_backward": ([_i32, _i32, _p, _p, _p, _p, _p, _p, _i64, _u32, _f32, _f32, _f32, _p], _i32),
     "sphops_forward": ([_p, _i32, _p, _p], _i32),
     "sphops_backward": ([_p, _i32, _i32, _i32, _i32, _p, _p], _i32),
     "sphops_neighbor_candidates": ([_p, _p, _p, _p, _p], _i32),

@@ -22,7 +22,8 @@ bruteforce   dense all-pairs float64/float32 torch restatement of
              ``sphops/torch_sph.py`` with autograd backward; pins ``sph`` and is
              the timed CPU baseline ("port").
 perceive     torch restatement of NPA.perceive's feature assembly (scaling,
-             log-normalisation, concatenation; ``models/npa.py:83-137``).
+             log-normalisation, concatenation; ``models/npa.py:83-137``) and of
+             step_euler's update (``models/npa.py:125-133, 154-204``).
 
 Pinning status (what checks each function; see tests/test_oracle_*.py)
 ---------------------------------------------------------------------
@@ -39,6 +40,9 @@ Pinning status (what checks each function; see tests/test_oracle_*.py)
 * perceive: the log-normalisation's closed form (length log(1 + |v|), direction
   of v, zero at zero), torch.autograd.gradcheck in float64, and an independent
   closed-form Jacobian (tests/test_perceive_glue.py).
+* euler_update: closed forms (|dx| = alpha eps u / (1 + u), direction of a,
+  masked particles unchanged, zero padding lane unchanged), gradcheck in
+  float64, and the kernel's closed-form gradient (tests/test_perceive_glue.py).
 No function is left "parity unpinned".  The reference holds no golden vectors
 for this path (it draws random data at run time, ``sphops/test.py:107-154``).
 """

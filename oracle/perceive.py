@@ -1,4 +1,5 @@
-"""NPA.perceive's feature assembly, restated in torch (TEST INFRASTRUCTURE ONLY).
+"""NPA.perceive's feature assembly and step_euler's update, restated in torch
+(TEST INFRASTRUCTURE ONLY).
 
 Follows ``models/npa.py:83-85`` (``_log_normalize_grad``) and
 ``models/npa.py:106-135`` (the scaling of the state gradient by eps/eps0, of the
@@ -36,3 +37,24 @@ def features(s, blur, grad_s, grad_rho, eps, eps0, log_norm_grad=True, log_norm_
             gr = log_normalize(gr)
         z.append(gr)
     return torch.cat(z, dim=-1)
+
+
+def euler_update(y, x_bin, s_bin, mask, noise, alpha, eps, dt=1.0, noise_std=0.0):
+    """The tail of NPA.forward and the update of step_euler
+    (models/npa.py:125-133, 189-200): dx = alpha * a * eps / (1 + |a|) from
+    y = [a, ds], padded with zeros to x's width; x + dt * dx * mask (+ noise *
+    noise_std * sqrt(dt) * mask), s + dt * ds * mask; and |dx| per particle.
+    mask (B, N, 1) or None (all ones), noise like x or None."""
+    D = y.shape[-1] - s_bin.shape[-1]
+    a = y[..., :D]
+    dx = alpha * a * eps / (1.0 + a.norm(dim=-1, keepdim=True))
+    dx_norm = dx.norm(dim=-1)
+    ds = y[..., D:]
+    if dx.shape[-1] != x_bin.shape[-1]:
+        dx = torch.cat([dx, torch.zeros_like(dx[..., :1])], dim=-1)
+    m = 1.0 if mask is None else mask
+    x = x_bin + dt * dx * m
+    s = s_bin + dt * ds * m
+    if noise is not None and noise_std > 0:
+        x = x + noise * noise_std * (dt ** 0.5) * m
+    return x, s, dx_norm
