@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 7
+#define SPHOPS_ABI_VERSION 8
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -292,6 +292,36 @@ int sphops_euler_update_forward(int dim, int P, const float* y, const float* x_b
 int sphops_euler_update_backward(int dim, int P, const float* y, const float* mask, const float* d_x_out,
                                  const float* d_s_out, const float* d_dx_norm, float* d_y, int64_t particles,
                                  uint32_t C, float alpha, float eps, float dt, void* stream);
+
+/* Differentiable 2D Gaussian splatting (utils/splatting.py:6-117; no
+ * counterpart in the reference's native module: the reference scatters with
+ * torch.scatter_add_).  Particles of image b are rows starts[b] ..
+ * starts[b + 1] - 1 of x (particles, 2) and color (particles, ncolor);
+ * starts (images + 1 int32, device) is ascending with starts[0] = 0 and
+ * starts[images] = particles.  out (images, img_size, img_size, 4) receives
+ * [r, g, b, density] per pixel: the sum over particles of w and w * rgb
+ * (rgb = the last three colour channels), with w the particle's Gaussian
+ * weight at the pixel over a (2r+1)^2 patch around floor(pos),
+ * pos = (x - lo) / (hi - lo) * (img_size - 1) (y flipped with y_up), all as
+ * the reference's splat_particles with the same arguments computes them.
+ * Sums run in ascending particle order (deterministic).  workspace holds
+ * sphops_splat_workspace_bytes(particles) bytes of per-particle records. */
+int sphops_splat_forward(const float* x, const float* color, const int32_t* starts, int64_t images,
+                         int64_t particles, int ncolor, int img_size, double sigma, double lo, double hi,
+                         int normalize_color, int y_up, double pixel_size, float* out, void* workspace,
+                         void* stream);
+
+/* Bytes of the workspace sphops_splat_forward needs for `particles`
+ * particles (32 per particle; the caller allocates it, 16-byte aligned). */
+int64_t sphops_splat_workspace_bytes(int64_t particles);
+
+/* Backward of sphops_splat_forward: from dL/dout (images, img_size, img_size,
+ * 4), writes dL/dx (particles, 2) and dL/dcolor (particles, ncolor; zero
+ * except the last three channels). */
+int sphops_splat_backward(const float* x, const float* color, const int32_t* starts, int64_t images,
+                          int64_t particles, int ncolor, int img_size, double sigma, double lo, double hi,
+                          int normalize_color, int y_up, double pixel_size, const float* d_out, float* d_x,
+                          float* d_color, void* stream);
 
 #ifdef __cplusplus
 }

@@ -70,6 +70,35 @@ void free_grid(Grid* g) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The splat constants as utils/splatting.py:40-76 computes them in Python
+// (double) before torch rounds them to fp32.
+SplatParams splat_params(int64_t images, int64_t particles, int ncolor, int img_size, double sigma, double lo,
+                         double hi, int normalize_color, int y_up, double pixel_size) {
+  require(images >= 0 && images <= 65535, "images must be in [0, 65535]");
+  require(particles >= 0 && particles < (int64_t)1 << 31, "particles must be in [0, 2^31)");
+  require(ncolor >= 3, "color needs at least 3 channels (the last three are r, g, b)");
+  require(img_size >= 1 && img_size <= 16384, "img_size must be in [1, 16384]");
+  require(hi != lo, "hi must differ from lo");
+  double s = sigma;
+  if (normalize_color) s = sigma * img_size * pixel_size / (hi - lo);
+  require(std::isfinite(s) && s > 0.0, "sigma (in pixels) must be positive and finite");
+  const double r = std::max(1.0, std::ceil(5.0 * s));
+  require(r <= kMaxSplatRadius, "splat radius ceil(5 sigma) exceeds " + std::to_string(kMaxSplatRadius) + " pixels");
+  const double kk = img_size * pixel_size / (hi - lo);
+  SplatParams sp;
+  sp.H = img_size;
+  sp.r = (int)r;
+  sp.lo = (float)lo;
+  sp.inv_span = 1.0f / (float)(hi - lo);
+  sp.scale = (float)(img_size - 1);
+  sp.inv_two_s2 = 1.0f / (float)(2.0 * s * s);
+  sp.K = (float)(kk * kk);
+  sp.normalize = normalize_color ? 1 : 0;
+  sp.y_up = y_up ? 1 : 0;
+  sp.ncolor = ncolor;
+  return sp;
+}
+
 void check_channels(uint32_t C) {
   require(C >= 1 && C <= kMaxChannels,
           "feature_dim must be in [1, " + std::to_string(kMaxChannels) + "], got " + std::to_string(C));
@@ -708,6 +737,37 @@ int sphops_euler_update_backward(int dim, int P, const float* y, const float* ma
     require(particles == 0 || (y && d_y), "null buffer");
     sphops::run_euler_backward(dim, y, mask, d_x_out, d_s_out, d_dx_norm, d_y, (uint64_t)particles, C, (uint32_t)P,
                                alpha, eps, dt, sphops::as_stream(stream));
+  });
+}
+
+int sphops_splat_forward(const float* x, const float* color, const int32_t* starts, int64_t images,
+                         int64_t particles, int ncolor, int img_size, double sigma, double lo, double hi,
+                         int normalize_color, int y_up, double pixel_size, float* out, void* workspace,
+                         void* stream) {
+  return guarded([&] {
+    const sphops::SplatParams sp = sphops::splat_params(images, particles, ncolor, img_size, sigma, lo, hi,
+                                                        normalize_color, y_up, pixel_size);
+    require(images == 0 || (starts && out), "null buffer");
+    require(particles == 0 || (x && color && workspace), "null buffer");
+    require(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
+    sphops::run_splat_forward(sp, x, color, starts, (int)images, particles, static_cast<float4*>(workspace), out,
+                              sphops::as_stream(stream));
+  });
+}
+
+int64_t sphops_splat_workspace_bytes(int64_t particles) { return particles > 0 ? 32 * particles : 0; }
+
+int sphops_splat_backward(const float* x, const float* color, const int32_t* starts, int64_t images,
+                          int64_t particles, int ncolor, int img_size, double sigma, double lo, double hi,
+                          int normalize_color, int y_up, double pixel_size, const float* d_out, float* d_x,
+                          float* d_color, void* stream) {
+  return guarded([&] {
+    const sphops::SplatParams sp = sphops::splat_params(images, particles, ncolor, img_size, sigma, lo, hi,
+                                                        normalize_color, y_up, pixel_size);
+    require(particles == 0 || (x && color && starts && d_out && d_x && d_color), "null buffer");
+    require(particles == 0 || images >= 1, "particles need at least one image");
+    sphops::run_splat_backward(sp, x, color, starts, (int)images, particles, d_out, d_x, d_color,
+                               sphops::as_stream(stream));
   });
 }
 

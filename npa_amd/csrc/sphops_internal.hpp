@@ -170,6 +170,24 @@ void run_euler_forward(int dim, const float* y, const float* x_bin, const float*
 void run_euler_backward(int dim, const float* y, const float* mask, const float* d_x_out, const float* d_s_out,
                         const float* d_dx_norm, float* d_y, uint64_t n, uint32_t C, uint32_t P, float alpha,
                         float eps, float dt, hipStream_t st);
+// splatting.hip: 2D Gaussian splatting (utils/splatting.py:6-117)
+struct SplatParams {
+  int H;             // image side (img_size)
+  int r;             // patch radius
+  float lo;          // world lower bound
+  float inv_span;    // 1 / (hi - lo), both in fp32
+  float scale;       // img_size - 1
+  float inv_two_s2;  // 1 / (2 sigma^2), sigma in pixels
+  float K;           // (img_size * pixel_size / (hi - lo))^2: patch weight total when normalising
+  int normalize;     // normalize_color
+  int y_up;
+  int ncolor;        // colour row width; the last three channels are r, g, b
+};
+constexpr int kMaxSplatRadius = 255;
+void run_splat_forward(const SplatParams& sp, const float* x, const float* color, const int32_t* starts, int images,
+                       int64_t n, float4* rec, float* out, hipStream_t st);
+void run_splat_backward(const SplatParams& sp, const float* x, const float* color, const int32_t* starts, int images,
+                        int64_t n, const float* d_img, float* d_x, float* d_color, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
 

@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -24,6 +24,7 @@ _i32 = ctypes.c_int
 _u32 = ctypes.c_uint32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
 
 _SIGNATURES = {
     "sphops_abi_version": ([], _i32),
@@ -57,6 +58,11 @@ _SIGNATURES = {
     "sphops_euler_update_forward": ([_i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _u32, _f32, _f32, _f32,
                                      _f32, _f32, _p], _i32),
     "sphops_euler_update_backward": ([_i32, _i32, _p, _p, _p, _p, _p, _p, _i64, _u32, _f32, _f32, _f32, _p], _i32),
+    "sphops_splat_forward": ([_p, _p, _p, _i64, _i64, _i32, _i32, _f64, _f64, _f64, _i32, _i32, _f64, _p, _p, _p],
+                             _i32),
+    "sphops_splat_workspace_bytes": ([_i64], _i64),
+    "sphops_splat_backward": ([_p, _p, _p, _i64, _i64, _i32, _i32, _f64, _f64, _f64, _i32, _i32, _f64, _p, _p, _p,
+                               _p], _i32),
     "sphops_forward": ([_p, _i32, _p, _p], _i32),
     "sphops_backward": ([_p, _i32, _i32, _i32, _i32, _p, _p], _i32),
     "sphops_neighbor_candidates": ([_p, _p, _p, _p, _p], _i32),
