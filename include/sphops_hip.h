@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 8
+#define SPHOPS_ABI_VERSION 9
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -180,6 +180,13 @@ typedef struct sphops_args {
   int32_t nbr_wave_count_split;     /* ... and its wave count (lane-split channel kernels) */
   const float* upstream2;      /* fused backward: dL/d(second output) */
   float* out2;                 /* fused forward: the second output */
+  /* Optional device copies of the two wave counts (the wave_count and
+   * wave_count_split words that sphops_neighbor_schedule writes).  When set,
+   * the kernels read the counts there, and nbr_wave_count(_split) need only
+   * bound them (sphops_neighbor_wave_capacity), so the caller never reads a
+   * count back: a step can be captured in a HIP graph. */
+  const int32_t* nbr_wave_count_device;
+  const int32_t* nbr_wave_count_split_device;
 } sphops_args;
 
 /* Forward operator `op` (SPHOPS_OP_*) on binned particles. */

@@ -534,6 +534,8 @@ static OpPtrs from_args(const sphops_args* a) {
   p.nwaves2 = (uint32_t)std::max(a->nbr_wave_count_split, 0);
   p.g2 = a->upstream2;
   p.out3 = a->out2;
+  p.nwaves_dev = a->nbr_wave_count_device;
+  p.nwaves2_dev = a->nbr_wave_count_split_device;
   return p;
 }
 
@@ -545,6 +547,9 @@ static void check_list(const sphops_args* a) {
   require(a->nbr_order == nullptr || a->nbr_waves != nullptr, "nbr_order needs nbr_waves");
   require(a->nbr_wave_count >= 0 && a->nbr_wave_count_split >= 0, "negative wave count");
   require(a->nbr_waves_split == nullptr || a->nbr_waves != nullptr, "nbr_waves_split needs nbr_waves");
+  require(a->nbr_wave_count_device == nullptr || a->nbr_waves != nullptr, "nbr_wave_count_device needs nbr_waves");
+  require(a->nbr_wave_count_split_device == nullptr || a->nbr_waves_split != nullptr,
+          "nbr_wave_count_split_device needs nbr_waves_split");
 }
 
 int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream) {
@@ -604,7 +609,7 @@ int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const in
     require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
     const hipStream_t st = sphops::as_stream(stream);
     if (grid->n_keys == 0) {
-      SPHOPS_HIP(hipMemsetAsync(cand_offsets, 0, sizeof(int32_t), st));
+      sphops::fill_u32(reinterpret_cast<uint32_t*>(cand_offsets), 1, 0u, st);
       return;
     }
     OpPtrs a;
@@ -652,8 +657,8 @@ int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, 
     require((nbr_waves_split == nullptr) == (wave_count_split == nullptr),
             "nbr_waves_split and wave_count_split go together");
     if (grid->n_keys == 0) {
-      SPHOPS_HIP(hipMemsetAsync(wave_count, 0, sizeof(int32_t), st));
-      if (wave_count_split) SPHOPS_HIP(hipMemsetAsync(wave_count_split, 0, sizeof(int32_t), st));
+      sphops::fill_u32(reinterpret_cast<uint32_t*>(wave_count), 1, 0u, st);
+      if (wave_count_split) sphops::fill_u32(reinterpret_cast<uint32_t*>(wave_count_split), 1, 0u, st);
       return;
     }
     sphops::run_neighbour_schedule(*grid, nbr_count, nbr_order, reinterpret_cast<uint2*>(nbr_waves), wave_count,

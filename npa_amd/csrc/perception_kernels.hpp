@@ -949,6 +949,21 @@ __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t*
   if (active) op.finish(g, a, k);
 }
 
+// The number of live waves: the device count when the caller passed one (the
+// launch is then sized by an upper bound), else the host count.
+__device__ __forceinline__ uint32_t wave_limit(uint32_t host, const int32_t* dev) {
+  return dev ? (uint32_t)*dev : host;
+}
+
+// This wave's index in the schedule, with the XCD-contiguous block mapping
+// taken over the live workgroups only, so that a launch sized by an upper
+// bound still spreads its live waves over all eight XCDs.
+__device__ __forceinline__ uint32_t schedule_wave(uint32_t live) {
+  const uint32_t per = kThreads / kWave;
+  const uint32_t b = xcd_block_id((live + per - 1) / per);
+  return b == 0xFFFFFFFFu ? b : b * per + (threadIdx.x >> 6);
+}
+
 // List traversal with a group of G lanes per particle, G by list-length class:
 // wave w serves the particles a.order[first .. first + n) of its descriptor
 // a.waves[w] = {first, G << 8 | n}; lane `sub` of a group takes pairs sub,
@@ -956,8 +971,9 @@ __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t*
 // neighbours; the group then sums its partials.
 template <int D, bool P, class OP>
 __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs a) {
-  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (wave >= a.nwaves) return;
+  const uint32_t live = wave_limit(a.nwaves, a.nwaves_dev);
+  const uint32_t wave = schedule_wave(live);
+  if (wave >= live) return;
   const uint2 wd = a.waves[wave];
   const int G = (int)(wd.y >> 8);
   const int lane = __lane_id();
@@ -1054,8 +1070,9 @@ __device__ __forceinline__ const float* row_slice(const float* __restrict__ base
 template <int D, bool P, int CW, bool FULL, bool OFF32>
 __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
-  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (wave >= a.nwaves2) return;
+  const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
+  const uint32_t wave = schedule_wave(live);
+  if (wave >= live) return;
   const uint2 wd = a.waves2[wave];
   const int G = (int)(wd.y >> 8);
   const int lane = __lane_id();
@@ -1221,8 +1238,9 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
 template <int D, bool P, int CW, bool OFF32>
 __global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
-  const uint32_t wave = xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (wave >= a.nwaves2) return;
+  const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
+  const uint32_t wave = schedule_wave(live);
+  if (wave >= live) return;
   const uint2 wd = a.waves2[wave];
   const int G = (int)(wd.y >> 8);
   const int lane = __lane_id();
@@ -1443,7 +1461,7 @@ __global__ __launch_bounds__(kThreads) void k_lane_fill(GridParams g, const floa
     constexpr int R = Walker<D, P>::kRowRanges;
     cnt = lane_fill_ranges<D, P, R>(g, xw, ranges + (uint64_t)k * R, xi, coff[k], cap, nidx);
   }
-  ncnt[k] = cnt;
+  ncnt[k] = (int32_t)max<int64_t>(0, min<int64_t>((int64_t)coff[k] + cnt, cap) - coff[k]);  // cut at the buffer's end
 }
 
 // Lane t's value of v (t wave-uniform).
@@ -1542,7 +1560,9 @@ __global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const floa
 #pragma unroll
     for (int t = 0; t < kUnitParticles; ++t)
       if ((int)lane == t) mine = (int32_t)at[t];
-    if (lane < ni) ncnt[i0 + lane] = mine - row0;
+    // a row is cut at the buffer's end (the caller detects start[B*N] > cap
+    // and refills), so no traversal reads past the entries written
+    if (lane < ni) ncnt[i0 + lane] = max(0, min(mine, (int32_t)cap32) - row0);
   }
 }
 
@@ -1591,13 +1611,20 @@ void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, const int3
   SPHOPS_LAUNCHED();
 }
 
+// Workgroups for a schedule of `waves` waves, rounded up to a multiple of 8
+// (schedule_wave's mapping covers the live waves with that many).
+inline uint32_t launch_groups(uint32_t waves) {
+  const uint32_t per = kThreads / kWave;
+  return ((waves + per - 1) / per + 7u) & ~7u;
+}
+
 template <int D, bool P, class OP>
 void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
   const uint64_t n = g.n_keys;
   if (n == 0) return;
   pack_for<D, OP>(g, a, st);
   if (a.nidx != nullptr && a.waves != nullptr) {
-    const uint32_t wgs = (a.nwaves + (kThreads / kWave) - 1) / (kThreads / kWave);
+    const uint32_t wgs = launch_groups(a.nwaves);
     if (wgs == 0) return;
     hipLaunchKernelGGL((k_pairs_grouped<D, P, OP>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else if (a.nidx != nullptr) {
@@ -1627,7 +1654,7 @@ inline bool row_offsets_fit_32(const Grid& g, uint32_t C) {
 template <int D, bool P>
 void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
-  const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
+  const uint32_t wgs = launch_groups(a.nwaves2);
   pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
   const bool off32 = row_offsets_fit_32(g, a.C);
@@ -1644,7 +1671,7 @@ void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
 template <int D, bool P, bool FULL>
 void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
-  const uint32_t wgs = (a.nwaves2 + (kThreads / kWave) - 1) / (kThreads / kWave);
+  const uint32_t wgs = launch_groups(a.nwaves2);
   pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
   const bool off32 = row_offsets_fit_32(g, a.C);

@@ -188,6 +188,16 @@ __device__ __forceinline__ uint32_t xcd_block_id() {
   return xcd * q + min(xcd, rem) + (x >> 3);
 }
 
+// The same mapping over the first nb_live logical ids of a launch of at least
+// 8 * ceil(nb_live / 8) workgroups (a launch sized by an upper bound);
+// workgroups past them get UINT32_MAX.
+__device__ __forceinline__ uint32_t xcd_block_id(uint32_t nb_live) {
+  const uint32_t x = blockIdx.x;
+  const uint32_t xcd = x & 7u, q = nb_live >> 3, rem = nb_live & 7u;
+  const uint32_t k = x >> 3;
+  return k < q + (xcd < rem ? 1u : 0u) ? xcd * q + min(xcd, rem) + k : 0xFFFFFFFFu;
+}
+
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 }  // namespace sphops

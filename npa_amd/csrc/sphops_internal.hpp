@@ -110,6 +110,10 @@ struct OpPtrs {
   uint32_t nwaves = 0;
   const uint2* waves2 = nullptr;  // descriptors for lane-split channel kernels (group sizes kSplitGroups)
   uint32_t nwaves2 = 0;
+  // optional device copies of the wave counts; when set the kernels read them
+  // and nwaves / nwaves2 only size the launch (an upper bound)
+  const int32_t* nwaves_dev = nullptr;
+  const int32_t* nwaves2_dev = nullptr;
   uint32_t C = 0;
   float tol = 1e-3f;
 };
@@ -157,6 +161,7 @@ constexpr GroupSizes kListGroups{{1, 1, 2, 4, 8, 16, 32, 64}};
 // 1, 1, 1, 1, 4, 8, 16, 16 streams per particle (about 12-48 pairs each)
 constexpr GroupSizes kSplitGroups{{4, 4, 4, 4, 16, 32, 64, 64}};
 void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
+void fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t st);
 // perceive_glue.hip: perception features of NPA.perceive (include/sphops_hip.h)
 void run_glue_forward(int dim, const float* s, const float* blur, const float* grad_s, const float* grad_rho,
                       float* z, uint64_t n, uint32_t C, float coef_s, float coef_rho, float total_mass, int flags,

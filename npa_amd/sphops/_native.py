@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -78,7 +78,8 @@ class Args(ctypes.Structure):
                 ("grad_state", _p), ("grad_rho", _p), ("feature_dim", _u32), ("tol", _f32),
                 ("bin_offsets", _p), ("nbr_start", _p), ("nbr_count", _p), ("nbr_index", _p), ("nbr_order", _p),
                 ("nbr_waves", _p), ("nbr_wave_count", ctypes.c_int32), ("nbr_waves_split", _p),
-                ("nbr_wave_count_split", ctypes.c_int32), ("upstream2", _p), ("out2", _p)]
+                ("nbr_wave_count_split", ctypes.c_int32), ("upstream2", _p), ("out2", _p),
+                ("nbr_wave_count_device", _p), ("nbr_wave_count_split_device", _p)]
 
 
 (OP_COUNT, OP_DENSITY, OP_DENSITY_GRADIENT, OP_MOMENT_MATRIX, OP_BLUR, OP_GRADIENT, OP_GRADIENT_HYBRID,

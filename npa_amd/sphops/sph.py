@@ -109,6 +109,26 @@ class HashGrid:
         return HashGridSnapshot(grid=self.hashgrid, bin_offsets=bin_offsets, permutation=permutation,
                                 block_info=block_info, dim=self.dim, total_blocks=total_blocks)
 
+    def set_capture_capacity(self, index_capacity):
+        """Make snapshots capturable in a HIP graph: neighbour lists of at most
+        ``index_capacity`` entries, built with no host synchronisation (no
+        counterpart in the reference, whose snapshots need no list).  0
+        restores the default.  See ``list_overflow``."""
+        self.hashgrid.set_capture_capacity(index_capacity)
+
+    def list_overflow(self):
+        """True if a list built in capture mode was cut at its capacity
+        (synchronises); ``reset_list_overflow`` clears the flag."""
+        return self.hashgrid.list_overflow()
+
+    def reset_list_overflow(self):
+        self.hashgrid.reset_list_overflow()
+
+    def list_capacity_hint(self):
+        """Index capacity the last eager list build would give the next one
+        (its candidate total plus 1/8), or 0 before the first build."""
+        return int(getattr(self.hashgrid, "_index_capacity", 0))
+
     def wrap_positions(self, x):
         """Wrap positions into ``[-L/2, L/2)`` per axis when periodic
         (``sphops/sph.py:107-123``); identity when clamped."""

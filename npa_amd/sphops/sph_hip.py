@@ -363,6 +363,9 @@ class _HashGridNative:
         waves2 = torch.empty(wcap, dtype=_I32, device=dev)
         small = torch.empty(3, dtype=_I32, device=dev)
         _check(_lib.sphops_neighbor_candidates(self._h, x, bo, ctypes.c_void_p(start.data_ptr()), st))
+        fixed = getattr(self, "_capture_capacity", 0)
+        if fixed:
+            return self._neighbor_list_fixed(x, bo, start, count, order, waves, waves2, small, fixed, st)
         prev = getattr(self, "_index_capacity", 0)
         cap = prev if prev else int(start[n].item())
         index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
@@ -385,7 +388,56 @@ class _HashGridNative:
             fill(index, cap)
         if total > prev:  # ~12% headroom, so that the next snapshot of a moving cloud fits
             self._index_capacity = total + total // 8
+        self._wave_counts = (nwaves, nwaves2)
         return start, count, index, order, waves, nwaves, waves2, nwaves2
+
+    def set_capture_capacity(self, index_capacity, wave_margin=1.25):
+        """Build neighbour lists with no host synchronisation, so that a whole
+        step can be captured in a HIP graph (``torch.cuda.graph``): every list
+        gets an index buffer of ``index_capacity`` entries, and the pair
+        kernels read their wave counts on the device.  Their launches are
+        sized for ``wave_margin`` times the wave counts of the last eager list
+        build (the whole wave capacity if there was none).  A list whose
+        candidate total exceeds the index capacity is cut at the buffer's end,
+        and waves beyond a launch are not run: both are memory-safe, give
+        wrong results and raise the flag that ``list_overflow`` returns.
+        ``index_capacity = 0`` returns to the default: the totals are read
+        back once per snapshot and buffers and launches sized from them.  Call
+        it outside the capture: it allocates the flag."""
+        self._capture_capacity = max(int(index_capacity), 0)
+        if self._capture_capacity:
+            self._overflow = torch.zeros(1, dtype=_I32, device=torch.device("cuda", torch.cuda.current_device()))
+            cap = max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 0)
+            hint = getattr(self, "_wave_counts", None)
+            self._wave_bounds = tuple(min(cap, int(c * wave_margin) + 64) for c in hint) if hint else (cap, cap)
+
+    def list_overflow(self):
+        """True if a list built since set_capture_capacity (or the last
+        reset_list_overflow) was cut at the index capacity.  Reads the flag
+        back (synchronises)."""
+        flag = getattr(self, "_overflow", None)
+        return bool(flag is not None and int(flag.item()) != 0)
+
+    def reset_list_overflow(self):
+        if getattr(self, "_overflow", None) is not None:
+            self._overflow.zero_()
+
+    def _neighbor_list_fixed(self, x, bo, start, count, order, waves, waves2, small, cap, st):
+        n = self._b * self._n
+        index = torch.empty(cap, dtype=_I32, device=start.device)
+        _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
+                                         ctypes.c_void_p(index.data_ptr()), cap,
+                                         ctypes.c_void_p(count.data_ptr()), st))
+        _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
+                                             ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
+                                             ctypes.c_void_p(small.data_ptr() + 4), ctypes.c_void_p(waves2.data_ptr()),
+                                             ctypes.c_void_p(small.data_ptr() + 8), st))
+        # flag |= total > cap or a wave count above its launch, on the device
+        b1, b2 = self._wave_bounds
+        torch.maximum(self._overflow, (start[n:n + 1] > cap).to(_I32), out=self._overflow)
+        torch.maximum(self._overflow, (small[1:2] > b1).to(_I32), out=self._overflow)
+        torch.maximum(self._overflow, (small[2:3] > b2).to(_I32), out=self._overflow)
+        return start, count, index, order, waves, b1, waves2, b2, small
 
     # Per operator: trailing dims of (first output, second output) after (B, N);
     # "C" stands for the channel count, "D" for the spatial dimension.
@@ -440,6 +492,9 @@ class _HashGridNative:
                 a.nbr_order, a.nbr_waves, a.nbr_wave_count = nbr[3].data_ptr(), nbr[4].data_ptr(), nbr[5]
             if len(nbr) > 6:
                 a.nbr_waves_split, a.nbr_wave_count_split = nbr[6].data_ptr(), nbr[7]
+            if len(nbr) > 8:  # capture mode: the wave counts stay on the device
+                a.nbr_wave_count_device = nbr[8].data_ptr() + 4
+                a.nbr_wave_count_split_device = nbr[8].data_ptr() + 8
         return a
 
     def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None):
