@@ -16,8 +16,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kItems = 16;
 constexpr int kTile = kThreads * kItems;  // 4096 keys per radix / scan tile
-constexpr int kRadixBits = 8;
-constexpr int kBins = 1 << kRadixBits;
+constexpr int kRadixBits = 10;  // cell keys below 2^30 sort in 3 passes (cfg5's 2e8 cells: 28 bits)
+constexpr int kBins = kRadixBins;
+static_assert(kBins == 1 << kRadixBits, "kRadixBins must match kRadixBits");
 constexpr int kChunkLog2 = 10;            // cells per bin_offsets workgroup
 constexpr int kChunk = 1 << kChunkLog2;
 
@@ -193,7 +194,7 @@ void device_exclusive_scan(const uint32_t* in, uint32_t* out, uint64_t n, uint32
 __global__ __launch_bounds__(kThreads) void k_radix_hist(const uint32_t* __restrict__ keys, uint32_t n, int shift,
                                                          uint32_t* __restrict__ hist, uint32_t ntiles) {
   __shared__ uint32_t h[kBins];
-  h[threadIdx.x] = 0;
+  for (int d = threadIdx.x; d < kBins; d += kThreads) h[d] = 0;
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile;
 #pragma unroll
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void k_radix_hist(const uint32_t* __restr
     if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & (kBins - 1)], 1u);
   }
   __syncthreads();
-  hist[threadIdx.x * ntiles + blockIdx.x] = h[threadIdx.x];
+  for (int d = threadIdx.x; d < kBins; d += kThreads) hist[d * ntiles + blockIdx.x] = h[d];
 }
 
 // Stable scatter of one radix digit.  Wave w of the tile owns keys
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint32_t* __re
   __shared__ uint32_t gbase[kBins];
   const int wave = threadIdx.x >> 6, lane = __lane_id();
   for (int i = threadIdx.x; i < (kThreads / 64) * kBins; i += kThreads) (&wcnt[0][0])[i] = 0;
-  gbase[threadIdx.x] = hist_scan[threadIdx.x * ntiles + blockIdx.x];
+  for (int d = threadIdx.x; d < kBins; d += kThreads) gbase[d] = hist_scan[d * ntiles + blockIdx.x];
   __syncthreads();
 
   const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
@@ -245,9 +246,8 @@ __global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint32_t* __re
     rank[t] = prior + before;
   }
   __syncthreads();
-  {
-    // exclusive prefix of the per-wave counts, digit by digit
-    const int d = threadIdx.x;
+  // exclusive prefix of the per-wave counts, digit by digit
+  for (int d = threadIdx.x; d < kBins; d += kThreads) {
     uint32_t run = 0;
 #pragma unroll
     for (int w = 0; w < kThreads / 64; ++w) {

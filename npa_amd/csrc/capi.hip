@@ -252,8 +252,9 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
         g->keys[i] = dalloc<uint32_t>(BN);
         g->vals[i] = dalloc<uint32_t>(BN);
       }
-      g->hist = dalloc<uint32_t>(256 * g->n_tiles);
-      const uint64_t scan_n = std::max<uint64_t>(std::max<uint64_t>(256 * g->n_tiles, BN + 1), g->n_chunks + 1);
+      g->hist = dalloc<uint32_t>((uint64_t)sphops::kRadixBins * g->n_tiles);
+      const uint64_t scan_n =
+          std::max<uint64_t>(std::max<uint64_t>((uint64_t)sphops::kRadixBins * g->n_tiles, BN + 1), g->n_chunks + 1);
       g->scan_tmp_len = sphops::scan_tmp_elems(scan_n);
       g->scan_tmp = dalloc<uint32_t>(g->scan_tmp_len);
       g->chunk_first = dalloc<uint32_t>(g->n_chunks);

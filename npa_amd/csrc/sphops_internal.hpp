@@ -195,5 +195,6 @@ void run_splat_backward(const SplatParams& sp, const float* x, const float* colo
                         int64_t n, const float* d_img, float* d_x, float* d_color, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
+constexpr int kRadixBins = 1024;  // digit values per radix-sort pass (10 bits)
 
 }  // namespace sphops
