@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE runs that fill roofline.traffic")
+    ap.add_argument("--extras", action="store_true",
+                    help="instead of the step: time the fused perceive glue, step_euler update, splatting and "
+                         "graph replay beside the reference's torch formulations (one JSON line each)")
     ap.add_argument("--pmc-child", default=None, help=argparse.SUPPRESS)
     return ap.parse_args()
 
@@ -117,6 +120,10 @@ def main():
         sys.exit(2)
     if args.pmc_child:
         return pmc_child(args)
+    if args.extras:
+        from npa_amd import bench_fused
+        bench_fused.run_all()
+        return
     # counter runs first, in child processes, before this process touches the GPU
     pmc = None
     if not args.no_traffic:

@@ -1,0 +1,235 @@
+"""Timings of the paths around the perception operators, each beside the
+reference's own torch formulation of the same computation on the same GPU
+(``python bench.py --extras``; one JSON line per measurement):
+
+* ``perceive``: NPA.perceive forward + backward (models/npa.py:87-137) with
+  the fused feature kernels, against the reference's torch feature assembly
+  over the same sphops operators;
+* ``step_euler``: perception, an NPA-shaped MLP (128 hidden units), the Euler
+  update and a loss on x, s and the |dx| stats, forward + backward
+  (models/npa.py:123-204), fused update against the reference's torch ops;
+* ``splat``: splat_particles_batch forward + backward (utils/splatting.py),
+  against the reference's torch scatter_add_ formulation;
+* ``graph``: the bench's perception step eager and replayed from a HIP graph
+  (the grid's capture mode), for every BASELINE configuration.
+
+The torch formulations here are measurement baselines, written as the
+reference writes them; the library never calls them.
+"""
+import json
+import math
+
+import torch
+
+import npa_amd.sphops as sp
+from npa_amd import perceive as fused_perceive
+from npa_amd import splatting, step, workloads
+
+
+def _time(fn, iters, warmup=3):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def _grid(wl):
+    return sp.HashGrid(dim=wl.dim, boundary="periodic" if wl.periodic else "clamped", mode=wl.mode,
+                       grid_size=list(wl.grid_size), eps=wl.h, num_particles=wl.N, batch_size=wl.B,
+                       max_particles_per_block=wl.maxp)
+
+
+# ---- the reference's torch formulations (measurement baselines)
+
+def _ref_log_normalize(v):  # models/npa.py:83-85
+    return torch.log(1.0 + v.norm(dim=-1, keepdim=True)) * torch.nn.functional.normalize(v, dim=-1)
+
+
+def _ref_perceive(x, s, grid, eps0=0.1):  # models/npa.py:87-137, all flags on, stopgrad_pos
+    B, N, C = s.shape
+    eps = grid.eps
+    with torch.no_grad():
+        snap = grid.instantiate(x)
+    x_bin, s_bin = sp.bin_particles(x, s, snap)
+    xp = x_bin.detach()
+    rho = sp.density(xp, snap)
+    z = [s_bin, sp.blur(xp, rho, s_bin, snap)]
+    coef = torch.tensor([eps], device=x.device) / torch.tensor([eps0], device=x.device)
+    g = _ref_log_normalize(sp.gradient_hybrid(xp, rho, s_bin, snap) * coef)
+    z.append(g.reshape(B, N, -1))
+    gr = sp.density_gradient(xp, snap) * (coef ** (1 + grid.dim)) / N
+    z.append(_ref_log_normalize(gr))
+    return torch.cat(z, dim=-1), x_bin, s_bin, snap
+
+
+def _ref_euler(y, x_bin, s_bin, D, alpha, eps, update_prob, dt=1.0):  # models/npa.py:125-133, 178-200
+    B, N, _ = s_bin.shape
+    dx = y[..., :D]
+    dx = alpha * dx * eps / (1.0 + dx.norm(dim=-1, keepdim=True))
+    ds = y[..., D:]
+    dn = dx.norm(dim=-1).mean()
+    m = (torch.rand(B, N, 1, device=y.device) < update_prob).float()
+    if dx.shape[-1] != x_bin.shape[-1]:
+        dx = torch.cat([dx, torch.zeros(B, N, 1, device=y.device)], dim=-1).contiguous()
+    return x_bin + dt * dx * m, s_bin + dt * ds * m, dn
+
+
+def _ref_splat(x, color, img_size, sigma, lo, hi, y_up, pixel_size):  # utils/splatting.py:6-92
+    dev = x.device
+    pos = (x - lo) / (hi - lo) * (img_size - 1)
+    if y_up:
+        pos = torch.stack([pos[:, 0], (img_size - 1) - pos[:, 1]], dim=1)
+    sigma = sigma * img_size * pixel_size / (hi - lo)
+    r = max(1, math.ceil(5 * float(sigma)))
+    offs = torch.arange(-r, r + 1, device=dev, dtype=torch.int64)
+    yy, xx = torch.meshgrid(offs, offs, indexing="ij")
+    dx, dy = xx.reshape(-1), yy.reshape(-1)
+    base = torch.floor(pos)
+    cx, cy = base[:, 0].long(), base[:, 1].long()
+    frac = pos - base
+    x_idx = cx[:, None] + dx[None, :]
+    y_idx = cy[:, None] + dy[None, :]
+    mask = (x_idx >= 0) & (x_idx < img_size) & (y_idx >= 0) & (y_idx < img_size)
+    g = torch.exp(-((dx[None, :] - frac[:, 0:1]) ** 2 + (dy[None, :] - frac[:, 1:2]) ** 2) / (2 * sigma * sigma))
+    g = g / (1e-8 + torch.sum(g, dim=-1, keepdim=True))
+    g = g * (img_size * pixel_size / (hi - lo)) ** 2.0
+    flat = (y_idx * img_size + x_idx)[mask]
+    w = g[mask]
+    c = color[..., -3:][:, None, :].expand(-1, dx.numel(), -1)[mask, :]
+    density = torch.zeros(img_size * img_size, 1, device=dev)
+    rgb = torch.zeros(img_size * img_size, 3, device=dev)
+    density.scatter_add_(0, flat[:, None], w[:, None])
+    rgb.scatter_add_(0, flat[:, None].expand(-1, 3), c * w[:, None])
+    return torch.cat([rgb, density], dim=1).view(img_size, img_size, 4)
+
+
+class _NPA(torch.nn.Module):
+    """The attributes of the reference's NPA that perception and step_euler
+    read (models/npa.py:15-63), with its MLP shape."""
+
+    def __init__(self, D, C, hidden=128):
+        super().__init__()
+        self.spatial_dims = D
+        self.register_buffer("eps0", torch.tensor([0.1]))
+        self.register_buffer("alpha", torch.tensor([1.0]))
+        self.state_grad = self.density_grad = self.log_norm_grad = self.log_norm_density_grad = True
+        self.stopgrad_pos, self.stopgrad_state = True, False
+        self.model = torch.nn.Sequential(torch.nn.Linear(2 * C + C * D + D, hidden), torch.nn.ReLU(),
+                                         torch.nn.Linear(hidden, D + C, bias=False))
+
+
+# ---- measurements
+
+def bench_perceive(cfg="cfg5", iters=20):
+    wl = workloads.make(cfg)
+    dev = torch.device("cuda", 0)
+    x, s = torch.from_numpy(wl.x).to(dev), torch.from_numpy(wl.s).to(dev)
+    grid = _grid(wl)
+    W = 2 * wl.C + wl.C * wl.dim + wl.dim
+    dz = torch.randn(wl.B, wl.N, W, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
+
+    def run(fused):
+        sr = s.detach().requires_grad_(True)
+        z = fused_perceive.perceive(x, sr, grid, eps0=0.1)[0] if fused else _ref_perceive(x, sr, grid)[0]
+        z.backward(dz)
+
+    return {"bench": "perceive", "config": cfg, "what": "NPA.perceive forward + backward (stopgrad_pos)",
+            "fused_ms": _time(lambda: run(True), iters), "reference_torch_ms": _time(lambda: run(False), iters)}
+
+
+def bench_step(cfg="cfg5", iters=10):
+    wl = workloads.make(cfg)
+    dev = torch.device("cuda", 0)
+    x, s = torch.from_numpy(wl.x).to(dev), torch.from_numpy(wl.s).to(dev)
+    grid = _grid(wl)
+    torch.manual_seed(0)
+    model = _NPA(wl.dim, wl.C).to(dev)
+
+    def run(fused):
+        sr = s.detach().requires_grad_(True)
+        if fused:
+            xn, sn, st = step.step_euler(model, x, sr, grid, update_prob=0.5, intermediate=True)
+            dn = st["dx_norm"]
+        else:
+            z, xb, sb, _ = _ref_perceive(x, sr, grid)
+            xn, sn, dn = _ref_euler(model.model(z), xb, sb, wl.dim, model.alpha, grid.eps, 0.5)
+        ((sn ** 2).mean() + (xn ** 2).mean() + dn).backward()
+
+    return {"bench": "step_euler", "config": cfg,
+            "what": "perception + MLP(128) + Euler update + loss, forward + backward",
+            "fused_ms": _time(lambda: run(True), iters), "reference_torch_ms": _time(lambda: run(False), iters)}
+
+
+def bench_splat(images=8, particles=4096, img_size=256, pixel_size=2.0 / 64, iters=10):
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.rand(images, particles, 2, device=dev, generator=g) - 0.5) * 1.6
+    c = torch.rand(images, particles, 8, device=dev, generator=g)
+    up = torch.randn(images, img_size, img_size, 4, device=dev, generator=g)
+    kw = dict(img_size=img_size, sigma=1.0, lo=-1.0, hi=1.0, y_up=True, pixel_size=pixel_size)
+
+    def run(fused):
+        xg, cg = x.clone().requires_grad_(True), c.clone().requires_grad_(True)
+        if fused:
+            img = splatting.splat_particles_batch(xg, cg, **kw)
+        else:
+            img = torch.stack([_ref_splat(xg[b], cg[b], **kw) for b in range(images)])
+        img.backward(up)
+
+    return {"bench": "splat", "config": f"{images} images x {particles} particles, {img_size}^2, sigma 1.0, "
+            f"pixel_size {pixel_size:.5g} ({img_size * pixel_size / 2:.1f} px)",
+            "what": "splat_particles_batch forward + backward",
+            "fused_ms": _time(lambda: run(True), iters), "reference_torch_ms": _time(lambda: run(False), iters)}
+
+
+def bench_graph(cfg, iters=20):
+    wl = workloads.make(cfg)
+    dev = torch.device("cuda", 0)
+    B, N, C, D = wl.B, wl.N, wl.C, wl.dim
+    x, s = torch.from_numpy(wl.x).to(dev), torch.from_numpy(wl.s).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    ups = [torch.randn(B, N, C, device=dev, generator=gen), torch.randn(B, N, C, D, device=dev, generator=gen),
+           torch.randn(B, N, D, device=dev, generator=gen)]
+    grid = _grid(wl)
+
+    def one(xx, ss):
+        xr, sr = xx.detach().requires_grad_(True), ss.detach().requires_grad_(True)
+        with torch.no_grad():
+            snap = grid.instantiate(xr)
+        xb, sb = sp.bin_particles(xr, sr, snap)
+        rho = sp.density(xb, snap)
+        torch.autograd.backward([sp.blur(xb, rho, sb, snap), sp.gradient_hybrid(xb, rho, sb, snap),
+                                 sp.density_gradient(xb, snap)], ups)
+
+    eager = _time(lambda: one(x, s), iters)
+    grid.set_capture_capacity(int(grid.list_capacity_hint() * 1.25))
+    sx, ss_ = x.clone(), s.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            one(sx, ss_)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        one(sx, ss_)
+    replay = _time(graph.replay, iters)
+    overflow = grid.list_overflow()
+    grid.set_capture_capacity(0)
+    return {"bench": "graph", "config": cfg, "what": "the bench's perception step, fwd + full bwd",
+            "eager_ms": eager, "graph_replay_ms": replay, "list_overflow": overflow}
+
+
+def run_all():
+    torch.cuda.set_device(0)
+    results = [bench_perceive(), bench_step(), bench_splat()]
+    results += [bench_graph(c) for c in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5")]
+    for r in results:
+        print(json.dumps(r), flush=True)
+    return results
