@@ -99,6 +99,7 @@ def pair_kernel(name, D, periodic, C):
 
 
 COPY_BYTES = 256 << 20
+CUS, XCDS = 256, 8  # MI355X
 
 
 def step_bytes(C, D, P, full=True):
@@ -202,6 +203,7 @@ def main():
     traffic = None
     if pmc is not None and pmc.get("kernel") == dom:
         traffic = pmc["bytes_per_launch"]
+    copy_gbs = measured_copy_gbs()
     print("[bench] kernel ms: " + ", ".join(f"{k}={v:.3f}" for k, v in sorted(kt.items(), key=lambda t: -t[1])),
           file=sys.stderr, flush=True)
 
@@ -244,11 +246,31 @@ def main():
             "alg_bytes_per_launch": alg,
             "avg_launch_ms": dom_ms,
             "pair_kernel": pair_kernel(dom, D, wl.periodic, C),
+            "valu_busy": pmc.get("valu_busy") if pmc is not None and pmc.get("kernel") == dom else None,
+            "measured_copy_gbs": copy_gbs,
             "pmc": pmc,
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def measured_copy_gbs(nbytes=COPY_BYTES, reps=20):
+    """Device copy bandwidth on this GPU (read + write bytes over time, HIP
+    events): the practical ceiling next to the 8 TB/s spec figure."""
+    import torch
+    src = torch.ones(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    return 2 * nbytes / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9
 
 
 def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps, only=None):
@@ -417,6 +439,11 @@ def measure_traffic(args, kernel):
             res[counter] = {"copy_kib": c, "kernel_kib": t, "scale": scale, "kernel_bytes": t * 1024.0 * scale}
             total += t * 1024.0 * scale
         res["bytes_per_launch"] = total
+        # VALU utilisation: VALU issue cycles per CU (one wave instruction per
+        # CU and clock at most) over the active clock of an XCD
+        valu = _pmc_run("SQ_ACTIVE_INST_VALU", kernel, frag, args)[1]
+        gui = _pmc_run("GRBM_GUI_ACTIVE", kernel, frag, args)[1]
+        res["valu_busy"] = valu / CUS / (gui / XCDS) if gui > 0 else None
         print(f"[bench] traffic of {kernel}: {total / 1e6:.1f} MB per launch "
               f"(fetch {res['FETCH_SIZE']['kernel_bytes'] / 1e6:.1f}, write {res['WRITE_SIZE']['kernel_bytes'] / 1e6:.1f})",
               file=sys.stderr, flush=True)
