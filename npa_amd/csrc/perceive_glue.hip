@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void k_glue_forward(const float* __restri
   const uint32_t t = (uint32_t)min<uint64_t>(T, n - k0);
   const TileMap mp = tile_map<D>(C, t, flags);
   const uint32_t tW = t * mp.W, tid = threadIdx.x;
-  const float f_rho = coef_rho / total_mass;
+  const float inv_mass = 1.0f / total_mass;
   s += k0 * C;
   blur += k0 * C;
   grad_s += k0 * mp.CD;
@@ -167,7 +167,8 @@ __global__ __launch_bounds__(kThreads) void k_glue_forward(const float* __restri
     if (i < tW) {
       uint32_t j, e;
       const int g = mp.seg_of(i, j, e);
-      tile[e] = val[m] * (g < 2 ? 1.0f : g == 2 ? coef_s : f_rho);
+      // grad_rho * coef_rho / N as torch rounds it: (g * coef_rho) * fp32(1 / N)
+      tile[e] = g < 2 ? val[m] : g == 2 ? val[m] * coef_s : val[m] * coef_rho * inv_mass;
     }
   }
   __syncthreads();
@@ -205,6 +206,7 @@ __global__ __launch_bounds__(kThreads) void k_glue_backward(const float* __restr
   const uint32_t t = (uint32_t)min<uint64_t>(T, n - k0);
   const TileMap mp = tile_map<D>(C, t, flags);
   const uint32_t tW = t * mp.W, tid = threadIdx.x;
+  const float inv_mass = 1.0f / total_mass;
   const float* dzt = dz + k0 * mp.W;
   {
     float val[kSlots];
@@ -235,12 +237,11 @@ __global__ __launch_bounds__(kThreads) void k_glue_backward(const float* __restr
     for (uint32_t p = tid; p < t; p += kThreads) {
       float g[D];
 #pragma unroll
-      for (int e = 0; e < D; ++e) g[e] = grad_rho[(k0 + p) * D + e] * coef_rho / total_mass;
+      for (int e = 0; e < D; ++e) g[e] = grad_rho[(k0 + p) * D + e] * coef_rho * inv_mass;
       log_normalize_backward<D>(g, &tile[p * mp.W + mp.o]);
     }
   }
   __syncthreads();
-  const float f_rho = coef_rho / total_mass;
   float* dst0 = d_s ? d_s + k0 * C : nullptr;
   float* dst1 = d_blur ? d_blur + k0 * C : nullptr;
   float* dst2 = d_grad_s ? d_grad_s + k0 * mp.CD : nullptr;
@@ -252,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void k_glue_backward(const float* __restr
       uint32_t j, e;
       const int g = mp.seg_of(i, j, e);
       float* dst = g == 0 ? dst0 : g == 1 ? dst1 : g == 2 ? dst2 : dst3;
-      if (dst) dst[j] = tile[e] * (g < 2 ? 1.0f : g == 2 ? coef_s : f_rho);
+      if (dst) dst[j] = g < 2 ? tile[e] : g == 2 ? tile[e] * coef_s : tile[e] * inv_mass * coef_rho;
     }
   }
 }

@@ -89,10 +89,12 @@ def perceive(x, s, grid, eps0=0.1, state_grad=True, density_grad=True, log_norm_
     s_p = s_bin.detach() if stopgrad_state else s_bin
     rho = density(x_p, snapshot)
     blur_s = blur(x_p, rho, s_p, snapshot)
-    # coef = eps / eps0 in fp32, as the reference's tensor arithmetic gives it
+    # coef = eps / eps0 and coef ** (1 + D) rounded as torch evaluates them on
+    # the model's fp32 buffer: a Python float over a tensor is the tensor's
+    # reciprocal times the float; the cube is c * c * c, other powers powf
     e0 = float(eps0.reshape(-1)[0]) if torch.is_tensor(eps0) else float(eps0)
-    coef = np.float32(np.float32(grid.eps) / np.float32(e0))
-    coef_rho = np.float32(coef ** np.float32(1 + D))
+    coef = np.float32(np.float32(1.0) / np.float32(e0)) * np.float32(grid.eps)
+    coef_rho = coef * coef * coef if D == 2 else np.power(coef, np.float32(1 + D))
     flags = 0
     grad_s = grad_rho = None
     if state_grad:

@@ -21,7 +21,9 @@ def features(s, blur, grad_s, grad_rho, eps, eps0, log_norm_grad=True, log_norm_
     """z of NPA.perceive from the operator outputs; grad_s / grad_rho may be
     None (state_grad / density_grad off).  eps0 as the model's float32 buffer."""
     B, N, C = s.shape
-    coef = torch.tensor([eps], dtype=torch.float32) / torch.tensor([eps0], dtype=torch.float32)
+    # eps / eps0 as the reference evaluates it: eps (Python float) over the
+    # model's fp32 eps0 buffer, i.e. reciprocal(eps0) * eps in fp32
+    coef = torch.reciprocal(torch.tensor([eps0], dtype=torch.float32)) * eps
     coef = coef.to(device=s.device, dtype=s.dtype)
     z = [s, blur]
     if grad_s is not None:

@@ -54,7 +54,7 @@ def test_features_match_oracle(dim, fi, C):
     f.update(FLAGS[fi])
     grid, _, _, sb, bl, gs, gr = _ops(dim, C, 100 + fi)
     eps, eps0 = grid.eps, 0.1
-    coef = np.float32(np.float32(eps) / np.float32(eps0))
+    coef = np.float32(np.float32(1.0) / np.float32(eps0)) * np.float32(eps)  # as the oracle and perceive()
     flags = ((PF.STATE_GRAD | (PF.LOG_NORM_GRAD if f["log_norm_grad"] else 0)) if f["state_grad"] else 0) | \
             ((PF.DENSITY_GRAD | (PF.LOG_NORM_DENSITY_GRAD if f["log_norm_density_grad"] else 0))
              if f["density_grad"] else 0)

@@ -29,7 +29,7 @@ def test_features_layout_and_gradcheck():
     z = P.features(s, bl, gs, gr, 0.05, 0.1)
     assert z.shape == (B, N, 2 * C + C * D + D)
     assert torch.equal(z[..., :C], s) and torch.equal(z[..., C:2 * C], bl)
-    coef = float(np.float32(0.05) / np.float32(0.1))
+    coef = float(np.float32(1.0) / np.float32(0.1) * np.float32(0.05))
     assert torch.allclose(z[..., 2 * C:2 * C + C * D], P.log_normalize(gs * coef).reshape(B, N, -1))
     assert torch.allclose(z[..., -D:], P.log_normalize(gr * coef ** (1 + D) / N))
     assert torch.autograd.gradcheck(lambda a, b, c, d: P.features(a, b, c, d, 0.05, 0.1), (s, bl, gs, gr))
