@@ -131,3 +131,20 @@ def step_euler_trace(model, x, s, grid, dt=1.0, update_prob=0.5, noise_std=0.0, 
         dx_bin = torch.cat([dx_bin, torch.zeros_like(dx_bin[..., :1])], dim=-1)
     dx_trace, ds_trace = unbin_particles(dx_bin.contiguous(), y[..., D:].contiguous(), model.last_snapshot)
     return x_trace, s_trace, dx_trace, ds_trace
+
+
+def step_euler_static(model, x, s, grid, dt=1.0, update_prob=0.5, channel_mask=None):
+    """step_euler of the state-only model (models/static_npa.py:15-38):
+    fused perception, the model's MLP giving ds only, positions unchanged
+    (x_bin + 0), s = s_bin + dt * ds * mask; returns (x, s) in binned order.
+    The update is a single elementwise expression, left to torch."""
+    B, N, C = s.shape
+    z, x_bin, s_bin, snapshot = _perceive(model, x, s, grid)
+    model.last_snapshot = snapshot
+    ds = model.model(z)
+    mask = 1.0
+    if update_prob < 1.0:
+        mask = (torch.rand(B, N, 1, device=x.device) < update_prob).float()
+    if channel_mask is not None:
+        ds = ds * channel_mask
+    return x_bin + 0, s_bin + dt * ds * mask

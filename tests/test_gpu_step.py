@@ -151,3 +151,44 @@ def test_step_euler_trace_order():
     assert torch.equal(xt, xb[0][perm[0]][None]) and torch.equal(st, sb[0][perm[0]][None])
     _close("x = x0 + dx", xt.cpu(), (x + dxt).cpu())
     _close("s = s0 + ds", st.cpu(), (s + dst).cpu())
+
+
+def test_step_euler_static_matches_torch_assembly():
+    """The state-only model's step (models/static_npa.py:24-38) with fused
+    perception against the same step over the torch feature assembly."""
+    import npa_amd.sphops as sp
+    from npa_amd import step as S
+    C, dim = 8, 2
+    c = H.random_case("static2d", 2, 400, C, dim, 12, 0.15, False, "grid", uniform=False, sigma=0.3, seed=6)
+    grid = sp.HashGrid(dim=dim, boundary="clamped", mode="grid", grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    torch.manual_seed(0)
+    model = _Model(dim, C).cuda()
+    model.model[2] = torch.nn.Linear(32, C, bias=False).cuda()  # ds only
+    x, s0 = torch.from_numpy(c.x).cuda(), torch.from_numpy(c.s).cuda()
+    cmask = (torch.arange(C, device="cuda") % 2).float()
+    out = []
+    for fused in (True, False):
+        s = s0.clone().requires_grad_(True)
+        model.zero_grad()
+        torch.manual_seed(4)
+        if fused:
+            xn, sn = S.step_euler_static(model, x, s, grid, dt=0.5, update_prob=0.5, channel_mask=cmask)
+        else:
+            with torch.no_grad():
+                snap = grid.instantiate(x)
+            xb, sb = sp.bin_particles(x, s, snap)
+            xp = xb.detach()
+            rho = sp.density(xp, snap)
+            z = P.features(sb, sp.blur(xp, rho, sb, snap), sp.gradient_hybrid(xp, rho, sb, snap),
+                           sp.density_gradient(xp, snap), grid.eps, 0.1)
+            ds = model.model(z) * cmask
+            m = (torch.rand(2, 400, 1, device="cuda") < 0.5).float()
+            xn, sn = xb + 0, sb + 0.5 * ds * m
+        (sn ** 2).sum().backward()
+        out.append((xn.detach().cpu(), sn.detach().cpu(), s.grad.cpu(), model.model[0].weight.grad.cpu()))
+    (xf, sf, gf, wf), (xr, sr, gr, wr) = out
+    assert torch.equal(xf, xr)
+    _close("s", sf, sr, rtol=1e-4, atol=1e-5)
+    _close("dL/ds", gf, gr, rtol=1e-4, atol=1e-5)
+    _close("dL/dW", wf, wr, rtol=1e-3, atol=1e-4)
