@@ -367,7 +367,8 @@ class _HashGridNative:
         if fixed:
             return self._neighbor_list_fixed(x, bo, start, count, order, waves, waves2, small, fixed, st)
         prev = getattr(self, "_index_capacity", 0)
-        cap = prev if prev else int(start[n].item())
+        limit = self.max_list_entries
+        cap = min(prev if prev else int(start[n].item()), limit)
         index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
 
         def fill(buf, capacity):
@@ -382,6 +383,9 @@ class _HashGridNative:
                                              ctypes.c_void_p(small.data_ptr() + 8), st))
         small[0:1].copy_(start[n:n + 1])
         total, nwaves, nwaves2 = small.cpu().tolist()
+        if total > limit:
+            # too large to store: the operators scan the stencil instead
+            return None
         if total > cap:
             cap = total
             index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
@@ -390,6 +394,12 @@ class _HashGridNative:
             self._index_capacity = total + total // 8
         self._wave_counts = (nwaves, nwaves2)
         return start, count, index, order, waves, nwaves, waves2, nwaves2
+
+    # Largest neighbour list (index entries = stencil candidates) a snapshot
+    # builds; above it neighbor_list returns None and the operators scan the
+    # cell stencil directly (no list memory, slower).  At most 2^30, the
+    # library's limit (32-bit byte offsets into the index buffer).
+    max_list_entries = 1 << 30
 
     def set_capture_capacity(self, index_capacity, wave_margin=1.25):
         """Build neighbour lists with no host synchronisation, so that a whole
@@ -405,6 +415,8 @@ class _HashGridNative:
         back once per snapshot and buffers and launches sized from them.  Call
         it outside the capture: it allocates the flag."""
         self._capture_capacity = max(int(index_capacity), 0)
+        if self._capture_capacity > self.max_list_entries:
+            raise RuntimeError(f"index_capacity above max_list_entries ({self.max_list_entries})")
         if self._capture_capacity:
             self._overflow = torch.zeros(1, dtype=_I32, device=torch.device("cuda", torch.cuda.current_device()))
             cap = max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 0)
