@@ -1,0 +1,57 @@
+"""A batch large enough that byte offsets into the (B*N, C*D) gradient rows
+exceed 32 bits (12M particles, C = 32), so the pass-B kernels take their
+64-bit-offset variants: each cloud's outputs and gradients must equal those
+of the same cloud run alone (B = 1, 32-bit offsets), bit for bit, since
+clouds are independent and every particle's sums run in the same order."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _step(sp, grid, x, s, ups):
+    xr, sr = x.detach().requires_grad_(True), s.detach().requires_grad_(True)
+    with torch.no_grad():
+        snap = grid.instantiate(xr)
+    xb, sb = sp.bin_particles(xr, sr, snap)
+    rho = sp.density(xb, snap)
+    outs = [sp.blur(xb, rho, sb, snap), sp.gradient_hybrid(xb, rho, sb, snap), sp.density_gradient(xb, snap)]
+    torch.autograd.backward(outs, ups)
+    return [t.detach() for t in outs + [rho]] + [xr.grad, sr.grad]
+
+
+def test_64bit_row_offsets_match_per_cloud_runs():
+    import npa_amd.sphops as sp
+    # 2.7 particles per cell: 74 stencil candidates and 11 in-radius
+    # neighbours per particle, so the list (0.9 G entries) stays below 2^30
+    N, C, D, G = 6_000_000, 32, 3, 130
+    h = 2.0 / G
+    assert 2 * N * C * D * 4 > 0xFFFFFFFF >= N * C * D * 4
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.zeros(2, N, 4, device=dev)
+    x[..., :3] = torch.rand(2, N, 3, device=dev, generator=gen) * 1.98 - 0.99
+    s = torch.randn(2, N, C, device=dev, generator=gen)
+    ups = [torch.randn(2, N, C, device=dev, generator=gen), torch.randn(2, N, C, D, device=dev, generator=gen),
+           torch.randn(2, N, D, device=dev, generator=gen)]
+    print(f"[large] B=2 N={N} C={C}", flush=True)
+
+    def grid_for(B):
+        return sp.HashGrid(dim=D, boundary="clamped", mode="grid", grid_size=[G, G, G], eps=h, num_particles=N,
+                           batch_size=B, max_particles_per_block=64)
+
+    g2 = grid_for(2)
+    for _ in range(2):  # the second step runs the fused passes
+        both = _step(sp, g2, x, s, ups)
+    assert g2.hashgrid._wave_counts is not None
+    del g2
+    names = ["blur", "gradient_hybrid", "density_gradient", "rho", "dL/dx", "dL/ds"]
+    for b in range(2):
+        g1 = grid_for(1)
+        for _ in range(2):
+            one = _step(sp, g1, x[b:b + 1], s[b:b + 1], [u[b:b + 1] for u in ups])
+        for name, a, r in zip(names, both, one):
+            assert torch.equal(a[b:b + 1], r), f"cloud {b}: {name} differs"
+        del g1, one
+        torch.cuda.empty_cache()
