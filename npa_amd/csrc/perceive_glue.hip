@@ -262,9 +262,10 @@ __global__ __launch_bounds__(kThreads) void k_glue_backward(const float* __restr
 // ---- Euler update of step_euler (models/npa.py:125-133, 178-200) --------
 // From the MLP output y = [a (D), ds (C)] per particle: dx = alpha * a * eps /
 // (1 + |a|), x_out = x_bin + dt * pad(dx) * m (+ noise * noise_std * sqrt_dt
-// * m), s_out = s_bin + dt * ds * m, |dx| per particle.  Thread (k, j): lane j
-// < C moves state channel j, lane j < P position lane j (lanes j >= D of x
-// are the zero padding), lane 0 the norm.
+// * m), s_out = s_bin + dt * ds * m, |dx| per particle.  One launch, two
+// kinds of waves: the first n * C threads stream the state channels (thread
+// (k, c)), the next n threads each take one particle's position row and |dx|,
+// so no wave carries the position arithmetic as a divergent branch.
 
 template <int D>
 __device__ __forceinline__ float scaled_step(const float* a, float alpha, float eps, float* dx) {
@@ -288,36 +289,43 @@ __global__ __launch_bounds__(kThreads) void k_euler_forward(const float* __restr
                                                             const float* __restrict__ mask,
                                                             const float* __restrict__ noise, float* __restrict__ x_out,
                                                             float* __restrict__ s_out, float* __restrict__ dx_norm,
-                                                            uint64_t n, uint32_t C, uint32_t P, uint32_t L, float alpha,
-                                                            float eps, float dt, float noise_std, float sqrt_dt) {
+                                                            uint64_t n, uint32_t C, uint32_t P, float alpha, float eps,
+                                                            float dt, float noise_std, float sqrt_dt) {
   const I t = (I)blockIdx.x * kThreads + threadIdx.x;
-  if (t >= (I)n * L) return;
-  const I k = t / L;  // 32-bit division whenever n * L fits
-  const uint32_t j = (uint32_t)(t - k * L);
-  const float m = mask ? mask[k] : 1.0f;
-  const float* yr = y + (uint64_t)k * (D + C);  // y rows may be wider than L: 64-bit
-  if (j < C) s_out[k * C + j] = s_bin[k * C + j] + dt * yr[D + j] * m;
-  if (j < P) {
-    float a[D], dx[D];
-#pragma unroll
-    for (int e = 0; e < D; ++e) a[e] = yr[e];
-    const float dn = scaled_step<D>(a, alpha, eps, dx);
-    float v = 0.0f;
-#pragma unroll
-    for (int e = 0; e < D; ++e) v = j == (uint32_t)e ? dx[e] : v;
-    float xo = x_bin[k * P + j] + dt * v * m;
-    if (noise) xo += noise[k * P + j] * noise_std * sqrt_dt * m;
-    x_out[k * P + j] = xo;
-    if (j == 0 && dx_norm) dx_norm[k] = dn;
+  const I nC = (I)n * C;
+  if (t < nC) {
+    const I k = t / C;  // 32-bit division whenever n * C fits
+    const uint32_t c = (uint32_t)(t - k * C);
+    const float m = mask ? mask[k] : 1.0f;
+    s_out[t] = s_bin[t] + dt * y[(uint64_t)k * (D + C) + D + c] * m;
+    return;
   }
+  const I k = t - nC;
+  if (k >= (I)n) return;
+  const float m = mask ? mask[k] : 1.0f;
+  const float* yr = y + (uint64_t)k * (D + C);
+  float a[D], dx[D];
+#pragma unroll
+  for (int e = 0; e < D; ++e) a[e] = yr[e];
+  const float dn = scaled_step<D>(a, alpha, eps, dx);
+  constexpr int PW = D == 2 ? 2 : 4;  // position row width (the C ABI checks P == PW)
+#pragma unroll
+  for (int e = 0; e < PW; ++e) {
+    const uint64_t o = (uint64_t)k * PW + e;
+    float xo = x_bin[o] + dt * (e < D ? dx[e < D ? e : 0] : 0.0f) * m;  // lanes >= D: the zero padding
+    if (noise) xo += noise[o] * noise_std * sqrt_dt * m;
+    x_out[o] = xo;
+  }
+  if (dx_norm) dx_norm[k] = dn;
 }
 
 // dL/dy from dL/dx_out, dL/ds_out and dL/d|dx| (each may be NULL: zero);
-// thread (k, j) for j < D + C writes dL/dy[k, j].
+// threads as in k_euler_forward (state channels, then one per particle).
 // With kappa = alpha * eps, u = |a|, g = dt * m * dL/dx_out[:D] + dL/d|dx| *
 // dx / |dx|: dL/da = kappa * (g / (1 + u) - (a.g) a / (u (1 + u)^2)), whose
 // second term and the |dx| term vanish at a = 0 (torch's norm has a zero
-// gradient there).
+// gradient there).  With r = 1 / (1 + u): dx = kappa a r and |dx| = |kappa|
+// u r, so the |dx| term of g is dL/d|dx| sign(kappa) a / u.
 template <int D, typename I>
 __global__ __launch_bounds__(kThreads) void k_euler_backward(const float* __restrict__ y,
                                                              const float* __restrict__ mask,
@@ -325,43 +333,41 @@ __global__ __launch_bounds__(kThreads) void k_euler_backward(const float* __rest
                                                              const float* __restrict__ d_s_out,
                                                              const float* __restrict__ d_dx_norm,
                                                              float* __restrict__ d_y, uint64_t n, uint32_t C,
-                                                             uint32_t P, uint32_t L, float alpha, float eps, float dt) {
+                                                             uint32_t P, float alpha, float eps, float dt) {
   const I t = (I)blockIdx.x * kThreads + threadIdx.x;
-  if (t >= (I)n * L) return;
-  const I k = t / L;  // 32-bit division whenever n * L fits
-  const uint32_t j = (uint32_t)(t - k * L);
+  const I nC = (I)n * C;
+  if (t < nC) {
+    const I k = t / C;
+    const uint32_t c = (uint32_t)(t - k * C);
+    const float m = mask ? mask[k] : 1.0f;
+    d_y[(uint64_t)k * (D + C) + D + c] = d_s_out ? dt * m * d_s_out[t] : 0.0f;
+    return;
+  }
+  const I k = t - nC;
+  if (k >= (I)n) return;
   const float m = mask ? mask[k] : 1.0f;
   const float* yr = y + (uint64_t)k * (D + C);
-  // lane j of a particle writes element j of its dL/dy row: one store covers the row
-  float out;
-  if (j >= (uint32_t)D) {
-    out = d_s_out ? dt * m * d_s_out[k * C + (j - D)] : 0.0f;
-  } else {
-    // with r = 1 / (1 + u): dx = kappa a r, |dx| = |kappa| u r, so the |dx|
-    // term of g is dL/d|dx| sign(kappa) a / u; two divisions per lane
-    float a[D];
-    float u2 = 0.0f;
+  float a[D], g[D];
+  float u2 = 0.0f;
 #pragma unroll
-    for (int e = 0; e < D; ++e) {
-      a[e] = yr[e];
-      u2 += a[e] * a[e];
-    }
-    const float u = sqrtf(u2);
-    const float kappa = alpha * eps;
-    const float r = 1.0f / (1.0f + u);
-    const float iu = u > 0.0f ? 1.0f / u : 0.0f;
-    const float gn = (d_dx_norm && kappa != 0.0f) ? (kappa < 0.0f ? -d_dx_norm[k] : d_dx_norm[k]) * iu : 0.0f;
-    float ag = 0.0f, aj = 0.0f, gj = 0.0f;
-#pragma unroll
-    for (int e = 0; e < D; ++e) {
-      const float ge = (d_x_out ? dt * m * d_x_out[k * P + e] : 0.0f) + gn * a[e];
-      ag += a[e] * ge;
-      aj = j == (uint32_t)e ? a[e] : aj;
-      gj = j == (uint32_t)e ? ge : gj;
-    }
-    out = kappa * r * (gj - ag * r * iu * aj);
+  for (int e = 0; e < D; ++e) {
+    a[e] = yr[e];
+    u2 += a[e] * a[e];
   }
-  d_y[(uint64_t)k * (D + C) + j] = out;
+  const float u = sqrtf(u2);
+  const float kappa = alpha * eps;
+  const float r = 1.0f / (1.0f + u);
+  const float iu = u > 0.0f ? 1.0f / u : 0.0f;
+  const float gn = (d_dx_norm && kappa != 0.0f) ? (kappa < 0.0f ? -d_dx_norm[k] : d_dx_norm[k]) * iu : 0.0f;
+  float ag = 0.0f;
+#pragma unroll
+  for (int e = 0; e < D; ++e) {
+    g[e] = (d_x_out ? dt * m * d_x_out[(uint64_t)k * P + e] : 0.0f) + gn * a[e];
+    ag += a[e] * g[e];
+  }
+  const float b = ag * r * iu;
+#pragma unroll
+  for (int e = 0; e < D; ++e) d_y[(uint64_t)k * (D + C) + e] = kappa * r * (g[e] - b * a[e]);
 }
 
 }  // namespace
@@ -402,13 +408,13 @@ void run_euler_forward(int dim, const float* y, const float* x_bin, const float*
                        const float* noise, float* x_out, float* s_out, float* dx_norm, uint64_t n, uint32_t C,
                        uint32_t P, float alpha, float eps, float dt, float noise_std, float sqrt_dt, hipStream_t st) {
   if (n == 0) return;
-  const uint32_t L = std::max(C, P);
-  const dim3 grid((uint32_t)((n * L + kThreads - 1) / kThreads));
-  const bool narrow = n * L + kThreads <= 0xFFFFFFFFull;
+  const uint64_t threads = n * (C + 1ull);  // n * C state threads, then n particle threads
+  const dim3 grid((uint32_t)((threads + kThreads - 1) / kThreads));
+  const bool narrow = threads + kThreads <= 0xFFFFFFFFull;
   auto kern = dim == 2 ? (narrow ? k_euler_forward<2, uint32_t> : k_euler_forward<2, uint64_t>)
                        : (narrow ? k_euler_forward<3, uint32_t> : k_euler_forward<3, uint64_t>);
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, y, x_bin, s_bin, mask, noise, x_out, s_out, dx_norm, n, C, P,
-                     L, alpha, eps, dt, noise_std, sqrt_dt);
+                     alpha, eps, dt, noise_std, sqrt_dt);
   SPHOPS_LAUNCHED();
 }
 
@@ -416,13 +422,13 @@ void run_euler_backward(int dim, const float* y, const float* mask, const float*
                         const float* d_dx_norm, float* d_y, uint64_t n, uint32_t C, uint32_t P, float alpha,
                         float eps, float dt, hipStream_t st) {
   if (n == 0) return;
-  const uint32_t L = (uint32_t)dim + C;  // one lane per element of a dL/dy row
-  const dim3 grid((uint32_t)((n * L + kThreads - 1) / kThreads));
-  const bool narrow = n * L + kThreads <= 0xFFFFFFFFull;
+  const uint64_t threads = n * (C + 1ull);
+  const dim3 grid((uint32_t)((threads + kThreads - 1) / kThreads));
+  const bool narrow = threads + kThreads <= 0xFFFFFFFFull;
   auto kern = dim == 2 ? (narrow ? k_euler_backward<2, uint32_t> : k_euler_backward<2, uint64_t>)
                        : (narrow ? k_euler_backward<3, uint32_t> : k_euler_backward<3, uint64_t>);
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, y, mask, d_x_out, d_s_out, d_dx_norm, d_y, n, C, P, L, alpha,
-                     eps, dt);
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, st, y, mask, d_x_out, d_s_out, d_dx_norm, d_y, n, C, P, alpha, eps,
+                     dt);
   SPHOPS_LAUNCHED();
 }
 
