@@ -24,14 +24,14 @@ def _step(sp, grid, x, s, ups):
     return outs + [rho, xr.grad, sr.grad]
 
 
-@pytest.mark.parametrize("dim,periodic", [(2, True), (3, False)])
-def test_captured_step_replays_match_eager(dim, periodic):
+@pytest.mark.parametrize("dim,periodic,mode", [(2, True, "grid"), (3, False, "grid"), (3, False, "particle")])
+def test_captured_step_replays_match_eager(dim, periodic, mode):
     import npa_amd.sphops as sp
     B, N, C = 2, 3000, 16
-    cases = [H.random_case(f"graph{dim}d", B, N, C, dim, 16, 0.06, periodic, "grid", uniform=True, sigma=0.45,
+    cases = [H.random_case(f"graph{dim}d", B, N, C, dim, 16, 0.06, periodic, mode, uniform=True, sigma=0.45,
                            seed=seed) for seed in (1, 2, 3, 4)]
     c0 = cases[0]
-    grid = sp.HashGrid(dim=dim, boundary="periodic" if periodic else "clamped", mode="grid",
+    grid = sp.HashGrid(dim=dim, boundary="periodic" if periodic else "clamped", mode=mode,
                        grid_size=list(c0.grid_size), eps=c0.eps, num_particles=N, batch_size=B,
                        max_particles_per_block=c0.maxp)
     gen = torch.Generator(device="cuda").manual_seed(0)
