@@ -30,7 +30,9 @@ MODE_GRID, MODE_PARTICLE = 0, 1
 
 
 def _stream(t):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """torch's current stream on t's device, as the raw handle (the C ABI's
+    `stream` argument); the raw query skips building a Stream object."""
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(t.device.index))
 
 
 def _arr(t, name, dtype, ndim):
@@ -52,11 +54,10 @@ def _validate_shape(t, expected, name):
     """``validate_array_shape`` (``sphops/utils.cuh:526-566``)."""
     if t.dim() != len(expected):
         raise RuntimeError(f"{name} must have {len(expected)} dimensions, got {t.dim()}")
-    for got, want in zip(t.shape, expected):
-        if got != want:
-            exp = "(" + ", ".join(str(v) for v in expected) + ")"
-            act = "(" + ", ".join(str(v) for v in t.shape) + ")"
-            raise RuntimeError(f"{name} must have shape {exp}, got {act}")
+    if tuple(t.shape) != tuple(expected):
+        exp = "(" + ", ".join(str(v) for v in expected) + ")"
+        act = "(" + ", ".join(str(v) for v in t.shape) + ")"
+        raise RuntimeError(f"{name} must have shape {exp}, got {act}")
 
 
 _F32, _I32 = torch.float32, torch.int32

@@ -38,7 +38,7 @@ class Splat(torch.autograd.Function):
         args = (x.shape[0], color.shape[1], img_size, float(sigma), float(lo), float(hi), int(bool(normalize_color)),
                 int(bool(y_up)), float(pixel_size))
         work = torch.empty(max(1, _lib.sphops_splat_workspace_bytes(x.shape[0])), dtype=torch.uint8, device=x.device)
-        st = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(x.device.index))
         _native.check(_lib.sphops_splat_forward(_ptr(x), _ptr(color), _ptr(starts), images, *args, _ptr(out),
                                                 _ptr(work), st))
         ctx.save_for_backward(x, color, starts)
@@ -51,7 +51,7 @@ class Splat(torch.autograd.Function):
         d_out = d_out.contiguous()
         d_x = torch.empty_like(x)
         d_color = torch.empty_like(color)
-        st = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(x.device.index))
         _native.check(_lib.sphops_splat_backward(_ptr(x), _ptr(color), _ptr(starts), starts.numel() - 1, *ctx.args,
                                                  _ptr(d_out), _ptr(d_x), _ptr(d_color), st))
         return d_x, d_color, None, None, None, None, None, None, None, None

@@ -57,7 +57,7 @@ class EulerUpdate(torch.autograd.Function):
         x_out = torch.empty_like(x_bin)
         s_out = torch.empty_like(s_bin)
         dx_norm = torch.empty(B, N, device=y.device)
-        st = ctypes.c_void_p(torch.cuda.current_stream(y.device).cuda_stream)
+        st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(y.device.index))
         _native.check(_lib.sphops_euler_update_forward(
             dim, P, _ptr(y), _ptr(x_bin), _ptr(s_bin), _ptr(mask), _ptr(noise), _ptr(x_out), _ptr(s_out),
             _ptr(dx_norm), B * N, C, alpha, eps, dt, noise_std, math.sqrt(dt), st))
@@ -76,7 +76,7 @@ class EulerUpdate(torch.autograd.Function):
             d_s = d_s.contiguous() if d_s is not None else None
             d_n = d_n.contiguous() if d_n is not None else None
             d_y = torch.empty_like(y)
-            st = ctypes.c_void_p(torch.cuda.current_stream(y.device).cuda_stream)
+            st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(y.device.index))
             _native.check(_lib.sphops_euler_update_backward(
                 dim, P, _ptr(y), _ptr(mask), _ptr(d_x), _ptr(d_s), _ptr(d_n), _ptr(d_y), B * N, C, alpha, eps, dt,
                 st))
