@@ -377,20 +377,27 @@ class _HashGridNative:
                                              ctypes.c_void_p(buf.data_ptr()), capacity,
                                              ctypes.c_void_p(count.data_ptr()), st))
 
+        def schedule():
+            _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
+                                                 ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
+                                                 ctypes.c_void_p(small.data_ptr() + 4),
+                                                 ctypes.c_void_p(waves2.data_ptr()),
+                                                 ctypes.c_void_p(small.data_ptr() + 8), st))
+            small[0:1].copy_(start[n:n + 1])
+            return small.cpu().tolist()
+
         fill(index, cap)
-        _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
-                                             ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
-                                             ctypes.c_void_p(small.data_ptr() + 4), ctypes.c_void_p(waves2.data_ptr()),
-                                             ctypes.c_void_p(small.data_ptr() + 8), st))
-        small[0:1].copy_(start[n:n + 1])
-        total, nwaves, nwaves2 = small.cpu().tolist()
+        total, nwaves, nwaves2 = schedule()
         if total > limit:
             # too large to store: the operators scan the stencil instead
             return None
         if total > cap:
+            # the first fill cut rows at the buffer's end (their counts too), so
+            # fill again and schedule from the full counts
             cap = total
             index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
             fill(index, cap)
+            total, nwaves, nwaves2 = schedule()
         if total > prev:  # ~12% headroom, so that the next snapshot of a moving cloud fits
             self._index_capacity = total + total // 8
         self._wave_counts = (nwaves, nwaves2)

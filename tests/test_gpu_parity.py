@@ -268,11 +268,17 @@ def test_neighbor_list(name):
         assert np.all(start[1:] >= start[:-1] + count), label   # rows do not overlap
         assert nbr[5] > 0 or c.B * c.N == 0
 
-    check(hg.neighbor_list(xb, bo), f"{name}:first")
+    first = hg.neighbor_list(xb, bo)
+    check(first, f"{name}:first")
     hg._index_capacity = 7            # force the too-small buffer and the second fill
     nbr = hg.neighbor_list(xb, bo)
     check(nbr, f"{name}:refill")
     assert hg._index_capacity >= int(nbr[0][-1].item())
+    # the schedule comes from the full counts, as without the refill
+    assert nbr[5] == first[5] and nbr[7] == first[7]
+    assert torch.equal(nbr[3], first[3])
+    assert torch.equal(nbr[4][:2 * nbr[5]], first[4][:2 * first[5]])
+    assert torch.equal(nbr[6][:2 * nbr[7]], first[6][:2 * first[7]])
 
 
 @pytest.mark.parametrize("name", NAMES)
