@@ -62,3 +62,19 @@ def test_args_struct_matches_header():
     body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
     names = [re.sub(r"\[.*\]", "", decl.split()[-1].lstrip("*")) for decl in body.split(";") if decl.strip()]
     assert names == [f[0] for f in _native.Args._fields_]
+
+
+def test_header_is_plain_c(tmp_path):
+    """The ABI header compiles as strict C99 (no C++ in the boundary), so a
+    cgo / FFI binding can include it as it is."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        import pytest
+        pytest.skip("gcc not available")
+    src = tmp_path / "abi.c"
+    src.write_text('#include "sphops_hip.h"\nint main(void) { return sizeof(sphops_args) ? 0 : 1; }\n')
+    r = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.dirname(HEADER),
+                        "-c", str(src), "-o", str(tmp_path / "abi.o")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
