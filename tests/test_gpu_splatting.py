@@ -19,7 +19,15 @@ CASES = [
     dict(img_size=256, sigma=2.0, normalize_color=True, y_up=True),  # the reference's defaults, y flipped: r = 20
     dict(img_size=50, sigma=1.5, normalize_color=False, y_up=False, lo=-1.5, hi=2.0),
     dict(img_size=17, sigma=1.0, pixel_size=2.0 / 8, normalize_color=True, y_up=True),  # tiles cut by the edge
+    dict(img_size=32, sigma=0.1, normalize_color=False, y_up=True),  # the smallest patch, r = 1
+    dict(img_size=96, sigma=12.0, normalize_color=False, y_up=False),  # r = 60: patches wider than tiles
+    dict(img_size=64, sigma=3.0, pixel_size=2.0 / 64, normalize_color=True, y_up=False, lo=-3.0, hi=1.0),
 ]
+PARTICLES = {5: 200}  # fewer particles where the patch is large (the float64 oracle is dense)
+# sigma = 0.1 px: the exponent -|offset - frac|^2 / (2 sigma^2) reaches -50 within a
+# pixel, so fp32 rounding of the position (about 2e-6 px at 30 px) moves a weight by
+# up to 1e-4 of itself, in the reference's fp32 arithmetic as much as here
+IMAGE_ATOL = {4: 2e-5}
 
 
 def _radius(kw):
@@ -37,7 +45,7 @@ def _close(name, got, ref, rtol=2e-5, atol=1e-6):
     assert not bad.any(), f"{name}: {bad.sum()} of {bad.size} off, max err {err.max():.3g} (max |ref| {scale:.3g})"
 
 
-def _check(images_fn, oracle_images, x, c, seed):
+def _check(images_fn, oracle_images, x, c, seed, image_atol=1e-6):
     xg = x.float().cuda().requires_grad_(True)
     cg = c.float().cuda().requires_grad_(True)
     img = images_fn(xg, cg)
@@ -45,7 +53,7 @@ def _check(images_fn, oracle_images, x, c, seed):
     cr = cg.detach().double().cpu().requires_grad_(True)
     ref = oracle_images(xr, cr)
     assert img.shape == ref.shape
-    _close("image", img.detach().cpu(), ref.detach())
+    _close("image", img.detach().cpu(), ref.detach(), atol=image_atol)
     up = torch.randn(ref.shape, generator=torch.Generator().manual_seed(seed), dtype=torch.float64)
     gx, gc = torch.autograd.grad(img, (xg, cg), up.float().cuda())
     rx, rc = torch.autograd.grad(ref, (xr, cr), up)
@@ -57,8 +65,10 @@ def _check(images_fn, oracle_images, x, c, seed):
 def test_single_image(ci):
     from npa_amd import splatting as SP
     kw = CASES[ci]
-    x, c = particles(700, kw["img_size"], _radius(kw), kw.get("lo", -1.0), kw.get("hi", 1.0), seed=ci, ncolor=5)
-    _check(lambda a, b: SP.splat_particles(a, b, **kw), lambda a, b: S.splat(a, b, **kw), x, c, ci)
+    x, c = particles(PARTICLES.get(ci, 700), kw["img_size"], _radius(kw), kw.get("lo", -1.0), kw.get("hi", 1.0),
+                     seed=ci, ncolor=3 + ci % 5)
+    _check(lambda a, b: SP.splat_particles(a, b, **kw), lambda a, b: S.splat(a, b, **kw), x, c, ci,
+           image_atol=IMAGE_ATOL.get(ci, 1e-6))
 
 
 def test_batch_and_sections():
