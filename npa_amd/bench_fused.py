@@ -10,6 +10,8 @@ reference's own torch formulation of the same computation on the same GPU
   (models/npa.py:123-204), fused update against the reference's torch ops;
 * ``splat``: splat_particles_batch forward + backward (utils/splatting.py),
   against the reference's torch scatter_add_ formulation;
+* ``rollout``: an 8-step step_euler rollout with its backward at the
+  reference's growing-config shape, eager and replayed from one HIP graph;
 * ``graph``: the bench's perception step eager and replayed from a HIP graph
   (the grid's capture mode), for every BASELINE configuration.
 
@@ -226,9 +228,58 @@ def bench_graph(cfg, iters=20):
             "eager_ms": eager, "graph_replay_ms": replay, "list_overflow": overflow}
 
 
+def bench_rollout(K=8, B=8, N=4096, C=16, iters=5):
+    """A K-step step_euler rollout with its backward, the shape of the
+    reference's training loop (train.py:227-237; growing config: batch 8 of
+    4096 2D particles, 16 channels), eager and replayed from one captured
+    graph.  No update mask (update_prob = 1): the mask's random draws would
+    need a graph-safe generator."""
+    from npa_amd import workloads as W
+    dev = torch.device("cuda", 0)
+    wl = W.make("cfg1")
+    rng = torch.Generator(device=dev).manual_seed(0)
+    x0 = torch.zeros(B, N, 2, device=dev)
+    r = torch.sqrt(torch.rand(B, N, device=dev, generator=rng)) * 0.5
+    th = torch.rand(B, N, device=dev, generator=rng) * 6.283185307179586
+    x0[..., 0], x0[..., 1] = r * torch.cos(th), r * torch.sin(th)
+    s0 = torch.randn(B, N, C, device=dev, generator=rng) * 0.1
+    grid = sp.HashGrid(dim=2, boundary="clamped", mode="grid", grid_size=list(wl.grid_size), eps=wl.h,
+                       num_particles=N, batch_size=B, max_particles_per_block=wl.maxp)
+    torch.manual_seed(0)
+    model = _NPA(2, C).to(dev)
+    up_x, up_s = torch.randn_like(x0), torch.randn_like(s0)
+
+    def run(xi, si):
+        x, s = xi, si.detach().requires_grad_(True)
+        for _ in range(K):
+            x, s, _ = step.step_euler(model, x, s, grid, update_prob=1.0)
+        torch.autograd.backward([x, s], [up_x, up_s])
+
+    for p in model.parameters():
+        p.grad = torch.zeros_like(p)
+    eager = _time(lambda: run(x0, s0), iters)
+    grid.set_capture_capacity(2 * grid.list_capacity_hint())
+    sx, ss_ = x0.clone(), s0.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run(sx, ss_)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(sx, ss_)
+    replay = _time(graph.replay, iters)
+    overflow = grid.list_overflow()
+    grid.set_capture_capacity(0)
+    return {"bench": "rollout", "config": f"{K} steps, batch {B} x {N} 2D particles, C = {C}, MLP 128",
+            "what": "step_euler rollout + backward", "eager_ms": eager, "graph_replay_ms": replay,
+            "list_overflow": overflow}
+
+
 def run_all():
     torch.cuda.set_device(0)
-    results = [bench_perceive(), bench_step(), bench_splat()]
+    results = [bench_perceive(), bench_step(), bench_splat(), bench_rollout()]
     results += [bench_graph(c) for c in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5")]
     for r in results:
         print(json.dumps(r), flush=True)

@@ -36,6 +36,21 @@ def _stream(t):
     return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(t.device.index))
 
 
+def buffer_value(t):
+    """The float value of a one-element model buffer (eps0, alpha), read from
+    the device once and remembered on the tensor object for its current
+    version: reading a GPU tensor on the host synchronises, which would stall
+    every step (and is not allowed while a HIP graph is being captured)."""
+    if not torch.is_tensor(t):
+        return float(t)
+    hit = getattr(t, "_npa_host_value", None)
+    if hit is not None and hit[0] == t._version:
+        return hit[1]
+    v = float(t.reshape(-1)[0])
+    t._npa_host_value = (t._version, v)
+    return v
+
+
 def feature_width(C, D, flags):
     return 2 * C + (C * D if flags & STATE_GRAD else 0) + (D if flags & DENSITY_GRAD else 0)
 
@@ -92,7 +107,7 @@ def perceive(x, s, grid, eps0=0.1, state_grad=True, density_grad=True, log_norm_
     # coef = eps / eps0 and coef ** (1 + D) rounded as torch evaluates them on
     # the model's fp32 buffer: a Python float over a tensor is the tensor's
     # reciprocal times the float; the cube is c * c * c, other powers powf
-    e0 = float(eps0.reshape(-1)[0]) if torch.is_tensor(eps0) else float(eps0)
+    e0 = buffer_value(eps0)
     coef = np.float32(np.float32(1.0) / np.float32(e0)) * np.float32(grid.eps)
     coef_rho = coef * coef * coef if D == 2 else np.power(coef, np.float32(1 + D))
     flags = 0

@@ -22,7 +22,7 @@ import math
 
 import torch
 
-from .perceive import perceive
+from .perceive import buffer_value, perceive
 from .sphops import _native, unbin_particles
 
 _lib = _native.lib
@@ -102,7 +102,7 @@ def _step(model, x, s, grid, dt, update_prob, noise_std):
     model.last_snapshot = snapshot
     y = model.model(z).contiguous()
     mask, noise = _draws(x, update_prob, noise_std)
-    alpha = float(model.alpha.reshape(-1)[0]) if torch.is_tensor(model.alpha) else float(model.alpha)
+    alpha = buffer_value(model.alpha)
     x_new, s_new, dx_norm = EulerUpdate.apply(y, x_bin.contiguous(), s_bin.contiguous(), mask, noise,
                                               model.spatial_dims, alpha, float(grid.eps), float(dt),
                                               float(noise_std))

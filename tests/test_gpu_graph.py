@@ -71,3 +71,86 @@ def test_captured_step_replays_match_eager(dim, periodic, mode):
         assert torch.equal(again[0], eager[0][0])
     assert not grid.list_overflow()
     grid.set_capture_capacity(0)
+
+
+class _TinyNPA(torch.nn.Module):
+    """The NPA attributes step_euler reads (models/npa.py:15-63), small MLP."""
+
+    def __init__(self, D, C):
+        super().__init__()
+        self.spatial_dims = D
+        self.register_buffer("eps0", torch.tensor([0.1]))
+        self.register_buffer("alpha", torch.tensor([1.0]))
+        self.state_grad = self.density_grad = self.log_norm_grad = self.log_norm_density_grad = True
+        self.stopgrad_pos, self.stopgrad_state = True, False
+        self.model = torch.nn.Sequential(torch.nn.Linear(2 * C + C * D + D, 32), torch.nn.ReLU(),
+                                         torch.nn.Linear(32, D + C, bias=False))
+
+
+def test_captured_rollout_matches_eager():
+    """A 3-step step_euler rollout with its backward (train.py:227-237 without
+    the random mask) captured as one graph: replays on new states match the
+    eager rollout."""
+    import npa_amd.sphops as sp
+    from npa_amd import step as S
+    B, N, C, D, K = 2, 1500, 8, 2, 3
+    cases = [H.random_case("rollout", B, N, C, D, 16, 0.06, False, "grid", uniform=False, sigma=0.3, seed=seed)
+             for seed in (11, 12, 13)]
+    c0 = cases[0]
+    grid = sp.HashGrid(dim=D, boundary="clamped", mode="grid", grid_size=list(c0.grid_size), eps=c0.eps,
+                       num_particles=N, batch_size=B, max_particles_per_block=c0.maxp)
+    torch.manual_seed(0)
+    model = _TinyNPA(D, C).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    up_x = torch.randn(B, N, c0.x.shape[-1], device="cuda", generator=gen)
+    up_s = torch.randn(B, N, C, device="cuda", generator=gen)
+
+    def run(x0, s0):
+        leaf = s0.detach().requires_grad_(True)
+        x, s = leaf_rollout(x0, leaf)
+        torch.autograd.backward([x, s], [up_x, up_s])
+        return [x.detach(), s.detach(), leaf.grad] + [p.grad for p in model.parameters()]
+
+    def leaf_rollout(x0, leaf):
+        x, s = x0, leaf
+        for _ in range(K):
+            x, s, _ = S.step_euler(model, x, s, grid, update_prob=1.0)
+        return x, s
+
+    xs = [torch.from_numpy(c.x).cuda() for c in cases]
+    ss = [torch.from_numpy(c.s).cuda() for c in cases]
+    for p in model.parameters():
+        p.grad = torch.zeros_like(p)
+    run(xs[0], ss[0])  # teaches the grid its fused passes
+    eager = []
+    for x0, s0 in zip(xs, ss):
+        for p in model.parameters():
+            p.grad.zero_()
+        eager.append([t.clone() for t in run(x0, s0)])
+    grid.set_capture_capacity(2 * grid.list_capacity_hint())
+    static_x, static_s = xs[0].clone(), ss[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            for p in model.parameters():
+                p.grad.zero_()
+            run(static_x, static_s)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    for p in model.parameters():
+        p.grad.zero_()
+    with torch.cuda.graph(graph):
+        outs = run(static_x, static_s)
+    names = ["x", "s", "dL/ds0"] + [f"dL/dW{i}" for i in range(len(list(model.parameters())))]
+    for k in (1, 2, 0):
+        static_x.copy_(xs[k])
+        static_s.copy_(ss[k])
+        for p in model.parameters():
+            p.grad.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(names, outs, eager[k]):
+            assert torch.allclose(got, ref, rtol=1e-6, atol=1e-7), f"replay {k}: {name}"
+    assert not grid.list_overflow()
+    grid.set_capture_capacity(0)
