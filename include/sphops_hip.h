@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 9
+#define SPHOPS_ABI_VERSION 10
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -329,6 +329,18 @@ int sphops_splat_backward(const float* x, const float* color, const int32_t* sta
                           int64_t particles, int ncolor, int img_size, double sigma, double lo, double hi,
                           int normalize_color, int y_up, double pixel_size, const float* d_out, float* d_x,
                           float* d_color, void* stream);
+
+/* Weight and bias gradients of a linear layer y = x W^T + b over `rows` rows
+ * (no counterpart in the reference's native module: the NPA MLP is
+ * torch.nn.Linear, models/npa.py:63-78).  x (rows, in_features) and dy
+ * (rows, out_features) row-major fp32; writes dw = dy^T x (out_features,
+ * in_features) and, unless NULL, db = the column sums of dy (out_features).
+ * Deterministic (chunk partial sums added in a fixed order).  workspace holds
+ * sphops_linear_weight_grad_workspace_bytes(rows, in_features, out_features)
+ * bytes. */
+int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows,
+                              int in_features, int out_features, void* workspace, void* stream);
+int64_t sphops_linear_weight_grad_workspace_bytes(int64_t rows, int in_features, int out_features);
 
 #ifdef __cplusplus
 }

@@ -8,6 +8,8 @@ reference's own torch formulation of the same computation on the same GPU
 * ``step_euler``: perception, an NPA-shaped MLP (128 hidden units), the Euler
   update and a loss on x, s and the |dx| stats, forward + backward
   (models/npa.py:123-204), fused update against the reference's torch ops;
+* ``mlp``: the NPA MLP forward + backward over 2^20 rows, torch's autograd
+  against npa_amd.mlp's row-chunked weight gradients;
 * ``splat``: splat_particles_batch forward + backward (utils/splatting.py),
   against the reference's torch scatter_add_ formulation;
 * ``rollout``: an 8-step step_euler rollout with its backward at the
@@ -158,7 +160,7 @@ def bench_step(cfg="cfg5", iters=10):
         if fused:
             xn, sn, st = step.step_euler(model, x, sr, grid, update_prob=0.5, intermediate=True)
             dn = st["dx_norm"]
-        else:
+        else:  # the reference's step: torch feature assembly, torch MLP, torch update
             z, xb, sb, _ = _ref_perceive(x, sr, grid)
             xn, sn, dn = _ref_euler(model.model(z), xb, sb, wl.dim, model.alpha, grid.eps, 0.5)
         ((sn ** 2).mean() + (xn ** 2).mean() + dn).backward()
@@ -228,6 +230,25 @@ def bench_graph(cfg, iters=20):
             "eager_ms": eager, "graph_replay_ms": replay, "list_overflow": overflow}
 
 
+def bench_mlp(rows=1 << 20, iters=10):
+    """The NPA MLP (83 -> 128 -> ReLU -> 19, the 3D C = 16 shape) forward +
+    backward over one row per particle: torch's own autograd against
+    npa_amd.mlp (row-chunked weight gradients)."""
+    from npa_amd import mlp as M
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    net = torch.nn.Sequential(torch.nn.Linear(83, 128), torch.nn.ReLU(), torch.nn.Linear(128, 19, bias=False)).to(dev)
+    z = torch.randn(rows, 83, device=dev)
+    up = torch.randn(rows, 19, device=dev)
+
+    def run(fused):
+        zz = z.detach().requires_grad_(True)
+        (M.mlp(net, zz) if fused else net(zz)).backward(up)
+
+    return {"bench": "mlp", "config": f"{rows} rows, 83 -> 128 -> 19", "what": "MLP forward + backward",
+            "fused_ms": _time(lambda: run(True), iters), "reference_torch_ms": _time(lambda: run(False), iters)}
+
+
 def bench_rollout(K=8, B=8, N=4096, C=16, iters=5):
     """A K-step step_euler rollout with its backward, the shape of the
     reference's training loop (train.py:227-237; growing config: batch 8 of
@@ -279,7 +300,7 @@ def bench_rollout(K=8, B=8, N=4096, C=16, iters=5):
 
 def run_all():
     torch.cuda.set_device(0)
-    results = [bench_perceive(), bench_step(), bench_splat(), bench_rollout()]
+    results = [bench_perceive(), bench_step(), bench_mlp(), bench_splat(), bench_rollout()]
     results += [bench_graph(c) for c in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5")]
     for r in results:
         print(json.dumps(r), flush=True)

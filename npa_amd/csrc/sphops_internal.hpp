@@ -194,6 +194,14 @@ void run_splat_forward(const SplatParams& sp, const float* x, const float* color
 void run_splat_backward(const SplatParams& sp, const float* x, const float* color, const int32_t* starts, int images,
                         int64_t n, const float* d_img, float* d_x, float* d_color, hipStream_t st);
 
+// linear_grad.hip: weight / bias gradients of a linear layer over many rows
+constexpr int64_t kMaxChunkRows = 8192;
+constexpr int64_t kMaxLinearRows = kMaxChunkRows * 65535;  // chunks index the grid's y dimension
+int64_t linear_grad_chunk_rows(int64_t rows);
+int64_t linear_grad_chunks(int64_t rows);
+void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows, int nin, int nout,
+                            float* work, hipStream_t st);
+
 constexpr uint32_t kMaxChannels = 64;
 constexpr int kRadixBins = 1024;  // digit values per radix-sort pass (10 bits)
 

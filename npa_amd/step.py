@@ -4,7 +4,8 @@
 ``step_euler(model, x, s, grid, dt, update_prob, intermediate, noise_std)``
 returns what the reference's ``step_euler`` returns for an ``NPA`` model:
 perception through ``npa_amd.perceive.perceive`` (fused features), the
-model's own MLP (``model.model``, torch linear layers), then one HIP kernel
+model's own MLP (``model.model``; its weight gradients through
+``npa_amd.mlp``'s row-chunked kernel), then one HIP kernel
 for the position-step scaling of NPA.forward, the update mask, the zero
 padding of 3D positions, the Euler update, the optional noise and the
 per-particle |dx| of the ``intermediate`` stats; one kernel maps the
@@ -22,6 +23,7 @@ import math
 
 import torch
 
+from .mlp import mlp
 from .perceive import buffer_value, perceive
 from .sphops import _native, unbin_particles
 
@@ -100,7 +102,7 @@ def _draws(x, update_prob, noise_std):
 def _step(model, x, s, grid, dt, update_prob, noise_std):
     z, x_bin, s_bin, snapshot = _perceive(model, x, s, grid)
     model.last_snapshot = snapshot
-    y = model.model(z).contiguous()
+    y = mlp(model.model, z).contiguous()
     mask, noise = _draws(x, update_prob, noise_std)
     alpha = buffer_value(model.alpha)
     x_new, s_new, dx_norm = EulerUpdate.apply(y, x_bin.contiguous(), s_bin.contiguous(), mask, noise,
@@ -141,7 +143,7 @@ def step_euler_static(model, x, s, grid, dt=1.0, update_prob=0.5, channel_mask=N
     B, N, C = s.shape
     z, x_bin, s_bin, snapshot = _perceive(model, x, s, grid)
     model.last_snapshot = snapshot
-    ds = model.model(z)
+    ds = mlp(model.model, z)
     mask = 1.0
     if update_prob < 1.0:
         mask = (torch.rand(B, N, 1, device=x.device) < update_prob).float()

@@ -1,0 +1,69 @@
+"""The row-chunked weight and bias gradients of a linear layer
+(``sphops_linear_weight_grad`` via npa_amd.mlp) against float64 sums, over
+row counts from 0 to 3e5 and layer shapes with one and several 128 x 128
+output tiles; and npa_amd.mlp.mlp against the module's own autograd."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(83, 128), (128, 19), (5, 3), (200, 130)]
+ROWS = [0, 1, 100, 1000, 33333, 300000]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("rows", ROWS)
+def test_weight_grad_matches_float64(shape, rows):
+    import ctypes
+    from npa_amd.sphops import _native
+    in_f, out_f = shape
+    g = torch.Generator(device="cuda").manual_seed(rows + in_f)
+    x = torch.randn(rows, in_f, device="cuda", generator=g)
+    dy = torch.randn(rows, out_f, device="cuda", generator=g)
+    dw = torch.full((out_f, in_f), float("nan"), device="cuda")
+    db = torch.full((out_f,), float("nan"), device="cuda")
+    nb = _native.lib.sphops_linear_weight_grad_workspace_bytes(rows, in_f, out_f)
+    work = torch.empty(max(nb // 4, 1), device="cuda")
+    st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(0))
+    _native.check(_native.lib.sphops_linear_weight_grad(
+        ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(dy.data_ptr()), ctypes.c_void_p(dw.data_ptr()),
+        ctypes.c_void_p(db.data_ptr()), rows, in_f, out_f, ctypes.c_void_p(work.data_ptr()), st))
+    xd, yd = x.double().cpu(), dy.double().cpu()
+    ref_w, ref_b = yd.T @ xd, yd.sum(0)
+    bound_w = (yd.abs().T @ xd.abs()) * 1e-5 + 1e-30   # fp32 summation error scale
+    bound_b = yd.abs().sum(0) * 1e-5 + 1e-30
+    assert torch.all((dw.cpu().double() - ref_w).abs() <= bound_w), f"dW rows={rows} shape={shape}"
+    assert torch.all((db.cpu().double() - ref_b).abs() <= bound_b), f"db rows={rows} shape={shape}"
+
+
+def test_weight_grad_is_deterministic():
+    from npa_amd import mlp as M
+    lin = torch.nn.Linear(83, 128).cuda()
+    x = torch.randn(200000, 83, device="cuda")
+    dy = torch.randn(200000, 128, device="cuda")
+    grads = []
+    for _ in range(2):
+        lin.zero_grad()
+        M.linear(x, lin).backward(dy)
+        grads.append((lin.weight.grad.clone(), lin.bias.grad.clone()))
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+
+
+@pytest.mark.parametrize("hidden", [None, 32])
+def test_mlp_matches_module_autograd(hidden):
+    from npa_amd import mlp as M
+    torch.manual_seed(0)
+    if hidden is None:
+        net = torch.nn.Linear(66, 18, bias=False).cuda()
+    else:
+        net = torch.nn.Sequential(torch.nn.Linear(66, hidden), torch.nn.ReLU(),
+                                  torch.nn.Linear(hidden, 18, bias=False)).cuda()
+    z = torch.randn(3, 5000, 66, device="cuda", requires_grad=True)
+    up = torch.randn(3, 5000, 18, device="cuda")
+    out = M.mlp(net, z)
+    assert torch.equal(out, net(z))  # the forward is torch's own
+    got = torch.autograd.grad(out, [z] + list(net.parameters()), up)
+    ref = torch.autograd.grad(net(z), [z] + list(net.parameters()), up)
+    for a, b in zip(got, ref):
+        assert torch.allclose(a, b, rtol=1e-4, atol=1e-4 * float(b.abs().max())), "gradient differs"
