@@ -7,7 +7,7 @@ tiny output and a reduction over 10^5-10^6 rows; the library GEMM takes that
 shape with few output tiles and runs at a few TFLOP/s.  ``LinearRows`` keeps
 torch's forward and input gradient (both large, well-shaped GEMMs) and
 replaces the weight and bias gradients by the row-chunked kernel.
-``mlp(seq, z)`` runs a module the way the module would run itself, with its
+``mlp(module, z)`` runs a module the way the module would run itself, with its
 ``torch.nn.Linear`` layers through ``LinearRows``; the parameters are the
 module's own, so optimisers and checkpoints see no difference.
 """
