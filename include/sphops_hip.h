@@ -335,7 +335,9 @@ int sphops_splat_backward(const float* x, const float* color, const int32_t* sta
  * torch.nn.Linear, models/npa.py:63-78).  x (rows, in_features) and dy
  * (rows, out_features) row-major fp32; writes dw = dy^T x (out_features,
  * in_features) and, unless NULL, db = the column sums of dy (out_features).
- * Deterministic (chunk partial sums added in a fixed order).  workspace holds
+ * in_features and out_features are at most 32768.  Computed on the fp32
+ * matrix cores; deterministic (chunk partial sums added in a fixed order).
+ * workspace holds
  * sphops_linear_weight_grad_workspace_bytes(rows, in_features, out_features)
  * bytes. */
 int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows,

@@ -779,7 +779,7 @@ int sphops_splat_backward(const float* x, const float* color, const int32_t* sta
 
 int64_t sphops_linear_weight_grad_workspace_bytes(int64_t rows, int in_features, int out_features) {
   if (rows < 0 || in_features < 1 || out_features < 1) return 0;
-  return 4 * sphops::linear_grad_chunks(rows) * ((int64_t)in_features * out_features + out_features);
+  return 4 * sphops::linear_grad_chunks(rows, in_features, out_features) * ((int64_t)in_features * out_features + out_features);
 }
 
 int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows,
@@ -787,7 +787,11 @@ int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float*
   return guarded([&] {
     require(rows >= 0 && rows <= sphops::kMaxLinearRows, "rows must be in [0, " +
                                                              std::to_string(sphops::kMaxLinearRows) + "]");
-    require(in_features >= 1 && out_features >= 1, "in_features and out_features must be >= 1");
+    require(in_features >= 1 && out_features >= 1 && in_features <= sphops::kMaxLinearFeatures &&
+                out_features <= sphops::kMaxLinearFeatures,
+            "in_features and out_features must be in [1, " + std::to_string(sphops::kMaxLinearFeatures) + "]");
+    require(sphops::linear_grad_fits(rows, in_features, out_features),
+            "layer too large: more than 2^25 (row chunk, 32-row output band) pairs");
     require(dw != nullptr && (rows == 0 || (x && dy && workspace)), "null buffer");
     sphops::run_linear_weight_grad(x, dy, dw, db, rows, in_features, out_features,
                                    static_cast<float*>(workspace), sphops::as_stream(stream));

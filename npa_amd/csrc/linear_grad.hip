@@ -5,139 +5,226 @@
 // dY (rows x out) row-major fp32.  The output is small (128 x 83 for the NPA
 // MLP's first layer) and the reduction is long (one row per particle, 10^6
 // at the 3D stress size); the library GEMM picks a handful of output tiles
-// for that shape and leaves most of the GPU idle.  Here the rows are split
-// into chunks: workgroup (tile, chunk) stages 32 rows at a time of its
-// 128 x 128 output tile's dY and X columns in LDS, and each thread
-// accumulates an 8 x 8 block of the tile in registers.  Each row of X and dY
-// is read from HBM once per tile (once in all for layers up to 128 x 128).
-// The per-chunk partial sums go to a workspace and a second kernel adds them
-// in chunk order, so the result is deterministic.
+// for that shape and leaves most of the GPU idle.  Here the reduction runs on
+// the fp32 matrix cores (v_mfma_f32_32x32x2_f32: a 32 x 32 tile, two rows per
+// instruction):
+// * the rows are split into chunks and the output into jobs of one 32-row
+//   band of dW by up to four 32-column tiles; each wave takes one (chunk,
+//   job), reads its rows straight from HBM (lanes 0-31 one row, lanes 32-63
+//   the next, 32 consecutive columns each, through buffer loads whose range
+//   check zeroes what lies past the chunk or the layer) 16 rows ahead of the
+//   matrix instructions, and keeps its tiles in registers;
+// * the waves of one workgroup share a chunk when a chunk has four or more
+//   jobs, so the X columns they all read come from one L1;
+// * each wave writes its tiles (and, for the jobs of the first column tile,
+//   the column sums of its dY band) as the chunk's partial sums, and a second
+//   kernel adds the partials in a fixed order, so the result is
+//   deterministic.
 #include "sphops_internal.hpp"
+#include "sphops_device.hpp"
 
 namespace sphops {
 
 namespace {
 
-constexpr int kLT = 128;        // output tile side (out and in)
-constexpr int kLR = 32;         // rows staged per LDS round
-constexpr int kLThreads = 256;  // 16 x 16 threads, 8 x 8 outputs each
-constexpr int kLB = 8;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-__global__ __launch_bounds__(kLThreads) void k_linear_partial(const float* __restrict__ x,
-                                                              const float* __restrict__ dy,
-                                                              float* __restrict__ part_w,
-                                                              float* __restrict__ part_b, int64_t rows, int nin,
-                                                              int nout, int tiles_in, int64_t chunk_rows) {
-  __shared__ float4 sy[kLR][kLT / 4];  // dY rows, this tile's out columns
-  __shared__ float4 sx[kLR][kLT / 4];  // X rows, this tile's in columns
-  const int tile = blockIdx.x;
-  const int o0 = (tile / tiles_in) * kLT, i0 = (tile % tiles_in) * kLT;
-  const int64_t chunk = blockIdx.y;
-  const int64_t r0 = chunk * chunk_rows;
-  const int64_t r1 = min<int64_t>(rows, r0 + chunk_rows);
-  const int tid = threadIdx.x;
-  const int to = (tid / 16) * kLB, ti = (tid % 16) * kLB;  // this thread's 8 x 8 block in the tile
-  float acc[kLB][kLB] = {};
-  float accb[kLB] = {};
-  const bool bias_lane = i0 == 0 && part_b != nullptr && ti == 0;
-  float* sy1 = reinterpret_cast<float*>(&sy[0][0]);
-  float* sx1 = reinterpret_cast<float*>(&sx[0][0]);
-  for (int64_t rb = r0; rb < r1; rb += kLR) {
-    const int nr = (int)min<int64_t>(kLR, r1 - rb);
-    // stage kLR rows x kLT columns of each operand (zeros past the edges)
-    for (int e = tid; e < kLR * kLT; e += kLThreads) {
-      const int r = e / kLT, c = e % kLT;
-      const bool rowok = r < nr;
-      sy1[e] = (rowok && o0 + c < nout) ? dy[(rb + r) * nout + o0 + c] : 0.0f;
-      sx1[e] = (rowok && i0 + c < nin) ? x[(rb + r) * nin + i0 + c] : 0.0f;
+constexpr int kMT = 32;             // matrix-core tile side
+constexpr int kPairs = 8;           // row pairs per load group (16 rows)
+constexpr int kGroupRows = 2 * kPairs;
+constexpr int kMaxTilesPerJob = 4;  // column tiles per wave
+constexpr int kWaveTarget = 2048;   // waves per launch at large row counts (two per SIMD)
+constexpr int64_t kMinChunkRows = 128;
+constexpr int kReduceWaves = 16;    // chunk-sum workgroup: 16 waves x 64 elements
+
+struct LinearPlan {
+  int o_tiles, i_tiles, i_groups, ti, jobs;
+  int64_t chunk_rows, chunks;
+};
+
+LinearPlan linear_plan(int64_t rows, int nin, int nout) {
+  LinearPlan p;
+  p.o_tiles = (nout + kMT - 1) / kMT;
+  p.i_tiles = (nin + kMT - 1) / kMT;
+  p.i_groups = (p.i_tiles + kMaxTilesPerJob - 1) / kMaxTilesPerJob;
+  p.ti = (p.i_tiles + p.i_groups - 1) / p.i_groups;
+  p.jobs = p.o_tiles * p.i_groups;
+  const int64_t want = std::max<int64_t>(1, kWaveTarget / p.jobs);
+  int64_t c = (rows + want - 1) / want;
+  c = (c + kGroupRows - 1) / kGroupRows * kGroupRows;
+  p.chunk_rows = std::min<int64_t>(kMaxChunkRows, std::max<int64_t>(kMinChunkRows, c));
+  p.chunks = rows > 0 ? (rows + p.chunk_rows - 1) / p.chunk_rows : 0;
+  return p;
+}
+
+// Operands are read through buffer resources that span one chunk's rows:
+// the hardware returns 0 for a byte offset at or past the resource's size, so
+// rows past the chunk and lanes whose column lies past the layer (offset
+// kOffLane) load zeros with no select after the load, and the next group's
+// loads stay in flight under the current group's matrix instructions.  The
+// offsets stay below 2^32 for features up to kMaxLinearFeatures.
+constexpr uint32_t kOffLane = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3: 32-bit raw data
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const float* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ float load_b32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// Wave `wid` = chunk * jobs + job.  Job j covers dW rows o0 = 32 (j / i_groups)
+// .. +31 and columns i0 = 32 TI (j % i_groups) .. + 32 TI - 1.  For the matrix
+// instruction, lane l supplies A[m = l % 32][k = l / 32] = dY[row_k][o0 + m]
+// and B[k = l / 32][n = l % 32] = X[row_k][i0 + 32 t + n]; result register r
+// of lane l holds tile row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+template <int TI>
+__global__ __launch_bounds__(256) void k_linear_mfma(const float* __restrict__ x, const float* __restrict__ dy,
+                                                     float* __restrict__ part, int64_t rows, int nin, int nout,
+                                                     int i_groups, int jobs, int64_t chunk_rows,
+                                                     uint32_t total_waves) {
+  const uint32_t wid = __builtin_amdgcn_readfirstlane(xcd_block_id() * 4u + threadIdx.x / 64u);
+  if (wid >= total_waves) return;
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int64_t chunk = wid / (uint32_t)jobs;
+  const int job = (int)(wid % (uint32_t)jobs);
+  const int o0 = (job / i_groups) * kMT, i0 = (job % i_groups) * TI * kMT;
+  const int64_t r0 = chunk * chunk_rows, r1 = min<int64_t>(rows, r0 + chunk_rows);
+  const bool a_col = o0 + c < nout;
+  const __amdgpu_buffer_rsrc_t ra = chunk_rsrc(dy + r0 * nout, (r1 - r0) * nout * 4);
+  const __amdgpu_buffer_rsrc_t rb = chunk_rsrc(x + r0 * nin, (r1 - r0) * nin * 4);
+  // byte offset of the lane's element in chunk row h
+  const uint32_t la = a_col ? (uint32_t)(h * nout + o0 + c) * 4u : kOffLane;
+  uint32_t lb[TI];
+#pragma unroll
+  for (int t = 0; t < TI; ++t) lb[t] = i0 + kMT * t + c < nin ? (uint32_t)(h * nin + i0 + kMT * t + c) * 4u : kOffLane;
+
+  f32x16 acc[TI];
+#pragma unroll
+  for (int t = 0; t < TI; ++t) acc[t] = f32x16{};
+  float accb = 0.0f;
+
+  // two load groups in ping-pong: group g + 16 loads while group g computes
+  float a0[kPairs], b0[kPairs][TI], a1[kPairs], b1[kPairs][TI];
+  auto load = [&](int64_t g, float (&va)[kPairs], float (&vb)[kPairs][TI]) {
+    const uint32_t lr = (uint32_t)(g - r0);
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) {
+      va[p] = load_b32(ra, la + (lr + 2 * p) * (uint32_t)nout * 4u);
+#pragma unroll
+      for (int t = 0; t < TI; ++t) vb[p][t] = load_b32(rb, lb[t] + (lr + 2 * p) * (uint32_t)nin * 4u);
     }
-    __syncthreads();
-    for (int r = 0; r < nr; ++r) {
-      const float4 a0 = sy[r][to / 4], a1 = sy[r][to / 4 + 1];
-      const float4 b0 = sx[r][ti / 4], b1 = sx[r][ti / 4 + 1];
-      const float a[kLB] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      const float b[kLB] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+  };
+  auto compute = [&](const float (&va)[kPairs], const float (&vb)[kPairs][TI]) {
 #pragma unroll
-      for (int u = 0; u < kLB; ++u) {
+    for (int p = 0; p < kPairs; ++p) {
+      accb += va[p];
 #pragma unroll
-        for (int v = 0; v < kLB; ++v) acc[u][v] += a[u] * b[v];
-      }
-      if (bias_lane) {
-#pragma unroll
-        for (int u = 0; u < kLB; ++u) accb[u] += a[u];
-      }
+      for (int t = 0; t < TI; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[p], vb[p][t], acc[t], 0, 0, 0);
     }
-    __syncthreads();
+  };
+  // Past the chunk's last row the loads return zeros, which add nothing.  The
+  // scheduling barriers keep the compiler from sinking a group's loads down
+  // to their first use, which would leave them no time in flight.
+  load(r0, a0, b0);
+  for (int64_t g = r0; g < r1; g += 2 * kGroupRows) {
+    load(g + kGroupRows, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(g + 2 * kGroupRows, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  float* pw = part_w + chunk * (int64_t)nout * nin;
+
+  const int64_t nw = (int64_t)nout * nin;
+  float* pw = part + chunk * (nw + nout);
 #pragma unroll
-  for (int u = 0; u < kLB; ++u) {
-    const int o = o0 + to + u;
-    if (o >= nout) continue;
+  for (int t = 0; t < TI; ++t) {
+    const int col = i0 + kMT * t + c;
+    if (col >= nin) continue;
 #pragma unroll
-    for (int v = 0; v < kLB; ++v) {
-      const int i = i0 + ti + v;
-      if (i < nin) pw[(int64_t)o * nin + i] = acc[u][v];
+    for (int r = 0; r < 16; ++r) {
+      const int m = o0 + 8 * (r / 4) + 4 * h + (r % 4);
+      if (m < nout) pw[(int64_t)m * nin + col] = acc[t][r];
     }
-    if (bias_lane) part_b[chunk * nout + o] = accb[u];
+  }
+  if (job % i_groups == 0) {
+    accb += __shfl_xor(accb, 32);
+    if (h == 0 && a_col) pw[nw + o0 + c] = accb;
   }
 }
 
-// out[e] = sum over chunks c of part[c * n + e], in a fixed order: eight
-// running sums over chunks c = 8q + k (k = 0..7, eight loads in flight),
-// then added k = 0..7.
-__global__ __launch_bounds__(256) void k_chunk_sum(const float* __restrict__ part, float* __restrict__ out,
-                                                   int64_t n, int64_t chunks) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= n) return;
+// out[e] = sum over chunks of part[chunk * n + e] (n = out * in + out: dW
+// then db), in a fixed order: wave q of the workgroup keeps eight running
+// sums over chunks q + 16 (8 s + k), k = 0..7, adds them k = 0..7, and wave 0
+// adds the 16 waves' sums q = 0..15.
+__global__ __launch_bounds__(64 * kReduceWaves) void k_chunk_reduce(const float* __restrict__ part,
+                                                                    float* __restrict__ dw,
+                                                                    float* __restrict__ db, int64_t nw, int nout,
+                                                                    int64_t chunks) {
+  __shared__ float red[kReduceWaves][64];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int64_t n = nw + nout;
+  const int64_t e = (int64_t)blockIdx.x * 64 + lane;
   float s[8] = {};
-  int64_t c = 0;
-  for (; c + 8 <= chunks; c += 8) {
+  if (e < n) {
+    int64_t c = q;
+    for (; c + 7 * kReduceWaves < chunks; c += 8 * kReduceWaves) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s[k] += part[(c + k) * n + e];
+      for (int k = 0; k < 8; ++k) s[k] += part[(c + k * kReduceWaves) * n + e];
+    }
+    for (int k = 0; c < chunks; c += kReduceWaves, ++k) s[k] += part[c * n + e];
   }
-  for (int k = 0; c < chunks; ++c, ++k) s[k] += part[c * n + e];
   float total = 0.0f;
 #pragma unroll
   for (int k = 0; k < 8; ++k) total += s[k];
-  out[e] = total;
+  red[q][lane] = total;
+  __syncthreads();
+  if (q == 0 && e < n) {
+    float t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kReduceWaves; ++k) t += red[k][lane];
+    if (e < nw) dw[e] = t;
+    else if (db) db[e - nw] = t;
+  }
+}
+
+template <int TI>
+void launch_mfma(const LinearPlan& p, const float* x, const float* dy, float* part, int64_t rows, int nin, int nout,
+                 hipStream_t st) {
+  const uint32_t waves = (uint32_t)(p.jobs * p.chunks);
+  hipLaunchKernelGGL(k_linear_mfma<TI>, dim3((waves + 3) / 4), dim3(256), 0, st, x, dy, part, rows, nin, nout,
+                     p.i_groups, p.jobs, p.chunk_rows, waves);
+  SPHOPS_LAUNCHED();
 }
 
 }  // namespace
 
-// Rows per chunk: enough chunks to fill the GPU (about 1024 workgroups per
-// output tile), at least 256 rows (so the partial sums stay small next to the
-// inputs) and at most kMaxChunkRows, a multiple of kLR.
-int64_t linear_grad_chunk_rows(int64_t rows) {
-  int64_t c = (rows + 1023) / 1024;
-  c = (c + kLR - 1) / kLR * kLR;
-  return std::min<int64_t>(kMaxChunkRows, std::max<int64_t>(256, c));
-}
+int64_t linear_grad_chunks(int64_t rows, int nin, int nout) { return linear_plan(rows, nin, nout).chunks; }
 
-int64_t linear_grad_chunks(int64_t rows) {
-  return rows > 0 ? (rows + linear_grad_chunk_rows(rows) - 1) / linear_grad_chunk_rows(rows) : 0;
+bool linear_grad_fits(int64_t rows, int nin, int nout) {
+  const LinearPlan p = linear_plan(rows, nin, nout);
+  return (int64_t)p.jobs * p.chunks <= kMaxLinearWaves;
 }
 
 void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows, int nin, int nout,
                             float* work, hipStream_t st) {
-  const int64_t chunks = linear_grad_chunks(rows);
+  const LinearPlan p = linear_plan(rows, nin, nout);
+  if (p.chunks > 0) {
+    switch (p.ti) {
+      case 1: launch_mfma<1>(p, x, dy, work, rows, nin, nout, st); break;
+      case 2: launch_mfma<2>(p, x, dy, work, rows, nin, nout, st); break;
+      case 3: launch_mfma<3>(p, x, dy, work, rows, nin, nout, st); break;
+      default: launch_mfma<4>(p, x, dy, work, rows, nin, nout, st); break;
+    }
+  }
   const int64_t nw = (int64_t)nout * nin;
-  float* part_w = work;
-  float* part_b = db ? work + chunks * nw : nullptr;
-  if (chunks > 0) {
-    const int tiles_in = (nin + kLT - 1) / kLT, tiles_out = (nout + kLT - 1) / kLT;
-    hipLaunchKernelGGL(k_linear_partial, dim3((uint32_t)(tiles_in * tiles_out), (uint32_t)chunks),
-                       dim3(kLThreads), 0, st, x, dy, part_w, part_b, rows, nin, nout, tiles_in,
-                       linear_grad_chunk_rows(rows));
-    SPHOPS_LAUNCHED();
-  }
-  hipLaunchKernelGGL(k_chunk_sum, dim3((uint32_t)((nw + 255) / 256)), dim3(256), 0, st, part_w, dw, nw, chunks);
+  hipLaunchKernelGGL(k_chunk_reduce, dim3((uint32_t)((nw + nout + 63) / 64)), dim3(64 * kReduceWaves), 0, st, work,
+                     dw, db, nw, nout, p.chunks);
   SPHOPS_LAUNCHED();
-  if (db) {
-    hipLaunchKernelGGL(k_chunk_sum, dim3((uint32_t)((nout + 255) / 256)), dim3(256), 0, st, part_b, db,
-                       (int64_t)nout, chunks);
-    SPHOPS_LAUNCHED();
-  }
 }
 
 }  // namespace sphops

@@ -196,9 +196,11 @@ void run_splat_backward(const SplatParams& sp, const float* x, const float* colo
 
 // linear_grad.hip: weight / bias gradients of a linear layer over many rows
 constexpr int64_t kMaxChunkRows = 8192;
-constexpr int64_t kMaxLinearRows = kMaxChunkRows * 65535;  // chunks index the grid's y dimension
-int64_t linear_grad_chunk_rows(int64_t rows);
-int64_t linear_grad_chunks(int64_t rows);
+constexpr int64_t kMaxLinearRows = kMaxChunkRows * 65535;
+constexpr int kMaxLinearFeatures = 32768;  // keeps chunk byte offsets below 2^31
+constexpr int64_t kMaxLinearWaves = int64_t(1) << 25;  // one wave per (row chunk, output job); 2^31 threads
+int64_t linear_grad_chunks(int64_t rows, int nin, int nout);
+bool linear_grad_fits(int64_t rows, int nin, int nout);
 void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows, int nin, int nout,
                             float* work, hipStream_t st);
 
