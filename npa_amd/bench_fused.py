@@ -305,3 +305,18 @@ def run_all():
     for r in results:
         print(json.dumps(r), flush=True)
     return results
+
+
+if __name__ == "__main__":
+    # python -m npa_amd.bench_fused [perceive|step|mlp|splat|rollout ...]: the
+    # named measurements only (all of them with no argument)
+    import sys
+    names = sys.argv[1:]
+    if not names:
+        run_all()
+    else:
+        torch.cuda.set_device(0)
+        table = {"perceive": bench_perceive, "step": bench_step, "mlp": bench_mlp, "splat": bench_splat,
+                 "rollout": bench_rollout}
+        for n in names:
+            print(json.dumps(table[n]()), flush=True)

@@ -6,7 +6,7 @@ Over one row per particle the weight gradient dW = dY^T X is a GEMM with a
 tiny output and a reduction over 10^5-10^6 rows; the library GEMM takes that
 shape with few output tiles and runs at a few TFLOP/s.  ``LinearRows`` keeps
 torch's forward and input gradient (both large, well-shaped GEMMs) and
-replaces the weight and bias gradients by the row-chunked kernel.
+replaces the weight and bias gradients by the row-chunked matrix-core kernel.
 ``mlp(module, z)`` runs a module the way the module would run itself, with its
 ``torch.nn.Linear`` layers through ``LinearRows``; the parameters are the
 module's own, so optimisers and checkpoints see no difference.

@@ -1,15 +1,17 @@
 """The row-chunked weight and bias gradients of a linear layer
 (``sphops_linear_weight_grad`` via npa_amd.mlp) against float64 sums, over
-row counts from 0 to 3e5 and layer shapes with one and several 128 x 128
-output tiles; and npa_amd.mlp.mlp against the module's own autograd."""
+row counts from 0 to 3e5 (inside one 16-row load group, across chunk ends)
+and layer shapes that take one to four 32-column tiles per wave, several
+32-row bands, exact tile multiples and ragged edges; the feature limit; and
+npa_amd.mlp.mlp against the module's own autograd."""
 import numpy as np
 import pytest
 import torch
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(83, 128), (128, 19), (5, 3), (200, 130)]
-ROWS = [0, 1, 100, 1000, 33333, 300000]
+SHAPES = [(83, 128), (128, 19), (5, 3), (200, 130), (32, 64), (300, 7), (66, 128)]
+ROWS = [0, 1, 17, 100, 1000, 33333, 131073, 300000]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -67,3 +69,14 @@ def test_mlp_matches_module_autograd(hidden):
     ref = torch.autograd.grad(net(z), [z] + list(net.parameters()), up)
     for a, b in zip(got, ref):
         assert torch.allclose(a, b, rtol=1e-4, atol=1e-4 * float(b.abs().max())), "gradient differs"
+
+
+def test_feature_limit_is_an_error():
+    import ctypes
+    from npa_amd.sphops import _native
+    x = torch.zeros(4, 1, device="cuda")
+    p = ctypes.c_void_p(x.data_ptr())
+    st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(0))
+    for in_f, out_f in ((32769, 1), (1, 32769)):
+        with pytest.raises(RuntimeError, match="in_features and out_features"):
+            _native.check(_native.lib.sphops_linear_weight_grad(p, p, p, p, 1, in_f, out_f, p, st))
