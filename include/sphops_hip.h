@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 10
+#define SPHOPS_ABI_VERSION 11
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -343,6 +343,17 @@ int sphops_splat_backward(const float* x, const float* color, const int32_t* sta
 int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows,
                               int in_features, int out_features, void* workspace, void* stream);
 int64_t sphops_linear_weight_grad_workspace_bytes(int64_t rows, int in_features, int out_features);
+
+/* Input gradient through a ReLU and a linear layer, y = relu(a) W^T + b
+ * (torch.nn.ReLU then torch.nn.Linear, models/npa.py:65-68; no counterpart in
+ * the reference's native module): dx = 0 where h <= 0, else dy W, with
+ * h = relu(a) (rows, in_features), dy (rows, out_features), w (out_features,
+ * in_features) and dx (rows, in_features) row-major fp32.  The zeroing follows
+ * torch's threshold_backward(grad, h, 0).  in_features is at most 32768 and
+ * out_features at most 64.  dy W runs on the fp32 matrix cores;
+ * deterministic. */
+int sphops_relu_linear_input_grad(const float* dy, const float* w, const float* h, float* dx, int64_t rows,
+                                  int in_features, int out_features, void* stream);
 
 #ifdef __cplusplus
 }

@@ -798,4 +798,18 @@ int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float*
   });
 }
 
+int sphops_relu_linear_input_grad(const float* dy, const float* w, const float* h, float* dx, int64_t rows,
+                                  int in_features, int out_features, void* stream) {
+  return guarded([&] {
+    require(rows >= 0, "rows must be >= 0");
+    require(in_features >= 1 && in_features <= sphops::kMaxLinearFeatures && out_features >= 1 &&
+                out_features <= sphops::kMaxReluLinearOut,
+            "in_features must be in [1, " + std::to_string(sphops::kMaxLinearFeatures) + "] and out_features in [1, " +
+                std::to_string(sphops::kMaxReluLinearOut) + "]");
+    require(sphops::relu_linear_input_grad_fits(rows, in_features), "too many rows x in_features");
+    require(rows == 0 || (dy && w && h && dx), "null buffer");
+    sphops::run_relu_linear_input_grad(dy, w, h, dx, rows, in_features, out_features, sphops::as_stream(stream));
+  });
+}
+
 }  // extern "C"

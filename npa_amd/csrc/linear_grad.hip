@@ -201,6 +201,98 @@ void launch_mfma(const LinearPlan& p, const float* x, const float* dy, float* pa
   SPHOPS_LAUNCHED();
 }
 
+// Input gradient through a ReLU and a linear layer, y = relu(a) W^T + b:
+// dA[r][n] = 0 where h[r][n] = relu(a)[r][n] <= 0 (torch's threshold_backward),
+// else (dY W)[r][n].  It replaces the dH = dY W product and the elementwise
+// ReLU backward, so dH never goes to memory: per row it reads dY and h and
+// writes dA.  dY W runs on the matrix cores (K = nout padded to 2 KS): one
+// wave per (kRLTiles tiles of 32 rows, 128 columns) keeps W's four 32-column
+// tiles as B operands in registers; for row tile i, lane l supplies A[m = l %
+// 32][k = l / 32] = dY[32 i + m][2 s + k] at step s, and result register j of
+// column tile t holds row 8 (j / 4) + 4 (l / 32) + j % 4, column 32 t + l % 32,
+// where h is read and dA written.  Buffer resources over the wave's rows
+// return zeros past the rows, past nout and past nin, and drop the stores
+// there.
+constexpr int kRLTiles = 4;
+
+template <int KS>
+__global__ __launch_bounds__(256) void k_relu_linear_dx(const float* __restrict__ dy, const float* __restrict__ w,
+                                                        const float* __restrict__ h, float* __restrict__ dx,
+                                                        int64_t rows, int nin, int nout, int col_blocks,
+                                                        uint32_t total_waves) {
+  const uint32_t wid = __builtin_amdgcn_readfirstlane(xcd_block_id() * 4u + threadIdx.x / 64u);
+  if (wid >= total_waves) return;
+  const int lane = threadIdx.x & 63, c = lane & 31, hh = lane >> 5;
+  const int n0 = (int)(wid % (uint32_t)col_blocks) * 128;
+  const int64_t r0 = (int64_t)(wid / (uint32_t)col_blocks) * (kRLTiles * kMT);
+  const int64_t nr = min<int64_t>(kRLTiles * kMT, rows - r0);
+  const __amdgpu_buffer_rsrc_t rdy = chunk_rsrc(dy + r0 * nout, nr * nout * 4);
+  const __amdgpu_buffer_rsrc_t rh = chunk_rsrc(h + r0 * nin, nr * nin * 4);
+  const __amdgpu_buffer_rsrc_t rdx = chunk_rsrc(dx + r0 * nin, nr * nin * 4);
+
+  float bw[4][KS];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int n = n0 + kMT * t + c;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int k = 2 * s + hh;
+      bw[t][s] = (k < nout && n < nin) ? w[(int64_t)k * nin + n] : 0.0f;
+    }
+  }
+  // byte offsets: the lane's dY entries (row c of the tile, k = 2 s + hh) and
+  // its h / dA column in each column tile
+  uint32_t ka[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) ka[s] = 2 * s + hh < nout ? (uint32_t)(c * nout + 2 * s + hh) * 4u : kOffLane;
+  uint32_t cn[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) cn[t] = n0 + kMT * t + c < nin ? (uint32_t)(n0 + kMT * t + c) * 4u : kOffLane;
+
+  for (int i = 0; i < kRLTiles; ++i) {
+    if (i * kMT >= nr) break;  // uniform
+    const uint32_t ra = (uint32_t)(i * kMT * nout) * 4u;
+    float a[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) a[s] = load_b32(rdy, ka[s] + ra);
+    float hv[4][16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t rr = (uint32_t)(i * kMT + 8 * (j / 4) + 4 * hh + (j % 4)) * (uint32_t)nin * 4u;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) hv[t][j] = load_b32(rh, cn[t] + rr);
+    }
+    f32x16 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], bw[t][s], acc[t], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t rr = (uint32_t)(i * kMT + 8 * (j / 4) + 4 * hh + (j % 4)) * (uint32_t)nin * 4u;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float v = hv[t][j] <= 0.0f ? 0.0f : acc[t][j];
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rdx, cn[t] + rr, 0, 0);
+      }
+    }
+  }
+}
+
+template <int KS>
+void launch_relu_dx(const float* dy, const float* w, const float* h, float* dx, int64_t rows, int nin, int nout,
+                    hipStream_t st) {
+  const int col_blocks = (nin + 127) / 128;
+  const int64_t rows_per_wave = kRLTiles * kMT;
+  const uint32_t waves = (uint32_t)(((rows + rows_per_wave - 1) / rows_per_wave) * col_blocks);
+  hipLaunchKernelGGL(k_relu_linear_dx<KS>, dim3((waves + 3) / 4), dim3(256), 0, st, dy, w, h, dx, rows, nin, nout,
+                     col_blocks, waves);
+  SPHOPS_LAUNCHED();
+}
+
 }  // namespace
 
 int64_t linear_grad_chunks(int64_t rows, int nin, int nout) { return linear_plan(rows, nin, nout).chunks; }
@@ -225,6 +317,31 @@ void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* d
   hipLaunchKernelGGL(k_chunk_reduce, dim3((uint32_t)((nw + nout + 63) / 64)), dim3(64 * kReduceWaves), 0, st, work,
                      dw, db, nw, nout, p.chunks);
   SPHOPS_LAUNCHED();
+}
+
+}  // namespace sphops
+
+namespace sphops {
+
+bool relu_linear_input_grad_fits(int64_t rows, int nin) {
+  const int64_t rows_per_wave = kRLTiles * kMT;
+  return ((rows + rows_per_wave - 1) / rows_per_wave) * ((nin + 127) / 128) <= kMaxLinearWaves;
+}
+
+// K = nout padded to a multiple of 2 (the instruction's two rows) from a short
+// list, so the padding wastes at most a quarter of the matrix work
+void run_relu_linear_input_grad(const float* dy, const float* w, const float* h, float* dx, int64_t rows, int nin,
+                                int nout, hipStream_t st) {
+  if (rows == 0) return;
+  if (nout <= 4) launch_relu_dx<2>(dy, w, h, dx, rows, nin, nout, st);
+  else if (nout <= 8) launch_relu_dx<4>(dy, w, h, dx, rows, nin, nout, st);
+  else if (nout <= 12) launch_relu_dx<6>(dy, w, h, dx, rows, nin, nout, st);
+  else if (nout <= 16) launch_relu_dx<8>(dy, w, h, dx, rows, nin, nout, st);
+  else if (nout <= 20) launch_relu_dx<10>(dy, w, h, dx, rows, nin, nout, st);
+  else if (nout <= 24) launch_relu_dx<12>(dy, w, h, dx, rows, nin, nout, st);
+  else if (nout <= 32) launch_relu_dx<16>(dy, w, h, dx, rows, nin, nout, st);
+  else if (nout <= 48) launch_relu_dx<24>(dy, w, h, dx, rows, nin, nout, st);
+  else launch_relu_dx<kMaxReluLinearOut / 2>(dy, w, h, dx, rows, nin, nout, st);
 }
 
 }  // namespace sphops

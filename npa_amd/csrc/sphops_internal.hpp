@@ -203,6 +203,10 @@ int64_t linear_grad_chunks(int64_t rows, int nin, int nout);
 bool linear_grad_fits(int64_t rows, int nin, int nout);
 void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows, int nin, int nout,
                             float* work, hipStream_t st);
+constexpr int kMaxReluLinearOut = 64;  // dY values per row kept against W columns in registers
+bool relu_linear_input_grad_fits(int64_t rows, int nin);
+void run_relu_linear_input_grad(const float* dy, const float* w, const float* h, float* dx, int64_t rows, int nin,
+                                int nout, hipStream_t st);
 
 constexpr uint32_t kMaxChannels = 64;
 constexpr int kRadixBins = 1024;  // digit values per radix-sort pass (10 bits)

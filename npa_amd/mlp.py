@@ -7,9 +7,11 @@ tiny output and a reduction over 10^5-10^6 rows; the library GEMM takes that
 shape with few output tiles and runs at a few TFLOP/s.  ``LinearRows`` keeps
 torch's forward and input gradient (both large, well-shaped GEMMs) and
 replaces the weight and bias gradients by the row-chunked matrix-core kernel.
-``mlp(module, z)`` runs a module the way the module would run itself, with its
-``torch.nn.Linear`` layers through ``LinearRows``; the parameters are the
-module's own, so optimisers and checkpoints see no difference.
+A ReLU followed by a Linear with at most 64 outputs (NPA's last layer) runs
+as ``ReluLinear``, whose backward computes the input gradient through both in
+one kernel.  ``mlp(module, z)`` runs a module the way the module would run
+itself, with its ``torch.nn.Linear`` layers through these; the parameters are
+the module's own, so optimisers and checkpoints see no difference.
 """
 import ctypes
 
@@ -45,33 +47,96 @@ class LinearRows(torch.autograd.Function):
         if need_x:
             dx = (dy2 @ weight).reshape(x.shape)
         if need_w or (need_b and ctx.has_bias):
-            x2 = x.reshape(-1, in_f)
-            if x2.dtype != torch.float32 or dy2.dtype != torch.float32 or not x2.is_cuda:
-                raise TypeError("LinearRows takes float32 GPU tensors")
-            x2, dy2 = x2.contiguous(), dy2.contiguous()
-            rows = x2.shape[0]
-            dw = torch.empty(out_f, in_f, device=x.device)
-            db = torch.empty(out_f, device=x.device) if ctx.has_bias else None
-            nbytes = _lib.sphops_linear_weight_grad_workspace_bytes(rows, in_f, out_f)
-            work = torch.empty(max(nbytes // 4, 1), device=x.device)
-            st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(x.device.index))
-            _native.check(_lib.sphops_linear_weight_grad(_ptr(x2), _ptr(dy2), _ptr(dw), _ptr(db), rows, in_f, out_f,
-                                                         _ptr(work), st))
+            dw, db = _weight_grad(x.reshape(-1, in_f), dy2, ctx.has_bias)
         return dx, (dw if need_w else None), (db if need_b else None)
+
+
+def _weight_grad(x2, dy2, has_bias):
+    """dW = dy2^T x2 and db = column sums of dy2 (None without a bias) through
+    ``sphops_linear_weight_grad``."""
+    if x2.dtype != torch.float32 or dy2.dtype != torch.float32 or not x2.is_cuda:
+        raise TypeError("the MLP kernels take float32 GPU tensors")
+    x2, dy2 = x2.contiguous(), dy2.contiguous()
+    rows, in_f = x2.shape
+    out_f = dy2.shape[1]
+    dw = torch.empty(out_f, in_f, device=x2.device)
+    db = torch.empty(out_f, device=x2.device) if has_bias else None
+    nbytes = _lib.sphops_linear_weight_grad_workspace_bytes(rows, in_f, out_f)
+    work = torch.empty(max(nbytes // 4, 1), device=x2.device)
+    st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(x2.device.index))
+    _native.check(_lib.sphops_linear_weight_grad(_ptr(x2), _ptr(dy2), _ptr(dw), _ptr(db), rows, in_f, out_f,
+                                                 _ptr(work), st))
+    return dw, db
+
+
+class ReluLinear(torch.autograd.Function):
+    """y = relu(a) W^T + b (``torch.nn.ReLU`` then ``torch.nn.Linear``).  The
+    forward is torch's; the backward takes dW and db from the row-chunked
+    kernel and da = (relu(a) > 0) * (dy W) from
+    ``sphops_relu_linear_input_grad``, one pass that never writes dy W."""
+
+    @staticmethod
+    def forward(ctx, a, weight, bias):
+        h = torch.relu(a)
+        ctx.save_for_backward(h, weight)
+        ctx.has_bias = bias is not None
+        return F.linear(h, weight, bias)
+
+    @staticmethod
+    def backward(ctx, dy):
+        h, weight = ctx.saved_tensors
+        need_a, need_w, need_b = ctx.needs_input_grad
+        out_f, in_f = weight.shape
+        h2 = h.reshape(-1, in_f)
+        dy2 = dy.reshape(-1, out_f).contiguous()
+        da = dw = db = None
+        if need_a:
+            if h2.dtype != torch.float32 or dy2.dtype != torch.float32 or not h2.is_cuda:
+                raise TypeError("the MLP kernels take float32 GPU tensors")
+            h2 = h2.contiguous()
+            w = weight.detach().contiguous()
+            da2 = torch.empty_like(h2)
+            st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(h2.device.index))
+            _native.check(_lib.sphops_relu_linear_input_grad(_ptr(dy2), _ptr(w), _ptr(h2), _ptr(da2), h2.shape[0],
+                                                             in_f, out_f, st))
+            da = da2.reshape(h.shape)
+        if need_w or (need_b and ctx.has_bias):
+            dw, db = _weight_grad(h2, dy2, ctx.has_bias)
+        return da, (dw if need_w else None), (db if need_b else None)
+
+
+# ReluLinear keeps a row's dy in one wave's lanes against W in registers
+RELU_LINEAR_MAX_OUT = 64
 
 
 def linear(x, layer):
     return LinearRows.apply(x, layer.weight, layer.bias)
 
 
+def relu_linear(a, layer):
+    """``layer(torch.relu(a))`` with the fused backward."""
+    return ReluLinear.apply(a, layer.weight, layer.bias)
+
+
 def mlp(module, z):
     """``module(z)`` for a ``torch.nn.Linear`` or a ``torch.nn.Sequential`` of
-    layers (the shapes NPA's _get_mlp builds), with every Linear through
-    ``LinearRows``; any other module runs as it is."""
+    layers (the shapes NPA's _get_mlp builds): a ReLU followed by a Linear of at
+    most RELU_LINEAR_MAX_OUT outputs through ``ReluLinear``, every other Linear
+    through ``LinearRows``; any other module runs as it is."""
     if isinstance(module, torch.nn.Linear):
         return linear(z, module)
     if isinstance(module, torch.nn.Sequential):
-        for layer in module:
+        layers = list(module)
+        i = 0
+        while i < len(layers):
+            layer = layers[i]
+            nxt = layers[i + 1] if i + 1 < len(layers) else None
+            if (type(layer) is torch.nn.ReLU and isinstance(nxt, torch.nn.Linear)
+                    and nxt.out_features <= RELU_LINEAR_MAX_OUT):
+                z = relu_linear(z, nxt)
+                i += 2
+                continue
             z = linear(z, layer) if isinstance(layer, torch.nn.Linear) else layer(z)
+            i += 1
         return z
     return module(z)

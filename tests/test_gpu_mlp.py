@@ -65,6 +65,8 @@ def test_mlp_matches_module_autograd(hidden):
     up = torch.randn(3, 5000, 18, device="cuda")
     out = M.mlp(net, z)
     assert torch.equal(out, net(z))  # the forward is torch's own
+    if hidden is not None:
+        assert type(out.grad_fn).__name__ == "ReluLinearBackward"  # the fused ReLU + Linear ran
     got = torch.autograd.grad(out, [z] + list(net.parameters()), up)
     ref = torch.autograd.grad(net(z), [z] + list(net.parameters()), up)
     for a, b in zip(got, ref):
@@ -80,3 +82,40 @@ def test_feature_limit_is_an_error():
     for in_f, out_f in ((32769, 1), (1, 32769)):
         with pytest.raises(RuntimeError, match="in_features and out_features"):
             _native.check(_native.lib.sphops_linear_weight_grad(p, p, p, p, 1, in_f, out_f, p, st))
+
+
+RELU_SHAPES = [(128, 19), (128, 18), (5, 3), (200, 64), (64, 1), (130, 33)]
+
+
+@pytest.mark.parametrize("shape", RELU_SHAPES)
+@pytest.mark.parametrize("rows", [0, 1, 9, 1000, 100003])
+def test_relu_linear_input_grad_matches_float64(shape, rows):
+    """da = 0 where h = relu(a) <= 0, else dy W (torch's threshold_backward of
+    the Linear's input gradient), against float64."""
+    import ctypes
+    from npa_amd.sphops import _native
+    in_f, out_f = shape
+    g = torch.Generator(device="cuda").manual_seed(7 * rows + in_f + out_f)
+    h = torch.relu(torch.randn(rows, in_f, device="cuda", generator=g))
+    dy = torch.randn(rows, out_f, device="cuda", generator=g)
+    w = torch.randn(out_f, in_f, device="cuda", generator=g)
+    da = torch.full((rows, in_f), float("nan"), device="cuda")
+    st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(0))
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    _native.check(_native.lib.sphops_relu_linear_input_grad(P(dy), P(w), P(h), P(da), rows, in_f, out_f, st))
+    hd, yd, wd = h.double().cpu(), dy.double().cpu(), w.double().cpu()
+    ref = torch.where(hd <= 0, torch.zeros((), dtype=torch.float64), yd @ wd)
+    bound = (yd.abs() @ wd.abs()) * 1e-5 + 1e-30
+    got = da.cpu().double()
+    assert torch.all(got[hd <= 0] == 0), "masked entries must be exactly zero"
+    assert torch.all((got - ref).abs() <= bound), f"da rows={rows} shape={shape}"
+
+
+def test_relu_linear_output_limit_is_an_error():
+    import ctypes
+    from npa_amd.sphops import _native
+    x = torch.zeros(4, 1, device="cuda")
+    p = ctypes.c_void_p(x.data_ptr())
+    st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(0))
+    with pytest.raises(RuntimeError, match="out_features"):
+        _native.check(_native.lib.sphops_relu_linear_input_grad(p, p, p, p, 1, 4, 65, p, st))
