@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 11
+#define SPHOPS_ABI_VERSION 12
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -354,6 +354,24 @@ int64_t sphops_linear_weight_grad_workspace_bytes(int64_t rows, int in_features,
  * deterministic. */
 int sphops_relu_linear_input_grad(const float* dy, const float* w, const float* h, float* dx, int64_t rows,
                                   int in_features, int out_features, void* stream);
+
+/* Forward through a ReLU and a linear layer (torch.nn.ReLU then
+ * torch.nn.Linear, models/npa.py:65-68; no counterpart in the reference's
+ * native module): y = relu(a) W^T + b, with a (rows, in_features), w
+ * (out_features, in_features), b (out_features, or NULL) and y (rows,
+ * out_features) row-major fp32; relu as torch's (NaN stays NaN).  in_features
+ * is a multiple of 4 up to 256, out_features at most 64, and a is 16-byte
+ * aligned.  relu(a) is not written; the backward takes a itself:
+ * sphops_relu_linear_input_grad(dy, w, a, ...) (a <= 0 exactly where
+ * relu(a) <= 0) and sphops_relu_linear_weight_grad.  On the fp32 matrix
+ * cores; deterministic. */
+int sphops_relu_linear_forward(const float* a, const float* w, const float* b, float* y, int64_t rows,
+                               int in_features, int out_features, void* stream);
+
+/* sphops_linear_weight_grad with x = relu(a): dw = dy^T relu(a), db = the
+ * column sums of dy; the same workspace size. */
+int sphops_relu_linear_weight_grad(const float* a, const float* dy, float* dw, float* db, int64_t rows,
+                                   int in_features, int out_features, void* workspace, void* stream);
 
 #ifdef __cplusplus
 }

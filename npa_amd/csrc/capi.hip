@@ -782,8 +782,12 @@ int64_t sphops_linear_weight_grad_workspace_bytes(int64_t rows, int in_features,
   return 4 * sphops::linear_grad_chunks(rows, in_features, out_features) * ((int64_t)in_features * out_features + out_features);
 }
 
-int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows,
-                              int in_features, int out_features, void* workspace, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows, int in_features,
+                       int out_features, void* workspace, bool relu_x, void* stream) {
   return guarded([&] {
     require(rows >= 0 && rows <= sphops::kMaxLinearRows, "rows must be in [0, " +
                                                              std::to_string(sphops::kMaxLinearRows) + "]");
@@ -794,7 +798,36 @@ int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float*
             "layer too large: more than 2^25 (row chunk, 32-row output band) pairs");
     require(dw != nullptr && (rows == 0 || (x && dy && workspace)), "null buffer");
     sphops::run_linear_weight_grad(x, dy, dw, db, rows, in_features, out_features,
-                                   static_cast<float*>(workspace), sphops::as_stream(stream));
+                                   static_cast<float*>(workspace), relu_x, sphops::as_stream(stream));
+  });
+}
+
+}  // namespace
+
+extern "C" {
+
+int sphops_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows,
+                              int in_features, int out_features, void* workspace, void* stream) {
+  return linear_weight_grad(x, dy, dw, db, rows, in_features, out_features, workspace, false, stream);
+}
+
+int sphops_relu_linear_weight_grad(const float* a, const float* dy, float* dw, float* db, int64_t rows,
+                                   int in_features, int out_features, void* workspace, void* stream) {
+  return linear_weight_grad(a, dy, dw, db, rows, in_features, out_features, workspace, true, stream);
+}
+
+int sphops_relu_linear_forward(const float* a, const float* w, const float* b, float* y, int64_t rows,
+                               int in_features, int out_features, void* stream) {
+  return guarded([&] {
+    require(rows >= 0, "rows must be >= 0");
+    require(in_features >= 4 && in_features <= sphops::kMaxReluLinearIn && in_features % 4 == 0,
+            "in_features must be a multiple of 4 in [4, " + std::to_string(sphops::kMaxReluLinearIn) + "]");
+    require(out_features >= 1 && out_features <= sphops::kMaxReluLinearOut,
+            "out_features must be in [1, " + std::to_string(sphops::kMaxReluLinearOut) + "]");
+    require(sphops::relu_linear_forward_fits(rows), "too many rows");
+    require(rows == 0 || (a && w && y), "null buffer");
+    require(reinterpret_cast<uintptr_t>(a) % 16 == 0, "a must be 16-byte aligned");
+    sphops::run_relu_linear_forward(a, w, b, y, rows, in_features, out_features, sphops::as_stream(stream));
   });
 }
 

@@ -28,6 +28,7 @@ namespace sphops {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMT = 32;             // matrix-core tile side
 constexpr int kPairs = 8;           // row pairs per load group (16 rows)
@@ -79,7 +80,7 @@ __device__ __forceinline__ float load_b32(__amdgpu_buffer_rsrc_t r, uint32_t off
 // instruction, lane l supplies A[m = l % 32][k = l / 32] = dY[row_k][o0 + m]
 // and B[k = l / 32][n = l % 32] = X[row_k][i0 + 32 t + n]; result register r
 // of lane l holds tile row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-template <int TI>
+template <int TI, bool RELU_X>
 __global__ __launch_bounds__(256) void k_linear_mfma(const float* __restrict__ x, const float* __restrict__ dy,
                                                      float* __restrict__ part, int64_t rows, int nin, int nout,
                                                      int i_groups, int jobs, int64_t chunk_rows,
@@ -121,7 +122,11 @@ __global__ __launch_bounds__(256) void k_linear_mfma(const float* __restrict__ x
     for (int p = 0; p < kPairs; ++p) {
       accb += va[p];
 #pragma unroll
-      for (int t = 0; t < TI; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[p], vb[p][t], acc[t], 0, 0, 0);
+      for (int t = 0; t < TI; ++t) {
+        // relu(x) as torch computes it: NaN stays NaN
+        const float bx = RELU_X ? (vb[p][t] <= 0.0f ? 0.0f : vb[p][t]) : vb[p][t];
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[p], bx, acc[t], 0, 0, 0);
+      }
     }
   };
   // Past the chunk's last row the loads return zeros, which add nothing.  The
@@ -194,10 +199,14 @@ __global__ __launch_bounds__(64 * kReduceWaves) void k_chunk_reduce(const float*
 
 template <int TI>
 void launch_mfma(const LinearPlan& p, const float* x, const float* dy, float* part, int64_t rows, int nin, int nout,
-                 hipStream_t st) {
+                 bool relu_x, hipStream_t st) {
   const uint32_t waves = (uint32_t)(p.jobs * p.chunks);
-  hipLaunchKernelGGL(k_linear_mfma<TI>, dim3((waves + 3) / 4), dim3(256), 0, st, x, dy, part, rows, nin, nout,
-                     p.i_groups, p.jobs, p.chunk_rows, waves);
+  if (relu_x)
+    hipLaunchKernelGGL((k_linear_mfma<TI, true>), dim3((waves + 3) / 4), dim3(256), 0, st, x, dy, part, rows, nin,
+                       nout, p.i_groups, p.jobs, p.chunk_rows, waves);
+  else
+    hipLaunchKernelGGL((k_linear_mfma<TI, false>), dim3((waves + 3) / 4), dim3(256), 0, st, x, dy, part, rows, nin,
+                       nout, p.i_groups, p.jobs, p.chunk_rows, waves);
   SPHOPS_LAUNCHED();
 }
 
@@ -293,6 +302,91 @@ void launch_relu_dx(const float* dy, const float* w, const float* h, float* dx, 
   SPHOPS_LAUNCHED();
 }
 
+// Forward through a ReLU and a linear layer, y = relu(a) W^T + b, for at most
+// 64 outputs and in_features a multiple of 4 up to 256, on the matrix cores:
+// one wave per kRLTiles tiles of 32 rows keeps W's 32-output tiles as B
+// operands in registers.  Lane l (row m = l % 32 of the tile, half q = l / 32)
+// loads a[m][8 g + 4 q .. + 3] as one 16-byte load per g; at step (g, j) it
+// supplies A[m][q] = relu(a[m][8 g + 4 q + j]) and B[q][n] = W[n][8 g + 4 q +
+// j], so the steps cover every k once.  relu(a) never goes to memory.
+template <int G, int NT>
+__global__ __launch_bounds__(256) void k_relu_linear_fwd(const float* __restrict__ a, const float* __restrict__ w,
+                                                         const float* __restrict__ b, float* __restrict__ y,
+                                                         int64_t rows, int nin, int nout, uint32_t total_waves) {
+  const uint32_t wid = __builtin_amdgcn_readfirstlane(xcd_block_id() * 4u + threadIdx.x / 64u);
+  if (wid >= total_waves) return;
+  const int lane = threadIdx.x & 63, c = lane & 31, hq = lane >> 5;
+  const int64_t r0 = (int64_t)wid * (kRLTiles * kMT);
+  const int64_t nr = min<int64_t>(kRLTiles * kMT, rows - r0);
+  const __amdgpu_buffer_rsrc_t ra = chunk_rsrc(a + r0 * nin, nr * nin * 4);
+  const __amdgpu_buffer_rsrc_t ry = chunk_rsrc(y + r0 * nout, nr * nout * 4);
+  float wr[NT][G][4];
+  float bias[NT];
+  uint32_t yc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = kMT * t + c;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = 8 * g + 4 * hq + j;
+        wr[t][g][j] = (n < nout && k < nin) ? w[(int64_t)n * nin + k] : 0.0f;
+      }
+    }
+    bias[t] = (b != nullptr && n < nout) ? b[n] : 0.0f;
+    yc[t] = n < nout ? (uint32_t)n * 4u : kOffLane;
+  }
+  // the lane's 16-byte column block of each row; blocks past nin read zeros
+  uint32_t ka[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) ka[g] = 8 * g + 4 * hq < nin ? (uint32_t)(8 * g + 4 * hq) * 4u : kOffLane;
+
+  for (int i = 0; i < kRLTiles; ++i) {
+    if (i * kMT >= nr) break;  // uniform
+    const uint32_t ro = (uint32_t)((i * kMT + c) * nin) * 4u;
+    f32x4 av[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      av[g] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, ka[g] + ro, 0, 0));
+    f32x16 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f32x16{};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v = av[g][j] <= 0.0f ? 0.0f : av[g][j];  // torch's relu: NaN stays NaN
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, wr[t][g][j], acc[t], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t rr = (uint32_t)((i * kMT + 8 * (j / 4) + 4 * hq + (j % 4)) * nout) * 4u;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[t][j] + bias[t]), ry, yc[t] + rr, 0,
+                                              0);
+      }
+    }
+  }
+}
+
+template <int G>
+void launch_relu_fwd(const float* a, const float* w, const float* b, float* y, int64_t rows, int nin, int nout,
+                     hipStream_t st) {
+  const int64_t rows_per_wave = kRLTiles * kMT;
+  const uint32_t waves = (uint32_t)((rows + rows_per_wave - 1) / rows_per_wave);
+  if (nout <= kMT)
+    hipLaunchKernelGGL((k_relu_linear_fwd<G, 1>), dim3((waves + 3) / 4), dim3(256), 0, st, a, w, b, y, rows, nin,
+                       nout, waves);
+  else
+    hipLaunchKernelGGL((k_relu_linear_fwd<G, 2>), dim3((waves + 3) / 4), dim3(256), 0, st, a, w, b, y, rows, nin,
+                       nout, waves);
+  SPHOPS_LAUNCHED();
+}
+
 }  // namespace
 
 int64_t linear_grad_chunks(int64_t rows, int nin, int nout) { return linear_plan(rows, nin, nout).chunks; }
@@ -303,14 +397,14 @@ bool linear_grad_fits(int64_t rows, int nin, int nout) {
 }
 
 void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows, int nin, int nout,
-                            float* work, hipStream_t st) {
+                            float* work, bool relu_x, hipStream_t st) {
   const LinearPlan p = linear_plan(rows, nin, nout);
   if (p.chunks > 0) {
     switch (p.ti) {
-      case 1: launch_mfma<1>(p, x, dy, work, rows, nin, nout, st); break;
-      case 2: launch_mfma<2>(p, x, dy, work, rows, nin, nout, st); break;
-      case 3: launch_mfma<3>(p, x, dy, work, rows, nin, nout, st); break;
-      default: launch_mfma<4>(p, x, dy, work, rows, nin, nout, st); break;
+      case 1: launch_mfma<1>(p, x, dy, work, rows, nin, nout, relu_x, st); break;
+      case 2: launch_mfma<2>(p, x, dy, work, rows, nin, nout, relu_x, st); break;
+      case 3: launch_mfma<3>(p, x, dy, work, rows, nin, nout, relu_x, st); break;
+      default: launch_mfma<4>(p, x, dy, work, rows, nin, nout, relu_x, st); break;
     }
   }
   const int64_t nw = (int64_t)nout * nin;
@@ -342,6 +436,27 @@ void run_relu_linear_input_grad(const float* dy, const float* w, const float* h,
   else if (nout <= 32) launch_relu_dx<16>(dy, w, h, dx, rows, nin, nout, st);
   else if (nout <= 48) launch_relu_dx<24>(dy, w, h, dx, rows, nin, nout, st);
   else launch_relu_dx<kMaxReluLinearOut / 2>(dy, w, h, dx, rows, nin, nout, st);
+}
+
+}  // namespace sphops
+
+namespace sphops {
+
+bool relu_linear_forward_fits(int64_t rows) {
+  return (rows + kRLTiles * kMT - 1) / (kRLTiles * kMT) <= kMaxLinearWaves;
+}
+
+// in_features padded to a multiple of 8 (16-byte blocks of two lane halves)
+void run_relu_linear_forward(const float* a, const float* w, const float* b, float* y, int64_t rows, int nin,
+                             int nout, hipStream_t st) {
+  if (rows == 0) return;
+  const int g = (nin + 7) / 8;
+  if (g <= 4) launch_relu_fwd<4>(a, w, b, y, rows, nin, nout, st);
+  else if (g <= 8) launch_relu_fwd<8>(a, w, b, y, rows, nin, nout, st);
+  else if (g <= 12) launch_relu_fwd<12>(a, w, b, y, rows, nin, nout, st);
+  else if (g <= 16) launch_relu_fwd<16>(a, w, b, y, rows, nin, nout, st);
+  else if (g <= 24) launch_relu_fwd<24>(a, w, b, y, rows, nin, nout, st);
+  else launch_relu_fwd<kMaxReluLinearIn / 8>(a, w, b, y, rows, nin, nout, st);
 }
 
 }  // namespace sphops

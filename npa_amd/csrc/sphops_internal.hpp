@@ -202,8 +202,12 @@ constexpr int64_t kMaxLinearWaves = int64_t(1) << 25;  // one wave per (row chun
 int64_t linear_grad_chunks(int64_t rows, int nin, int nout);
 bool linear_grad_fits(int64_t rows, int nin, int nout);
 void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* db, int64_t rows, int nin, int nout,
-                            float* work, hipStream_t st);
-constexpr int kMaxReluLinearOut = 64;  // dY values per row kept against W columns in registers
+                            float* work, bool relu_x, hipStream_t st);
+constexpr int kMaxReluLinearOut = 64;  // two 32-wide tiles of W kept in registers
+constexpr int kMaxReluLinearIn = 256;  // forward: W's columns for one output in registers
+bool relu_linear_forward_fits(int64_t rows);
+void run_relu_linear_forward(const float* a, const float* w, const float* b, float* y, int64_t rows, int nin,
+                             int nout, hipStream_t st);
 bool relu_linear_input_grad_fits(int64_t rows, int nin);
 void run_relu_linear_input_grad(const float* dy, const float* w, const float* h, float* dx, int64_t rows, int nin,
                                 int nout, hipStream_t st);

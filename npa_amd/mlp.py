@@ -51,9 +51,10 @@ class LinearRows(torch.autograd.Function):
         return dx, (dw if need_w else None), (db if need_b else None)
 
 
-def _weight_grad(x2, dy2, has_bias):
-    """dW = dy2^T x2 and db = column sums of dy2 (None without a bias) through
-    ``sphops_linear_weight_grad``."""
+def _weight_grad(x2, dy2, has_bias, relu_x=False):
+    """dW = dy2^T x2 (dy2^T relu(x2) with relu_x) and db = column sums of dy2
+    (None without a bias) through ``sphops_linear_weight_grad`` or
+    ``sphops_relu_linear_weight_grad``."""
     if x2.dtype != torch.float32 or dy2.dtype != torch.float32 or not x2.is_cuda:
         raise TypeError("the MLP kernels take float32 GPU tensors")
     x2, dy2 = x2.contiguous(), dy2.contiguous()
@@ -64,49 +65,71 @@ def _weight_grad(x2, dy2, has_bias):
     nbytes = _lib.sphops_linear_weight_grad_workspace_bytes(rows, in_f, out_f)
     work = torch.empty(max(nbytes // 4, 1), device=x2.device)
     st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(x2.device.index))
-    _native.check(_lib.sphops_linear_weight_grad(_ptr(x2), _ptr(dy2), _ptr(dw), _ptr(db), rows, in_f, out_f,
-                                                 _ptr(work), st))
+    fn = _lib.sphops_relu_linear_weight_grad if relu_x else _lib.sphops_linear_weight_grad
+    _native.check(fn(_ptr(x2), _ptr(dy2), _ptr(dw), _ptr(db), rows, in_f, out_f, _ptr(work), st))
     return dw, db
 
 
 class ReluLinear(torch.autograd.Function):
-    """y = relu(a) W^T + b (``torch.nn.ReLU`` then ``torch.nn.Linear``).  The
-    forward is torch's; the backward takes dW and db from the row-chunked
-    kernel and da = (relu(a) > 0) * (dy W) from
-    ``sphops_relu_linear_input_grad``, one pass that never writes dy W."""
+    """y = relu(a) W^T + b (``torch.nn.ReLU`` then ``torch.nn.Linear``).  For
+    in_features a multiple of 4 up to 256 the forward is one kernel
+    (``sphops_relu_linear_forward``) that never writes relu(a), and the
+    backward keeps ``a``; otherwise the forward is torch's and the backward
+    keeps h = relu(a).  The backward takes da = (relu(a) > 0) * (dy W) from
+    ``sphops_relu_linear_input_grad`` (a <= 0 exactly where relu(a) <= 0, so
+    either saved tensor gives the mask) and dW, db from the row-chunked
+    kernel."""
 
     @staticmethod
     def forward(ctx, a, weight, bias):
-        h = torch.relu(a)
-        ctx.save_for_backward(h, weight)
+        out_f, in_f = weight.shape
+        fused = (a.is_cuda and a.dtype == torch.float32 and weight.dtype == torch.float32
+                 and in_f % 4 == 0 and 4 <= in_f <= RELU_LINEAR_MAX_IN and out_f <= RELU_LINEAR_MAX_OUT)
         ctx.has_bias = bias is not None
-        return F.linear(h, weight, bias)
+        ctx.pre = fused
+        if not fused:
+            h = torch.relu(a)
+            ctx.save_for_backward(h, weight)
+            return F.linear(h, weight, bias)
+        a2 = a.reshape(-1, in_f).contiguous()
+        if a2.data_ptr() % 16:
+            a2 = a2.clone()
+        w = weight.detach().contiguous()
+        b = None if bias is None else bias.detach().contiguous()
+        y = torch.empty(a2.shape[0], out_f, device=a.device)
+        st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(a.device.index))
+        _native.check(_lib.sphops_relu_linear_forward(_ptr(a2), _ptr(w), _ptr(b), _ptr(y), a2.shape[0], in_f,
+                                                      out_f, st))
+        ctx.save_for_backward(a2, weight)
+        return y.reshape(*a.shape[:-1], out_f)
 
     @staticmethod
     def backward(ctx, dy):
-        h, weight = ctx.saved_tensors
+        s, weight = ctx.saved_tensors  # a (ctx.pre) or relu(a)
         need_a, need_w, need_b = ctx.needs_input_grad
         out_f, in_f = weight.shape
-        h2 = h.reshape(-1, in_f)
+        s2 = s.reshape(-1, in_f)
         dy2 = dy.reshape(-1, out_f).contiguous()
         da = dw = db = None
         if need_a:
-            if h2.dtype != torch.float32 or dy2.dtype != torch.float32 or not h2.is_cuda:
+            if s2.dtype != torch.float32 or dy2.dtype != torch.float32 or not s2.is_cuda:
                 raise TypeError("the MLP kernels take float32 GPU tensors")
-            h2 = h2.contiguous()
+            s2 = s2.contiguous()
             w = weight.detach().contiguous()
-            da2 = torch.empty_like(h2)
-            st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(h2.device.index))
-            _native.check(_lib.sphops_relu_linear_input_grad(_ptr(dy2), _ptr(w), _ptr(h2), _ptr(da2), h2.shape[0],
+            da2 = torch.empty_like(s2)
+            st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(s2.device.index))
+            _native.check(_lib.sphops_relu_linear_input_grad(_ptr(dy2), _ptr(w), _ptr(s2), _ptr(da2), s2.shape[0],
                                                              in_f, out_f, st))
-            da = da2.reshape(h.shape)
+            da = da2.reshape(dy.shape[:-1] + (in_f,))
         if need_w or (need_b and ctx.has_bias):
-            dw, db = _weight_grad(h2, dy2, ctx.has_bias)
+            dw, db = _weight_grad(s2, dy2, ctx.has_bias, relu_x=ctx.pre)
         return da, (dw if need_w else None), (db if need_b else None)
 
 
-# ReluLinear keeps a row's dy in one wave's lanes against W in registers
+# ReluLinear keeps W's 32-output tiles in registers (the fused forward also
+# all of a row's in_features)
 RELU_LINEAR_MAX_OUT = 64
+RELU_LINEAR_MAX_IN = 256
 
 
 def linear(x, layer):

@@ -64,9 +64,12 @@ def test_mlp_matches_module_autograd(hidden):
     z = torch.randn(3, 5000, 66, device="cuda", requires_grad=True)
     up = torch.randn(3, 5000, 18, device="cuda")
     out = M.mlp(net, z)
-    assert torch.equal(out, net(z))  # the forward is torch's own
-    if hidden is not None:
+    if hidden is None:
+        assert torch.equal(out, net(z))  # the forward is torch's own
+    else:
         assert type(out.grad_fn).__name__ == "ReluLinearBackward"  # the fused ReLU + Linear ran
+        ref_out = net(z).detach()
+        assert torch.allclose(out, ref_out, rtol=1e-5, atol=1e-5 * float(ref_out.abs().max()))
     got = torch.autograd.grad(out, [z] + list(net.parameters()), up)
     ref = torch.autograd.grad(net(z), [z] + list(net.parameters()), up)
     for a, b in zip(got, ref):
@@ -119,3 +122,50 @@ def test_relu_linear_output_limit_is_an_error():
     st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(0))
     with pytest.raises(RuntimeError, match="out_features"):
         _native.check(_native.lib.sphops_relu_linear_input_grad(p, p, p, p, 1, 4, 65, p, st))
+
+
+@pytest.mark.parametrize("shape", [(128, 19), (128, 18), (4, 3), (256, 64), (64, 1), (132, 33), (20, 40)])
+@pytest.mark.parametrize("rows", [0, 1, 9, 1000, 100003])
+def test_relu_linear_forward_matches_float64(shape, rows):
+    """y = relu(a) W^T + b (with and without b) against float64, and the
+    weight gradient with relu applied to its input against dy^T relu(a)."""
+    import ctypes
+    from npa_amd.sphops import _native
+    in_f, out_f = shape
+    g = torch.Generator(device="cuda").manual_seed(11 * rows + in_f + out_f)
+    a = torch.randn(rows, in_f, device="cuda", generator=g)
+    w = torch.randn(out_f, in_f, device="cuda", generator=g)
+    b = torch.randn(out_f, device="cuda", generator=g)
+    st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(0))
+    P = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
+    hd, wd = torch.relu(a).double().cpu(), w.double().cpu()
+    for bias in (b, None):
+        bd = torch.zeros(out_f, dtype=torch.float64) if bias is None else bias.double().cpu()
+        bound = (hd @ wd.abs().T + bd.abs()) * 1e-5 + 1e-30  # fp32 sums, then the rounded + b
+        y = torch.full((rows, out_f), float("nan"), device="cuda")
+        _native.check(_native.lib.sphops_relu_linear_forward(P(a), P(w), P(bias), P(y), rows, in_f, out_f, st))
+        ref = hd @ wd.T + bd
+        assert torch.all((y.cpu().double() - ref).abs() <= bound), f"y rows={rows} shape={shape} bias={bias is not None}"
+    dy = torch.randn(rows, out_f, device="cuda", generator=g)
+    dw = torch.full((out_f, in_f), float("nan"), device="cuda")
+    db = torch.full((out_f,), float("nan"), device="cuda")
+    nb = _native.lib.sphops_linear_weight_grad_workspace_bytes(rows, in_f, out_f)
+    work = torch.empty(max(nb // 4, 1), device="cuda")
+    _native.check(_native.lib.sphops_relu_linear_weight_grad(P(a), P(dy), P(dw), P(db), rows, in_f, out_f, P(work),
+                                                            st))
+    yd = dy.double().cpu()
+    assert torch.all((dw.cpu().double() - yd.T @ hd).abs() <= (yd.abs().T @ hd) * 1e-5 + 1e-30)
+    assert torch.all((db.cpu().double() - yd.sum(0)).abs() <= yd.abs().sum(0) * 1e-5 + 1e-30)
+
+
+def test_relu_linear_forward_limits_are_errors():
+    import ctypes
+    from npa_amd.sphops import _native
+    x = torch.zeros(64, device="cuda")
+    p = ctypes.c_void_p(x.data_ptr())
+    st = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(0))
+    for in_f, out_f, msg in ((6, 3, "multiple of 4"), (260, 3, "multiple of 4"), (8, 65, "out_features")):
+        with pytest.raises(RuntimeError, match=msg):
+            _native.check(_native.lib.sphops_relu_linear_forward(p, p, p, p, 1, in_f, out_f, st))
+    with pytest.raises(RuntimeError, match="aligned"):
+        _native.check(_native.lib.sphops_relu_linear_forward(ctypes.c_void_p(x.data_ptr() + 4), p, p, p, 1, 8, 3, st))
