@@ -342,13 +342,16 @@ __global__ __launch_bounds__(256) void k_relu_linear_fwd(const float* __restrict
 #pragma unroll
   for (int g = 0; g < G; ++g) ka[g] = 8 * g + 4 * hq < nin ? (uint32_t)(8 * g + 4 * hq) * 4u : kOffLane;
 
-  for (int i = 0; i < kRLTiles; ++i) {
-    if (i * kMT >= nr) break;  // uniform
+  // Tile i + 1 loads while tile i computes.  Tiles past the wave's rows load
+  // zeros and their stores are dropped by the range check, so the four tiles
+  // run unconditionally.
+  auto load = [&](int i, f32x4 (&av)[G]) {
     const uint32_t ro = (uint32_t)((i * kMT + c) * nin) * 4u;
-    f32x4 av[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
       av[g] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, ka[g] + ro, 0, 0));
+  };
+  auto compute_store = [&](int i, const f32x4 (&av)[G]) {
     f32x16 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f32x16{};
@@ -370,6 +373,20 @@ __global__ __launch_bounds__(256) void k_relu_linear_fwd(const float* __restrict
                                               0);
       }
     }
+  };
+  static_assert(kRLTiles % 2 == 0, "tiles run in ping-pong pairs");
+  f32x4 av0[G], av1[G];
+  load(0, av0);
+#pragma unroll
+  for (int i = 0; i < kRLTiles; i += 2) {
+    load(i + 1, av1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute_store(i, av0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 2 < kRLTiles) load(i + 2, av0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute_store(i + 1, av1);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
