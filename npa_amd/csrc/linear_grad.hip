@@ -215,7 +215,7 @@ void launch_mfma(const LinearPlan& p, const float* x, const float* dy, float* pa
 // else (dY W)[r][n].  It replaces the dH = dY W product and the elementwise
 // ReLU backward, so dH never goes to memory: per row it reads dY and h and
 // writes dA.  dY W runs on the matrix cores (K = nout padded to 2 KS): one
-// wave per (kRLTiles tiles of 32 rows, 128 columns) keeps W's four 32-column
+// wave per (TILES tiles of 32 rows, 128 columns) keeps W's four 32-column
 // tiles as B operands in registers; for row tile i, lane l supplies A[m = l %
 // 32][k = l / 32] = dY[32 i + m][2 s + k] at step s, and result register j of
 // column tile t holds row 8 (j / 4) + 4 (l / 32) + j % 4, column 32 t + l % 32,
@@ -224,7 +224,11 @@ void launch_mfma(const LinearPlan& p, const float* x, const float* dy, float* pa
 // there.
 constexpr int kRLTiles = 4;
 
-template <int KS>
+// Row tiles per wave: kRLTiles for long inputs, one (four times the waves)
+// below 2^17 rows, where a quarter as many waves would leave most SIMDs idle.
+int relu_linear_tiles(int64_t rows) { return rows >= (int64_t(1) << 17) ? kRLTiles : 1; }
+
+template <int KS, int TILES>
 __global__ __launch_bounds__(256) void k_relu_linear_dx(const float* __restrict__ dy, const float* __restrict__ w,
                                                         const float* __restrict__ h, float* __restrict__ dx,
                                                         int64_t rows, int nin, int nout, int col_blocks,
@@ -233,8 +237,8 @@ __global__ __launch_bounds__(256) void k_relu_linear_dx(const float* __restrict_
   if (wid >= total_waves) return;
   const int lane = threadIdx.x & 63, c = lane & 31, hh = lane >> 5;
   const int n0 = (int)(wid % (uint32_t)col_blocks) * 128;
-  const int64_t r0 = (int64_t)(wid / (uint32_t)col_blocks) * (kRLTiles * kMT);
-  const int64_t nr = min<int64_t>(kRLTiles * kMT, rows - r0);
+  const int64_t r0 = (int64_t)(wid / (uint32_t)col_blocks) * (TILES * kMT);
+  const int64_t nr = min<int64_t>(TILES * kMT, rows - r0);
   const __amdgpu_buffer_rsrc_t rdy = chunk_rsrc(dy + r0 * nout, nr * nout * 4);
   const __amdgpu_buffer_rsrc_t rh = chunk_rsrc(h + r0 * nin, nr * nin * 4);
   const __amdgpu_buffer_rsrc_t rdx = chunk_rsrc(dx + r0 * nin, nr * nin * 4);
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(256) void k_relu_linear_dx(const float* __restrict_
 #pragma unroll
   for (int t = 0; t < 4; ++t) cn[t] = n0 + kMT * t + c < nin ? (uint32_t)(n0 + kMT * t + c) * 4u : kOffLane;
 
-  for (int i = 0; i < kRLTiles; ++i) {
+  for (int i = 0; i < TILES; ++i) {
     if (i * kMT >= nr) break;  // uniform
     const uint32_t ra = (uint32_t)(i * kMT * nout) * 4u;
     float a[KS];
@@ -295,29 +299,34 @@ template <int KS>
 void launch_relu_dx(const float* dy, const float* w, const float* h, float* dx, int64_t rows, int nin, int nout,
                     hipStream_t st) {
   const int col_blocks = (nin + 127) / 128;
-  const int64_t rows_per_wave = kRLTiles * kMT;
+  const int tiles = relu_linear_tiles(rows);
+  const int64_t rows_per_wave = tiles * kMT;
   const uint32_t waves = (uint32_t)(((rows + rows_per_wave - 1) / rows_per_wave) * col_blocks);
-  hipLaunchKernelGGL(k_relu_linear_dx<KS>, dim3((waves + 3) / 4), dim3(256), 0, st, dy, w, h, dx, rows, nin, nout,
-                     col_blocks, waves);
+  if (tiles == kRLTiles)
+    hipLaunchKernelGGL((k_relu_linear_dx<KS, kRLTiles>), dim3((waves + 3) / 4), dim3(256), 0, st, dy, w, h, dx, rows,
+                       nin, nout, col_blocks, waves);
+  else
+    hipLaunchKernelGGL((k_relu_linear_dx<KS, 1>), dim3((waves + 3) / 4), dim3(256), 0, st, dy, w, h, dx, rows, nin,
+                       nout, col_blocks, waves);
   SPHOPS_LAUNCHED();
 }
 
 // Forward through a ReLU and a linear layer, y = relu(a) W^T + b, for at most
 // 64 outputs and in_features a multiple of 4 up to 256, on the matrix cores:
-// one wave per kRLTiles tiles of 32 rows keeps W's 32-output tiles as B
+// one wave per TILES tiles of 32 rows keeps W's 32-output tiles as B
 // operands in registers.  Lane l (row m = l % 32 of the tile, half q = l / 32)
 // loads a[m][8 g + 4 q .. + 3] as one 16-byte load per g; at step (g, j) it
 // supplies A[m][q] = relu(a[m][8 g + 4 q + j]) and B[q][n] = W[n][8 g + 4 q +
 // j], so the steps cover every k once.  relu(a) never goes to memory.
-template <int G, int NT>
+template <int G, int NT, int TILES>
 __global__ __launch_bounds__(256) void k_relu_linear_fwd(const float* __restrict__ a, const float* __restrict__ w,
                                                          const float* __restrict__ b, float* __restrict__ y,
                                                          int64_t rows, int nin, int nout, uint32_t total_waves) {
   const uint32_t wid = __builtin_amdgcn_readfirstlane(xcd_block_id() * 4u + threadIdx.x / 64u);
   if (wid >= total_waves) return;
   const int lane = threadIdx.x & 63, c = lane & 31, hq = lane >> 5;
-  const int64_t r0 = (int64_t)wid * (kRLTiles * kMT);
-  const int64_t nr = min<int64_t>(kRLTiles * kMT, rows - r0);
+  const int64_t r0 = (int64_t)wid * (TILES * kMT);
+  const int64_t nr = min<int64_t>(TILES * kMT, rows - r0);
   const __amdgpu_buffer_rsrc_t ra = chunk_rsrc(a + r0 * nin, nr * nin * 4);
   const __amdgpu_buffer_rsrc_t ry = chunk_rsrc(y + r0 * nout, nr * nout * 4);
   float wr[NT][G][4];
@@ -374,34 +383,41 @@ __global__ __launch_bounds__(256) void k_relu_linear_fwd(const float* __restrict
       }
     }
   };
-  static_assert(kRLTiles % 2 == 0, "tiles run in ping-pong pairs");
   f32x4 av0[G], av1[G];
   load(0, av0);
 #pragma unroll
-  for (int i = 0; i < kRLTiles; i += 2) {
-    load(i + 1, av1);
+  for (int i = 0; i < TILES; i += 2) {
+    if (i + 1 < TILES) load(i + 1, av1);
     __builtin_amdgcn_sched_barrier(0);
     compute_store(i, av0);
     __builtin_amdgcn_sched_barrier(0);
-    if (i + 2 < kRLTiles) load(i + 2, av0);
+    if (i + 2 < TILES) load(i + 2, av0);
     __builtin_amdgcn_sched_barrier(0);
-    compute_store(i + 1, av1);
+    if (i + 1 < TILES) compute_store(i + 1, av1);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+template <int G, int NT>
+void launch_relu_fwd_nt(const float* a, const float* w, const float* b, float* y, int64_t rows, int nin, int nout,
+                        hipStream_t st) {
+  const int tiles = relu_linear_tiles(rows);
+  const int64_t rows_per_wave = tiles * kMT;
+  const uint32_t waves = (uint32_t)((rows + rows_per_wave - 1) / rows_per_wave);
+  if (tiles == kRLTiles)
+    hipLaunchKernelGGL((k_relu_linear_fwd<G, NT, kRLTiles>), dim3((waves + 3) / 4), dim3(256), 0, st, a, w, b, y,
+                       rows, nin, nout, waves);
+  else
+    hipLaunchKernelGGL((k_relu_linear_fwd<G, NT, 1>), dim3((waves + 3) / 4), dim3(256), 0, st, a, w, b, y, rows, nin,
+                       nout, waves);
+  SPHOPS_LAUNCHED();
 }
 
 template <int G>
 void launch_relu_fwd(const float* a, const float* w, const float* b, float* y, int64_t rows, int nin, int nout,
                      hipStream_t st) {
-  const int64_t rows_per_wave = kRLTiles * kMT;
-  const uint32_t waves = (uint32_t)((rows + rows_per_wave - 1) / rows_per_wave);
-  if (nout <= kMT)
-    hipLaunchKernelGGL((k_relu_linear_fwd<G, 1>), dim3((waves + 3) / 4), dim3(256), 0, st, a, w, b, y, rows, nin,
-                       nout, waves);
-  else
-    hipLaunchKernelGGL((k_relu_linear_fwd<G, 2>), dim3((waves + 3) / 4), dim3(256), 0, st, a, w, b, y, rows, nin,
-                       nout, waves);
-  SPHOPS_LAUNCHED();
+  if (nout <= kMT) launch_relu_fwd_nt<G, 1>(a, w, b, y, rows, nin, nout, st);
+  else launch_relu_fwd_nt<G, 2>(a, w, b, y, rows, nin, nout, st);
 }
 
 }  // namespace
@@ -435,7 +451,7 @@ void run_linear_weight_grad(const float* x, const float* dy, float* dw, float* d
 namespace sphops {
 
 bool relu_linear_input_grad_fits(int64_t rows, int nin) {
-  const int64_t rows_per_wave = kRLTiles * kMT;
+  const int64_t rows_per_wave = relu_linear_tiles(rows) * kMT;
   return ((rows + rows_per_wave - 1) / rows_per_wave) * ((nin + 127) / 128) <= kMaxLinearWaves;
 }
 
@@ -460,7 +476,8 @@ void run_relu_linear_input_grad(const float* dy, const float* w, const float* h,
 namespace sphops {
 
 bool relu_linear_forward_fits(int64_t rows) {
-  return (rows + kRLTiles * kMT - 1) / (kRLTiles * kMT) <= kMaxLinearWaves;
+  const int64_t rows_per_wave = relu_linear_tiles(rows) * kMT;
+  return (rows + rows_per_wave - 1) / rows_per_wave <= kMaxLinearWaves;
 }
 
 // in_features padded to a multiple of 8 (16-byte blocks of two lane halves)

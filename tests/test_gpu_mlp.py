@@ -91,7 +91,7 @@ RELU_SHAPES = [(128, 19), (128, 18), (5, 3), (200, 64), (64, 1), (130, 33)]
 
 
 @pytest.mark.parametrize("shape", RELU_SHAPES)
-@pytest.mark.parametrize("rows", [0, 1, 9, 1000, 100003])
+@pytest.mark.parametrize("rows", [0, 1, 9, 1000, 100003, 131073])
 def test_relu_linear_input_grad_matches_float64(shape, rows):
     """da = 0 where h = relu(a) <= 0, else dy W (torch's threshold_backward of
     the Linear's input gradient), against float64."""
@@ -125,7 +125,7 @@ def test_relu_linear_output_limit_is_an_error():
 
 
 @pytest.mark.parametrize("shape", [(128, 19), (128, 18), (4, 3), (256, 64), (64, 1), (132, 33), (20, 40)])
-@pytest.mark.parametrize("rows", [0, 1, 9, 1000, 100003])
+@pytest.mark.parametrize("rows", [0, 1, 9, 1000, 100003, 131073])
 def test_relu_linear_forward_matches_float64(shape, rows):
     """y = relu(a) W^T + b (with and without b) against float64, and the
     weight gradient with relu applied to its input against dy^T relu(a)."""
