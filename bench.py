@@ -122,8 +122,8 @@ def main():
     if args.pmc_child:
         return pmc_child(args)
     if args.extras:
-        from npa_amd import bench_fused
-        bench_fused.run_all()
+        import bench_extras
+        bench_extras.run_all()
         return
     # counter runs first, in child processes, before this process touches the GPU
     pmc = None
@@ -156,7 +156,7 @@ def main():
                        max_particles_per_block=wl.maxp)
     full = args.variant == "full"
 
-    def step():
+    def step(full=full):
         xr = x.detach().requires_grad_(full)
         sr = s.detach().requires_grad_(True)
         with torch.no_grad():
@@ -177,22 +177,29 @@ def main():
     snap0, xb0 = step()
     with torch.no_grad():
         pairs = float(sp.count(xb0.detach(), snap0).sum().item())
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-    print(f"[bench] {args.steps} steps: {ms:.3f} ms/step, {pairs / (ms * 1e-3) / 1e9:.3f} G pairs/s",
+    def timed_steps(variant_full):
+        for _ in range(args.warmup):
+            step(variant_full)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            step(variant_full)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    ms = timed_steps(full)
+    print(f"[bench] {args.steps} steps ({args.variant}): {ms:.3f} ms/step, {pairs / (ms * 1e-3) / 1e9:.3f} G pairs/s",
           file=sys.stderr, flush=True)
+    # the other backward variant of the same step, reported alongside
+    other = "npa" if full else "full"
+    ms_other = timed_steps(not full)
+    print(f"[bench] {args.steps} steps ({other}): {ms_other:.3f} ms/step", file=sys.stderr, flush=True)
 
     # ---- per-kernel timing (HIP events on the launch stream)
-    kt = kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, args.kernel_reps)
+    kt = kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, True, args.kernel_reps)
     ppb = per_particle_bytes(C, D, P)
     dom = max(STEP_KERNELS[args.variant], key=lambda k: kt[k])
     dom_ms = kt[dom]
@@ -200,6 +207,9 @@ def main():
     achieved = alg / (dom_ms * 1e-3) / 1e9
     pp, pc = step_bytes(C, D, P, full)
     step_alg = pp * B * N + pc * cells
+    po, pco = step_bytes(C, D, P, not full)
+    other_alg = po * B * N + pco * cells
+    other_dom = max(STEP_KERNELS[other], key=lambda k: kt[k])
     traffic = None
     if pmc is not None and pmc.get("kernel") == dom:
         traffic = pmc["bytes_per_launch"]
@@ -234,9 +244,24 @@ def main():
             "step_alg_bytes": step_alg,
             "step_roofline_frac": step_alg / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
             "kernel_ms": kt,
+            "other_variant": {
+                "variant": "npa-default (stopgrad_pos: dL/ds only, no density gradient; models/npa.py:28,95-96)"
+                           if full else "full backward",
+                "ms_per_step": ms_other,
+                "pairs_per_s": pairs / (ms_other * 1e-3),
+                "particles_per_s": B * N / (ms_other * 1e-3),
+                "step_alg_bytes": other_alg,
+                "step_roofline_frac": other_alg / (ms_other * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                "dominant_kernel": other_dom,
+                "dominant_kernel_ms": kt[other_dom],
+            },
         },
         "roofline": {
+            # the roofline the fraction is reported against (the path is a
+            # sparse gather with no dense contraction: HBM, not MFMA); what the
+            # counters show limits the kernel is `limiter`
             "bound": "hbm",
+            "limiter": limiter(pmc, traffic, dom_ms) if pmc is not None and pmc.get("kernel") == dom else None,
             "kernel": dom,
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
@@ -247,12 +272,28 @@ def main():
             "avg_launch_ms": dom_ms,
             "pair_kernel": pair_kernel(dom, D, wl.periodic, C),
             "valu_busy": pmc.get("valu_busy") if pmc is not None and pmc.get("kernel") == dom else None,
+            "ta_busy": pmc.get("ta_busy") if pmc is not None and pmc.get("kernel") == dom else None,
+            "td_busy": pmc.get("td_busy") if pmc is not None and pmc.get("kernel") == dom else None,
             "measured_copy_gbs": copy_gbs,
             "pmc": pmc,
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def limiter(pmc, traffic, dom_ms):
+    """What bounds the dominant kernel, from its counters: the busiest of the
+    VALU issue (valu_busy), the vector-memory address/data path that carries
+    neighbour rows from L2 (TA / TD busy) and HBM (measured traffic over time
+    against the 8 TB/s peak)."""
+    util = {"valu": pmc.get("valu_busy"), "vmem-l2 (TA/TD)": max(pmc.get("ta_busy") or 0.0, pmc.get("td_busy") or 0.0),
+            "hbm": traffic / (dom_ms * 1e-3) / (HBM_PEAK_GBS * 1e9) if traffic else None}
+    util = {k: v for k, v in util.items() if v is not None}
+    if not util:
+        return None
+    name = max(util, key=util.get)
+    return {"name": name, "utilisation": util}
 
 
 def measured_copy_gbs(nbytes=COPY_BYTES, reps=20):
@@ -376,8 +417,9 @@ def pmc_child(args):
 
 
 def _pmc_run(counter, kernel, frag, args):
-    """One rocprofv3 --pmc run of the child; returns {kernel name: mean value
-    per dispatch} for the copy kernel and the operator's pair kernel."""
+    """One rocprofv3 --pmc run of the child for one or more counters
+    (space-separated, all in one pass); returns (copy, kernel) mean values
+    per dispatch, or dicts of them by counter name when several."""
     import csv
     import shutil
     import subprocess
@@ -386,7 +428,8 @@ def _pmc_run(counter, kernel, frag, args):
     if prof is None:
         raise RuntimeError("rocprofv3 not on PATH")
     out = tempfile.mkdtemp(prefix="npa_pmc_", dir="/tmp")
-    cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "run", "--",
+    names = counter.split()
+    cmd = [prof, "--pmc", *names, "--output-format", "csv", "-d", out, "-o", "run", "--",
            sys.executable, os.path.abspath(__file__), "--pmc-child", kernel, "--config", args.config,
            "--variant", args.variant, "--mode", args.mode]
     env = dict(os.environ, TMPDIR="/tmp")
@@ -403,22 +446,27 @@ def _pmc_run(counter, kernel, frag, args):
     per_dispatch = {}
     with open(path) as fh:
         for row in csv.DictReader(fh):
-            if row["Counter_Name"] != counter:
+            if row["Counter_Name"] not in names:
                 continue
-            key = (row["Dispatch_Id"], row["Kernel_Name"])
+            key = (row["Counter_Name"], row["Dispatch_Id"], row["Kernel_Name"])
             per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
     shutil.rmtree(out, ignore_errors=True)
-    copy, target = [], []
-    for (_, name), v in per_dispatch.items():
-        if "copy" in name.lower():
-            copy.append(v)
-        elif frag in name:
-            target.append(v)
-    if not copy or not target:
-        raise RuntimeError(f"{counter}: kernels not found in the counter output")
-    # the largest copy dispatches are the calibration copies
-    copy = sorted(copy)[-3:]
-    return sum(copy) / len(copy), sum(target) / len(target)
+    res = {}
+    for cn in names:
+        copy, target = [], []
+        for (c, _, name), v in per_dispatch.items():
+            if c != cn:
+                continue
+            if "copy" in name.lower():
+                copy.append(v)
+            elif frag in name:
+                target.append(v)
+        if not copy or not target:
+            raise RuntimeError(f"{cn}: kernels not found in the counter output")
+        # the largest copy dispatches are the calibration copies
+        copy = sorted(copy)[-3:]
+        res[cn] = (sum(copy) / len(copy), sum(target) / len(target))
+    return res[names[0]] if len(names) == 1 else res
 
 
 def measure_traffic(args, kernel):
@@ -441,9 +489,14 @@ def measure_traffic(args, kernel):
         res["bytes_per_launch"] = total
         # VALU utilisation: VALU issue cycles per CU (one wave instruction per
         # CU and clock at most) over the active clock of an XCD
-        valu = _pmc_run("SQ_ACTIVE_INST_VALU", kernel, frag, args)[1]
-        gui = _pmc_run("GRBM_GUI_ACTIVE", kernel, frag, args)[1]
-        res["valu_busy"] = valu / CUS / (gui / XCDS) if gui > 0 else None
+        # and the vector-memory path: TA / TD busy cycles summed over the 256
+        # instances (one per CU) over the same clock
+        busy = _pmc_run("SQ_ACTIVE_INST_VALU TA_TA_BUSY_sum TD_TD_BUSY_sum GRBM_GUI_ACTIVE", kernel, frag, args)
+        gui = busy["GRBM_GUI_ACTIVE"][1] / XCDS
+        if gui > 0:
+            res["valu_busy"] = busy["SQ_ACTIVE_INST_VALU"][1] / CUS / gui
+            res["ta_busy"] = busy["TA_TA_BUSY_sum"][1] / CUS / gui
+            res["td_busy"] = busy["TD_TD_BUSY_sum"][1] / CUS / gui
         print(f"[bench] traffic of {kernel}: {total / 1e6:.1f} MB per launch "
               f"(fetch {res['FETCH_SIZE']['kernel_bytes'] / 1e6:.1f}, write {res['WRITE_SIZE']['kernel_bytes'] / 1e6:.1f})",
               file=sys.stderr, flush=True)
@@ -463,6 +516,16 @@ def cpu_baseline(wl, pairs_per_step):
     from oracle import bruteforce
 
     threads = torch.get_num_threads()
+    affinity = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for ln in fh:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     x = torch.from_numpy(wl.x[..., :wl.dim].astype(np.float32))
     s = torch.from_numpy(wl.s)
     N = wl.N
@@ -485,6 +548,8 @@ def cpu_baseline(wl, pairs_per_step):
         "value": pairs_per_step / t_step,
         "unit": "pair-interactions/s",
         "cores": threads,
+        "affinity_cores": affinity,
+        "cpu_model": model,
         "kind": "port",
         "sample": f"{nblk} blocks of {rows} rows x all {N} columns of the same cloud, fp32 torch CPU "
                   f"fwd+bwd; {t_total:.1f}s measured, extrapolated linearly to {N} rows "

@@ -17,13 +17,17 @@ reference's own torch formulation of the same computation on the same GPU
 * ``graph``: the bench's perception step eager and replayed from a HIP graph
   (the grid's capture mode), for every BASELINE configuration.
 
-The torch formulations here are measurement baselines, written as the
-reference writes them; the library never calls them.
+The reference's torch formulations are restated in oracle/torch_ref.py (test
+and measurement infrastructure, never called by the library); this file
+imports them only inside the baseline leg of each measurement.
 """
 import json
-import math
+import os
+import sys
 
 import torch
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 
 import npa_amd.sphops as sp
 from npa_amd import perceive as fused_perceive
@@ -43,74 +47,16 @@ def _time(fn, iters, warmup=3):
     return e0.elapsed_time(e1) / iters
 
 
+def _baseline():
+    """The reference's torch formulations: the baseline leg only."""
+    from oracle import torch_ref
+    return torch_ref
+
+
 def _grid(wl):
     return sp.HashGrid(dim=wl.dim, boundary="periodic" if wl.periodic else "clamped", mode=wl.mode,
                        grid_size=list(wl.grid_size), eps=wl.h, num_particles=wl.N, batch_size=wl.B,
                        max_particles_per_block=wl.maxp)
-
-
-# ---- the reference's torch formulations (measurement baselines)
-
-def _ref_log_normalize(v):  # models/npa.py:83-85
-    return torch.log(1.0 + v.norm(dim=-1, keepdim=True)) * torch.nn.functional.normalize(v, dim=-1)
-
-
-def _ref_perceive(x, s, grid, eps0=0.1):  # models/npa.py:87-137, all flags on, stopgrad_pos
-    B, N, C = s.shape
-    eps = grid.eps
-    with torch.no_grad():
-        snap = grid.instantiate(x)
-    x_bin, s_bin = sp.bin_particles(x, s, snap)
-    xp = x_bin.detach()
-    rho = sp.density(xp, snap)
-    z = [s_bin, sp.blur(xp, rho, s_bin, snap)]
-    coef = torch.tensor([eps], device=x.device) / torch.tensor([eps0], device=x.device)
-    g = _ref_log_normalize(sp.gradient_hybrid(xp, rho, s_bin, snap) * coef)
-    z.append(g.reshape(B, N, -1))
-    gr = sp.density_gradient(xp, snap) * (coef ** (1 + grid.dim)) / N
-    z.append(_ref_log_normalize(gr))
-    return torch.cat(z, dim=-1), x_bin, s_bin, snap
-
-
-def _ref_euler(y, x_bin, s_bin, D, alpha, eps, update_prob, dt=1.0):  # models/npa.py:125-133, 178-200
-    B, N, _ = s_bin.shape
-    dx = y[..., :D]
-    dx = alpha * dx * eps / (1.0 + dx.norm(dim=-1, keepdim=True))
-    ds = y[..., D:]
-    dn = dx.norm(dim=-1).mean()
-    m = (torch.rand(B, N, 1, device=y.device) < update_prob).float()
-    if dx.shape[-1] != x_bin.shape[-1]:
-        dx = torch.cat([dx, torch.zeros(B, N, 1, device=y.device)], dim=-1).contiguous()
-    return x_bin + dt * dx * m, s_bin + dt * ds * m, dn
-
-
-def _ref_splat(x, color, img_size, sigma, lo, hi, y_up, pixel_size):  # utils/splatting.py:6-92
-    dev = x.device
-    pos = (x - lo) / (hi - lo) * (img_size - 1)
-    if y_up:
-        pos = torch.stack([pos[:, 0], (img_size - 1) - pos[:, 1]], dim=1)
-    sigma = sigma * img_size * pixel_size / (hi - lo)
-    r = max(1, math.ceil(5 * float(sigma)))
-    offs = torch.arange(-r, r + 1, device=dev, dtype=torch.int64)
-    yy, xx = torch.meshgrid(offs, offs, indexing="ij")
-    dx, dy = xx.reshape(-1), yy.reshape(-1)
-    base = torch.floor(pos)
-    cx, cy = base[:, 0].long(), base[:, 1].long()
-    frac = pos - base
-    x_idx = cx[:, None] + dx[None, :]
-    y_idx = cy[:, None] + dy[None, :]
-    mask = (x_idx >= 0) & (x_idx < img_size) & (y_idx >= 0) & (y_idx < img_size)
-    g = torch.exp(-((dx[None, :] - frac[:, 0:1]) ** 2 + (dy[None, :] - frac[:, 1:2]) ** 2) / (2 * sigma * sigma))
-    g = g / (1e-8 + torch.sum(g, dim=-1, keepdim=True))
-    g = g * (img_size * pixel_size / (hi - lo)) ** 2.0
-    flat = (y_idx * img_size + x_idx)[mask]
-    w = g[mask]
-    c = color[..., -3:][:, None, :].expand(-1, dx.numel(), -1)[mask, :]
-    density = torch.zeros(img_size * img_size, 1, device=dev)
-    rgb = torch.zeros(img_size * img_size, 3, device=dev)
-    density.scatter_add_(0, flat[:, None], w[:, None])
-    rgb.scatter_add_(0, flat[:, None].expand(-1, 3), c * w[:, None])
-    return torch.cat([rgb, density], dim=1).view(img_size, img_size, 4)
 
 
 class _NPA(torch.nn.Module):
@@ -140,7 +86,7 @@ def bench_perceive(cfg="cfg5", iters=20):
 
     def run(fused):
         sr = s.detach().requires_grad_(True)
-        z = fused_perceive.perceive(x, sr, grid, eps0=0.1)[0] if fused else _ref_perceive(x, sr, grid)[0]
+        z = fused_perceive.perceive(x, sr, grid, eps0=0.1)[0] if fused else _baseline().perceive(x, sr, grid)[0]
         z.backward(dz)
 
     return {"bench": "perceive", "config": cfg, "what": "NPA.perceive forward + backward (stopgrad_pos)",
@@ -161,8 +107,9 @@ def bench_step(cfg="cfg5", iters=10):
             xn, sn, st = step.step_euler(model, x, sr, grid, update_prob=0.5, intermediate=True)
             dn = st["dx_norm"]
         else:  # the reference's step: torch feature assembly, torch MLP, torch update
-            z, xb, sb, _ = _ref_perceive(x, sr, grid)
-            xn, sn, dn = _ref_euler(model.model(z), xb, sb, wl.dim, model.alpha, grid.eps, 0.5)
+            ref = _baseline()
+            z, xb, sb, _ = ref.perceive(x, sr, grid)
+            xn, sn, dn = ref.euler(model.model(z), xb, sb, wl.dim, model.alpha, grid.eps, 0.5)
         ((sn ** 2).mean() + (xn ** 2).mean() + dn).backward()
 
     return {"bench": "step_euler", "config": cfg,
@@ -183,7 +130,7 @@ def bench_splat(images=8, particles=4096, img_size=256, pixel_size=2.0 / 64, ite
         if fused:
             img = splatting.splat_particles_batch(xg, cg, **kw)
         else:
-            img = torch.stack([_ref_splat(xg[b], cg[b], **kw) for b in range(images)])
+            img = torch.stack([_baseline().splat(xg[b], cg[b], **kw) for b in range(images)])
         img.backward(up)
 
     return {"bench": "splat", "config": f"{images} images x {particles} particles, {img_size}^2, sigma 1.0, "
@@ -308,7 +255,7 @@ def run_all():
 
 
 if __name__ == "__main__":
-    # python -m npa_amd.bench_fused [perceive|step|mlp|splat|rollout ...]: the
+    # python bench_extras.py [perceive|step|mlp|splat|rollout ...]: the
     # named measurements only (all of them with no argument)
     import sys
     names = sys.argv[1:]

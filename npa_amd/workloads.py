@@ -201,9 +201,14 @@ def make(name, scale=1.0, seed=SEED, h=None, mode="grid"):
         h = CALIBRATED_H[name]
         if h is None:
             h = calibrate(name, 1.0)
-        if name != "cfg2":
-            N = x.shape[1]
-            full = {"cfg1": 4096, "cfg3": 512, "cfg4": 65536, "cfg5": 1048576}[name]
+        N = x.shape[1]
+        full = {"cfg1": 4096, "cfg2": 16384, "cfg3": 512, "cfg4": 65536, "cfg5": 1048576}[name]
+        if name == "cfg2":
+            # the periodic unit box must hold a whole number of cells of side h:
+            # fewer particles get fewer, wider cells at the same mean count
+            if N != full:
+                h = 1.0 / max(3, round(47 * math.sqrt(N / full)))
+        else:
             h = float(np.float32(h * (full / N) ** (1.0 / D)))
     periodic = name == "cfg2"
     gs = grid_for(x, h, 1.0 if periodic else None)

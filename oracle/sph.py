@@ -26,7 +26,11 @@ def _seg_sum(vals, pairs):
 
 
 def _kernels(r, h):
-    """poly6 value, spiky vector K(r) and spiky Jacobian dK/dr at float64 ``r``."""
+    """poly6 value, spiky vector K(r), poly6 gradient and spiky Jacobian
+    dK/dr = a I - b r r^T at float64 ``r``, plus the Jacobian's elementary
+    magnitude |a| I + |b| |r| |r|^T: for |r| << h the two terms of a diagonal
+    element are ~3 h^2 / |r| each and cancel to ~6 h, so fp32 rounding scales
+    with them, not with the cancelled |J|."""
     r = np.asarray(r, dtype=np.float64)
     d2 = np.sum(r * r, axis=-1)
     d = np.sqrt(d2)
@@ -42,7 +46,8 @@ def _kernels(r, h):
     a = np.where(inside, 3.0 * (h - ds) ** 2 / ds, 0.0)[:, None, None]
     b = np.where(inside, 3.0 * (h2 - ds * ds) / ds ** 3, 0.0)[:, None, None]
     J = a * eye - b * (r[:, :, None] * r[:, None, :])
-    return W, K, gW, J
+    Jmag = np.abs(a) * eye + np.abs(b) * (np.abs(r)[:, :, None] * np.abs(r)[:, None, :])
+    return W, K, gW, J, Jmag
 
 
 class Context:
@@ -53,8 +58,8 @@ class Context:
         self.spec = spec
         self.h = float(np.float32(spec.eps))
         self.c6, self.cs = spec.coefficients()
-        self.W, self.K, _, _ = _kernels(pairs.r, self.h)
-        self.Wb, self.Kb, self.gWb, self.Jb = _kernels(pairs.rb, self.h)
+        self.W, self.K, _, _, _ = _kernels(pairs.r, self.h)
+        self.Wb, self.Kb, self.gWb, self.Jb, self.Jb_mag = _kernels(pairs.rb, self.h)
 
 
 def count(ctx):
@@ -181,7 +186,7 @@ def gradient_backward(ctx, m, rho, s, g):
     u = np.sum(delta[:, :, None] * c, axis=1)
     au = np.sum(np.abs(delta)[:, :, None] * ac, axis=1)
     t_x = ctx.cs * np.einsum("pab,pb->pa", ctx.Jb, u)
-    m_x = ctx.cs * np.einsum("pab,pb->pa", np.abs(ctx.Jb), au)
+    m_x = ctx.cs * np.einsum("pab,pb->pa", ctx.Jb_mag, au)
     return [(_seg_sum(t_x, p), _seg_sum(m_x, p)), (_seg_sum(t_s, p), _seg_sum(m_s, p)),
             (_seg_sum(t_r, p), _seg_sum(m_r, p))]
 
@@ -192,7 +197,7 @@ def density_gradient_backward(ctx, m, g):
     diff = g[p.j] * m[p.i][:, None] - g[p.i] * m[p.j][:, None]
     adiff = np.abs(g[p.j] * m[p.i][:, None]) + np.abs(g[p.i] * m[p.j][:, None])
     t = ctx.cs * np.einsum("pab,pb->pa", ctx.Jb, diff)
-    mt = ctx.cs * np.einsum("pab,pb->pa", np.abs(ctx.Jb), adiff)
+    mt = ctx.cs * np.einsum("pab,pb->pa", ctx.Jb_mag, adiff)
     return _seg_sum(t, p), _seg_sum(mt, p)
 
 
@@ -212,7 +217,7 @@ def moment_matrix_backward(ctx, m, rho, g):
     direct = np.einsum("pab,pb->pa", c, w)
     a_direct = np.einsum("pab,pb->pa", ac, np.abs(w))
     via_j = np.einsum("pcb,pab->pc", ctx.Jb, r[:, :, None] * c)
-    a_via = np.einsum("pcb,pab->pc", np.abs(ctx.Jb), np.abs(r)[:, :, None] * ac)
+    a_via = np.einsum("pcb,pab->pc", ctx.Jb_mag, np.abs(r)[:, :, None] * ac)
     t_x = ctx.cs * (direct + via_j)
     m_x = ctx.cs * (a_direct + a_via)
     return [(_seg_sum(t_x, p), _seg_sum(m_x, p)), (_seg_sum(t_r, p), _seg_sum(m_r, p))]

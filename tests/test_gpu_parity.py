@@ -44,13 +44,101 @@ def _cases():
 
 def _workload_cases():
     out = []
-    for name, scale in (("cfg1", 1.0), ("cfg2", 0.125), ("cfg3", 0.0625), ("cfg4", 1 / 32), ("cfg5", 1 / 256)):
+    # cfg2 at its full size: 4 clouds x 16384 particles, h = 1/47, ~24 neighbours
+    for name, scale in (("cfg1", 1.0), ("cfg2", 1.0), ("cfg3", 0.0625), ("cfg4", 1 / 32), ("cfg5", 1 / 256)):
         wl = workloads.make(name, scale)
         out.append(H.workload_case(wl))
     return out
 
 
 CASES = {c.name: c for c in _cases() + _workload_cases()}
+
+CHAIN_STEPS = 32
+
+
+@functools.lru_cache(maxsize=None)
+def _chain(seed=3):
+    """cfg2's workload: 32 chained perception + update
+    steps on the GPU with the full backward through all of them, as the
+    reference's training loop chains NPA steps (train.py:225-238).  The update
+    is a seeded NPA-shaped MLP over the perception features [s, blur,
+    gradient_hybrid, density_gradient] (models/npa.py:106-137) giving a
+    bounded position step and a state increment; positions are wrapped into
+    the periodic box after every step.  Returns the inputs (x, s) of every
+    step (each in the previous step's binned order) and the gradient of a fixed loss on the final
+    particles with respect to the initial ones."""
+    import npa_amd.sphops as sp
+    wl = workloads.make("cfg2", 1.0)
+    B, N, C, D = wl.B, wl.N, wl.C, wl.dim
+    print(f"[case] cfg2 chain: {CHAIN_STEPS} steps B={B} N={N} C={C}", flush=True)
+    grid = sp.HashGrid(dim=D, boundary="periodic", mode="grid", grid_size=list(wl.grid_size), eps=wl.h,
+                       num_particles=N, batch_size=B, max_particles_per_block=wl.maxp)
+    gen = torch.Generator().manual_seed(seed)
+    width = 2 * C + C * D + D
+    w1 = (torch.randn(width, 32, generator=gen) / width ** 0.5).cuda()
+    w2 = (torch.randn(32, D + C, generator=gen) / 32 ** 0.5).cuda()
+    u_x = torch.randn(B, N, D, generator=gen).cuda()
+    u_s = torch.randn(B, N, C, generator=gen).cuda()
+    x0 = dev(grid.wrap_positions(torch.from_numpy(wl.x))).requires_grad_(True)
+    s0 = dev(wl.s).requires_grad_(True)
+    x, s = x0, s0
+    inputs = []
+    for _ in range(CHAIN_STEPS):
+        inputs.append((x.detach().cpu().numpy(), s.detach().cpu().numpy()))
+        with torch.no_grad():
+            snap = grid.instantiate(x)
+        xb, sb = sp.bin_particles(x, s, snap)
+        rho = sp.density(xb, snap)
+        bl = sp.blur(xb, rho, sb, snap)
+        gh = sp.gradient_hybrid(xb, rho, sb, snap)
+        dg = sp.density_gradient(xb, snap)
+        z = torch.cat([sb, bl, gh.flatten(-2), dg], -1)
+        y = torch.tanh(z @ w1) @ w2
+        # step_euler returns the updated particles in binned order, which the
+        # next step bins again (models/npa.py:189-204)
+        x = grid.wrap_positions(xb + (0.25 * wl.h) * torch.tanh(y[..., :D])).contiguous()
+        s = (sb + 0.1 * torch.tanh(y[..., D:])).contiguous()
+    loss = (x * u_x).sum() + (s * u_s).sum()
+    gx, gs = torch.autograd.grad(loss, (x0, s0))
+    torch.cuda.synchronize()
+    return wl, inputs, gx.cpu().numpy(), gs.cpu().numpy()
+
+
+def _chain_case(step):
+    wl, inputs, _, _ = _chain()
+    x, s = inputs[step]
+    c = H.workload_case(wl)
+    c.name = f"cfg2-chain-step{step}"
+    c.x, c.s = np.ascontiguousarray(x), np.ascontiguousarray(s)
+    return c
+
+
+def _cfg5_full_case():
+    """cfg5 at its full size (1,048,576 particles, 206 M cells, cells of up to
+    121 particles); perception is checked on a sample of queries: 2000 binned
+    slots drawn uniformly plus every particle of the 16 fullest cells."""
+    wl = workloads.make("cfg5", 1.0)
+    c = H.workload_case(wl)
+    c.name = "cfg5-full"
+    ob = H.oracle_binning(c)
+    bo = ob["bin_offsets"]
+    cells = np.flatnonzero(np.diff(bo))
+    occ = np.diff(bo)[cells]
+    full = cells[np.argsort(occ, kind="stable")[-16:]]
+    dense = np.concatenate([np.arange(bo[k], bo[k + 1]) for k in full])
+    rng = np.random.default_rng(17)
+    c.queries = np.unique(np.concatenate([rng.choice(c.B * c.N, 2000, replace=False), dense]))
+    c.extra["binning"] = ob
+    return c
+
+
+LAZY = {f"cfg2-chain-step{t}": functools.partial(_chain_case, t) for t in (0, CHAIN_STEPS - 1)}
+LAZY["cfg5-full"] = _cfg5_full_case
+
+
+@functools.lru_cache(maxsize=None)
+def case(name):
+    return CASES[name] if name in CASES else LAZY[name]()
 
 
 def dev(a, dtype=None):
@@ -62,7 +150,7 @@ def dev(a, dtype=None):
 def run(name):
     """GPU results plus the oracle's, in binned order, for one case."""
     import npa_amd.sphops as sp
-    c = CASES[name]
+    c = case(name)
     print(f"[case] {name} B={c.B} N={c.N} C={c.C} grid={c.grid_size} eps={c.eps} "
           f"{c.boundary} {c.mode}", flush=True)
     grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
@@ -137,7 +225,7 @@ def run(name):
     torch.cuda.synchronize()
 
     # ---- oracle on the same binned inputs
-    ob = H.oracle_binning(c)
+    ob = c.extra["binning"] if "binning" in c.extra else H.oracle_binning(c)
     ctx = H.oracle_context(c, res["xb"], ob["bin_offsets"])
     q = ctx.p.queries
     P = c.x.shape[-1]
@@ -160,7 +248,7 @@ def run(name):
     return c, res, ora
 
 
-NAMES = list(CASES)
+NAMES = list(CASES) + list(LAZY)
 
 
 @pytest.mark.parametrize("name", NAMES)
@@ -426,3 +514,27 @@ def test_deterministic_replay(name):
         for k in ("x", "s", "rho"):
             if res[key][k] is not None:
                 np.testing.assert_array_equal(res[key][k], res2[key][k])
+
+
+def test_cfg2_chain_is_deterministic_and_moves():
+    """The 32-step cfg2 rollout with its backward through every step, run
+    twice: bitwise identical gradients (no float atomics anywhere), finite
+    and nonzero; the particles of the last step have moved and rebinned.
+    The inputs of its first and last step are parity cases above
+    (cfg2-chain-step0, cfg2-chain-step31)."""
+    wl, inputs, gx, gs = _chain()
+    _chain.cache_clear()
+    _, inputs2, gx2, gs2 = _chain()
+    np.testing.assert_array_equal(inputs[-1][0], inputs2[-1][0])
+    np.testing.assert_array_equal(gx, gx2)
+    np.testing.assert_array_equal(gs, gs2)
+    assert np.isfinite(gx).all() and np.isfinite(gs).all()
+    assert np.abs(gx).max() > 0 and np.abs(gs).max() > 0
+    # rebinning reorders the particles: compare the clouds as sets of rows
+    # (positions of the first and last step, then states), which share
+    # almost no row once every particle has moved
+    for k in (0, 1):
+        first = {r.tobytes() for r in inputs[0][k].reshape(-1, inputs[0][k].shape[-1])}
+        last = [r.tobytes() for r in inputs[-1][k].reshape(-1, inputs[-1][k].shape[-1])]
+        assert sum(r in first for r in last) < 0.01 * len(last)
+    assert np.isfinite(inputs[-1][0]).all() and np.isfinite(inputs[-1][1]).all()

@@ -225,6 +225,126 @@ def test_backward_formulas_equal_autograd(dim, periodic):
             assert err < tol, f"{name}: {err}"
 
 
+@pytest.mark.parametrize("dim,periodic", [(2, False), (3, False), (2, True), (3, True)])
+def test_forwards_equal_bruteforce(dim, periodic):
+    """The oracle's forward sums equal the dense all-pairs forwards of
+    oracle/bruteforce.py on the same pair set, with non-uniform masses so that
+    the volume m/rho differs between the two ends of a pair.  The brute force
+    weights blur, gradient and moment_matrix by the neighbour's volume v_j
+    (``torch_sph.py:289-290, 372-373, 460-461``); its forwards are the ones
+    whose autograd equals the reference's gather-form backward
+    (test_backward_formulas_equal_autograd), so a v_j -> v_i change in the
+    oracle fails here."""
+    B, N, C, spec, ctx, xb, sb, mb, r_val, mask = _dense_pins(dim, periodic, 20 + dim)
+    L, _ = spec.box_f32()
+    h = float(np.float32(spec.eps))
+    xt = torch.tensor(xb[..., :dim].astype(np.float64))
+    P = bf.Pairs(xt, h, periodic, torch.tensor(L.astype(np.float64)), torch.tensor(r_val), torch.tensor(mask))
+    c6, cs = spec.coefficients()
+    mf = mb.reshape(-1).astype(np.float64)
+    sf = sb.reshape(-1, C).astype(np.float64)
+    mt = torch.tensor(mb.astype(np.float64))
+    st = torch.tensor(sf.reshape(B, N, C))
+    rho = sph.density(ctx, mf)[0]
+    rt = torch.tensor(rho.reshape(B, N))
+    assert np.ptp(mf / rho) > 0.3 * np.mean(mf / rho)  # volumes really differ between particles
+    cases = [
+        ("count", sph.count(ctx)[0], bf.count(P)),
+        ("density", rho, bf.density(P, mt, c6)),
+        ("blur", sph.blur(ctx, mf, rho, sf)[0], bf.blur(P, mt, rt, st, c6)),
+        ("gradient", sph.gradient(ctx, mf, rho, sf)[0], bf.gradient(P, mt, rt, st, cs)),
+        ("density_gradient", sph.density_gradient(ctx, mf)[0], bf.density_gradient(P, mt, cs)),
+        ("moment_matrix", sph.moment_matrix(ctx, mf, rho)[0], bf.moment_matrix(P, mt, rt, cs)),
+    ]
+    for name, got, ref in cases:
+        ref = ref.numpy().reshape(got.shape)
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        assert err < 1e-12, f"{name}: {err}"
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_three_particle_closed_forms_with_unequal_volumes(dim):
+    """blur, gradient and moment_matrix of three collinear particles with
+    masses 1, 2, 5 written out by hand: each neighbour term carries the
+    NEIGHBOUR's volume m_j / rho_j (poly6 W = (h^2 - d^2)^3, spiky
+    K = 3 (h - d)^2 / d * r, r = x_j - x_i)."""
+    h, d1, d2 = 0.3, 0.1, 0.17
+    P = 2 if dim == 2 else 4
+    x = np.zeros((1, 3, P), np.float32)
+    x[0, 1, 0], x[0, 2, 0] = d1, -d2
+    gs = (8,) * dim
+    spec, inst, xb, ctx = _setup(x, gs, h, False)
+    c6, cs = spec.coefficients()
+    perm = inst["permutation"][0]           # input index -> binned slot
+    m_in = np.array([1.0, 2.0, 5.0])
+    s_in = np.array([[1.0, -2.0], [0.5, 3.0], [-1.5, 0.25]])
+    mb = np.empty(3)
+    mb[perm] = m_in
+    sb = np.empty((3, 2))
+    sb[perm] = s_in
+    hh = float(np.float32(h))
+    X = np.array([0.0, float(np.float32(d1)), float(np.float32(-d2))])
+    rho_in = np.zeros(3)
+    for i in range(3):
+        for j in range(3):
+            dd = abs(X[j] - X[i])
+            if dd < hh:
+                rho_in[i] += c6 * m_in[j] * (hh * hh - dd * dd) ** 3
+    rho_b = np.empty(3)
+    rho_b[perm] = rho_in
+    v = m_in / rho_in
+    blur_e = np.zeros((3, 2))
+    grad_e = np.zeros((3, 2, dim))
+    mom_e = np.zeros((3, dim, dim))
+    for i in range(3):
+        for j in range(3):
+            r = X[j] - X[i]
+            dd = abs(r)
+            if dd >= hh:
+                continue
+            blur_e[i] += c6 * v[j] * (hh * hh - dd * dd) ** 3 * s_in[j]
+            if dd > 0:
+                K = 3.0 * (hh - dd) ** 2 / dd * r
+                grad_e[i, :, 0] += cs * v[j] * (s_in[j] - s_in[i]) * K
+                mom_e[i, 0, 0] += cs * v[j] * r * K
+    rho, _ = sph.density(ctx, mb)
+    np.testing.assert_allclose(rho[perm], rho_in, rtol=1e-6)
+    np.testing.assert_allclose(sph.blur(ctx, mb, rho_b, sb)[0][perm], blur_e, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(sph.gradient(ctx, mb, rho_b, sb)[0][perm], grad_e, rtol=1e-6,
+                               atol=1e-9 * np.abs(grad_e).max())
+    np.testing.assert_allclose(sph.moment_matrix(ctx, mb, rho_b)[0][perm], mom_e, rtol=1e-6,
+                               atol=1e-9 * np.abs(mom_e).max())
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_blur_of_constant_field_on_lattice(dim):
+    """Shepard check: blur of a constant field, with rho from the density
+    operator, returns the constant.  On a lattice every particle whose
+    2h-neighbourhood is complete sees the same rho as its neighbours, so
+    c6 sum_j (m / rho_j) W_ij = rho_i / rho = 1 up to rounding."""
+    h = 0.5
+    a = h / (10 if dim == 2 else 5)
+    hw = int(math.ceil(2.5 * h / a)) + 1
+    pts = _lattice(dim, a, hw)
+    x = np.zeros((1, pts.shape[0], 2 if dim == 2 else 4), np.float32)
+    x[0, :, :dim] = pts
+    gs = (16,) * dim
+    spec = nb.GridSpec(gs, h, False, "grid", 16)
+    inst = binning.instantiate(x, gs, h, False, "grid", 16)
+    xb, _, _ = binning.bin_particles(x, np.zeros((1, pts.shape[0], 1), np.float32),
+                                     np.ones((1, pts.shape[0]), np.float32), inst["permutation"])
+    box = np.max(np.abs(xb[0, :, :dim]), axis=1)
+    near = np.flatnonzero(box < 1.5 * h + 1e-6)   # every neighbour of an inner point
+    inner = np.flatnonzero(box < 0.5 * h + 1e-6)
+    m = np.full(pts.shape[0], a ** dim)
+    rho = np.full(pts.shape[0], np.nan)            # outside `near` never read
+    rho[near] = sph.density(sph.Context(nb.candidate_pairs(xb, inst["bin_offsets"], spec, near), spec), m)[0]
+    ctx = sph.Context(nb.candidate_pairs(xb, inst["bin_offsets"], spec, inner), spec)
+    out, _ = sph.blur(ctx, m, rho, np.full((pts.shape[0], 2), 3.25))
+    assert inner.size > 10 and np.isfinite(out).all()
+    np.testing.assert_allclose(out, 3.25, rtol=1e-6)  # fp32 lattice positions
+
+
 def test_gradcheck_small():
     """torch.autograd.gradcheck of the dense float64 forward (clamped 2D)."""
     B, N, C, spec, ctx, xb, sb, mb, r_val, mask = _dense_pins(2, False, 3)
