@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 12
+#define SPHOPS_ABI_VERSION 13
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -66,6 +66,22 @@ int sphops_grid_coefficients(const sphops_grid* grid, float* poly6, float* spiky
  * per snapshot instead of inside the grid. */
 int sphops_initialize(sphops_grid* grid, const float* positions, int32_t* permutation, int32_t* bin_offsets,
                       int32_t* block_info, int32_t* total_blocks, void* stream);
+
+/* sphops_initialize without a grid object and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * (or host) memory while they run -- code under HIP-graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  The grid is described by
+ * the arguments of sphops_grid_create; the outputs are sphops_initialize's,
+ * bit for bit.  The sort, scan and block-table scratch comes from one static
+ * device array per GPU (about 24 MiB, held until the process ends), so
+ * batch_size * particle_count must be at most 2^20 and batch_size * cell count
+ * at most 2^28; larger grids fail with an error and no work queued.  Calls
+ * that overlap on one GPU share the array and race: serialise them (one
+ * stream, or events). */
+int sphops_initialize_noalloc(int dim, int boundary, int mode, const int32_t* grid_size, float eps,
+                              uint32_t particle_count, uint32_t batch_size, uint32_t max_particles_per_block,
+                              const float* positions, int32_t* permutation, int32_t* bin_offsets,
+                              int32_t* block_info, int32_t* total_blocks, void* stream);
 
 /* HashGrid::bin_particles (sph_cuda.cu:1994-2024): out[b, perm[b,i]] = in[b,i]. */
 int sphops_bin_particles(const sphops_grid* grid, const float* in_pos, const float* in_state,

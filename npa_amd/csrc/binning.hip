@@ -153,15 +153,7 @@ constexpr uint64_t kFlatScanTiles = 8192;
 
 }  // namespace
 
-uint64_t scan_tmp_elems(uint64_t n) {
-  // partial sums for every recursion level, each padded to a tile
-  uint64_t total = 0;
-  while (n > (uint64_t)kTile) {
-    n = (n + kTile - 1) / kTile;
-    total += n + kTile;
-  }
-  return total + 1;
-}
+static_assert(kScanTile == (uint64_t)kTile, "scan_tmp_elems assumes the scan tile");
 
 namespace {
 

@@ -1,4 +1,5 @@
 // extern "C" entry points of libsphops_hip.so (declared in include/sphops_hip.h).
+#include <atomic>
 #include <cmath>
 #include <string>
 
@@ -30,6 +31,11 @@ int guarded(F&& f) {
   return -1;
 }
 
+// The message is turned into a std::string only on failure, so a passing
+// check allocates nothing.
+void require(bool ok, const char* msg) {
+  if (!ok) throw Error(msg);
+}
 void require(bool ok, const std::string& msg) {
   if (!ok) throw Error(msg);
 }
@@ -45,6 +51,85 @@ uint32_t spread_host(uint32_t v, int dim) {
   uint32_t out = 0;
   for (int b = 0; b < 10; ++b) out |= ((v >> b) & 1u) << (b * dim);
   return out;
+}
+
+// Validates the grid arguments and fills the parameters and scratch sizes of
+// `g` (HashGrid::_init, sphops/sph_cuda.cu:1836-1878; Python checks of
+// sphops/sph.py:48-78).  Allocates nothing.
+void setup_grid(Grid& g, int dim, int boundary, int mode, const int32_t* grid_size, float eps,
+                uint32_t particle_count, uint32_t batch_size, uint32_t max_particles_per_block) {
+  require(dim == 2 || dim == 3, "dim must be 2 or 3");
+  require(boundary == SPHOPS_CLAMPED || boundary == SPHOPS_PERIODIC, "boundary must be clamped or periodic");
+  require(mode == SPHOPS_MODE_GRID || mode == SPHOPS_MODE_PARTICLE, "mode must be grid or particle");
+  require(grid_size != nullptr, "grid_size must not be NULL");
+  require(std::isfinite(eps) && eps > 0.0f, "eps must be a positive finite number");
+  require(max_particles_per_block >= 1, "max_particles_per_block must be >= 1");
+  uint64_t G = 1;
+  for (int d = 0; d < dim; ++d) {
+    require(grid_size[d] >= 1, "grid sizes must be >= 1");
+    if (boundary == SPHOPS_PERIODIC)
+      require(grid_size[d] >= 3, "periodic grids need at least 3 cells per axis (fewer double-count neighbours)");
+    G *= (uint64_t)grid_size[d];
+  }
+  const uint64_t BG = G * batch_size, BN = (uint64_t)particle_count * batch_size;
+  require(BG + 1 < (1ull << 32), "batch_size * cell_count must be below 2^32 - 1");
+  require(BN < (1ull << 31), "batch_size * particle_count must be below 2^31");
+  if (mode == SPHOPS_MODE_PARTICLE) {
+    uint32_t hmax = 0;
+    for (int d = 0; d < dim; ++d) {
+      const int gsz = grid_size[d];
+      require((gsz & (gsz - 1)) == 0, "particle mode needs power-of-two grid sizes");
+      require(gsz <= 1024, "particle mode supports at most 1024 cells per axis");
+      hmax |= spread_host((uint32_t)gsz - 1, dim) << d;
+    }
+    require(hmax < G, "particle mode: the Morton hash of this grid shape exceeds the cell count "
+                      "(use equal sizes, or sizes non-increasing along x, y, z)");
+  }
+  g.dim = dim;
+  g.periodic = boundary == SPHOPS_PERIODIC;
+  g.particle_mode = mode == SPHOPS_MODE_PARTICLE;
+  auto& p = g.p;
+  for (int d = 0; d < 3; ++d) {
+    p.gs[d] = d < dim ? grid_size[d] : 1;
+    p.half_gs[d] = p.gs[d] / 2;
+  }
+  p.eps = eps;
+  p.inv_eps = 1.0f / eps;
+  p.eps2 = eps * eps;
+  for (int d = 0; d < 3; ++d) {
+    p.L[d] = static_cast<float>(p.gs[d]) * eps;
+    p.half_L[d] = 0.5f * p.L[d];
+  }
+  // coefficients exactly as HashGrid::_init derives them (fp32 powers of
+  // 1/eps, double constant, rounded to fp32)
+  const float ie = p.inv_eps, ie2 = ie * ie, ie4 = ie2 * ie2;
+  if (dim == 2) {
+    const float ie5 = ie4 * ie, ie8 = ie4 * ie4;
+    p.c6 = (float)(4.0 / M_PI * (double)ie8);
+    p.cs = (float)(10.0 / M_PI * (double)ie5);
+  } else {
+    const float ie6 = ie4 * ie2, ie9 = ie4 * ie4 * ie;
+    p.c6 = (float)((315.0 / (64.0 * M_PI)) * (double)ie9);
+    p.cs = (float)((15.0 / M_PI) * (double)ie6);
+  }
+  p.N = particle_count;
+  p.B = batch_size;
+  p.G = (uint32_t)G;
+  p.maxp = max_particles_per_block;
+  p.morton = g.particle_mode ? 1 : 0;
+  if (!g.particle_mode) {
+    const uint64_t per = std::min<uint64_t>(particle_count,
+                                            G + (particle_count + max_particles_per_block - 1) /
+                                                    max_particles_per_block);
+    g.max_blocks = per * batch_size;
+  } else {
+    g.max_blocks = 1;
+  }
+  g.n_keys = BN;
+  g.n_cells = BG;
+  g.n_tiles = (BN + 4095) / 4096;
+  g.n_chunks = (BG + 1 + 1023) / 1024;
+  g.n_ranges = g.particle_mode ? (dim == 2 ? 9 : 27) : (dim == 2 ? 3 : 9) * (g.periodic ? 2 : 1);
 }
 
 void free_grid(Grid* g) {
@@ -174,88 +259,19 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
   return guarded([&] {
     require(out != nullptr, "out must not be NULL");
     *out = nullptr;
-    require(dim == 2 || dim == 3, "dim must be 2 or 3");
-    require(boundary == SPHOPS_CLAMPED || boundary == SPHOPS_PERIODIC, "boundary must be clamped or periodic");
-    require(mode == SPHOPS_MODE_GRID || mode == SPHOPS_MODE_PARTICLE, "mode must be grid or particle");
-    require(grid_size != nullptr, "grid_size must not be NULL");
-    require(std::isfinite(eps) && eps > 0.0f, "eps must be a positive finite number");
-    require(max_particles_per_block >= 1, "max_particles_per_block must be >= 1");
-    uint64_t G = 1;
-    for (int d = 0; d < dim; ++d) {
-      require(grid_size[d] >= 1, "grid sizes must be >= 1");
-      if (boundary == SPHOPS_PERIODIC)
-        require(grid_size[d] >= 3, "periodic grids need at least 3 cells per axis (fewer double-count neighbours)");
-      G *= (uint64_t)grid_size[d];
-    }
-    const uint64_t BG = G * batch_size, BN = (uint64_t)particle_count * batch_size;
-    require(BG + 1 < (1ull << 32), "batch_size * cell_count must be below 2^32 - 1");
-    require(BN < (1ull << 31), "batch_size * particle_count must be below 2^31");
-    if (mode == SPHOPS_MODE_PARTICLE) {
-      uint32_t hmax = 0;
-      for (int d = 0; d < dim; ++d) {
-        const int gsz = grid_size[d];
-        require((gsz & (gsz - 1)) == 0, "particle mode needs power-of-two grid sizes");
-        require(gsz <= 1024, "particle mode supports at most 1024 cells per axis");
-        hmax |= spread_host((uint32_t)gsz - 1, dim) << d;
-      }
-      require(hmax < G, "particle mode: the Morton hash of this grid shape exceeds the cell count "
-                        "(use equal sizes, or sizes non-increasing along x, y, z)");
-    }
-    auto* g = new sphops_grid();
+    sphops_grid shape;
+    sphops::setup_grid(shape, dim, boundary, mode, grid_size, eps, particle_count, batch_size,
+                       max_particles_per_block);
+    auto* g = new sphops_grid(shape);
+    const uint64_t BN = g->n_keys;
     try {
       SPHOPS_HIP(hipGetDevice(&g->device));
-      g->dim = dim;
-      g->periodic = boundary == SPHOPS_PERIODIC;
-      g->particle_mode = mode == SPHOPS_MODE_PARTICLE;
-      auto& p = g->p;
-      for (int d = 0; d < 3; ++d) {
-        p.gs[d] = d < dim ? grid_size[d] : 1;
-        p.half_gs[d] = p.gs[d] / 2;
-      }
-      p.eps = eps;
-      p.inv_eps = 1.0f / eps;
-      p.eps2 = eps * eps;
-      for (int d = 0; d < 3; ++d) {
-        p.L[d] = static_cast<float>(p.gs[d]) * eps;
-        p.half_L[d] = 0.5f * p.L[d];
-      }
-      // coefficients exactly as HashGrid::_init derives them (fp32 powers of
-      // 1/eps, double constant, rounded to fp32)
-      const float ie = p.inv_eps, ie2 = ie * ie, ie4 = ie2 * ie2;
-      if (dim == 2) {
-        const float ie5 = ie4 * ie, ie8 = ie4 * ie4;
-        p.c6 = (float)(4.0 / M_PI * (double)ie8);
-        p.cs = (float)(10.0 / M_PI * (double)ie5);
-      } else {
-        const float ie6 = ie4 * ie2, ie9 = ie4 * ie4 * ie;
-        p.c6 = (float)((315.0 / (64.0 * M_PI)) * (double)ie9);
-        p.cs = (float)((15.0 / M_PI) * (double)ie6);
-      }
-      p.N = particle_count;
-      p.B = batch_size;
-      p.G = (uint32_t)G;
-      p.maxp = max_particles_per_block;
-      p.morton = g->particle_mode ? 1 : 0;
-      if (!g->particle_mode) {
-        const uint64_t per = std::min<uint64_t>(particle_count,
-                                                G + (particle_count + max_particles_per_block - 1) /
-                                                        max_particles_per_block);
-        g->max_blocks = per * batch_size;
-      } else {
-        g->max_blocks = 1;
-      }
-      g->n_keys = BN;
-      g->n_cells = BG;
-      g->n_tiles = (BN + 4095) / 4096;
-      g->n_chunks = (BG + 1 + 1023) / 1024;
       for (int i = 0; i < 2; ++i) {
         g->keys[i] = dalloc<uint32_t>(BN);
         g->vals[i] = dalloc<uint32_t>(BN);
       }
       g->hist = dalloc<uint32_t>((uint64_t)sphops::kRadixBins * g->n_tiles);
-      const uint64_t scan_n =
-          std::max<uint64_t>(std::max<uint64_t>((uint64_t)sphops::kRadixBins * g->n_tiles, BN + 1), g->n_chunks + 1);
-      g->scan_tmp_len = sphops::scan_tmp_elems(scan_n);
+      g->scan_tmp_len = sphops::scan_tmp_elems(sphops::scan_words(*g));
       g->scan_tmp = dalloc<uint32_t>(g->scan_tmp_len);
       g->chunk_first = dalloc<uint32_t>(g->n_chunks);
       g->chunk_end = dalloc<uint32_t>(g->n_chunks);
@@ -266,7 +282,6 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->unit_len = dalloc<int32_t>(BN);
       g->units = dalloc<uint2>(BN);
       g->unit_total = dalloc<int32_t>(1);
-      g->n_ranges = g->particle_mode ? (dim == 2 ? 9 : 27) : (dim == 2 ? 3 : 9) * (g->periodic ? 2 : 1);
       g->ranges = dalloc<uint2>(BN * (uint64_t)g->n_ranges);
     } catch (...) {
       sphops::free_grid(g);
@@ -288,16 +303,21 @@ int sphops_grid_coefficients(const sphops_grid* grid, float* poly6, float* spiky
   });
 }
 
+static void check_initialize_args(const Grid& g, const float* positions, const int32_t* permutation,
+                                  const int32_t* bin_offsets, const int32_t* block_info) {
+  require(bin_offsets != nullptr, "bin_offsets must not be NULL");
+  require(g.n_keys == 0 || (positions && permutation), "positions and permutation must not be NULL");
+  require(g.particle_mode || block_info != nullptr, "block_info must not be NULL in grid mode");
+  require(sphops::pk::aligned16(bin_offsets), "bin_offsets must be 16-byte aligned");
+  require(g.particle_mode || sphops::pk::aligned16(block_info), "block_info must be 16-byte aligned");
+  require(g.dim == 2 || sphops::pk::aligned16(positions), "3D positions must be 16-byte aligned");
+}
+
 int sphops_initialize(sphops_grid* grid, const float* positions, int32_t* permutation, int32_t* bin_offsets,
                       int32_t* block_info, int32_t* total_blocks, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(bin_offsets != nullptr, "bin_offsets must not be NULL");
-    require(grid->n_keys == 0 || (positions && permutation), "positions and permutation must not be NULL");
-    require(grid->particle_mode || block_info != nullptr, "block_info must not be NULL in grid mode");
-    require(sphops::pk::aligned16(bin_offsets), "bin_offsets must be 16-byte aligned");
-    require(grid->particle_mode || sphops::pk::aligned16(block_info), "block_info must be 16-byte aligned");
-    require(grid->dim == 2 || sphops::pk::aligned16(positions), "3D positions must be 16-byte aligned");
+    check_initialize_args(*grid, positions, permutation, bin_offsets, block_info);
     sphops::run_instantiate(*grid, positions, permutation, bin_offsets, block_info, total_blocks,
                             sphops::as_stream(stream));
   });
@@ -846,3 +866,121 @@ int sphops_relu_linear_input_grad(const float* dy, const float* w, const float* 
 }
 
 }  // extern "C"
+
+// ------------------------------------------------ binning without allocation
+//
+// sphops_initialize_noalloc runs sphops_initialize's kernels with their
+// scratch (sort keys and values, radix histograms, scan partials, chunk
+// tables, block flags) carved from `scratch`, a file-scope device array, so a
+// call allocates nothing, on the device or the host.  Each GPU the library
+// runs on holds its own copy of the array until the process ends.  Host code
+// never uses the array's name as an address: the device address comes from
+// hipGetSymbolAddress, once per device, on the first call with that device
+// current.  Every call on one GPU shares that GPU's array; each call writes
+// (or clears) every word it later reads, so the previous call's contents do
+// not matter, but calls that overlap on one GPU race.
+
+namespace {
+
+constexpr uint64_t kNoAllocMaxKeys = 1ull << 20;   // B * N
+constexpr uint64_t kNoAllocMaxCells = 1ull << 28;  // B * G
+constexpr int kNoAllocMaxDevices = 64;
+
+// Word offsets of the scratch pieces for a grid of n_keys particles, n_tiles
+// radix tiles and n_chunks cell chunks; each piece starts on 256 bytes.
+struct NoAllocLayout {
+  uint64_t keys[2], vals[2], hist, flags, chunk_first, chunk_end, chunk_lo, scan, scan_len, words;
+};
+
+constexpr uint64_t pad_words(uint64_t w) { return (w + 63) & ~uint64_t(63); }
+
+constexpr NoAllocLayout noalloc_layout(uint64_t n_keys, uint64_t n_tiles, uint64_t n_chunks) {
+  NoAllocLayout l{};
+  uint64_t at = 0;
+  for (int i = 0; i < 2; ++i) {
+    l.keys[i] = at;
+    at += pad_words(n_keys);
+    l.vals[i] = at;
+    at += pad_words(n_keys);
+  }
+  l.hist = at;
+  at += pad_words((uint64_t)sphops::kRadixBins * n_tiles);
+  l.flags = at;
+  at += pad_words(n_keys + 1);
+  l.chunk_first = at;
+  at += pad_words(n_chunks);
+  l.chunk_end = at;
+  at += pad_words(n_chunks);
+  l.chunk_lo = at;
+  at += pad_words(n_chunks + 1);
+  l.scan = at;
+  l.scan_len = sphops::scan_tmp_elems(sphops::scan_words(n_keys, n_tiles, n_chunks));
+  at += pad_words(l.scan_len);
+  l.words = at;
+  return l;
+}
+
+// Every piece grows with its size, so the largest grid the entry point
+// accepts bounds every layout: about 24 MiB.
+constexpr uint64_t kNoAllocWords =
+    noalloc_layout(kNoAllocMaxKeys, (kNoAllocMaxKeys + 4095) / 4096, (kNoAllocMaxCells + 1 + 1023) / 1024).words;
+
+std::atomic<uint32_t*> g_scratch_addr[kNoAllocMaxDevices];
+
+}  // namespace
+
+static __device__ __align__(256) uint32_t scratch[kNoAllocWords];
+
+namespace {
+
+// Device address of `scratch` on the current device (looked up once per device).
+uint32_t* scratch_on_current_device(int* device) {
+  int dev = 0;
+  SPHOPS_HIP(hipGetDevice(&dev));
+  require(dev >= 0 && dev < kNoAllocMaxDevices, "sphops_initialize_noalloc: device ordinal above 63");
+  uint32_t* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    void* q = nullptr;
+    SPHOPS_HIP(hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)));
+    p = static_cast<uint32_t*>(q);
+    g_scratch_addr[dev].store(p, std::memory_order_release);
+  }
+  *device = dev;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sphops_initialize_noalloc(int dim, int boundary, int mode, const int32_t* grid_size, float eps,
+                              uint32_t particle_count, uint32_t batch_size, uint32_t max_particles_per_block,
+                              const float* positions, int32_t* permutation, int32_t* bin_offsets,
+                              int32_t* block_info, int32_t* total_blocks, void* stream) {
+  return guarded([&] {
+    Grid g;
+    sphops::setup_grid(g, dim, boundary, mode, grid_size, eps, particle_count, batch_size, max_particles_per_block);
+    require(g.n_keys <= kNoAllocMaxKeys, "sphops_initialize_noalloc: batch_size * particle_count above 2^20");
+    require(g.n_cells <= kNoAllocMaxCells, "sphops_initialize_noalloc: batch_size * cell_count above 2^28");
+    check_initialize_args(g, positions, permutation, bin_offsets, block_info);
+    const NoAllocLayout l = noalloc_layout(g.n_keys, g.n_tiles, g.n_chunks);
+    require(l.words <= kNoAllocWords, "sphops_initialize_noalloc: scratch layout exceeds the static array");
+    uint32_t* s = scratch_on_current_device(&g.device);
+    for (int i = 0; i < 2; ++i) {
+      g.keys[i] = s + l.keys[i];
+      g.vals[i] = s + l.vals[i];
+    }
+    g.hist = s + l.hist;
+    g.flags = s + l.flags;
+    g.chunk_first = s + l.chunk_first;
+    g.chunk_end = s + l.chunk_end;
+    g.chunk_lo = s + l.chunk_lo;
+    g.scan_tmp = s + l.scan;
+    g.scan_tmp_len = l.scan_len;
+    sphops::run_instantiate(g, positions, permutation, bin_offsets, block_info, total_blocks,
+                            sphops::as_stream(stream));
+  });
+}
+
+}  // extern "C"
+

@@ -68,7 +68,25 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bin_offs
 void run_bin_particles(const Grid& g, const float* in_pos, const float* in_state, const float* in_mass,
                        const int32_t* perm, float* out_pos, float* out_state, float* out_mass,
                        uint32_t C, bool forward, hipStream_t st);
-uint64_t scan_tmp_elems(uint64_t n);
+// Words of partial sums a device scan of n words needs (every recursion
+// level padded to a tile of 4096).
+constexpr uint64_t kScanTile = 4096;
+constexpr uint64_t scan_tmp_elems(uint64_t n) {
+  uint64_t total = 0;
+  while (n > kScanTile) {
+    n = (n + kScanTile - 1) / kScanTile;
+    total += n + kScanTile;
+  }
+  return total + 1;
+}
+
+// Words of the longest device scan run on a grid's scratch: the radix
+// histograms, the block flags (B*N + 1) and the chunk starts.
+constexpr uint64_t scan_words(uint64_t n_keys, uint64_t n_tiles, uint64_t n_chunks) {
+  const uint64_t a = 1024ull * n_tiles, b = n_keys + 1, c = n_chunks + 1;
+  return a > b ? (a > c ? a : c) : (b > c ? b : c);
+}
+inline uint64_t scan_words(const Grid& g) { return scan_words(g.n_keys, g.n_tiles, g.n_chunks); }
 // in-place exclusive scan of n <= B*N+1 words with the grid's scratch
 void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* total, hipStream_t st);
 
