@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--variant", default="full", choices=["full", "npa"])
     ap.add_argument("--mode", default="grid", choices=["grid", "particle"],
                     help="the reference's HashGrid mode (particle: Morton order, cubic power-of-two grid)")
+    ap.add_argument("--tiles", action="store_true",
+                    help="use the opt-in cell-tiled pass-B backward (sphops_neighbor_tiles)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--no-traffic", action="store_true",
@@ -155,6 +157,7 @@ def main():
                        grid_size=list(wl.grid_size), eps=wl.h, num_particles=N, batch_size=B,
                        max_particles_per_block=wl.maxp)
     full = args.variant == "full"
+    grid.hashgrid.tiles_enabled = args.tiles
 
     def step(full=full):
         xr = x.detach().requires_grad_(full)
@@ -411,6 +414,7 @@ def pmc_child(args):
     grid = sp.HashGrid(dim=D, boundary="periodic" if wl.periodic else "clamped", mode=wl.mode,
                        grid_size=list(wl.grid_size), eps=wl.h, num_particles=N, batch_size=B,
                        max_particles_per_block=wl.maxp)
+    grid.hashgrid.tiles_enabled = args.tiles
     kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, args.variant == "full", 3, only=args.pmc_child)
     torch.cuda.synchronize()
     print(f"[pmc-child] {args.pmc_child} done", flush=True)
@@ -431,7 +435,7 @@ def _pmc_run(counter, kernel, frag, args):
     names = counter.split()
     cmd = [prof, "--pmc", *names, "--output-format", "csv", "-d", out, "-o", "run", "--",
            sys.executable, os.path.abspath(__file__), "--pmc-child", kernel, "--config", args.config,
-           "--variant", args.variant, "--mode", args.mode]
+           "--variant", args.variant, "--mode", args.mode] + (["--tiles"] if args.tiles else [])
     env = dict(os.environ, TMPDIR="/tmp")
     r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=240)
     if r.returncode != 0 or b"[pmc-child]" not in r.stdout:

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 13
+#define SPHOPS_ABI_VERSION 14
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -203,6 +203,17 @@ typedef struct sphops_args {
    * count back: a step can be captured in a HIP graph. */
   const int32_t* nbr_wave_count_device;
   const int32_t* nbr_wave_count_split_device;
+  /* Optional cell tiles from sphops_neighbor_tiles, used by the
+   * BLUR_GRADIENT_HYBRID backward at C = 16 (with the split schedule above):
+   * the units ({first particle, particles} pairs) and their device count,
+   * and the split schedule of the particles outside the units (order, wave
+   * descriptors, a bound of the wave count for the launch, the device count). */
+  const uint32_t* tile_units;
+  const int32_t* tile_unit_count;
+  const int32_t* nbr_order_sparse;
+  const uint32_t* nbr_waves_sparse;
+  int32_t nbr_wave_count_sparse;
+  const int32_t* nbr_wave_count_sparse_device;
 } sphops_args;
 
 /* Forward operator `op` (SPHOPS_OP_*) on binned particles. */
@@ -254,6 +265,24 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,
                              uint32_t* nbr_waves, int32_t* wave_count, uint32_t* nbr_waves_split,
                              int32_t* wave_count_split, void* stream);
+
+/* Cell tiles of a snapshot for the pass-B backward (no reference
+ * counterpart).  Cells holding at least 8 binned particles are cut into units of up to 32
+ * consecutive particles: tile_units receives {first particle, particles} per
+ * unit (capacity sphops_neighbor_tile_capacity pairs), tile_unit_count (one
+ * device int32) their number.  The backward then stages each unit's stencil
+ * rows in LDS once instead of loading a neighbour's rows once per pair.  The
+ * other particles get the split schedule of sphops_neighbor_schedule, over
+ * their own order: nbr_order_sparse (B*N), nbr_waves_sparse (capacity
+ * sphops_neighbor_wave_capacity), wave_count_sparse (device int32).  Needs
+ * the snapshot's x_bin, bin_offsets and list lengths (sphops_neighbor_fill). */
+int sphops_neighbor_tiles(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
+                          const int32_t* nbr_count, uint32_t* tile_units, int32_t* tile_unit_count,
+                          int32_t* nbr_order_sparse, uint32_t* nbr_waves_sparse, int32_t* wave_count_sparse,
+                          void* stream);
+
+/* Capacity (unit descriptors) tile_units must have for this grid. */
+int64_t sphops_neighbor_tile_capacity(const sphops_grid* grid);
 
 /* Number of wave descriptors nbr_waves must hold for this grid (B*N + 8 per tile of 4096). */
 int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid);

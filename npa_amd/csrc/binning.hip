@@ -635,6 +635,11 @@ void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, co
 
 uint64_t neighbour_wave_capacity(const Grid& g) { return g.n_keys + (uint64_t)kNumClasses * g.n_tiles; }
 
+void run_split_schedule(const Grid& g, const int32_t* len, int32_t* order, uint2* waves, int32_t* wave_total,
+                        hipStream_t st) {
+  tiled_schedule<false>(g, len, kListClasses, kSplitGroups, order, waves, wave_total, st);
+}
+
 void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
                             uint2* waves2, int32_t* wave_total2, hipStream_t st) {
   tiled_schedule<false>(g, ncnt, kListClasses, kListGroups, order, waves, wave_total, st, &kSplitGroups, waves2,

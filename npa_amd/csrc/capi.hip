@@ -557,6 +557,12 @@ static OpPtrs from_args(const sphops_args* a) {
   p.out3 = a->out2;
   p.nwaves_dev = a->nbr_wave_count_device;
   p.nwaves2_dev = a->nbr_wave_count_split_device;
+  p.tile_units = reinterpret_cast<const uint2*>(a->tile_units);
+  p.tile_count = a->tile_unit_count;
+  p.order_sparse = a->nbr_order_sparse;
+  p.waves_sparse = reinterpret_cast<const uint2*>(a->nbr_waves_sparse);
+  p.nwaves_sparse = (uint32_t)std::max(a->nbr_wave_count_sparse, 0);
+  p.nwaves_sparse_dev = a->nbr_wave_count_sparse_device;
   return p;
 }
 
@@ -571,6 +577,11 @@ static void check_list(const sphops_args* a) {
   require(a->nbr_wave_count_device == nullptr || a->nbr_waves != nullptr, "nbr_wave_count_device needs nbr_waves");
   require(a->nbr_wave_count_split_device == nullptr || a->nbr_waves_split != nullptr,
           "nbr_wave_count_split_device needs nbr_waves_split");
+  const bool tiles = a->tile_units != nullptr;
+  require(!tiles || (a->tile_unit_count != nullptr && a->nbr_order_sparse != nullptr &&
+                     a->nbr_waves_sparse != nullptr && a->nbr_waves_split != nullptr),
+          "tile_units needs tile_unit_count, nbr_order_sparse, nbr_waves_sparse and the split schedule");
+  require(a->nbr_wave_count_sparse >= 0, "negative wave count");
 }
 
 int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream) {
@@ -685,6 +696,42 @@ int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, 
     sphops::run_neighbour_schedule(*grid, nbr_count, nbr_order, reinterpret_cast<uint2*>(nbr_waves), wave_count,
                                    reinterpret_cast<uint2*>(nbr_waves_split), wave_count_split, st);
   });
+}
+
+int sphops_neighbor_tiles(const sphops_grid* grid, const float* x, const int32_t* bo, const int32_t* nbr_count,
+                          uint32_t* tile_units, int32_t* tile_unit_count, int32_t* nbr_order_sparse,
+                          uint32_t* nbr_waves_sparse, int32_t* wave_count_sparse, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(bo != nullptr && tile_unit_count != nullptr && wave_count_sparse != nullptr, "null buffer");
+    const hipStream_t st = sphops::as_stream(stream);
+    if (grid->n_keys == 0) {
+      sphops::fill_u32(reinterpret_cast<uint32_t*>(tile_unit_count), 1, 0u, st);
+      sphops::fill_u32(reinterpret_cast<uint32_t*>(wave_count_sparse), 1, 0u, st);
+      return;
+    }
+    require(x != nullptr && nbr_count != nullptr && tile_units != nullptr && nbr_order_sparse != nullptr &&
+                nbr_waves_sparse != nullptr,
+            "null buffer");
+    require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
+    OpPtrs a;
+    a.x = x;
+    a.ncnt = nbr_count;
+    a.tile_units = reinterpret_cast<const uint2*>(tile_units);
+    a.tile_count = tile_unit_count;
+    a.order_sparse = nbr_order_sparse;
+    a.waves_sparse = reinterpret_cast<const uint2*>(nbr_waves_sparse);
+    a.nwaves_sparse_dev = wave_count_sparse;
+    sphops::forward(*grid, Op::NeighbourTiles, bo, a, st);
+  });
+}
+
+int64_t sphops_neighbor_tile_capacity(const sphops_grid* grid) {
+  if (grid == nullptr) {
+    sphops::g_last_error = "grid must not be NULL";
+    return -1;
+  }
+  return (int64_t)(grid->n_keys / sphops::pk::kTileMinOcc + 1);
 }
 
 int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid) {

@@ -1566,6 +1566,14 @@ __global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const floa
   }
 }
 
+}  // namespace pk
+}  // namespace sphops
+
+#include "perception_tiled.hpp"
+
+namespace sphops {
+namespace pk {
+
 inline dim3 grid_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) / kThreads)); }
 
 template <int D, class OP>
@@ -1668,11 +1676,11 @@ void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   SPHOPS_LAUNCHED();
 }
 
+// The lane-split pass-B backward over the schedule a.waves2 (positions and
+// volumes already packed into a.xw).
 template <int D, bool P, bool FULL>
-void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
-  if (g.n_keys == 0) return;
+void launch_blur_hybrid_bwd_quad_packed(const Grid& g, const OpPtrs& a, hipStream_t st) {
   const uint32_t wgs = launch_groups(a.nwaves2);
-  pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
   const bool off32 = row_offsets_fit_32(g, a.C);
   if (a.C == 16) {
@@ -1683,6 +1691,49 @@ void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
     else hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   }
   SPHOPS_LAUNCHED();
+}
+
+template <int D, bool P, bool FULL>
+void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
+  if (g.n_keys == 0) return;
+  pack_for<D, VolumeWeights>(g, a, st);
+  launch_blur_hybrid_bwd_quad_packed<D, P, FULL>(g, a, st);
+}
+
+// Pass-B backward with cell tiles: the tiled kernel serves the particles of
+// the units, the lane-split list kernel the others (their own schedule).
+template <int D, bool P, bool FULL>
+void launch_blur_hybrid_bwd_tiles(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
+  if (g.n_keys == 0) return;
+  pack_for<D, VolumeWeights>(g, a, st);
+  hipLaunchKernelGGL((k_blur_hybrid_bwd_tiled<D, P, FULL>), dim3(kTileWorkgroups), dim3(kTileThreads), 0, st, g.p,
+                     a, bo);
+  SPHOPS_LAUNCHED();
+  OpPtrs b = a;
+  b.order = a.order_sparse;
+  b.waves2 = a.waves_sparse;
+  b.nwaves2 = a.nwaves_sparse;
+  b.nwaves2_dev = a.nwaves_sparse_dev;
+  launch_blur_hybrid_bwd_quad_packed<D, P, FULL>(g, b, st);
+}
+
+// Cell tiles of a snapshot (see perception_tiled.hpp): units of up to kTileP
+// particles of cells with at least kTileMinOcc, their count on the device,
+// and the lane-split schedule of the particles outside them.
+template <int D, bool P>
+void neighbour_tiles(const Grid& g, const int32_t* bo, const float* x, const int32_t* ncnt, uint2* units,
+                     int32_t* unit_count, int32_t* order_sparse, uint2* waves_sparse, int32_t* wave_count_sparse,
+                     hipStream_t st) {
+  const uint32_t n = (uint32_t)g.n_keys;
+  hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL((k_tile_flags<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, ncnt, g.flags,
+                     g.unit_len, g.sparse_len);
+  SPHOPS_LAUNCHED();
+  exclusive_scan_u32(g, g.flags, n, reinterpret_cast<uint32_t*>(unit_count), st);
+  hipLaunchKernelGGL(k_tile_units, grid_for(n), dim3(kThreads), 0, st, g.unit_len, g.flags, n, units);
+  SPHOPS_LAUNCHED();
+  run_split_schedule(g, g.sparse_len, order_sparse, waves_sparse, wave_count_sparse, st);
 }
 
 // Pick the register-channel configuration for C.
@@ -1726,6 +1777,12 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
     case Op::NeighbourFill:
       if (g.n_keys) neighbour_fill<D, P>(g, bo, a.x, a.nptr, a.iout, a.iout2, a.cap, st);
       return;
+    case Op::NeighbourTiles:
+      if (g.n_keys)
+        neighbour_tiles<D, P>(g, bo, a.x, a.ncnt, const_cast<uint2*>(a.tile_units), const_cast<int32_t*>(a.tile_count),
+                              const_cast<int32_t*>(a.order_sparse), const_cast<uint2*>(a.waves_sparse),
+                              const_cast<int32_t*>(a.nwaves_sparse_dev), st);
+      return;
   }
   throw Error("unknown forward operator");
 }
@@ -1745,6 +1802,10 @@ void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const
       return launch_channels<D, P, GradientBwdDs>(g, bo, a, st);
     case Op::DensityPair: return launch_pairs<D, P, OpDensityPairBwd<D, P>>(g, bo, a, st);
     case Op::BlurGradientHybrid: {
+      if (split_ok(a) && a.C == 16 && a.tile_units != nullptr && a.waves_sparse != nullptr) {
+        if (full) return launch_blur_hybrid_bwd_tiles<D, P, true>(g, bo, a, st);
+        return launch_blur_hybrid_bwd_tiles<D, P, false>(g, bo, a, st);
+      }
       if (split_ok(a)) {
         if (full) return launch_blur_hybrid_bwd_quad<D, P, true>(g, a, st);
         return launch_blur_hybrid_bwd_quad<D, P, false>(g, a, st);

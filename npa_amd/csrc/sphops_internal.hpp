@@ -103,6 +103,7 @@ enum class Op : int {
   BlurGradientHybrid = 8,  // blur + gradient_hybrid in one pass
   NeighbourCandidates = 9,  // scanned stencil candidate counts (int32, the list's row offsets)
   NeighbourFill = 10,       // in-radius neighbour indices and counts (int32)
+  NeighbourTiles = 11,      // cell tiles of the pass-B backward and the schedule of the other particles
 };
 
 struct OpPtrs {
@@ -132,6 +133,14 @@ struct OpPtrs {
   // and nwaves / nwaves2 only size the launch (an upper bound)
   const int32_t* nwaves_dev = nullptr;
   const int32_t* nwaves2_dev = nullptr;
+  // optional cell tiles of the pass-B backward (sphops_neighbor_tiles): the
+  // units, their device count, and the split schedule of the other particles
+  const uint2* tile_units = nullptr;
+  const int32_t* tile_count = nullptr;
+  const int32_t* order_sparse = nullptr;
+  const uint2* waves_sparse = nullptr;
+  uint32_t nwaves_sparse = 0;
+  const int32_t* nwaves_sparse_dev = nullptr;
   uint32_t C = 0;
   float tol = 1e-3f;
 };
@@ -145,6 +154,10 @@ void run_backward(const Grid& g, Op op, bool full, const int32_t* bin_offsets, c
 // order; one descriptor per wave {first slot in order, group size << 8 | particles}.
 void run_neighbour_schedule(const Grid& g, const int32_t* ncnt, int32_t* order, uint2* waves, int32_t* wave_total,
                             uint2* waves2, int32_t* wave_total2, hipStream_t st);
+// The split-group schedule alone (kSplitGroups) over lengths `len`; items of
+// negative length are left out.
+void run_split_schedule(const Grid& g, const int32_t* len, int32_t* order, uint2* waves, int32_t* wave_total,
+                        hipStream_t st);
 // upper bound of the number of waves a schedule can hold
 uint64_t neighbour_wave_capacity(const Grid& g);
 // Units of the cell-major fill: units[u] = {first particle, count} for every

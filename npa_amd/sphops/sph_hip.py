@@ -17,6 +17,7 @@ Every call enqueues work on the current HIP stream of the tensor's device and
 returns without synchronising.
 """
 import ctypes
+import os
 
 import torch
 
@@ -61,6 +62,20 @@ def _validate_shape(t, expected, name):
 
 
 _F32, _I32 = torch.float32, torch.int32
+
+
+class NeighborPlan(tuple):
+    """A snapshot's neighbour list and its schedules (``neighbor_list``):
+    the tuple ``(start, count, index, order, waves, wave_count, waves_split,
+    wave_count_split[, device counts])``, plus ``tiles``: the cell tiles of
+    the pass-B backward ``(units, unit count (device), order of the other
+    particles, their split waves, their wave count (host bound), its device
+    copy)``, or None."""
+
+    def __new__(cls, *items):
+        return super().__new__(cls, items)
+
+    tiles = None
 
 
 class _HashGridNative:
@@ -362,11 +377,26 @@ class _HashGridNative:
         wcap = 2 * max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 1)
         waves = torch.empty(wcap, dtype=_I32, device=dev)
         waves2 = torch.empty(wcap, dtype=_I32, device=dev)
-        small = torch.empty(3, dtype=_I32, device=dev)
-        _check(_lib.sphops_neighbor_candidates(self._h, x, bo, ctypes.c_void_p(start.data_ptr()), st))
+        small = torch.empty(5, dtype=_I32, device=dev)
+        tiles = self._tile_buffers(dev, n, wcap) if self.tiles_enabled else None
+
+        def candidates():
+            _check(_lib.sphops_neighbor_candidates(self._h, x, bo, ctypes.c_void_p(start.data_ptr()), st))
+
+        def build_tiles():
+            # after the last fill: the tile build reuses the grid scratch that
+            # holds the fill's work split
+            if tiles is not None:
+                _check(_lib.sphops_neighbor_tiles(
+                    self._h, x, bo, ctypes.c_void_p(count.data_ptr()), ctypes.c_void_p(tiles[0].data_ptr()),
+                    ctypes.c_void_p(small.data_ptr() + 12), ctypes.c_void_p(tiles[1].data_ptr()),
+                    ctypes.c_void_p(tiles[2].data_ptr()), ctypes.c_void_p(small.data_ptr() + 16), st))
+
+        candidates()
         fixed = getattr(self, "_capture_capacity", 0)
         if fixed:
-            return self._neighbor_list_fixed(x, bo, start, count, order, waves, waves2, small, fixed, st)
+            return self._neighbor_list_fixed(x, bo, start, count, order, waves, waves2, small, fixed, st,
+                                             build_tiles, tiles)
         prev = getattr(self, "_index_capacity", 0)
         limit = self.max_list_entries
         cap = min(prev if prev else int(start[n].item()), limit)
@@ -383,25 +413,42 @@ class _HashGridNative:
                                                  ctypes.c_void_p(small.data_ptr() + 4),
                                                  ctypes.c_void_p(waves2.data_ptr()),
                                                  ctypes.c_void_p(small.data_ptr() + 8), st))
+            build_tiles()
             small[0:1].copy_(start[n:n + 1])
             return small.cpu().tolist()
 
         fill(index, cap)
-        total, nwaves, nwaves2 = schedule()
+        total, nwaves, nwaves2, nunits, nwaves_s = schedule()
         if total > limit:
             # too large to store: the operators scan the stencil instead
             return None
         if total > cap:
             # the first fill cut rows at the buffer's end (their counts too), so
-            # fill again and schedule from the full counts
+            # fill again (after the candidates pass that sets up the fill's
+            # work split again) and schedule from the full counts
             cap = total
             index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
+            candidates()
             fill(index, cap)
-            total, nwaves, nwaves2 = schedule()
+            total, nwaves, nwaves2, nunits, nwaves_s = schedule()
         if total > prev:  # ~12% headroom, so that the next snapshot of a moving cloud fits
             self._index_capacity = total + total // 8
-        self._wave_counts = (nwaves, nwaves2)
-        return start, count, index, order, waves, nwaves, waves2, nwaves2
+        self._wave_counts = (nwaves, nwaves2, nwaves_s)
+        plan = NeighborPlan(start, count, index, order, waves, nwaves, waves2, nwaves2)
+        if tiles is not None:
+            plan.tiles = (tiles[0], small[3:4], tiles[1], tiles[2], nwaves_s, small[4:5])
+        return plan
+
+    # Cell tiles for the pass-B backward (sphops_neighbor_tiles): opt-in
+    # (NPA_SPHOPS_TILES=1, or this attribute), because at cfg5 the tiled
+    # kernel is slower than the lane-split list kernel it replaces for
+    # well-filled cells.
+    tiles_enabled = os.environ.get("NPA_SPHOPS_TILES", "0") == "1"
+
+    def _tile_buffers(self, dev, n, wcap):
+        cap = max(int(_lib.sphops_neighbor_tile_capacity(self._h)), 1)
+        return (torch.empty(2 * cap, dtype=_I32, device=dev), torch.empty(max(n, 1), dtype=_I32, device=dev),
+                torch.empty(wcap, dtype=_I32, device=dev))
 
     # Largest neighbour list (index entries = stencil candidates) a snapshot
     # builds; above it neighbor_list returns None and the operators scan the
@@ -429,7 +476,7 @@ class _HashGridNative:
             self._overflow = torch.zeros(1, dtype=_I32, device=torch.device("cuda", torch.cuda.current_device()))
             cap = max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 0)
             hint = getattr(self, "_wave_counts", None)
-            self._wave_bounds = tuple(min(cap, int(c * wave_margin) + 64) for c in hint) if hint else (cap, cap)
+            self._wave_bounds = tuple(min(cap, int(c * wave_margin) + 64) for c in hint) if hint else (cap, cap, cap)
 
     def list_overflow(self):
         """True if a list built since set_capture_capacity (or the last
@@ -442,7 +489,7 @@ class _HashGridNative:
         if getattr(self, "_overflow", None) is not None:
             self._overflow.zero_()
 
-    def _neighbor_list_fixed(self, x, bo, start, count, order, waves, waves2, small, cap, st):
+    def _neighbor_list_fixed(self, x, bo, start, count, order, waves, waves2, small, cap, st, build_tiles, tiles):
         n = self._b * self._n
         index = torch.empty(cap, dtype=_I32, device=start.device)
         _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
@@ -452,12 +499,17 @@ class _HashGridNative:
                                              ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
                                              ctypes.c_void_p(small.data_ptr() + 4), ctypes.c_void_p(waves2.data_ptr()),
                                              ctypes.c_void_p(small.data_ptr() + 8), st))
+        build_tiles()
         # flag |= total > cap or a wave count above its launch, on the device
-        b1, b2 = self._wave_bounds
+        b1, b2, b3 = self._wave_bounds
         torch.maximum(self._overflow, (start[n:n + 1] > cap).to(_I32), out=self._overflow)
         torch.maximum(self._overflow, (small[1:2] > b1).to(_I32), out=self._overflow)
         torch.maximum(self._overflow, (small[2:3] > b2).to(_I32), out=self._overflow)
-        return start, count, index, order, waves, b1, waves2, b2, small
+        plan = NeighborPlan(start, count, index, order, waves, b1, waves2, b2, small)
+        if tiles is not None:
+            torch.maximum(self._overflow, (small[4:5] > b3).to(_I32), out=self._overflow)
+            plan.tiles = (tiles[0], small[3:4], tiles[1], tiles[2], b3, small[4:5])
+        return plan
 
     # Per operator: trailing dims of (first output, second output) after (B, N);
     # "C" stands for the channel count, "D" for the spatial dimension.
@@ -512,9 +564,14 @@ class _HashGridNative:
                 a.nbr_order, a.nbr_waves, a.nbr_wave_count = nbr[3].data_ptr(), nbr[4].data_ptr(), nbr[5]
             if len(nbr) > 6:
                 a.nbr_waves_split, a.nbr_wave_count_split = nbr[6].data_ptr(), nbr[7]
-            if len(nbr) > 8:  # capture mode: the wave counts stay on the device
+            if len(nbr) > 8 and nbr[8] is not None:  # capture mode: the wave counts stay on the device
                 a.nbr_wave_count_device = nbr[8].data_ptr() + 4
                 a.nbr_wave_count_split_device = nbr[8].data_ptr() + 8
+            tiles = getattr(nbr, "tiles", None)
+            if tiles is not None:
+                a.tile_units, a.tile_unit_count = tiles[0].data_ptr(), tiles[1].data_ptr()
+                a.nbr_order_sparse, a.nbr_waves_sparse = tiles[2].data_ptr(), tiles[3].data_ptr()
+                a.nbr_wave_count_sparse, a.nbr_wave_count_sparse_device = tiles[4], tiles[5].data_ptr()
         return a
 
     def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None):

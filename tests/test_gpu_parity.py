@@ -36,6 +36,12 @@ def _cases():
     cs.append(H.random_case("dense3d", 1, 1200, 4, 3, 8, 0.25, False, "grid", uniform=False, sigma=0.07))
     cs.append(H.random_case("dense3d-particle", 1, 1200, 4, 3, 8, 0.25, False, "particle", uniform=False,
                             sigma=0.07))
+    # dense 3D clusters at C = 16 (the channel count of the cell-tiled backward)
+    d3 = H.random_case("dense3d-per-c16", 1, 1500, 16, 3, 8, 0.25, True, "grid", uniform=False, sigma=0.08)
+    d3.x[..., :3] += 0.9  # across the periodic boundary
+    cs.append(d3)
+    cs.append(H.random_case("dense3d-particle-c16", 1, 1500, 16, 3, 8, 0.25, False, "particle", uniform=False,
+                            sigma=0.08))
     d = H.random_case("dense2d-per", 1, 1000, 16, 2, 8, 0.125, True, "grid", uniform=False, sigma=0.05)
     d.x[..., :2] += 0.5  # the cluster straddles the periodic boundary
     cs.append(d)
@@ -538,3 +544,44 @@ def test_cfg2_chain_is_deterministic_and_moves():
         last = [r.tobytes() for r in inputs[-1][k].reshape(-1, inputs[-1][k].shape[-1])]
         assert sum(r in first for r in last) < 0.01 * len(last)
     assert np.isfinite(inputs[-1][0]).all() and np.isfinite(inputs[-1][1]).all()
+
+
+@pytest.mark.parametrize("name", ["cfg5", "dense2d-per", "dense3d-per-c16", "dense3d-particle-c16", "randn-2d", "cfg1"])
+def test_cell_tiles_backward(name):
+    """The opt-in cell-tiled pass-B backward (sphops_neighbor_tiles + the
+    tiled kernel for the particles of cells with 8 or more particles, the
+    lane-split list kernel for the others) against the oracle: dL/dx, dL/ds
+    and dL/drho of blur + gradient_hybrid, and dL/ds alone."""
+    import npa_amd.sphops as sp
+    from npa_amd.sphops.sph import BlurGradientHybrid
+    c, res, ora = run(name)
+    q = ora["q"]
+    D = c.dim
+    grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    grid.hashgrid.tiles_enabled = True
+    snap = grid.instantiate(dev(c.x))
+    xb, sb, mb, rho = dev(res["xb"]), dev(res["sb"]), dev(res["mb"]), dev(res["rho"])
+    rng = np.random.default_rng(11)
+    B, N, C = c.B, c.N, c.C
+    rng.standard_normal((B, N))
+    g_blur = rng.standard_normal((B, N, C)).astype(np.float32)
+    g_grad = rng.standard_normal((B, N, C, D)).astype(np.float32)
+    from npa_amd.sphops.sph import _plan
+    plan = _plan(snap, xb)
+    assert plan.tiles is not None
+    units = int(plan.tiles[1].item())
+    assert units > 0, f"{name}: no cell has 8 or more particles"
+    for need in (("x", "s", "rho"), ("s",)):
+        xr = xb.detach().clone().requires_grad_("x" in need)
+        sr = sb.detach().clone().requires_grad_(True)
+        rr = rho.detach().clone().requires_grad_("rho" in need)
+        snap.plan = None
+        torch.autograd.backward(BlurGradientHybrid.apply(xr, sr, rr, mb, snap, 1e-3), [dev(g_blur), dev(g_grad)])
+        got = {"x": xr.grad, "s": sr.grad, "rho": rr.grad}
+        for i, k in enumerate(("x", "s", "rho")):
+            if k not in need:
+                continue
+            (ra, ma), (rb, mb_) = ora["b_blur"][i], ora["b_grad"][i]
+            H.assert_close(f"{name}:tiles.d{k}", _flat(got[k].cpu().numpy(), q, D if k == "x" else None), ra + rb,
+                           ma + mb_)
