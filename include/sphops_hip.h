@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 14
+#define SPHOPS_ABI_VERSION 15
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -186,7 +186,7 @@ typedef struct sphops_args {
   uint32_t feature_dim;        /* C */
   float tol;                   /* gradient_hybrid: safe-inverse threshold */
   const int32_t* bin_offsets;  /* (B*G+1) from sphops_initialize */
-  const int32_t* nbr_start;    /* optional list row start per particle: cand_offsets of sphops_neighbor_fill */
+  const int32_t* nbr_start;    /* optional list row start per particle (sphops_neighbor_fill) */
   const int32_t* nbr_count;    /* optional list length per particle from sphops_neighbor_fill */
   const int32_t* nbr_index;    /* optional list entries from sphops_neighbor_fill; NULL: scan the stencil */
   const int32_t* nbr_order;    /* optional schedule from sphops_neighbor_schedule: particle order ... */
@@ -227,26 +227,28 @@ int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, voi
 int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLdrho, const sphops_args* args,
                     void* stream);
 
-/* Row offsets of the neighbour list: for every binned particle the number of
- * particles in its 3^D cell stencil (the cells the reference traverses, an
- * upper bound of its in-radius count), exclusive-scanned into cand_offsets
- * (B*N+1); cand_offsets[B*N] is the total.  Also leaves in the grid's
- * scratch what sphops_neighbor_fill reads: the stencil ranges and the split
- * of the particles between the cell-major and the per-particle fill. */
-int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
-                               int32_t* cand_offsets, void* stream);
+/* First step of the neighbour list: for every binned particle its 3^D cell
+ * stencil (the cells the reference traverses) and the split of the fill's
+ * work, left in the grid's scratch for sphops_neighbor_fill. */
+int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bin_offsets, void* stream);
 
 /* In-radius neighbours (pairs |r| < eps incl. self) of every binned particle,
- * in stencil order: the binned indices go to nbr_index[cand_offsets[i] ..),
- * their number (the reference's `count`) to nbr_count[i] (B*N).  Entries at
- * or past index_capacity are not written: a caller that sized nbr_index below
- * cand_offsets[B*N] checks that total afterwards and fills again;
- * index_capacity is at most 2^30.  Must follow
+ * in stencil order: row i is nbr_index[nbr_start[i] .. nbr_start[i] +
+ * nbr_count[i]) (nbr_start and nbr_count have B*N entries).  Rows are
+ * compact, allocated in blocks from a counter, so nbr_index needs the number
+ * of in-radius pairs, which *nbr_total (one device int64) receives -- also
+ * when it exceeds index_capacity.  A row that does not fit below
+ * index_capacity is not stored: its nbr_count is -1 - (the particle's stencil
+ * candidates), and every operator walks that particle's stencil instead, so
+ * results never depend on the capacity (a caller sizes the next snapshot's
+ * buffer from *nbr_total, read back whenever convenient).  Where a row lands
+ * depends on the order blocks are taken; rows, their order and all results do
+ * not.  index_capacity is at most 2^30.  Must follow
  * sphops_neighbor_candidates on the same grid with the same x and bin_offsets
  * (checked by pointer; their contents must not change in between), with no
  * other candidates call on that grid in between. */
-int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
-                         const int32_t* cand_offsets, int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count,
+int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bin_offsets, int32_t* nbr_start,
+                         int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, int64_t* nbr_total,
                          void* stream);
 
 /* Schedule for list traversal.  The binned particles are cut into tiles of

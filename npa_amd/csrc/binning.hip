@@ -476,10 +476,14 @@ __device__ __forceinline__ uint32_t length_class(int32_t len, const ClassBounds&
 }
 
 // Length of item idx: from CSR offsets (CSR) or a plain length array.
+// A plain length of -1 marks an item that is not scheduled; below -1 it
+// encodes a particle whose list row was not stored, -1 - (its stencil
+// candidates), scheduled by its candidates (the pair kernels walk them).
 template <bool CSR>
 __device__ __forceinline__ int32_t item_length(const int32_t* __restrict__ src, uint32_t idx) {
   if constexpr (CSR) return src[idx + 1] - src[idx];
-  return src[idx];
+  const int32_t v = src[idx];
+  return v >= -1 ? v : -1 - v;
 }
 
 // Per tile of kTile items: the number of items of each class, written to

@@ -145,6 +145,7 @@ void free_grid(Grid* g) {
   (void)hipFree(g->chunk_lo);
   (void)hipFree(g->flags);
   (void)hipFree(g->packed);
+  (void)hipFree(g->cand);
   (void)hipFree(g->sparse_len);
   (void)hipFree(g->unit_len);
   (void)hipFree(g->units);
@@ -278,6 +279,7 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
       g->flags = dalloc<uint32_t>(BN + 1);
       g->packed = dalloc<float4>(BN);
+      g->cand = dalloc<int32_t>(BN);
       g->sparse_len = dalloc<int32_t>(BN);
       g->unit_len = dalloc<int32_t>(BN);
       g->units = dalloc<uint2>(BN);
@@ -633,47 +635,47 @@ int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLd
   }
 }
 
-int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* cand_offsets,
-                               void* stream) {
+int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bo, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(bo != nullptr && cand_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
+    require(bo != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
     require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
-    const hipStream_t st = sphops::as_stream(stream);
-    if (grid->n_keys == 0) {
-      sphops::fill_u32(reinterpret_cast<uint32_t*>(cand_offsets), 1, 0u, st);
-      return;
-    }
+    if (grid->n_keys == 0) return;
     OpPtrs a;
     a.x = x;
-    a.iout = cand_offsets;
-    sphops::forward(*grid, Op::NeighbourCandidates, bo, a, st);
+    sphops::forward(*grid, Op::NeighbourCandidates, bo, a, sphops::as_stream(stream));
     grid->split_key[0] = x;
     grid->split_key[1] = bo;
   });
 }
 
-int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, const int32_t* cand_offsets,
-                         int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, void* stream) {
+int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* nbr_start,
+                         int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, int64_t* nbr_total,
+                         void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(bo != nullptr && cand_offsets != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
+    require(bo != nullptr && nbr_total != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
     require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
     require(index_capacity >= 0, "negative index capacity");
-    require(index_capacity <= sphops::kMaxListEntries,
-            "neighbour list too large: at most 2^30 index entries (stencil candidates) per grid");
-    if (grid->n_keys == 0) return;
-    require(nbr_count != nullptr && (nbr_index != nullptr || index_capacity == 0), "null buffer");
+    require(index_capacity <= sphops::kMaxListEntries, "index_capacity above 2^30 entries");
+    const hipStream_t st = sphops::as_stream(stream);
+    if (grid->n_keys == 0) {
+      sphops::fill_u32(reinterpret_cast<uint32_t*>(nbr_total), 2, 0u, st);
+      return;
+    }
+    require(nbr_start != nullptr && nbr_count != nullptr && (nbr_index != nullptr || index_capacity == 0),
+            "null buffer");
     require(grid->split_key[0] == x && grid->split_key[1] == bo,
             "sphops_neighbor_fill must follow sphops_neighbor_candidates on the same grid with the same "
             "positions and bin_offsets");
     OpPtrs a;
     a.x = x;
-    a.nptr = cand_offsets;
+    a.iout3 = nbr_start;
     a.iout = nbr_index;
     a.iout2 = nbr_count;
+    a.used = reinterpret_cast<unsigned long long*>(nbr_total);
     a.cap = index_capacity;
-    sphops::forward(*grid, Op::NeighbourFill, bo, a, sphops::as_stream(stream));
+    sphops::forward(*grid, Op::NeighbourFill, bo, a, st);
   });
 }
 

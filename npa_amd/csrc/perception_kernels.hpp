@@ -831,6 +831,35 @@ struct OpDensityPairBwd {
   }
 };
 
+// ---- stencil walk for particles whose row did not fit
+
+// Candidate number t (0-based, in stencil order) of particle k, found by
+// walking the stencil ranges from the start.  Slow, and only for particles
+// the fill could not store (count < 0).
+template <int D, bool P>
+__device__ __forceinline__ uint32_t stencil_candidate(const GridParams& g, const int32_t* __restrict__ bo,
+                                                   const float* xi, uint32_t k, uint32_t t) {
+  Walker<D, P> w;
+  w.init(g, xi, k);
+  for (int r = 0;; ++r) {
+    if (!w.fetch(g, bo, r)) return k;  // past the stencil: cannot happen for t < candidates
+    const uint32_t len = w.jend - w.j;
+    if (t < len) return w.j + t;
+    t -= len;
+  }
+}
+
+// Row of particle k: its list entries, or (count < 0) its stencil candidates.
+struct Row {
+  int32_t start, end;
+  bool stencil;
+  __device__ __forceinline__ static Row of(const OpPtrs& a, uint32_t k) {
+    const int32_t c = a.ncnt[k];
+    if (c >= 0) return Row{a.nptr[k], a.nptr[k] + c, false};
+    return Row{0, -1 - c, true};
+  }
+};
+
 // ---------------------------------------------------------------- driver
 
 // (x, y, z|0, weight) per particle into the scratch array the pair kernels read.
@@ -867,10 +896,20 @@ __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t*
     op.init(g, a, k);
   }
   if constexpr (TRAV == kList) {
-    if (active) {
+    const Row row = active ? Row::of(a, k) : Row{0, 0, false};
+    if (row.stencil) {
+      for (int t = 0; t < row.end; ++t) {
+        const uint32_t j = stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)t);
+        const float4 pj = xw[j];
+        float xj[3], r[3];
+        unpack(pj, xj);
+        const float d2 = displacement<D, P>(g, xi, xj, r);
+        if (d2 < g.eps2) op.pair(g, a, xi, xj, pj.w, r, d2, j);
+      }
+    } else if (active) {
       const int32_t* __restrict__ nidx = a.nidx;
-      int t = a.nptr[k];
-      const int end = t + a.ncnt[k];
+      int t = row.start;
+      const int end = row.end;
       for (; t + 1 < end; t += 2) {
         const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + 1];
         const float4 p0 = xw[j0], p1 = xw[j1];
@@ -955,13 +994,23 @@ __device__ __forceinline__ uint32_t wave_limit(uint32_t host, const int32_t* dev
   return dev ? (uint32_t)*dev : host;
 }
 
-// This wave's index in the schedule, with the XCD-contiguous block mapping
-// taken over the live workgroups only, so that a launch sized by an upper
-// bound still spreads its live waves over all eight XCDs.
+// The schedule's waves are served in rounds of (at most) the launched waves:
+// this wave's first index, with the XCD-contiguous block mapping taken over
+// the workgroups the round needs, so that a launch larger than the schedule
+// still spreads its live waves over all eight XCDs; and the round's stride.
+// Any launch (a multiple of eight workgroups) serves every live wave, so the
+// launch can be sized from an estimate and the count read on the device.
+__device__ __forceinline__ uint32_t schedule_blocks(uint32_t live) {
+  const uint32_t per = kThreads / kWave;
+  return min((live + per - 1) / per, gridDim.x);
+}
 __device__ __forceinline__ uint32_t schedule_wave(uint32_t live) {
   const uint32_t per = kThreads / kWave;
-  const uint32_t b = xcd_block_id((live + per - 1) / per);
+  const uint32_t b = xcd_block_id(schedule_blocks(live));
   return b == 0xFFFFFFFFu ? b : b * per + (threadIdx.x >> 6);
+}
+__device__ __forceinline__ uint32_t schedule_stride(uint32_t live) {
+  return schedule_blocks(live) * (kThreads / kWave);
 }
 
 // List traversal with a group of G lanes per particle, G by list-length class:
@@ -972,47 +1021,58 @@ __device__ __forceinline__ uint32_t schedule_wave(uint32_t live) {
 template <int D, bool P, class OP>
 __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs a) {
   const uint32_t live = wave_limit(a.nwaves, a.nwaves_dev);
-  const uint32_t wave = schedule_wave(live);
-  if (wave >= live) return;
-  const uint2 wd = a.waves[wave];
-  const int G = (int)(wd.y >> 8);
-  const int lane = __lane_id();
-  const uint32_t slot = (uint32_t)(lane / G);
-  const int sub = lane & (G - 1);
-  const bool active = slot < (wd.y & 0xFFu);
-  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
-  const float4* __restrict__ xw = a.xw;
-  OP op;
-  float xi[3] = {0.0f, 0.0f, 0.0f};
-  if (active) {
-    unpack(xw[k], xi);
-    op.init(g, a, k);
-    const int32_t* __restrict__ nidx = a.nidx;
-    const int start = a.nptr[k];
-    const int end = start + a.ncnt[k];
-    int t = start + sub;
-    for (; t + G < end; t += 2 * G) {
-      const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + G];
-      const float4 p0 = xw[j0], p1 = xw[j1];
-      float x0[3], x1[3], r0[3], r1[3];
-      unpack(p0, x0);
-      unpack(p1, x1);
-      const float d0 = displacement<D, P>(g, xi, x0, r0);
-      const float d1 = displacement<D, P>(g, xi, x1, r1);
-      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
-      op.pair(g, a, xi, x1, p1.w, r1, d1, j1);
+  const uint32_t stride = schedule_stride(live);
+  for (uint32_t wave = schedule_wave(live); wave < live; wave += stride) {
+    const uint2 wd = a.waves[wave];
+    const int G = (int)(wd.y >> 8);
+    const int lane = __lane_id();
+    const uint32_t slot = (uint32_t)(lane / G);
+    const int sub = lane & (G - 1);
+    const bool active = slot < (wd.y & 0xFFu);
+    const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
+    const float4* __restrict__ xw = a.xw;
+    OP op;
+    float xi[3] = {0.0f, 0.0f, 0.0f};
+    if (active) {
+      unpack(xw[k], xi);
+      op.init(g, a, k);
+      const int32_t* __restrict__ nidx = a.nidx;
+      const Row row = Row::of(a, k);
+      const int end = row.end;
+      int t = row.start + sub;
+      if (row.stencil) {
+        for (; t < end; t += G) {
+          const uint32_t j = stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)t);
+          const float4 pj = xw[j];
+          float xj[3], r[3];
+          unpack(pj, xj);
+          const float d2 = displacement<D, P>(g, xi, xj, r);
+          if (d2 < g.eps2) op.pair(g, a, xi, xj, pj.w, r, d2, j);
+        }
+      }
+      for (; t + G < end; t += 2 * G) {
+        const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + G];
+        const float4 p0 = xw[j0], p1 = xw[j1];
+        float x0[3], x1[3], r0[3], r1[3];
+        unpack(p0, x0);
+        unpack(p1, x1);
+        const float d0 = displacement<D, P>(g, xi, x0, r0);
+        const float d1 = displacement<D, P>(g, xi, x1, r1);
+        op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+        op.pair(g, a, xi, x1, p1.w, r1, d1, j1);
+      }
+      if (t < end) {
+        const uint32_t j0 = (uint32_t)nidx[t];
+        const float4 p0 = xw[j0];
+        float x0[3], r0[3];
+        unpack(p0, x0);
+        const float d0 = displacement<D, P>(g, xi, x0, r0);
+        op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+      }
     }
-    if (t < end) {
-      const uint32_t j0 = (uint32_t)nidx[t];
-      const float4 p0 = xw[j0];
-      float x0[3], r0[3];
-      unpack(p0, x0);
-      const float d0 = displacement<D, P>(g, xi, x0, r0);
-      op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
-    }
+    op.reduce(G);
+    if (active && sub == 0) op.finish(g, a, k);
   }
-  op.reduce(G);
-  if (active && sub == 0) op.finish(g, a, k);
 }
 
 // ------------------------------------------------ lane-split channel kernels
@@ -1071,159 +1131,171 @@ template <int D, bool P, int CW, bool FULL, bool OFF32>
 __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
   const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
-  const uint32_t wave = schedule_wave(live);
-  if (wave >= live) return;
-  const uint2 wd = a.waves2[wave];
-  const int G = (int)(wd.y >> 8);
-  const int lane = __lane_id();
-  const uint32_t slot = (uint32_t)(lane / G);
-  const int sub = lane & (G - 1);
-  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
-  const bool active = slot < (wd.y & 0xFFu);
-  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
-  const uint32_t c0 = (uint32_t)slice * CW;
-  const float4* __restrict__ xw = a.xw;
-  float xi[3] = {0.0f, 0.0f, 0.0f};
-  float vi = 0.0f, mr2 = 0.0f;
-  float si[FULL ? CW : 1] = {}, gbi[FULL ? CW : 1] = {};
-  float ggi[CW * D] = {};
-  float dsb[CW] = {}, dsg[CW] = {};
-  float wsum[D] = {};
-  float dxb[D] = {}, dxg[D] = {};
-  float drb = 0.0f, drg = 0.0f;
-  if (active) {
-    unpack(xw[k], xi);
-    const float mi = a.m[k], ri = a.rho[k];
-    vi = mi / ri;
-    mr2 = mi / (ri * ri);
-    load_span<CW * D, true>(a.g2 + ((uint64_t)k * C + c0) * D, ggi);
-    if constexpr (FULL) {
-      load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
-      load_span<CW, true>(a.g + (uint64_t)k * C + c0, gbi);
-    }
-    const int32_t* __restrict__ nidx = a.nidx;
-    const int start = a.nptr[k];
-    const int end = start + a.ncnt[k];
-    for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
-      // geometry of the pair this lane owns
-      const int to = t0 + slice * S;
-      uint32_t jo = 0u;
-      float vo = 0.0f, Wo = 0.0f, t2o = 0.0f, jao = 0.0f, jbo = 0.0f;
-      float rbo[3] = {0.0f, 0.0f, 0.0f}, wo[3] = {0.0f, 0.0f, 0.0f};
-      if (to < end) {
-        jo = (uint32_t)nidx[to];
-        const float4 pj = xw[jo];
-        float xj[3], r[3];
-        unpack(pj, xj);
-        vo = pj.w;
-        const float d2 = displacement<D, P>(g, xi, xj, r);
-        const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
-        Wo = poly6(g.eps2, db);
-        float d;
-        const float mag = spiky_mag(g.eps, db, &d);
-#pragma unroll
-        for (int e = 0; e < D; ++e) {
-          wo[e] = mag * rbo[e];
-          wsum[e] += vo * wo[e];
-        }
-        if (db != 0.0f && db < g.eps2) {
-          const float tt = g.eps2 - db;
-          t2o = tt * tt;
-          const float di = fast_rcp(d);
-          jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
-          jbo = 3.0f * (g.eps2 - db) * di * di * di;
-        }
+  const uint32_t stride = schedule_stride(live);
+  for (uint32_t wave = schedule_wave(live); wave < live; wave += stride) {
+    const uint2 wd = a.waves2[wave];
+    const int G = (int)(wd.y >> 8);
+    const int lane = __lane_id();
+    const uint32_t slot = (uint32_t)(lane / G);
+    const int sub = lane & (G - 1);
+    const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
+    const bool active = slot < (wd.y & 0xFFu);
+    const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
+    const uint32_t c0 = (uint32_t)slice * CW;
+    const float4* __restrict__ xw = a.xw;
+    float xi[3] = {0.0f, 0.0f, 0.0f};
+    float vi = 0.0f, mr2 = 0.0f;
+    float si[FULL ? CW : 1] = {}, gbi[FULL ? CW : 1] = {};
+    float ggi[CW * D] = {};
+    float dsb[CW] = {}, dsg[CW] = {};
+    float wsum[D] = {};
+    float dxb[D] = {}, dxg[D] = {};
+    float drb = 0.0f, drg = 0.0f;
+    if (active) {
+      unpack(xw[k], xi);
+      const float mi = a.m[k], ri = a.rho[k];
+      vi = mi / ri;
+      mr2 = mi / (ri * ri);
+      load_span<CW * D, true>(a.g2 + ((uint64_t)k * C + c0) * D, ggi);
+      if constexpr (FULL) {
+        load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
+        load_span<CW, true>(a.g + (uint64_t)k * C + c0, gbi);
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (t0 + q * S >= end) break;  // uniform over the quad
-        uint32_t j;
-        float vj, W, t2, ja, jb, rb[3], w[3];
-#define SPHOPS_QUAD_FETCH(QQ)                                                   \
-  j = quad_get<QQ>(jo);                                                         \
-  vj = quad_get<QQ>(vo);                                                        \
-  W = quad_get<QQ>(Wo);                                                         \
-  t2 = quad_get<QQ>(t2o);                                                       \
-  ja = quad_get<QQ>(jao);                                                       \
-  jb = quad_get<QQ>(jbo);                                                       \
-  for (int e = 0; e < D; ++e) {                                                 \
-    rb[e] = quad_get<QQ>(rbo[e]);                                               \
-    w[e] = quad_get<QQ>(wo[e]);                                                 \
-  }
-        if (q == 0) { SPHOPS_QUAD_FETCH(0) }
-        else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
-        else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
-        else { SPHOPS_QUAD_FETCH(3) }
-#undef SPHOPS_QUAD_FETCH
-        float gbj[CW], ggj[CW * D];
-        load_span<CW, true>(row_slice<OFF32>(a.g, j, C, c0), gbj);
-        load_span<CW * D, true>(row_slice<OFF32>(a.g2, j, C * D, c0 * D), ggj);
-        if constexpr (!FULL) {
-#pragma unroll
-          for (int f = 0; f < CW; ++f) {
-            dsb[f] += W * gbj[f];
-#pragma unroll
-            for (int e = 0; e < D; ++e) dsg[f] += ggj[f * D + e] * w[e];
-          }
-        } else {
-          float sj[CW];
-          load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
-          float A = 0.0f, Bv = 0.0f;
-          float u1[D] = {}, u2[D] = {};
-#pragma unroll
-          for (int f = 0; f < CW; ++f) {
-            dsb[f] += W * gbj[f];
-            A += gbi[f] * sj[f];
-            Bv += gbj[f] * si[f];
-            const float df = si[f] - sj[f];
-#pragma unroll
-            for (int e = 0; e < D; ++e) {
-              dsg[f] += ggj[f * D + e] * w[e];
-              u1[e] += df * ggj[f * D + e];
-              u2[e] += df * ggi[f * D + e];
-            }
-          }
-          const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
-          float u[D], uw = 0.0f, rv = 0.0f;
-#pragma unroll
+      const int32_t* __restrict__ nidx = a.nidx;
+      const Row row = Row::of(a, k);
+      const int start = row.start;
+      const int end = row.end;
+      for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
+        // geometry of the pair this lane owns (all zero for a stencil
+        // candidate out of radius)
+        const int to = t0 + slice * S;
+        uint32_t jo = k;
+        float vo = 0.0f, Wo = 0.0f, t2o = 0.0f, jao = 0.0f, jbo = 0.0f;
+        float rbo[3] = {0.0f, 0.0f, 0.0f}, wo[3] = {0.0f, 0.0f, 0.0f};
+        float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float d2 = 0.0f, r[3] = {0.0f, 0.0f, 0.0f};
+        bool inr = false;
+        if (to < end) {
+          const uint32_t jc = row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
+          pj = xw[jc];
+          float xj[3];
+          unpack(pj, xj);
+          d2 = displacement<D, P>(g, xi, xj, r);
+          inr = !row.stencil || d2 < g.eps2;
+          if (inr) jo = jc;
+        }
+        if (inr) {
+          float xj[3];
+          unpack(pj, xj);
+          vo = pj.w;
+          const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
+          Wo = poly6(g.eps2, db);
+          float d;
+          const float mag = spiky_mag(g.eps, db, &d);
+  #pragma unroll
           for (int e = 0; e < D; ++e) {
-            dxb[e] += m6 * rb[e];
-            uw += u1[e] * w[e];
-            u[e] = vi * u1[e] + vj * u2[e];
-            rv += rb[e] * u[e];
+            wo[e] = mag * rbo[e];
+            wsum[e] += vo * wo[e];
           }
-          drg += uw;
-#pragma unroll
-          for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
+          if (db != 0.0f && db < g.eps2) {
+            const float tt = g.eps2 - db;
+            t2o = tt * tt;
+            const float di = fast_rcp(d);
+            jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
+            jbo = 3.0f * (g.eps2 - db) * di * di * di;
+          }
+        }
+  #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (t0 + q * S >= end) break;  // uniform over the quad
+          uint32_t j;
+          float vj, W, t2, ja, jb, rb[3], w[3];
+  #define SPHOPS_QUAD_FETCH(QQ)                                                   \
+    j = quad_get<QQ>(jo);                                                         \
+    vj = quad_get<QQ>(vo);                                                        \
+    W = quad_get<QQ>(Wo);                                                         \
+    t2 = quad_get<QQ>(t2o);                                                       \
+    ja = quad_get<QQ>(jao);                                                       \
+    jb = quad_get<QQ>(jbo);                                                       \
+    for (int e = 0; e < D; ++e) {                                                 \
+      rb[e] = quad_get<QQ>(rbo[e]);                                               \
+      w[e] = quad_get<QQ>(wo[e]);                                                 \
+    }
+          if (q == 0) { SPHOPS_QUAD_FETCH(0) }
+          else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
+          else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
+          else { SPHOPS_QUAD_FETCH(3) }
+  #undef SPHOPS_QUAD_FETCH
+          float gbj[CW], ggj[CW * D];
+          load_span<CW, true>(row_slice<OFF32>(a.g, j, C, c0), gbj);
+          load_span<CW * D, true>(row_slice<OFF32>(a.g2, j, C * D, c0 * D), ggj);
+          if constexpr (!FULL) {
+  #pragma unroll
+            for (int f = 0; f < CW; ++f) {
+              dsb[f] += W * gbj[f];
+  #pragma unroll
+              for (int e = 0; e < D; ++e) dsg[f] += ggj[f * D + e] * w[e];
+            }
+          } else {
+            float sj[CW];
+            load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
+            float A = 0.0f, Bv = 0.0f;
+            float u1[D] = {}, u2[D] = {};
+  #pragma unroll
+            for (int f = 0; f < CW; ++f) {
+              dsb[f] += W * gbj[f];
+              A += gbi[f] * sj[f];
+              Bv += gbj[f] * si[f];
+              const float df = si[f] - sj[f];
+  #pragma unroll
+              for (int e = 0; e < D; ++e) {
+                dsg[f] += ggj[f * D + e] * w[e];
+                u1[e] += df * ggj[f * D + e];
+                u2[e] += df * ggi[f * D + e];
+              }
+            }
+            const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
+            float u[D], uw = 0.0f, rv = 0.0f;
+  #pragma unroll
+            for (int e = 0; e < D; ++e) {
+              dxb[e] += m6 * rb[e];
+              uw += u1[e] * w[e];
+              u[e] = vi * u1[e] + vj * u2[e];
+              rv += rb[e] * u[e];
+            }
+            drg += uw;
+  #pragma unroll
+            for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
+          }
         }
       }
+      if constexpr (FULL) {  // blur's dL/drho: sum_j W_j g_j . s_i = s_i . sum_j W_j g_j
+  #pragma unroll
+        for (int f = 0; f < CW; ++f) drb += si[f] * dsb[f];
+      }
     }
-    if constexpr (FULL) {  // blur's dL/drho: sum_j W_j g_j . s_i = s_i . sum_j W_j g_j
-#pragma unroll
-      for (int f = 0; f < CW; ++f) drb += si[f] * dsb[f];
-    }
-  }
-  grp_sum_streams(G, dsb, dsg);
-  grp_sum(G, wsum);
-  if constexpr (FULL) grp_sum(G, dxb, dxg, drb, drg);
-#pragma unroll
-  for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
-  if (active && stream == 0) {
-    const float sb = vi * g.c6;
-#pragma unroll
-    for (int f = 0; f < CW; ++f) {
-      float t = vi * dsg[f];
-#pragma unroll
-      for (int e = 0; e < D; ++e) t += ggi[f * D + e] * wsum[e];
-      a.out1[(uint64_t)k * C + c0 + f] = dsb[f] * sb + t * g.cs;
-    }
-    if constexpr (FULL) {
-      if (slice == 0) {
-        a.out2[k] = -mr2 * (drb * g.c6 + drg * g.cs);
-        float dx[D];
-#pragma unroll
-        for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6 + dxg[e] * g.cs;
-        store_pos_grad<D>(a.out0, k, dx, 1.0f);
+    grp_sum_streams(G, dsb, dsg);
+    grp_sum(G, wsum);
+    if constexpr (FULL) grp_sum(G, dxb, dxg, drb, drg);
+  #pragma unroll
+    for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
+    if (active && stream == 0) {
+      const float sb = vi * g.c6;
+  #pragma unroll
+      for (int f = 0; f < CW; ++f) {
+        float t = vi * dsg[f];
+  #pragma unroll
+        for (int e = 0; e < D; ++e) t += ggi[f * D + e] * wsum[e];
+        a.out1[(uint64_t)k * C + c0 + f] = dsb[f] * sb + t * g.cs;
+      }
+      if constexpr (FULL) {
+        if (slice == 0) {
+          a.out2[k] = -mr2 * (drb * g.c6 + drg * g.cs);
+          float dx[D];
+  #pragma unroll
+          for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6 + dxg[e] * g.cs;
+          store_pos_grad<D>(a.out0, k, dx, 1.0f);
+        }
       }
     }
   }
@@ -1239,98 +1311,110 @@ template <int D, bool P, int CW, bool OFF32>
 __global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
   const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
-  const uint32_t wave = schedule_wave(live);
-  if (wave >= live) return;
-  const uint2 wd = a.waves2[wave];
-  const int G = (int)(wd.y >> 8);
-  const int lane = __lane_id();
-  const uint32_t slot = (uint32_t)(lane / G);
-  const int sub = lane & (G - 1);
-  const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
-  const bool active = slot < (wd.y & 0xFFu);
-  const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
-  const uint32_t c0 = (uint32_t)slice * CW;
-  const float4* __restrict__ xw = a.xw;
-  float xi[3] = {0.0f, 0.0f, 0.0f};
-  float si[CW] = {};
-  float blur[CW] = {};
-  float acc[CW * D] = {};
-  float M[D * D] = {};
-  if (active) {
-    unpack(xw[k], xi);
-    load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
-    const int32_t* __restrict__ nidx = a.nidx;
-    const int start = a.nptr[k];
-    const int end = start + a.ncnt[k];
-    for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
-      const int to = t0 + slice * S;
-      uint32_t jo = 0u;
-      float wo = 0.0f, to_ = 0.0f, ro[3] = {0.0f, 0.0f, 0.0f};
-      if (to < end) {
-        jo = (uint32_t)nidx[to];
-        const float4 pj = xw[jo];
-        float xj[3];
-        unpack(pj, xj);
-        const float d2 = displacement<D, P>(g, xi, xj, ro);
-        wo = poly6(g.eps2, d2) * pj.w;
-        float d;
-        to_ = spiky_mag(g.eps, d2, &d) * pj.w;
-#pragma unroll
-        for (int p = 0; p < D; ++p)
-#pragma unroll
-          for (int q = p; q < D; ++q) M[p * D + q] += to_ * ro[p] * ro[q];
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (t0 + q * S >= end) break;  // uniform over the quad
-        uint32_t j;
-        float w, t, r[3];
-#define SPHOPS_QUAD_FETCH(QQ)             \
-  j = quad_get<QQ>(jo);                   \
-  w = quad_get<QQ>(wo);                   \
-  t = quad_get<QQ>(to_);                  \
-  for (int e = 0; e < D; ++e) r[e] = quad_get<QQ>(ro[e]);
-        if (q == 0) { SPHOPS_QUAD_FETCH(0) }
-        else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
-        else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
-        else { SPHOPS_QUAD_FETCH(3) }
-#undef SPHOPS_QUAD_FETCH
-        float sj[CW];
-        load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
-#pragma unroll
-        for (int f = 0; f < CW; ++f) {
-          blur[f] += w * sj[f];
-          const float qf = t * (sj[f] - si[f]);
-#pragma unroll
-          for (int e = 0; e < D; ++e) acc[f * D + e] += qf * r[e];
+  const uint32_t stride = schedule_stride(live);
+  for (uint32_t wave = schedule_wave(live); wave < live; wave += stride) {
+    const uint2 wd = a.waves2[wave];
+    const int G = (int)(wd.y >> 8);
+    const int lane = __lane_id();
+    const uint32_t slot = (uint32_t)(lane / G);
+    const int sub = lane & (G - 1);
+    const int slice = sub & 3, stream = sub >> 2, S = G >> 2;
+    const bool active = slot < (wd.y & 0xFFu);
+    const uint32_t k = active ? (uint32_t)a.order[wd.x + slot] : 0u;
+    const uint32_t c0 = (uint32_t)slice * CW;
+    const float4* __restrict__ xw = a.xw;
+    float xi[3] = {0.0f, 0.0f, 0.0f};
+    float si[CW] = {};
+    float blur[CW] = {};
+    float acc[CW * D] = {};
+    float M[D * D] = {};
+    if (active) {
+      unpack(xw[k], xi);
+      load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
+      const int32_t* __restrict__ nidx = a.nidx;
+      const Row row = Row::of(a, k);
+      const int start = row.start;
+      const int end = row.end;
+      for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
+        const int to = t0 + slice * S;
+        uint32_t jo = k;
+        float wo = 0.0f, to_ = 0.0f, ro[3] = {0.0f, 0.0f, 0.0f};
+        float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float d2 = 0.0f, rr[3] = {0.0f, 0.0f, 0.0f};
+        bool inr = false;
+        if (to < end) {
+          const uint32_t jc = row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
+          pj = xw[jc];
+          float xj[3];
+          unpack(pj, xj);
+          d2 = displacement<D, P>(g, xi, xj, rr);
+          inr = !row.stencil || d2 < g.eps2;
+          if (inr) jo = jc;
+        }
+        if (inr) {
+          ro[0] = rr[0];
+          ro[1] = rr[1];
+          ro[2] = rr[2];
+          wo = poly6(g.eps2, d2) * pj.w;
+          float d;
+          to_ = spiky_mag(g.eps, d2, &d) * pj.w;
+  #pragma unroll
+          for (int p = 0; p < D; ++p)
+  #pragma unroll
+            for (int q = p; q < D; ++q) M[p * D + q] += to_ * ro[p] * ro[q];
+        }
+  #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (t0 + q * S >= end) break;  // uniform over the quad
+          uint32_t j;
+          float w, t, r[3];
+  #define SPHOPS_QUAD_FETCH(QQ)             \
+    j = quad_get<QQ>(jo);                   \
+    w = quad_get<QQ>(wo);                   \
+    t = quad_get<QQ>(to_);                  \
+    for (int e = 0; e < D; ++e) r[e] = quad_get<QQ>(ro[e]);
+          if (q == 0) { SPHOPS_QUAD_FETCH(0) }
+          else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
+          else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
+          else { SPHOPS_QUAD_FETCH(3) }
+  #undef SPHOPS_QUAD_FETCH
+          float sj[CW];
+          load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
+  #pragma unroll
+          for (int f = 0; f < CW; ++f) {
+            blur[f] += w * sj[f];
+            const float qf = t * (sj[f] - si[f]);
+  #pragma unroll
+            for (int e = 0; e < D; ++e) acc[f * D + e] += qf * r[e];
+          }
         }
       }
     }
-  }
-  grp_sum_streams(G, blur, acc);
-  grp_sum(G, M);
-#pragma unroll
-  for (int q = 0; q < D * D; ++q) M[q] = quad_get<0>(M[q]);  // the group total, to the four slice lanes
-  if (active && stream == 0) {
-#pragma unroll
-    for (int f = 0; f < CW; ++f) a.out0[(uint64_t)k * C + c0 + f] = blur[f] * g.c6;
-    float Ms[D * D], L[D * D];
-#pragma unroll
-    for (int p = 0; p < D; ++p)
-#pragma unroll
-      for (int q = 0; q < D; ++q) Ms[p * D + q] = (q >= p ? M[p * D + q] : M[q * D + p]) * g.cs;
-    safe_inv_sym<D>(Ms, a.tol, L);
-#pragma unroll
-    for (int f = 0; f < CW; ++f) {
-      float raw[D];
-#pragma unroll
-      for (int e = 0; e < D; ++e) raw[e] = acc[f * D + e] * g.cs;
-#pragma unroll
-      for (int e = 0; e < D; ++e) {
-        float o = 0.0f;
-#pragma unroll
-        for (int q = 0; q < D; ++q) o += raw[q] * L[q * D + e];
-        a.out3[((uint64_t)k * C + c0 + f) * D + e] = o;
+    grp_sum_streams(G, blur, acc);
+    grp_sum(G, M);
+  #pragma unroll
+    for (int q = 0; q < D * D; ++q) M[q] = quad_get<0>(M[q]);  // the group total, to the four slice lanes
+    if (active && stream == 0) {
+  #pragma unroll
+      for (int f = 0; f < CW; ++f) a.out0[(uint64_t)k * C + c0 + f] = blur[f] * g.c6;
+      float Ms[D * D], L[D * D];
+  #pragma unroll
+      for (int p = 0; p < D; ++p)
+  #pragma unroll
+        for (int q = 0; q < D; ++q) Ms[p * D + q] = (q >= p ? M[p * D + q] : M[q * D + p]) * g.cs;
+      safe_inv_sym<D>(Ms, a.tol, L);
+  #pragma unroll
+      for (int f = 0; f < CW; ++f) {
+        float raw[D];
+  #pragma unroll
+        for (int e = 0; e < D; ++e) raw[e] = acc[f * D + e] * g.cs;
+  #pragma unroll
+        for (int e = 0; e < D; ++e) {
+          float o = 0.0f;
+  #pragma unroll
+          for (int q = 0; q < D; ++q) o += raw[q] * L[q * D + e];
+          a.out3[((uint64_t)k * C + c0 + f) * D + e] = o;
+        }
       }
     }
   }
@@ -1416,52 +1500,93 @@ __host__ __device__ constexpr int ranges_per_particle(bool morton) {
   return morton ? Walker<D, P>::kCellRanges : Walker<D, P>::kRowRanges;
 }
 
-// List fill of lone particles with few candidates: one lane per particle,
-// walking its stored stencil ranges in turn (the row keeps stencil order).
+// ---- row allocation
+//
+// Rows hold a particle's in-radius neighbours only, allocated from one 64-bit
+// counter (`used`, zeroed before the fill): a unit of particles, or a wave of
+// lone particles, first counts its hits, then takes one block of the index
+// buffer with an atomic add and writes its rows there.  Row contents and
+// order (stencil order) are fixed; only where a row lands depends on the
+// order in which units reach the counter, which no result depends on.  A
+// row that does not fit below `cap` is not written: the particle's count is
+// set to -1 - (its stencil candidates) and the pair kernels walk its stencil
+// instead (stencil_candidate).  `used` ends as the total number of in-radius
+// pairs, stored or not.
+
+// Lone particles with few candidates: one lane per particle, its stored
+// stencil ranges walked twice (count, then write).
 template <int D, bool P, int R>
-__device__ __forceinline__ int32_t lane_fill_ranges(const GridParams& g, const float4* __restrict__ xw,
-                                                    const uint2* __restrict__ rp, const float* xi, int64_t pos,
-                                                    int64_t cap, int32_t* __restrict__ nidx) {
-  uint2 rg[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) rg[r] = rp[r];
-  int32_t cnt = 0;
+__device__ __forceinline__ uint64_t lane_fill_mask(const GridParams& g, const float4* __restrict__ xw,
+                                                   const uint2* __restrict__ rp, const float* xi) {
+  uint64_t mask = 0;
+  uint32_t pos = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    for (uint32_t j = rg[r].x; j < rg[r].y; ++j) {
+    const uint2 rg = rp[r];
+    for (uint32_t j = rg.x; j < rg.y; ++j, ++pos) {
       float xj[3], rr[3];
       unpack(xw[j], xj);
-      if (displacement<D, P>(g, xi, xj, rr) < g.eps2) {
-        if (pos < cap) nidx[pos] = (int32_t)j;
-        ++pos;
-        ++cnt;
-      }
+      if (displacement<D, P>(g, xi, xj, rr) < g.eps2) mask |= 1ull << pos;
     }
   }
-  return cnt;
+  return mask;
+}
+
+template <int R>
+__device__ __forceinline__ void lane_fill_write(const uint2* __restrict__ rp, uint64_t mask, uint64_t at,
+                                                int32_t* __restrict__ nidx) {
+  uint32_t pos = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint2 rg = rp[r];
+    for (uint32_t j = rg.x; j < rg.y; ++j, ++pos)
+      if ((mask >> pos) & 1ull) nidx[at++] = (int32_t)j;
+  }
 }
 
 template <int D, bool P>
 __global__ __launch_bounds__(kThreads) void k_lane_fill(GridParams g, const float4* __restrict__ xw,
-                                                        const int32_t* __restrict__ coff,
                                                         const int32_t* __restrict__ lane_len,
                                                         const uint2* __restrict__ ranges,
-                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ ncnt,
-                                                        int64_t cap) {
+                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
+                                                        int32_t* __restrict__ ncnt,
+                                                        unsigned long long* __restrict__ used, int64_t cap) {
   const uint32_t n = g.B * g.N;
-  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
-  if (k >= n || lane_len[k] < 0) return;
-  float xi[3];
-  unpack(xw[k], xi);
-  int32_t cnt;
-  if (g.morton) {
-    constexpr int R = Walker<D, P>::kCellRanges;
-    cnt = lane_fill_ranges<D, P, R>(g, xw, ranges + (uint64_t)k * R, xi, coff[k], cap, nidx);
-  } else {
-    constexpr int R = Walker<D, P>::kRowRanges;
-    cnt = lane_fill_ranges<D, P, R>(g, xw, ranges + (uint64_t)k * R, xi, coff[k], cap, nidx);
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+  const int32_t cand = k < n ? lane_len[k] : -1;  // lone particles have fewer than 64 candidates
+  const bool mine = cand >= 0;
+  const int R = ranges_per_particle<D, P>(g.morton != 0);
+  float xi[3] = {0.0f, 0.0f, 0.0f};
+  uint64_t mask = 0;
+  if (mine) {
+    unpack(xw[k], xi);
+    if (g.morton) mask = lane_fill_mask<D, P, Walker<D, P>::kCellRanges>(g, xw, ranges + (uint64_t)k * R, xi);
+    else mask = lane_fill_mask<D, P, Walker<D, P>::kRowRanges>(g, xw, ranges + (uint64_t)k * R, xi);
   }
-  ncnt[k] = (int32_t)max<int64_t>(0, min<int64_t>((int64_t)coff[k] + cnt, cap) - coff[k]);  // cut at the buffer's end
+  const uint32_t cnt = (uint32_t)__popcll(mask);
+  // one block of the index buffer for the wave's lone particles
+  const int lane = __lane_id();
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint32_t v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+  const uint32_t wtot = __shfl(incl, kWave - 1, kWave);
+  unsigned long long b = 0;
+  if (lane == 0 && wtot) b = atomicAdd(used, (unsigned long long)wtot);
+  b = __shfl(b, 0, kWave);
+  const uint64_t at = b + incl - cnt;
+  if (!mine) return;
+  if (at + cnt > (uint64_t)cap) {
+    nstart[k] = 0;
+    ncnt[k] = -1 - cand;
+    return;
+  }
+  if (g.morton) lane_fill_write<Walker<D, P>::kCellRanges>(ranges + (uint64_t)k * R, mask, at, nidx);
+  else lane_fill_write<Walker<D, P>::kRowRanges>(ranges + (uint64_t)k * R, mask, at, nidx);
+  nstart[k] = (int32_t)at;
+  ncnt[k] = (int32_t)cnt;
 }
 
 // Lane t's value of v (t wave-uniform).
@@ -1469,76 +1594,100 @@ __device__ __forceinline__ float lane_float(float v, uint32_t t) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)t));
 }
 
+// Wave-uniform cursor over a unit's stencil ranges (lane r holds range r):
+// `candidate` gives this lane's candidate of the next round of 64.
+struct RangeCursor {
+  uint32_t rlo, rhi;  // this lane's range (lanes < R)
+  int r, R;
+  uint32_t cj, cend;
+  __device__ __forceinline__ void reset() {
+    r = 0;
+    cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, 0);
+    cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, 0);
+    while (cj >= cend && ++r < R) {
+      cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
+      cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
+    }
+  }
+  // Candidate of this lane in the next round (valid = false past the stencil's end).
+  __device__ __forceinline__ uint32_t round(uint32_t lane, uint32_t fallback, bool& valid) {
+    uint32_t j = fallback;
+    valid = false;
+    uint32_t covered = 0;
+    while (covered < (uint32_t)kWave && r < R) {
+      const uint32_t take = min(cend - cj, (uint32_t)kWave - covered);
+      if (lane >= covered && lane < covered + take) {
+        j = cj + (lane - covered);
+        valid = true;
+      }
+      covered += take;
+      cj += take;
+      while (cj >= cend && ++r < R) {
+        cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
+        cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
+      }
+    }
+    return j;
+  }
+};
+
+// Ballots of the first kFillRounds rounds a wave keeps for the write pass.
+constexpr int kFillRounds = 48;
+
 // Cell-major neighbour-list fill: one wave per unit (up to kUnitParticles
 // consecutive particles of one cell, which share the cell's stencil).  The
 // wave walks the stencil ranges (stored by the unit's first particle) 64
 // candidates at a time, lane l taking the l-th candidate, and tests each
-// candidate against every particle of the unit, whose positions and next
-// list slots are wave-uniform values; a ballot ranks the in-radius
-// candidates, so each particle's row keeps stencil order.
+// candidate against every particle of the unit, whose positions are
+// wave-uniform values; a ballot per particle and round marks the in-radius
+// candidates.  Pass one counts them (keeping the ballots of the first
+// kFillRounds rounds in LDS), the unit then takes one block of the index
+// buffer, and pass two writes each particle's row in stencil order, ranking
+// the hits of a round with mbcnt.
 template <int D, bool P>
 __global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const float4* __restrict__ xw,
-                                                        const int32_t* __restrict__ coff,
+                                                        const int32_t* __restrict__ cand,
                                                         const uint2* __restrict__ ranges,
                                                         const uint2* __restrict__ units,
                                                         const int32_t* __restrict__ unit_total,
-                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ ncnt,
-                                                        int64_t cap) {
+                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
+                                                        int32_t* __restrict__ ncnt,
+                                                        unsigned long long* __restrict__ used, int64_t cap) {
+  __shared__ uint64_t ballots[kThreads / kWave][kFillRounds][kUnitParticles];
   const uint32_t total = (uint32_t)*unit_total;
   const uint32_t nwaves = gridDim.x * (kThreads / kWave);
   const uint32_t lane = (uint32_t)__lane_id();
-  const uint32_t cap32 = (uint32_t)min<int64_t>(cap, kMaxListEntries);  // byte offsets fit in 32 bits
+  const int wv = threadIdx.x >> 6;
   for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < total; u += nwaves) {
     const uint2 ud = units[u];
     const uint32_t i0 = __builtin_amdgcn_readfirstlane(ud.x);
     const uint32_t ni = __builtin_amdgcn_readfirstlane(ud.y);
     const uint32_t it = i0 + min(lane, ni - 1u);
     const float4 pt = xw[it];
-    const int32_t row0 = coff[it];
-    const int32_t ncand = __builtin_amdgcn_readfirstlane(coff[i0 + 1] - coff[i0]);
-    // wave-uniform copies: positions and next list slots of the unit's particles
+    const int32_t ncand = __builtin_amdgcn_readfirstlane(cand[i0]);
+    // wave-uniform copies of the unit's particle positions
     float xs[kUnitParticles][3];
-    uint32_t at[kUnitParticles];
 #pragma unroll
     for (int t = 0; t < kUnitParticles; ++t) {
       xs[t][0] = lane_float(pt.x, t);
       xs[t][1] = lane_float(pt.y, t);
       xs[t][2] = lane_float(pt.z, t);
-      at[t] = (uint32_t)__builtin_amdgcn_readlane(row0, t);
     }
-    // the stencil ranges of the unit's cell (stored by its first particle), lane r holding range r
-    const int R = ranges_per_particle<D, P>(g.morton != 0);
-    uint32_t rlo = 0, rhi = 0;
-    if ((int)lane < R) {
-      const uint2 rr = ranges[(uint64_t)i0 * R + lane];
-      rlo = rr.x;
-      rhi = rr.y;
+    RangeCursor rc;
+    rc.R = ranges_per_particle<D, P>(g.morton != 0);
+    rc.rlo = rc.rhi = 0;
+    if ((int)lane < rc.R) {
+      const uint2 rr = ranges[(uint64_t)i0 * rc.R + lane];
+      rc.rlo = rr.x;
+      rc.rhi = rr.y;
     }
-    // wave-uniform cursor over the ranges: position cj of range r, which ends at cend
-    int r = 0;
-    uint32_t cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, 0), cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, 0);
-    while (cj >= cend && ++r < R) {
-      cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
-      cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
-    }
-    for (int32_t base = 0; base < ncand; base += kWave) {
-      // candidate of this lane: position base + lane of the concatenated ranges
-      uint32_t j = i0;
-      bool valid = false;
-      uint32_t covered = 0;
-      while (covered < (uint32_t)kWave && r < R) {
-        const uint32_t take = min(cend - cj, (uint32_t)kWave - covered);
-        if (lane >= covered && lane < covered + take) {
-          j = cj + (lane - covered);
-          valid = true;
-        }
-        covered += take;
-        cj += take;
-        while (cj >= cend && ++r < R) {
-          cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
-          cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
-        }
-      }
+    // pass one: count, keeping the first rounds' ballots
+    uint32_t cnt[kUnitParticles] = {};
+    rc.reset();
+    int rd = 0;
+    for (int32_t base = 0; base < ncand; base += kWave, ++rd) {
+      bool valid;
+      const uint32_t j = rc.round(lane, i0, valid);
       float xj[3];
       unpack(xw[j], xj);
       if (!valid) xj[0] = __int_as_float(0x7FC00000);  // NaN: never in radius
@@ -1546,25 +1695,77 @@ __global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const floa
       for (int t = 0; t < kUnitParticles; ++t) {
         if (t < (int)ni) {
           float r[3];
-          const bool in = displacement<D, P>(g, xs[t], xj, r) < g.eps2;
-          const uint64_t m = __ballot(in);
-          const uint32_t rank =
-              __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          const uint32_t pos = at[t] + rank;
-          if (in && pos < cap32) *reinterpret_cast<int32_t*>(reinterpret_cast<char*>(nidx) + pos * 4u) = (int32_t)j;
-          at[t] += (uint32_t)__popcll(m);
+          const uint64_t m = __ballot(displacement<D, P>(g, xs[t], xj, r) < g.eps2);
+          if (rd < kFillRounds && lane == 0) ballots[wv][rd][t] = m;
+          cnt[t] += (uint32_t)__popcll(m);
         }
       }
     }
-    int32_t mine = 0;
+    // the unit's block of the index buffer
+    uint32_t tot = 0;
+#pragma unroll
+    for (int t = 0; t < kUnitParticles; ++t) tot += cnt[t];
+    unsigned long long b = 0;
+    if (lane == 0 && tot) b = atomicAdd(used, (unsigned long long)tot);
+    b = __shfl(b, 0, kWave);
+    if (b + tot > (unsigned long long)cap) {
+      if (lane < ni) {
+        nstart[i0 + lane] = 0;
+        ncnt[i0 + lane] = -1 - ncand;
+      }
+      continue;
+    }
+    uint64_t at[kUnitParticles];
+    {
+      uint64_t run = b;
+#pragma unroll
+      for (int t = 0; t < kUnitParticles; ++t) {
+        at[t] = run;
+        run += cnt[t];
+      }
+    }
+    int32_t mine_start = 0, mine_cnt = 0;
 #pragma unroll
     for (int t = 0; t < kUnitParticles; ++t)
-      if ((int)lane == t) mine = (int32_t)at[t];
-    // a row is cut at the buffer's end (the caller detects start[B*N] > cap
-    // and refills), so no traversal reads past the entries written
-    if (lane < ni) ncnt[i0 + lane] = max(0, min(mine, (int32_t)cap32) - row0);
+      if ((int)lane == t) {
+        mine_start = (int32_t)at[t];
+        mine_cnt = (int32_t)cnt[t];
+      }
+    // pass two: write the rows
+    rc.reset();
+    rd = 0;
+    for (int32_t base = 0; base < ncand; base += kWave, ++rd) {
+      bool valid;
+      const uint32_t j = rc.round(lane, i0, valid);
+      float xj[3];
+      if (rd >= kFillRounds) {
+        unpack(xw[j], xj);
+        if (!valid) xj[0] = __int_as_float(0x7FC00000);
+      }
+#pragma unroll
+      for (int t = 0; t < kUnitParticles; ++t) {
+        if (t < (int)ni) {
+          uint64_t m;
+          if (rd < kFillRounds) {
+            m = ballots[wv][rd][t];
+          } else {
+            float r[3];
+            m = __ballot(displacement<D, P>(g, xs[t], xj, r) < g.eps2);
+          }
+          const uint32_t rank =
+              __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          if ((m >> lane) & 1ull) nidx[at[t] + rank] = (int32_t)j;
+          at[t] += (uint64_t)__popcll(m);
+        }
+      }
+    }
+    if (lane < ni) {
+      nstart[i0 + lane] = mine_start;
+      ncnt[i0 + lane] = mine_cnt;
+    }
   }
 }
+
 
 }  // namespace pk
 }  // namespace sphops
@@ -1587,35 +1788,36 @@ void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
 
 constexpr uint32_t kPersistentWorkgroups = 2048;
 
-// Stencil candidate counts of every binned particle, exclusive-scanned into
-// coff (B*N+1, total in coff[B*N]), and the fill's work split, unit table
-// and stencil ranges in the grid's scratch (read by neighbour_fill).
+// Stencil candidate counts of every binned particle (g.cand), and the fill's
+// work split, unit table and stencil ranges in the grid's scratch (read by
+// neighbour_fill).
 template <int D, bool P>
-void neighbour_candidates(const Grid& g, const int32_t* bo, const float* x, int32_t* coff, hipStream_t st) {
+void neighbour_candidates(const Grid& g, const int32_t* bo, const float* x, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, coff,
+  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, g.cand,
                      g.sparse_len, g.unit_len, g.flags, g.ranges);
   SPHOPS_LAUNCHED();
-  exclusive_scan_u32(g, reinterpret_cast<uint32_t*>(coff), n, reinterpret_cast<uint32_t*>(coff) + n, st);
   run_unit_schedule(g, st);
 }
 
-// Fill the rows at coff: cells with several particles (and lone particles
-// with many candidates) cell-major, the other lone particles a lane each,
-// with the work split and ranges neighbour_candidates left in the grid.
+// Fill the rows (compact, allocated from the counter `used`): cells with
+// several particles (and lone particles with many candidates) cell-major,
+// the other lone particles a lane each, with the work split and ranges
+// neighbour_candidates left in the grid.
 template <int D, bool P>
-void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, const int32_t* coff, int32_t* nidx,
-                    int32_t* ncnt, int64_t cap, hipStream_t st) {
+void neighbour_fill(const Grid& g, const float* x, int32_t* nstart, int32_t* nidx, int32_t* ncnt,
+                    unsigned long long* used, int64_t cap, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_unit_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, coff,
-                     g.ranges, g.units, g.unit_total, nidx, ncnt, cap);
+  fill_u32(reinterpret_cast<uint32_t*>(used), 2, 0u, st);
+  hipLaunchKernelGGL((k_unit_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, g.cand,
+                     g.ranges, g.units, g.unit_total, nidx, nstart, ncnt, used, cap);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_lane_fill<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, g.packed, coff, g.sparse_len,
-                     g.ranges, nidx, ncnt, cap);
+  hipLaunchKernelGGL((k_lane_fill<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, g.packed, g.sparse_len,
+                     g.ranges, nidx, nstart, ncnt, used, cap);
   SPHOPS_LAUNCHED();
 }
 
@@ -1626,13 +1828,22 @@ inline uint32_t launch_groups(uint32_t waves) {
   return ((waves + per - 1) / per + 7u) & ~7u;
 }
 
+// Launch of a schedule whose wave count the kernel reads on the device
+// (`dev`): `waves` is only an estimate, and the kernels loop until every
+// live wave is served, so at least 64 workgroups go out even when the
+// estimate is zero.
+inline uint32_t schedule_groups(uint32_t waves, const int32_t* dev) {
+  const uint32_t w = launch_groups(waves);
+  return dev != nullptr ? std::max<uint32_t>(w, 64u) : w;
+}
+
 template <int D, bool P, class OP>
 void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
   const uint64_t n = g.n_keys;
   if (n == 0) return;
   pack_for<D, OP>(g, a, st);
   if (a.nidx != nullptr && a.waves != nullptr) {
-    const uint32_t wgs = launch_groups(a.nwaves);
+    const uint32_t wgs = schedule_groups(a.nwaves, a.nwaves_dev);
     if (wgs == 0) return;
     hipLaunchKernelGGL((k_pairs_grouped<D, P, OP>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else if (a.nidx != nullptr) {
@@ -1662,7 +1873,7 @@ inline bool row_offsets_fit_32(const Grid& g, uint32_t C) {
 template <int D, bool P>
 void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
-  const uint32_t wgs = launch_groups(a.nwaves2);
+  const uint32_t wgs = schedule_groups(a.nwaves2, a.nwaves2_dev);
   pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
   const bool off32 = row_offsets_fit_32(g, a.C);
@@ -1680,7 +1891,7 @@ void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
 // volumes already packed into a.xw).
 template <int D, bool P, bool FULL>
 void launch_blur_hybrid_bwd_quad_packed(const Grid& g, const OpPtrs& a, hipStream_t st) {
-  const uint32_t wgs = launch_groups(a.nwaves2);
+  const uint32_t wgs = schedule_groups(a.nwaves2, a.nwaves2_dev);
   if (wgs == 0) return;
   const bool off32 = row_offsets_fit_32(g, a.C);
   if (a.C == 16) {
@@ -1758,7 +1969,9 @@ template <int D, bool P, int CM, bool EX> using GradientBwdFullAcc = OpGradientB
 template <int D, bool P, int CM, bool EX> using GradientBwdDsAcc = OpGradientBwd<D, P, CM, EX, false, true>;
 
 template <int D, bool P>
-void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a_in, hipStream_t st) {
+  OpPtrs a = a_in;
+  a.bo = bo;
   switch (op) {
     case Op::Count: return launch_pairs<D, P, OpCount<D, P>>(g, bo, a, st);
     case Op::Density: return launch_pairs<D, P, OpDensity<D, P>>(g, bo, a, st);
@@ -1772,10 +1985,10 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
       if (split_ok(a)) return launch_blur_hybrid_fwd_quad<D, P>(g, a, st);
       return launch_channels<D, P, OpBlurGradientHybrid>(g, bo, a, st);
     case Op::NeighbourCandidates:
-      if (g.n_keys) neighbour_candidates<D, P>(g, bo, a.x, a.iout, st);
+      if (g.n_keys) neighbour_candidates<D, P>(g, bo, a.x, st);
       return;
     case Op::NeighbourFill:
-      if (g.n_keys) neighbour_fill<D, P>(g, bo, a.x, a.nptr, a.iout, a.iout2, a.cap, st);
+      if (g.n_keys) neighbour_fill<D, P>(g, a.x, a.iout3, a.iout, a.iout2, a.used, a.cap, st);
       return;
     case Op::NeighbourTiles:
       if (g.n_keys)
@@ -1788,7 +2001,9 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a, 
 }
 
 template <int D, bool P>
-void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
+void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a_in, hipStream_t st) {
+  OpPtrs a = a_in;
+  a.bo = bo;
   switch (op) {
     case Op::Density: return launch_pairs<D, P, OpDensityBwd<D, P>>(g, bo, a, st);
     case Op::DensityGradient: return launch_pairs<D, P, OpDensityGradientBwd<D, P>>(g, bo, a, st);

@@ -51,6 +51,7 @@ struct Grid {
   uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
   float4* packed = nullptr;       // B*N (x, y, z|0, weight) read by the pair kernels
   // work split of the neighbour-list fill:
+  int32_t* cand = nullptr;        // B*N: stencil candidates of each particle
   int32_t* sparse_len = nullptr;  // B*N: candidate count of particles filled a lane each, -1 for the others
   int32_t* unit_len = nullptr;    // B*N: particles of the unit starting at this particle, 0 if none starts here
   uint2* units = nullptr;         // B*N: unit descriptors {first particle, particles}
@@ -117,9 +118,12 @@ struct OpPtrs {
   float* out1 = nullptr;      // grad_s
   float* out2 = nullptr;      // grad_rho
   float* out3 = nullptr;      // second forward output (fused forward)
-  int32_t* iout = nullptr;    // candidate offsets / neighbour indices (list build)
+  int32_t* iout = nullptr;    // neighbour indices (list build)
   int32_t* iout2 = nullptr;   // neighbour counts (list build)
+  int32_t* iout3 = nullptr;   // list row starts (list build)
+  unsigned long long* used = nullptr;  // entries the fill asked for (list build)
   int64_t cap = 0;            // capacity of iout for the fill
+  const int32_t* bo = nullptr;     // bin_offsets (set by the dispatch; the stencil walk of unstored rows)
   const int32_t* nptr = nullptr;  // list row start per particle (B*N)
   const int32_t* ncnt = nullptr;  // list length per particle (B*N)
   const int32_t* nidx = nullptr;  // neighbour indices; non-null selects list traversal

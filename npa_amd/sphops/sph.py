@@ -110,23 +110,26 @@ class HashGrid:
                                 block_info=block_info, dim=self.dim, total_blocks=total_blocks)
 
     def set_capture_capacity(self, index_capacity):
-        """Make snapshots capturable in a HIP graph: neighbour lists of at most
-        ``index_capacity`` entries, built with no host synchronisation (no
-        counterpart in the reference, whose snapshots need no list).  0
-        restores the default.  See ``list_overflow``."""
+        """Fix the buffer and launch sizes of neighbour lists so that a step
+        can be captured in a HIP graph and replayed (no counterpart in the
+        reference, whose snapshots need no list): lists of at most
+        ``index_capacity`` entries.  Rows that do not fit are walked on the
+        stencil, with the same results.  0 restores the default sizing."""
         self.hashgrid.set_capture_capacity(index_capacity)
 
     def list_overflow(self):
-        """True if a list built in capture mode was cut at its capacity
-        (synchronises); ``reset_list_overflow`` clears the flag."""
+        """True if the last list did not store every row (its rows were
+        walked on the stencil instead; synchronises)."""
         return self.hashgrid.list_overflow()
 
     def reset_list_overflow(self):
         self.hashgrid.reset_list_overflow()
 
     def list_capacity_hint(self):
-        """Index capacity the last eager list build would give the next one
-        (its candidate total plus 1/8), or 0 before the first build."""
+        """Index capacity the next list build would get (the last total read
+        back plus 1/8), or 0 before any list was built.  Waits for the
+        last total to arrive."""
+        self.hashgrid._consume_readback(wait=True)
         return int(getattr(self.hashgrid, "_index_capacity", 0))
 
     def wrap_positions(self, x):

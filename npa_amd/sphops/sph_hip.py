@@ -76,6 +76,7 @@ class NeighborPlan(tuple):
         return super().__new__(cls, items)
 
     tiles = None
+    capacity = 0
 
 
 class _HashGridNative:
@@ -358,86 +359,113 @@ class _HashGridNative:
     # ---- generic operator interface with an optional neighbour list
     def neighbor_list(self, x_bin, bin_offsets):
         """In-radius neighbour list of the binned particles plus its
-        traversal schedule: ``(start (B*N+1,), count (B*N,), index, order
-        (B*N,), waves (2 words per wave), wave_count (host int), waves_split,
-        wave_count_split)``.  Row i is
-        ``index[start[i] : start[i] + count[i]]``; rows start at the scanned
-        stencil candidate counts, so ``index`` needs ``start[B*N]`` entries.
-        The index buffer is sized from the previous call's total and the
-        total is read back with the wave count (one synchronisation); the
-        fill is repeated in the rare case that the buffer was too small."""
+        traversal schedules, as a :class:`NeighborPlan`: ``(start (B*N,),
+        count (B*N,), index, order (B*N,), waves (2 words per wave), wave
+        launch estimate, waves_split, its estimate, device counts)``.  Row i
+        is ``index[start[i] : start[i] + count[i]]``; a particle whose row did
+        not fit in ``index`` has ``count = -1 - (its stencil candidates)``
+        and the operators walk its stencil instead, so results never depend
+        on the buffer sizes.  Nothing is read back synchronously: the index
+        capacity and the launch sizes are estimates from the previous
+        snapshot's totals, copied to the host asynchronously; the kernels
+        read the true wave counts on the device."""
         x = self._pos(x_bin, "binned_positions")
         bo = self._offsets(bin_offsets)
         dev = x_bin.device
         n = self._b * self._n
         st = _stream(x_bin)
-        start = torch.empty(n + 1, dtype=_I32, device=dev)
+        capturing = torch.cuda.is_current_stream_capturing()
+        if not capturing:
+            self._consume_readback()
+        start = torch.empty(max(n, 1), dtype=_I32, device=dev)
         count = torch.empty(max(n, 1), dtype=_I32, device=dev)
         order = torch.empty(max(n, 1), dtype=_I32, device=dev)
         wcap = 2 * max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 1)
         waves = torch.empty(wcap, dtype=_I32, device=dev)
         waves2 = torch.empty(wcap, dtype=_I32, device=dev)
-        small = torch.empty(5, dtype=_I32, device=dev)
+        # device counts: [0:2] in-radius pairs (int64), [2] waves, [3] split
+        # waves, [4] tile units, [5] waves of the particles outside the tiles
+        small = torch.zeros(8, dtype=_I32, device=dev)
+        cap = self._capacity(n)
+        index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
         tiles = self._tile_buffers(dev, n, wcap) if self.tiles_enabled else None
+        _check(_lib.sphops_neighbor_candidates(self._h, x, bo, st))
+        _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
+                                         ctypes.c_void_p(index.data_ptr()), cap, ctypes.c_void_p(count.data_ptr()),
+                                         ctypes.c_void_p(small.data_ptr()), st))
+        _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
+                                             ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
+                                             ctypes.c_void_p(small.data_ptr() + 8), ctypes.c_void_p(waves2.data_ptr()),
+                                             ctypes.c_void_p(small.data_ptr() + 12), st))
+        if tiles is not None:
+            # after the fill: the tile build reuses the grid scratch that holds
+            # the fill's work split
+            _check(_lib.sphops_neighbor_tiles(
+                self._h, x, bo, ctypes.c_void_p(count.data_ptr()), ctypes.c_void_p(tiles[0].data_ptr()),
+                ctypes.c_void_p(small.data_ptr() + 16), ctypes.c_void_p(tiles[1].data_ptr()),
+                ctypes.c_void_p(tiles[2].data_ptr()), ctypes.c_void_p(small.data_ptr() + 20), st))
+        if not capturing:
+            self._start_readback(small)
+        e1, e2, e3 = self._wave_estimates(n)
+        plan = NeighborPlan(start, count, index, order, waves, e1, waves2, e2, small)
+        plan.capacity = cap
+        if tiles is not None:
+            plan.tiles = (tiles[0], small[4:5], tiles[1], tiles[2], e3, small[5:6])
+        self._last_plan = plan
+        return plan
 
-        def candidates():
-            _check(_lib.sphops_neighbor_candidates(self._h, x, bo, ctypes.c_void_p(start.data_ptr()), st))
+    # Largest index buffer (entries) a snapshot allocates; rows that do not
+    # fit are walked on the stencil instead.  At most 2^30 (the library's
+    # limit).
+    max_list_entries = 1 << 30
+    # Index entries per particle for a grid's first snapshot, before any
+    # total has been read back.
+    first_capacity_per_particle = 40
 
-        def build_tiles():
-            # after the last fill: the tile build reuses the grid scratch that
-            # holds the fill's work split
-            if tiles is not None:
-                _check(_lib.sphops_neighbor_tiles(
-                    self._h, x, bo, ctypes.c_void_p(count.data_ptr()), ctypes.c_void_p(tiles[0].data_ptr()),
-                    ctypes.c_void_p(small.data_ptr() + 12), ctypes.c_void_p(tiles[1].data_ptr()),
-                    ctypes.c_void_p(tiles[2].data_ptr()), ctypes.c_void_p(small.data_ptr() + 16), st))
-
-        candidates()
+    def _capacity(self, n):
         fixed = getattr(self, "_capture_capacity", 0)
         if fixed:
-            return self._neighbor_list_fixed(x, bo, start, count, order, waves, waves2, small, fixed, st,
-                                             build_tiles, tiles)
-        prev = getattr(self, "_index_capacity", 0)
-        limit = self.max_list_entries
-        cap = min(prev if prev else int(start[n].item()), limit)
-        index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
+            return fixed
+        est = getattr(self, "_index_capacity", 0)
+        if not est:
+            est = self.first_capacity_per_particle * max(n, 1)
+        return int(min(est, self.max_list_entries))
 
-        def fill(buf, capacity):
-            _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
-                                             ctypes.c_void_p(buf.data_ptr()), capacity,
-                                             ctypes.c_void_p(count.data_ptr()), st))
+    def _wave_estimates(self, n):
+        bounds = getattr(self, "_wave_bounds", None)
+        if getattr(self, "_capture_capacity", 0) and bounds:
+            return bounds
+        hint = getattr(self, "_wave_counts", None)
+        if hint:
+            return tuple(int(c) + c // 16 + 8 for c in hint)
+        first = max(n // 8, 1)
+        return (first, first, first)
 
-        def schedule():
-            _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
-                                                 ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
-                                                 ctypes.c_void_p(small.data_ptr() + 4),
-                                                 ctypes.c_void_p(waves2.data_ptr()),
-                                                 ctypes.c_void_p(small.data_ptr() + 8), st))
-            build_tiles()
-            small[0:1].copy_(start[n:n + 1])
-            return small.cpu().tolist()
+    def _start_readback(self, small):
+        """Copy the device counts to pinned host memory without waiting."""
+        rb = getattr(self, "_rb", None)
+        if rb is None:
+            self._rb = rb = torch.empty(8, dtype=_I32, pin_memory=True)
+        rb.copy_(small, non_blocking=True)
+        self._rb_event = torch.cuda.Event()
+        self._rb_event.record()
 
-        fill(index, cap)
-        total, nwaves, nwaves2, nunits, nwaves_s = schedule()
-        if total > limit:
-            # too large to store: the operators scan the stencil instead
-            return None
-        if total > cap:
-            # the first fill cut rows at the buffer's end (their counts too), so
-            # fill again (after the candidates pass that sets up the fill's
-            # work split again) and schedule from the full counts
-            cap = total
-            index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
-            candidates()
-            fill(index, cap)
-            total, nwaves, nwaves2, nunits, nwaves_s = schedule()
-        if total > prev:  # ~12% headroom, so that the next snapshot of a moving cloud fits
-            self._index_capacity = total + total // 8
-        self._wave_counts = (nwaves, nwaves2, nwaves_s)
-        plan = NeighborPlan(start, count, index, order, waves, nwaves, waves2, nwaves2)
-        if tiles is not None:
-            plan.tiles = (tiles[0], small[3:4], tiles[1], tiles[2], nwaves_s, small[4:5])
-        return plan
+    def _consume_readback(self, wait=False):
+        """Take the counts of an earlier snapshot once they have arrived
+        (waits only with ``wait``): they size the next index buffer and
+        launches."""
+        ev = getattr(self, "_rb_event", None)
+        if ev is None:
+            return
+        if wait:
+            ev.synchronize()
+        elif not ev.query():
+            return
+        v = self._rb.tolist()
+        total = (v[0] & 0xFFFFFFFF) | (v[1] << 32)
+        self._index_capacity = total + total // 8 + 1024
+        self._wave_counts = (v[2], v[3], v[5])
+        self._rb_event = None
 
     # Cell tiles for the pass-B backward (sphops_neighbor_tiles): opt-in
     # (NPA_SPHOPS_TILES=1, or this attribute), because at cfg5 the tiled
@@ -450,66 +478,40 @@ class _HashGridNative:
         return (torch.empty(2 * cap, dtype=_I32, device=dev), torch.empty(max(n, 1), dtype=_I32, device=dev),
                 torch.empty(wcap, dtype=_I32, device=dev))
 
-    # Largest neighbour list (index entries = stencil candidates) a snapshot
-    # builds; above it neighbor_list returns None and the operators scan the
-    # cell stencil directly (no list memory, slower).  At most 2^30, the
-    # library's limit (32-bit byte offsets into the index buffer).
-    max_list_entries = 1 << 30
-
     def set_capture_capacity(self, index_capacity, wave_margin=1.25):
-        """Build neighbour lists with no host synchronisation, so that a whole
-        step can be captured in a HIP graph (``torch.cuda.graph``): every list
-        gets an index buffer of ``index_capacity`` entries, and the pair
-        kernels read their wave counts on the device.  Their launches are
-        sized for ``wave_margin`` times the wave counts of the last eager list
-        build (the whole wave capacity if there was none).  A list whose
-        candidate total exceeds the index capacity is cut at the buffer's end,
-        and waves beyond a launch are not run: both are memory-safe, give
-        wrong results and raise the flag that ``list_overflow`` returns.
-        ``index_capacity = 0`` returns to the default: the totals are read
-        back once per snapshot and buffers and launches sized from them.  Call
-        it outside the capture: it allocates the flag."""
+        """Fix the sizes a list build uses, so that a whole step can be
+        captured in a HIP graph (``torch.cuda.graph``) and replayed: every
+        list gets an index buffer of ``index_capacity`` entries, and the pair
+        kernels launch for ``wave_margin`` times the wave counts of the last
+        eager build (the kernels read the true counts on the device and
+        serve every wave whatever the launch).  Rows that do not fit are
+        walked on the stencil (slower, same results); ``list_overflow`` tells
+        whether that happened.  ``index_capacity = 0`` returns to the
+        default sizing from the read-back totals."""
+        self._consume_readback(wait=True)
         self._capture_capacity = max(int(index_capacity), 0)
         if self._capture_capacity > self.max_list_entries:
             raise RuntimeError(f"index_capacity above max_list_entries ({self.max_list_entries})")
         if self._capture_capacity:
-            self._overflow = torch.zeros(1, dtype=_I32, device=torch.device("cuda", torch.cuda.current_device()))
             cap = max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 0)
             hint = getattr(self, "_wave_counts", None)
-            self._wave_bounds = tuple(min(cap, int(c * wave_margin) + 64) for c in hint) if hint else (cap, cap, cap)
+            n = self._b * self._n
+            self._wave_bounds = (tuple(min(cap, int(c * wave_margin) + 64) for c in hint) if hint
+                                 else (max(n // 8, 1),) * 3)
 
     def list_overflow(self):
-        """True if a list built since set_capture_capacity (or the last
-        reset_list_overflow) was cut at the index capacity.  Reads the flag
-        back (synchronises)."""
-        flag = getattr(self, "_overflow", None)
-        return bool(flag is not None and int(flag.item()) != 0)
+        """True if the last list built did not store every row (its total
+        exceeded the index capacity; those rows were walked on the stencil).
+        Reads the total back (synchronises)."""
+        plan = getattr(self, "_last_plan", None)
+        if plan is None:
+            return False
+        v = plan[8][:2].cpu().tolist()
+        total = (v[0] & 0xFFFFFFFF) | (v[1] << 32)
+        return total > plan.capacity
 
     def reset_list_overflow(self):
-        if getattr(self, "_overflow", None) is not None:
-            self._overflow.zero_()
-
-    def _neighbor_list_fixed(self, x, bo, start, count, order, waves, waves2, small, cap, st, build_tiles, tiles):
-        n = self._b * self._n
-        index = torch.empty(cap, dtype=_I32, device=start.device)
-        _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
-                                         ctypes.c_void_p(index.data_ptr()), cap,
-                                         ctypes.c_void_p(count.data_ptr()), st))
-        _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
-                                             ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
-                                             ctypes.c_void_p(small.data_ptr() + 4), ctypes.c_void_p(waves2.data_ptr()),
-                                             ctypes.c_void_p(small.data_ptr() + 8), st))
-        build_tiles()
-        # flag |= total > cap or a wave count above its launch, on the device
-        b1, b2, b3 = self._wave_bounds
-        torch.maximum(self._overflow, (start[n:n + 1] > cap).to(_I32), out=self._overflow)
-        torch.maximum(self._overflow, (small[1:2] > b1).to(_I32), out=self._overflow)
-        torch.maximum(self._overflow, (small[2:3] > b2).to(_I32), out=self._overflow)
-        plan = NeighborPlan(start, count, index, order, waves, b1, waves2, b2, small)
-        if tiles is not None:
-            torch.maximum(self._overflow, (small[4:5] > b3).to(_I32), out=self._overflow)
-            plan.tiles = (tiles[0], small[3:4], tiles[1], tiles[2], b3, small[4:5])
-        return plan
+        self._last_plan = None
 
     # Per operator: trailing dims of (first output, second output) after (B, N);
     # "C" stands for the channel count, "D" for the spatial dimension.
@@ -564,9 +566,9 @@ class _HashGridNative:
                 a.nbr_order, a.nbr_waves, a.nbr_wave_count = nbr[3].data_ptr(), nbr[4].data_ptr(), nbr[5]
             if len(nbr) > 6:
                 a.nbr_waves_split, a.nbr_wave_count_split = nbr[6].data_ptr(), nbr[7]
-            if len(nbr) > 8 and nbr[8] is not None:  # capture mode: the wave counts stay on the device
-                a.nbr_wave_count_device = nbr[8].data_ptr() + 4
-                a.nbr_wave_count_split_device = nbr[8].data_ptr() + 8
+            if len(nbr) > 8 and nbr[8] is not None:  # the wave counts on the device
+                a.nbr_wave_count_device = nbr[8].data_ptr() + 8
+                a.nbr_wave_count_split_device = nbr[8].data_ptr() + 12
             tiles = getattr(nbr, "tiles", None)
             if tiles is not None:
                 a.tile_units, a.tile_unit_count = tiles[0].data_ptr(), tiles[1].data_ptr()

@@ -109,7 +109,9 @@ class Pairs:
     """In-radius pairs grouped by query.  ``q`` indexes the query list,
     ``i``/``j`` are flat binned indices (``b*N + slot``), ``r`` is the fp32
     displacement ``x_j - x_i`` and ``rb`` the fp32 displacement ``x_i - x_j``
-    (both wrapped), ``starts`` the first pair of each query."""
+    (both wrapped), ``starts`` the first pair of each query, ``ncand`` the
+    number of stencil candidates (particles in the query's 3^D cells) of
+    each query."""
     q: np.ndarray
     i: np.ndarray
     j: np.ndarray
@@ -117,6 +119,7 @@ class Pairs:
     rb: np.ndarray
     starts: np.ndarray
     queries: np.ndarray
+    ncand: np.ndarray = None
 
 
 def candidate_pairs(xb, bin_offsets, spec, queries=None):
@@ -159,4 +162,4 @@ def candidate_pairs(xb, bin_offsets, spec, queries=None):
     rb = displacement_f32(flat[j], flat[i], spec)
     counts = np.bincount(qidx, minlength=Q)
     starts = np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.int64)
-    return Pairs(q=qidx, i=i, j=j, r=r, rb=rb, starts=starts, queries=queries)
+    return Pairs(q=qidx, i=i, j=j, r=r, rb=rb, starts=starts, queries=queries, ncand=cnt.sum(axis=1))

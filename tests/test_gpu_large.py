@@ -44,7 +44,7 @@ def test_64bit_row_offsets_match_per_cloud_runs():
     g2 = grid_for(2)
     for _ in range(2):  # the second step runs the fused passes
         both = _step(sp, g2, x, s, ups)
-    assert g2.hashgrid._wave_counts is not None
+    assert g2.list_capacity_hint() > 0
     del g2
     names = ["blur", "gradient_hybrid", "density_gradient", "rho", "dL/dx", "dL/ds"]
     for b in range(2):

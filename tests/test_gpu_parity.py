@@ -339,7 +339,10 @@ def test_backward(name):
 def test_neighbor_list(name):
     """The per-snapshot list holds exactly the oracle's in-radius pairs of
     every particle (as sets; the row order is the stencil traversal order),
-    also when the index buffer was sized too small and the fill is redone."""
+    in compact rows that do not overlap.  A row that does not fit the index
+    buffer is not stored and its count encodes -1 - (stencil candidates):
+    forced with a tiny buffer, then gone once the grid sizes the buffer from
+    the total it read back."""
     import npa_amd.sphops as sp
     c, res, ora = run(name)
     grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
@@ -348,31 +351,39 @@ def test_neighbor_list(name):
     xb, bo = dev(res["xb"]), dev(res["bo"])
     p = ora["ctx"].p
     q = p.queries
-    ref = np.lexsort((p.j, p.q))
-    ref_q, ref_j = p.q[ref], p.j[ref]
+    ref_cnt = np.bincount(p.q, minlength=len(q))
 
     def check(nbr, label):
         start, count, index = (t.cpu().numpy() for t in nbr[:3])
-        np.testing.assert_array_equal(count[q], np.bincount(p.q, minlength=len(q)), err_msg=label)
-        gq = np.repeat(np.arange(len(q)), count[q])
-        gj = np.concatenate([index[start[k]:start[k] + count[k]] for k in q]) if len(q) else np.zeros(0)
+        total = int(nbr[8][:2].cpu().view(torch.int64).item())
+        assert total == int(ora["count"][0].sum()) or len(q) < c.B * c.N, label
+        stored = count[q] >= 0
+        np.testing.assert_array_equal(count[q][~stored], -1 - p.ncand[~stored], err_msg=label)
+        np.testing.assert_array_equal(count[q][stored], ref_cnt[stored], err_msg=label)
+        qs = np.flatnonzero(stored)
+        sel = np.isin(p.q, qs)
+        gq = np.repeat(qs, count[q][qs])
+        gj = np.concatenate([index[start[k]:start[k] + count[k]] for k in q[qs]]) if len(qs) else np.zeros(0)
         o = np.lexsort((gj, gq))
-        np.testing.assert_array_equal(gq[o], ref_q, err_msg=label)
-        np.testing.assert_array_equal(gj[o], ref_j, err_msg=label)
-        assert np.all(start[1:] >= start[:-1] + count), label   # rows do not overlap
-        assert nbr[5] > 0 or c.B * c.N == 0
+        r = np.lexsort((p.j[sel], p.q[sel]))
+        np.testing.assert_array_equal(gq[o], p.q[sel][r], err_msg=label)
+        np.testing.assert_array_equal(gj[o], p.j[sel][r], err_msg=label)
+        # the stored rows of all particles lie inside the buffer and do not overlap
+        allc = count[: c.B * c.N]
+        ks = np.flatnonzero(allc > 0)
+        lo, hi = start[ks], start[ks] + allc[ks]
+        so = np.argsort(lo)
+        assert np.all(lo >= 0) and np.all(hi <= nbr.capacity), label
+        assert np.all(lo[so][1:] >= hi[so][:-1]), label
+        return stored.all()
 
-    first = hg.neighbor_list(xb, bo)
-    check(first, f"{name}:first")
-    hg._index_capacity = 7            # force the too-small buffer and the second fill
-    nbr = hg.neighbor_list(xb, bo)
-    check(nbr, f"{name}:refill")
-    assert hg._index_capacity >= int(nbr[0][-1].item())
-    # the schedule comes from the full counts, as without the refill
-    assert nbr[5] == first[5] and nbr[7] == first[7]
-    assert torch.equal(nbr[3], first[3])
-    assert torch.equal(nbr[4][:2 * nbr[5]], first[4][:2 * first[5]])
-    assert torch.equal(nbr[6][:2 * nbr[7]], first[6][:2 * first[7]])
+    check(hg.neighbor_list(xb, bo), f"{name}:first")
+    hg.max_list_entries = 7  # a tiny buffer: almost no row is stored
+    check(hg.neighbor_list(xb, bo), f"{name}:tiny")
+    del hg.max_list_entries
+    torch.cuda.synchronize()
+    hg._consume_readback()
+    assert check(hg.neighbor_list(xb, bo), f"{name}:sized"), f"{name}: rows missing after sizing"
 
 
 @pytest.mark.parametrize("name", NAMES)
