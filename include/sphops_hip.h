@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 15
+#define SPHOPS_ABI_VERSION 16
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -227,23 +227,27 @@ int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, voi
 int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLdrho, const sphops_args* args,
                     void* stream);
 
-/* First step of the neighbour list: for every binned particle its 3^D cell
- * stencil (the cells the reference traverses) and the split of the fill's
- * work, left in the grid's scratch for sphops_neighbor_fill. */
+/* First step of the neighbour list: the split of the fill's work (units of
+ * up to 8 particles of one cell with two or more particles, which share the
+ * cell's 3^D stencil, the cells the reference traverses; particles alone in
+ * their cell), left in the grid's scratch for sphops_neighbor_fill. */
 int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bin_offsets, void* stream);
 
 /* In-radius neighbours (pairs |r| < eps incl. self) of every binned particle,
  * in stencil order: row i is nbr_index[nbr_start[i] .. nbr_start[i] +
  * nbr_count[i]) (nbr_start and nbr_count have B*N entries).  Rows are
- * compact, allocated in blocks from a counter, so nbr_index needs the number
- * of in-radius pairs, which *nbr_total (one device int64) receives -- also
- * when it exceeds index_capacity.  A row that does not fit below
- * index_capacity is not stored: its nbr_count is -1 - (the particle's stencil
- * candidates), and every operator walks that particle's stencil instead, so
- * results never depend on the capacity (a caller sizes the next snapshot's
- * buffer from *nbr_total, read back whenever convenient).  Where a row lands
- * depends on the order blocks are taken; rows, their order and all results do
- * not.  index_capacity is at most 2^30.  Must follow
+ * compact, allocated in blocks from counters that each own an equal slice of
+ * nbr_index (up to 256 slices of at least 2^15 entries), so nbr_index needs
+ * the number of in-radius pairs plus a margin for uneven slices.  nbr_total
+ * (two device int64) receives the number of in-radius pairs, stored or not,
+ * and the number of pairs in rows that were not stored (0: the list is
+ * complete).  A row that does not fit in its slice is not stored: its
+ * nbr_count is -1 - (the particle's stencil candidates), and every operator
+ * walks that particle's stencil instead, so results never depend on the
+ * capacity (a caller sizes the next snapshot's buffer from nbr_total, read
+ * back whenever convenient).  Where a row lands depends on the order blocks
+ * are taken; rows, their order and all results do not.  index_capacity is at
+ * most 2^30.  Must follow
  * sphops_neighbor_candidates on the same grid with the same x and bin_offsets
  * (checked by pointer; their contents must not change in between), with no
  * other candidates call on that grid in between. */

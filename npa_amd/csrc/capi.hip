@@ -129,7 +129,6 @@ void setup_grid(Grid& g, int dim, int boundary, int mode, const int32_t* grid_si
   g.n_cells = BG;
   g.n_tiles = (BN + 4095) / 4096;
   g.n_chunks = (BG + 1 + 1023) / 1024;
-  g.n_ranges = g.particle_mode ? (dim == 2 ? 9 : 27) : (dim == 2 ? 3 : 9) * (g.periodic ? 2 : 1);
 }
 
 void free_grid(Grid* g) {
@@ -145,12 +144,11 @@ void free_grid(Grid* g) {
   (void)hipFree(g->chunk_lo);
   (void)hipFree(g->flags);
   (void)hipFree(g->packed);
-  (void)hipFree(g->cand);
   (void)hipFree(g->sparse_len);
   (void)hipFree(g->unit_len);
   (void)hipFree(g->units);
   (void)hipFree(g->unit_total);
-  (void)hipFree(g->ranges);
+  (void)hipFree(g->stripes);
   delete g;
 }
 
@@ -279,12 +277,11 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
       g->flags = dalloc<uint32_t>(BN + 1);
       g->packed = dalloc<float4>(BN);
-      g->cand = dalloc<int32_t>(BN);
       g->sparse_len = dalloc<int32_t>(BN);
       g->unit_len = dalloc<int32_t>(BN);
       g->units = dalloc<uint2>(BN);
       g->unit_total = dalloc<int32_t>(1);
-      g->ranges = dalloc<uint2>(BN * (uint64_t)g->n_ranges);
+      g->stripes = dalloc<unsigned long long>((uint64_t)sphops::kFillStripes * sphops::kStripeWords);
     } catch (...) {
       sphops::free_grid(g);
       throw;
@@ -660,7 +657,7 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
     require(index_capacity <= sphops::kMaxListEntries, "index_capacity above 2^30 entries");
     const hipStream_t st = sphops::as_stream(stream);
     if (grid->n_keys == 0) {
-      sphops::fill_u32(reinterpret_cast<uint32_t*>(nbr_total), 2, 0u, st);
+      sphops::fill_u32(reinterpret_cast<uint32_t*>(nbr_total), 4, 0u, st);
       return;
     }
     require(nbr_start != nullptr && nbr_count != nullptr && (nbr_index != nullptr || index_capacity == 0),

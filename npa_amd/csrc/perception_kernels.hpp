@@ -1422,79 +1422,39 @@ __global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g,
 
 // ------------------------------------------------- neighbour-list build
 //
-// Candidates of particle k = the concatenation of its stencil ranges.  The
-// count and fill passes serve k with a group of G lanes (G by candidate-count
-// class): lane `sub` tests candidate positions sub, sub+G, ...  The fill
-// ranks each round's in-radius hits by ballot inside the group, so the list
-// keeps stencil order.  Both kernels are persistent: the grid is fixed and
-// waves loop over work units computed from the device-side class sizes.
+// Row i of the list holds particle i's in-radius neighbours in stencil order:
+// the order of the concatenated stencil ranges Walker::fetch(0), fetch(1), ...
+// visits.  Work split (k_fill_split, then run_unit_schedule): the particles
+// of a cell with two or more particles form units, runs of up to
+// kUnitParticles consecutive particles of one cell, which share the cell's
+// stencil; a particle alone in its cell is "lone".  k_fill serves every unit
+// with one wave, then every chunk of 64 consecutive particles for its lone
+// members, a lane each (a wave for a lone particle with many candidates).
 
-// Stencil ranges of a particle's cell, all fetched before any is used so
-// that their loads overlap; range r is the one Walker::fetch(r) visits.
-template <int D, bool P, int R>
-__device__ __forceinline__ uint32_t fetch_ranges(const GridParams& g, const int32_t* __restrict__ bo,
-                                                 Walker<D, P>& w, uint2 (&rg)[R]) {
-  uint32_t total = 0;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    w.fetch(g, bo, r);
-    rg[r] = make_uint2(w.j, w.jend);
-    total += w.jend - w.j;
-  }
-  return total;
-}
-
-// Candidate count of every binned particle and the work split of the list
-// fill.  Cells with at least two particles, and lone particles with at least
-// kLaneMaxCand candidates, are filled cell-major by k_unit_fill (unit_len and
-// flags mark the first particle of every run of kUnitParticles particles of
-// the cell); the other lone particles by k_lane_fill (lane_len = candidate
-// count, -1 elsewhere).  The first particle of every unit, and every lone
-// particle, stores its cell's stencil ranges (ranges[k * R + r]).
-template <int D, bool P, int R>
-__device__ __forceinline__ void candidates_of(const GridParams& g, const int32_t* __restrict__ bo, uint32_t k,
-                                              const float* xi, int32_t* __restrict__ cand,
-                                              int32_t* __restrict__ lane_len, int32_t* __restrict__ unit_len,
-                                              uint32_t* __restrict__ flags, uint2* __restrict__ ranges) {
-  Walker<D, P> w;
-  w.init(g, xi, k);
-  uint2 rg[R];
-  const int32_t total = (int32_t)fetch_ranges<D, P, R>(g, bo, w, rg);
-  const uint32_t h = w.base + cell_hash<D>(g, w.c);
-  const int32_t cs = bo[h], ce = bo[h + 1];
-  const bool unit = ce - cs >= 2 || total >= kLaneMaxCand;
-  const int32_t off = (int32_t)k - cs;
-  const bool first = off % kUnitParticles == 0;
-  const int32_t ul = (unit && first) ? min(kUnitParticles, ce - (int32_t)k) : 0;
-  cand[k] = total;
-  lane_len[k] = unit ? -1 : total;
-  unit_len[k] = ul;
-  flags[k] = ul > 0 ? 1u : 0u;
-  if (first) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) ranges[(uint64_t)k * R + r] = rg[r];
-  }
-}
-
+// unit_len[k] = particles of the unit starting at k (> 0), 0 for the other
+// particles of a cell with two or more, -1 for a lone particle; flags[k] = 1
+// where a unit starts (scanned by run_unit_schedule).
 template <int D, bool P>
-__global__ __launch_bounds__(kThreads) void k_candidates(GridParams g, const int32_t* __restrict__ bo,
-                                                         const float4* __restrict__ xw, int32_t* __restrict__ cand,
-                                                         int32_t* __restrict__ lane_len,
-                                                         int32_t* __restrict__ unit_len, uint32_t* __restrict__ flags,
-                                                         uint2* __restrict__ ranges) {
+__global__ __launch_bounds__(kThreads) void k_fill_split(GridParams g, const int32_t* __restrict__ bo,
+                                                         const float* __restrict__ x,
+                                                         int32_t* __restrict__ unit_len,
+                                                         uint32_t* __restrict__ flags) {
   const uint32_t n = g.B * g.N;
-  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
+  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
   if (k >= n) return;
   float xi[3];
-  unpack(xw[k], xi);
-  if (g.morton) {
-    candidates_of<D, P, Walker<D, P>::kCellRanges>(g, bo, k, xi, cand, lane_len, unit_len, flags, ranges);
-  } else {
-    candidates_of<D, P, Walker<D, P>::kRowRanges>(g, bo, k, xi, cand, lane_len, unit_len, flags, ranges);
-  }
+  load_pos<D>(x, k, xi);
+  Walker<D, P> w;
+  w.init(g, xi, k);
+  const uint32_t h = w.base + cell_hash<D>(g, w.c);
+  const int32_t cs = bo[h], ce = bo[h + 1];
+  const int32_t off = (int32_t)k - cs;
+  const int32_t ul = ce - cs < 2 ? -1 : off % kUnitParticles == 0 ? min(kUnitParticles, ce - (int32_t)k) : 0;
+  unit_len[k] = ul;
+  flags[k] = ul > 0 ? 1u : 0u;
 }
 
-// Stencil ranges per particle in the grid's range table.
+// Stencil ranges per particle.
 template <int D, bool P>
 __host__ __device__ constexpr int ranges_per_particle(bool morton) {
   return morton ? Walker<D, P>::kCellRanges : Walker<D, P>::kRowRanges;
@@ -1502,267 +1462,377 @@ __host__ __device__ constexpr int ranges_per_particle(bool morton) {
 
 // ---- row allocation
 //
-// Rows hold a particle's in-radius neighbours only, allocated from one 64-bit
-// counter (`used`, zeroed before the fill): a unit of particles, or a wave of
-// lone particles, first counts its hits, then takes one block of the index
-// buffer with an atomic add and writes its rows there.  Row contents and
-// order (stencil order) are fixed; only where a row lands depends on the
-// order in which units reach the counter, which no result depends on.  A
-// row that does not fit below `cap` is not written: the particle's count is
-// set to -1 - (its stencil candidates) and the pair kernels walk its stencil
-// instead (stencil_candidate).  `used` ends as the total number of in-radius
-// pairs, stored or not.
-
-// Lone particles with few candidates: one lane per particle, its stored
-// stencil ranges walked twice (count, then write).
-template <int D, bool P, int R>
-__device__ __forceinline__ uint64_t lane_fill_mask(const GridParams& g, const float4* __restrict__ xw,
-                                                   const uint2* __restrict__ rp, const float* xi) {
-  uint64_t mask = 0;
-  uint32_t pos = 0;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint2 rg = rp[r];
-    for (uint32_t j = rg.x; j < rg.y; ++j, ++pos) {
-      float xj[3], rr[3];
-      unpack(xw[j], xj);
-      if (displacement<D, P>(g, xi, xj, rr) < g.eps2) mask |= 1ull << pos;
+// Rows hold a particle's in-radius neighbours only.  A unit of particles, or
+// a wave's lone particles, first counts its hits, then takes one block of
+// the index buffer with an atomic add on a 64-bit counter and writes its rows
+// there.  The buffer is cut into S equal slices of `slen` entries (S a power
+// of two, smask = S - 1), slice s allocated by the counter at
+// stripes[s * kStripeWords], zeroed before the fill; wave w takes its blocks
+// from slice w & smask, or, when a block does not fit there, from one of the
+// next kFillProbes - 1 slices.  Row contents and order (stencil order) are
+// fixed; only where a row lands depends on the order in which blocks reach a
+// counter, which no result depends on.  A block that fits nowhere is not
+// written: its particles' counts are set to -1 - (their stencil candidates)
+// and the pair kernels walk their stencils instead (stencil_candidate).
+// Counter words: [0] entries taken (a failed attempt's block included), [1]
+// entries of failed attempts, [2] entries of blocks not written.
+constexpr uint32_t kFillProbes = 4;
+struct FillStripes {
+  unsigned long long* ctr;  // kFillStripes * kStripeWords
+  uint32_t smask;
+  uint64_t slen;
+  // Block of `need` entries for wave `wave` (lane 0's value is used, the
+  // result is wave-uniform): its first index-buffer position, or ~0 if it
+  // does not fit.
+  __device__ __forceinline__ uint64_t take(uint32_t wave, uint32_t need) const {
+    if (need == 0) return 0;
+    const bool first = __lane_id() == 0;
+    const uint32_t probes = min(kFillProbes, smask + 1);
+    for (uint32_t i = 0; i < probes; ++i) {
+      const uint32_t s = (wave + i) & smask;
+      unsigned long long* c = ctr + (uint64_t)s * kStripeWords;
+      unsigned long long b = 0;
+      if (first) b = atomicAdd(c, (unsigned long long)need);
+      b = __shfl(b, 0, kWave);
+      if (b + need <= slen) return (uint64_t)s * slen + b;
+      if (first) atomicAdd(c + 1, (unsigned long long)need);
     }
+    if (first) atomicAdd(ctr + (uint64_t)(wave & smask) * kStripeWords + 2, (unsigned long long)need);
+    return ~0ull;
   }
-  return mask;
-}
-
-template <int R>
-__device__ __forceinline__ void lane_fill_write(const uint2* __restrict__ rp, uint64_t mask, uint64_t at,
-                                                int32_t* __restrict__ nidx) {
-  uint32_t pos = 0;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint2 rg = rp[r];
-    for (uint32_t j = rg.x; j < rg.y; ++j, ++pos)
-      if ((mask >> pos) & 1ull) nidx[at++] = (int32_t)j;
-  }
-}
-
-template <int D, bool P>
-__global__ __launch_bounds__(kThreads) void k_lane_fill(GridParams g, const float4* __restrict__ xw,
-                                                        const int32_t* __restrict__ lane_len,
-                                                        const uint2* __restrict__ ranges,
-                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
-                                                        int32_t* __restrict__ ncnt,
-                                                        unsigned long long* __restrict__ used, int64_t cap) {
-  const uint32_t n = g.B * g.N;
-  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
-  const int32_t cand = k < n ? lane_len[k] : -1;  // lone particles have fewer than 64 candidates
-  const bool mine = cand >= 0;
-  const int R = ranges_per_particle<D, P>(g.morton != 0);
-  float xi[3] = {0.0f, 0.0f, 0.0f};
-  uint64_t mask = 0;
-  if (mine) {
-    unpack(xw[k], xi);
-    if (g.morton) mask = lane_fill_mask<D, P, Walker<D, P>::kCellRanges>(g, xw, ranges + (uint64_t)k * R, xi);
-    else mask = lane_fill_mask<D, P, Walker<D, P>::kRowRanges>(g, xw, ranges + (uint64_t)k * R, xi);
-  }
-  const uint32_t cnt = (uint32_t)__popcll(mask);
-  // one block of the index buffer for the wave's lone particles
-  const int lane = __lane_id();
-  uint32_t incl = cnt;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint32_t v = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += v;
-  }
-  const uint32_t wtot = __shfl(incl, kWave - 1, kWave);
-  unsigned long long b = 0;
-  if (lane == 0 && wtot) b = atomicAdd(used, (unsigned long long)wtot);
-  b = __shfl(b, 0, kWave);
-  const uint64_t at = b + incl - cnt;
-  if (!mine) return;
-  if (at + cnt > (uint64_t)cap) {
-    nstart[k] = 0;
-    ncnt[k] = -1 - cand;
-    return;
-  }
-  if (g.morton) lane_fill_write<Walker<D, P>::kCellRanges>(ranges + (uint64_t)k * R, mask, at, nidx);
-  else lane_fill_write<Walker<D, P>::kRowRanges>(ranges + (uint64_t)k * R, mask, at, nidx);
-  nstart[k] = (int32_t)at;
-  ncnt[k] = (int32_t)cnt;
-}
+};
 
 // Lane t's value of v (t wave-uniform).
 __device__ __forceinline__ float lane_float(float v, uint32_t t) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)t));
 }
 
-// Wave-uniform cursor over a unit's stencil ranges (lane r holds range r):
-// `candidate` gives this lane's candidate of the next round of 64.
-struct RangeCursor {
-  uint32_t rlo, rhi;  // this lane's range (lanes < R)
-  int r, R;
-  uint32_t cj, cend;
-  __device__ __forceinline__ void reset() {
-    r = 0;
-    cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, 0);
-    cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, 0);
-    while (cj >= cend && ++r < R) {
-      cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
-      cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
-    }
-  }
-  // Candidate of this lane in the next round (valid = false past the stencil's end).
-  __device__ __forceinline__ uint32_t round(uint32_t lane, uint32_t fallback, bool& valid) {
-    uint32_t j = fallback;
-    valid = false;
-    uint32_t covered = 0;
-    while (covered < (uint32_t)kWave && r < R) {
-      const uint32_t take = min(cend - cj, (uint32_t)kWave - covered);
-      if (lane >= covered && lane < covered + take) {
-        j = cj + (lane - covered);
-        valid = true;
-      }
-      covered += take;
-      cj += take;
-      while (cj >= cend && ++r < R) {
-        cj = (uint32_t)__builtin_amdgcn_readlane((int)rlo, r);
-        cend = (uint32_t)__builtin_amdgcn_readlane((int)rhi, r);
-      }
-    }
-    return j;
-  }
-};
+// Index-buffer store at element offset `at` (< 2^30, so the byte offset fits
+// 32 bits and the store takes the buffer base as a scalar).
+__device__ __forceinline__ void store_entry(int32_t* __restrict__ nidx, uint32_t at, int32_t j) {
+  *reinterpret_cast<int32_t*>(reinterpret_cast<char*>(nidx) + at * 4u) = j;
+}
 
-// Ballots of the first kFillRounds rounds a wave keeps for the write pass.
+// Rounds of 64 candidates whose hit bytes a unit keeps in LDS for its write
+// pass (later rounds are tested again).
 constexpr int kFillRounds = 48;
 
-// Cell-major neighbour-list fill: one wave per unit (up to kUnitParticles
-// consecutive particles of one cell, which share the cell's stencil).  The
-// wave walks the stencil ranges (stored by the unit's first particle) 64
-// candidates at a time, lane l taking the l-th candidate, and tests each
-// candidate against every particle of the unit, whose positions are
-// wave-uniform values; a ballot per particle and round marks the in-radius
-// candidates.  Pass one counts them (keeping the ballots of the first
-// kFillRounds rounds in LDS), the unit then takes one block of the index
-// buffer, and pass two writes each particle's row in stencil order, ranking
-// the hits of a round with mbcnt.
-template <int D, bool P>
-__global__ __launch_bounds__(kThreads) void k_unit_fill(GridParams g, const float4* __restrict__ xw,
-                                                        const int32_t* __restrict__ cand,
-                                                        const uint2* __restrict__ ranges,
-                                                        const uint2* __restrict__ units,
-                                                        const int32_t* __restrict__ unit_total,
-                                                        int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
-                                                        int32_t* __restrict__ ncnt,
-                                                        unsigned long long* __restrict__ used, int64_t cap) {
-  __shared__ uint64_t ballots[kThreads / kWave][kFillRounds][kUnitParticles];
-  const uint32_t total = (uint32_t)*unit_total;
-  const uint32_t nwaves = gridDim.x * (kThreads / kWave);
+// Rows of the unit i0 .. i0 + ni - 1 (ni <= kUnitParticles particles of one
+// cell, or one lone particle), one wave.  Lane r < R fetches stencil range r
+// of the cell; round q tests candidate positions 64q .. 64q + 63 of the
+// concatenated ranges, lane l taking position 64q + l, against every
+// particle of the unit (wave-uniform positions).  Pass one counts the hits
+// per particle and keeps, per lane and round, the byte of the unit's
+// particles its candidate hit (`hits`, this wave's kFillRounds * 64 bytes of
+// LDS); the unit takes one block of the index buffer; pass two writes each
+// particle's row, ranking the hits of a round with mbcnt.
+template <int D, bool P, int R>
+__device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __restrict__ xw,
+                                          const int32_t* __restrict__ bo, uint32_t i0, uint32_t ni,
+                                          uint32_t wave, uint8_t* __restrict__ hits,
+                                          int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
+                                          int32_t* __restrict__ ncnt, const FillStripes& fs) {
   const uint32_t lane = (uint32_t)__lane_id();
-  const int wv = threadIdx.x >> 6;
-  for (uint32_t u = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6); u < total; u += nwaves) {
-    const uint2 ud = units[u];
-    const uint32_t i0 = __builtin_amdgcn_readfirstlane(ud.x);
-    const uint32_t ni = __builtin_amdgcn_readfirstlane(ud.y);
-    const uint32_t it = i0 + min(lane, ni - 1u);
-    const float4 pt = xw[it];
-    const int32_t ncand = __builtin_amdgcn_readfirstlane(cand[i0]);
-    // wave-uniform copies of the unit's particle positions
-    float xs[kUnitParticles][3];
+  const float4 pt = xw[i0 + min(lane, ni - 1u)];
+  float xs[kUnitParticles][3];
+#pragma unroll
+  for (int t = 0; t < kUnitParticles; ++t) {
+    xs[t][0] = lane_float(pt.x, t);
+    xs[t][1] = lane_float(pt.y, t);
+    xs[t][2] = lane_float(pt.z, t);
+  }
+  // stencil range `lane` of the cell: start and length
+  uint32_t lo = 0, len = 0;
+  if ((int)lane < R) {
+    Walker<D, P> w;
+    w.init(g, xs[0], i0);
+    w.fetch(g, bo, (int)lane);
+    lo = w.j;
+    len = w.jend - w.j;
+  }
+  // exclusive prefix of the lengths (R <= 32 lanes) and the candidate total
+  uint32_t pre = len;
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) {
+    const uint32_t v = __shfl_up(pre, off, kWave);
+    if ((int)lane >= off) pre += v;
+  }
+  const uint32_t ncand = (uint32_t)__builtin_amdgcn_readlane((int)pre, 31);
+  pre -= len;
+  // candidate at position p < ncand: p + offs of the last range starting at
+  // or before p.  The starts do not decrease, so that offset is offs of range
+  // 0 plus the steps dof[r] = offs[r] - offs[r - 1] of the ranges 1 .. r
+  // starting at or before p (a sum, which the compiler keeps in registers).
+  const int32_t offs = (int32_t)(lo - pre);
+  const int32_t dof = offs - __shfl_up(offs, 1, kWave);
+  const int32_t off0 = __builtin_amdgcn_readlane(offs, 0);
+  // wave-uniform values kept in vector registers (the scalar file holds the
+  // unit's positions)
+  uint32_t spre[R];
+  int32_t sdof[R];
+#pragma unroll
+  for (int r = 1; r < R; ++r) {
+    spre[r] = (uint32_t)__shfl((int)pre, r, kWave);
+    sdof[r] = __shfl(dof, r, kWave);
+  }
+  auto candidate = [&](uint32_t p) -> uint32_t {
+    int32_t o = off0;
+#pragma unroll
+    for (int r = 1; r < R; ++r) o += p >= spre[r] ? sdof[r] : 0;
+    return p < ncand ? (uint32_t)((int32_t)p + o) : i0;
+  };
+  const uint32_t rounds = (ncand + kWave - 1) / kWave;
+  // pass one: count, keeping the hit bytes; the next round's positions are
+  // loaded while this round is tested
+  uint32_t cnt[kUnitParticles] = {};
+  float4 nx = xw[candidate(lane)];
+  for (uint32_t rd = 0; rd < rounds; ++rd) {
+    const uint32_t p = rd * kWave + lane;
+    float xj[3];
+    unpack(nx, xj);
+    if (p >= ncand) xj[0] = __int_as_float(0x7FC00000);  // NaN: never in radius
+    if (rd + 1 < rounds) nx = xw[candidate(p + kWave)];
+    uint32_t bits = 0;
 #pragma unroll
     for (int t = 0; t < kUnitParticles; ++t) {
-      xs[t][0] = lane_float(pt.x, t);
-      xs[t][1] = lane_float(pt.y, t);
-      xs[t][2] = lane_float(pt.z, t);
-    }
-    RangeCursor rc;
-    rc.R = ranges_per_particle<D, P>(g.morton != 0);
-    rc.rlo = rc.rhi = 0;
-    if ((int)lane < rc.R) {
-      const uint2 rr = ranges[(uint64_t)i0 * rc.R + lane];
-      rc.rlo = rr.x;
-      rc.rhi = rr.y;
-    }
-    // pass one: count, keeping the first rounds' ballots
-    uint32_t cnt[kUnitParticles] = {};
-    rc.reset();
-    int rd = 0;
-    for (int32_t base = 0; base < ncand; base += kWave, ++rd) {
-      bool valid;
-      const uint32_t j = rc.round(lane, i0, valid);
-      float xj[3];
-      unpack(xw[j], xj);
-      if (!valid) xj[0] = __int_as_float(0x7FC00000);  // NaN: never in radius
-#pragma unroll
-      for (int t = 0; t < kUnitParticles; ++t) {
-        if (t < (int)ni) {
-          float r[3];
-          const uint64_t m = __ballot(displacement<D, P>(g, xs[t], xj, r) < g.eps2);
-          if (rd < kFillRounds && lane == 0) ballots[wv][rd][t] = m;
-          cnt[t] += (uint32_t)__popcll(m);
-        }
+      if (t < (int)ni) {
+        float r[3];
+        const bool in = displacement<D, P>(g, xs[t], xj, r) < g.eps2;
+        cnt[t] += (uint32_t)__popcll(__ballot(in));
+        bits |= (in ? 1u : 0u) << t;
       }
     }
-    // the unit's block of the index buffer
-    uint32_t tot = 0;
+    if (rd < (uint32_t)kFillRounds) hits[rd * kWave + lane] = (uint8_t)bits;
+  }
+  // the unit's block of the index buffer
+  uint32_t tot = 0;
 #pragma unroll
-    for (int t = 0; t < kUnitParticles; ++t) tot += cnt[t];
-    unsigned long long b = 0;
-    if (lane == 0 && tot) b = atomicAdd(used, (unsigned long long)tot);
-    b = __shfl(b, 0, kWave);
-    if (b + tot > (unsigned long long)cap) {
-      if (lane < ni) {
-        nstart[i0 + lane] = 0;
-        ncnt[i0 + lane] = -1 - ncand;
-      }
-      continue;
+  for (int t = 0; t < kUnitParticles; ++t) tot += cnt[t];
+  const uint64_t b = fs.take(wave, tot);
+  if (b == ~0ull) {
+    if (lane < ni) {
+      nstart[i0 + lane] = 0;
+      ncnt[i0 + lane] = -1 - (int32_t)ncand;
     }
-    uint64_t at[kUnitParticles];
-    {
-      uint64_t run = b;
+    return;
+  }
+  uint32_t at[kUnitParticles];
+  int32_t mine_start = 0, mine_cnt = 0;
+  {
+    uint32_t run = (uint32_t)b;
 #pragma unroll
-      for (int t = 0; t < kUnitParticles; ++t) {
-        at[t] = run;
-        run += cnt[t];
-      }
-    }
-    int32_t mine_start = 0, mine_cnt = 0;
-#pragma unroll
-    for (int t = 0; t < kUnitParticles; ++t)
+    for (int t = 0; t < kUnitParticles; ++t) {
+      at[t] = run;
+      run += cnt[t];
       if ((int)lane == t) {
         mine_start = (int32_t)at[t];
         mine_cnt = (int32_t)cnt[t];
       }
-    // pass two: write the rows
-    rc.reset();
-    rd = 0;
-    for (int32_t base = 0; base < ncand; base += kWave, ++rd) {
-      bool valid;
-      const uint32_t j = rc.round(lane, i0, valid);
+    }
+  }
+  // pass two: write the rows
+  for (uint32_t rd = 0; rd < rounds; ++rd) {
+    const uint32_t p = rd * kWave + lane;
+    const uint32_t j = candidate(p);
+    uint32_t bits;
+    if (rd < (uint32_t)kFillRounds) {
+      bits = hits[rd * kWave + lane];
+    } else {
       float xj[3];
-      if (rd >= kFillRounds) {
-        unpack(xw[j], xj);
-        if (!valid) xj[0] = __int_as_float(0x7FC00000);
-      }
+      unpack(xw[j], xj);
+      if (p >= ncand) xj[0] = __int_as_float(0x7FC00000);
+      bits = 0;
 #pragma unroll
       for (int t = 0; t < kUnitParticles; ++t) {
-        if (t < (int)ni) {
-          uint64_t m;
-          if (rd < kFillRounds) {
-            m = ballots[wv][rd][t];
-          } else {
-            float r[3];
-            m = __ballot(displacement<D, P>(g, xs[t], xj, r) < g.eps2);
-          }
-          const uint32_t rank =
-              __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          if ((m >> lane) & 1ull) nidx[at[t] + rank] = (int32_t)j;
-          at[t] += (uint64_t)__popcll(m);
+        float r[3];
+        if (t < (int)ni && displacement<D, P>(g, xs[t], xj, r) < g.eps2) bits |= 1u << t;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kUnitParticles; ++t) {
+      if (t < (int)ni) {
+        const bool in = (bits >> t) & 1u;
+        const uint64_t m = __ballot(in);
+        const uint32_t rank =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (in) store_entry(nidx, at[t] + rank, (int32_t)j);
+        at[t] += (uint32_t)__popcll(m);
+      }
+    }
+  }
+  if (lane < ni) {
+    nstart[i0 + lane] = mine_start;
+    ncnt[i0 + lane] = mine_cnt;
+  }
+}
+
+// Lone particles of the chunk of 64 particles starting at k0, one lane each:
+// a first walk over the stencil counts the candidates and marks the in-radius
+// ones among the first 64 (a 64-bit mask, the first four also kept in
+// registers), the wave takes one block for all of its rows, and the rows are
+// written from the registers or, for more than four hits, by a second walk.
+// A lone particle with more than 64 candidates is served afterwards by the
+// whole wave (unit_rows, ni = 1).
+template <int D, bool P, int R>
+__device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __restrict__ xw,
+                                          const int32_t* __restrict__ bo, const int32_t* __restrict__ unit_len,
+                                          uint32_t k0, uint32_t wave, uint8_t* __restrict__ hits,
+                                          int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
+                                          int32_t* __restrict__ ncnt, const FillStripes& fs) {
+  const uint32_t n = g.B * g.N;
+  const uint32_t lane = (uint32_t)__lane_id();
+  const uint32_t k = k0 + lane;
+  const bool lone = k < n && unit_len[k] < 0;
+  float xi[3] = {0.0f, 0.0f, 0.0f};
+  uint64_t mask = 0;
+  uint32_t cand = 0, c = 0;
+  int32_t h0 = 0, h1 = 0, h2 = 0, h3 = 0;
+  Walker<D, P> w{};
+  if (lone) {
+    unpack(xw[k], xi);
+    w.init(g, xi, k);
+#pragma unroll 1
+    for (int r = 0; r < R; ++r) {
+      w.fetch(g, bo, r);
+      const uint32_t len = w.jend - w.j;
+      const uint32_t take = cand < (uint32_t)kWave ? min(len, (uint32_t)kWave - cand) : 0u;
+      for (uint32_t q = 0; q < take; ++q) {
+        float xj[3], rr[3];
+        unpack(xw[w.j + q], xj);
+        if (displacement<D, P>(g, xi, xj, rr) < g.eps2) {
+          mask |= 1ull << (cand + q);
+          const int32_t j = (int32_t)(w.j + q);
+          h0 = c == 0 ? j : h0;
+          h1 = c == 1 ? j : h1;
+          h2 = c == 2 ? j : h2;
+          h3 = c == 3 ? j : h3;
+          ++c;
+        }
+      }
+      cand += len;
+    }
+  }
+  const bool light = lone && cand <= (uint32_t)kWave;
+  const uint32_t cnt = light ? c : 0u;
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint32_t v = __shfl_up(incl, off, kWave);
+    if ((int)lane >= off) incl += v;
+  }
+  const uint32_t wtot = __shfl(incl, kWave - 1, kWave);
+  const uint64_t b = fs.take(wave, wtot);
+  if (light) {
+    if (b == ~0ull) {
+      nstart[k] = 0;
+      ncnt[k] = -1 - (int32_t)cand;
+    } else {
+      uint32_t at = (uint32_t)b + incl - cnt;
+      nstart[k] = (int32_t)at;
+      ncnt[k] = (int32_t)cnt;
+      if (cnt <= 4) {
+        if (cnt > 0) store_entry(nidx, at, h0);
+        if (cnt > 1) store_entry(nidx, at + 1, h1);
+        if (cnt > 2) store_entry(nidx, at + 2, h2);
+        if (cnt > 3) store_entry(nidx, at + 3, h3);
+      } else {
+        uint32_t pos = 0;
+#pragma unroll 1
+        for (int r = 0; r < R && pos < (uint32_t)kWave && (mask >> pos) != 0; ++r) {
+          w.fetch(g, bo, r);
+          for (uint32_t j = w.j; j < w.jend; ++j, ++pos)
+            if ((mask >> pos) & 1ull) store_entry(nidx, at++, (int32_t)j);
         }
       }
     }
-    if (lane < ni) {
-      nstart[i0 + lane] = mine_start;
-      ncnt[i0 + lane] = mine_cnt;
+  }
+  uint64_t heavy = __ballot(lone && !light);
+  while (heavy) {
+    const uint32_t l = (uint32_t)__builtin_ctzll(heavy);
+    heavy &= heavy - 1;
+    unit_rows<D, P, R>(g, xw, bo, k0 + l, 1, wave, hits, nidx, nstart, ncnt, fs);
+  }
+}
+
+// The list fill: a persistent grid whose waves take the units u = wave,
+// wave + (waves in the grid), ... (units[u] = {first particle, particles})
+// and the chunks of 64 particles c = wave, wave + (waves in the grid), ...
+// (k0 = 64 c).  Even waves take their chunks first, odd waves their units
+// first, so that the memory-bound lone walks overlap the ALU-bound units.
+template <int D, bool P, int R>
+__device__ __forceinline__ void fill_items(const GridParams& g, const float4* __restrict__ xw,
+                                           const int32_t* __restrict__ bo, const int32_t* __restrict__ unit_len,
+                                           const uint2* __restrict__ units, uint32_t nunits, uint8_t* hits,
+                                           int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
+                                           int32_t* __restrict__ ncnt, const FillStripes& fs) {
+  const uint32_t n = g.B * g.N;
+  const uint32_t nchunks = (n + kWave - 1) / kWave;
+  const uint32_t nwaves = gridDim.x * (kThreads / kWave);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(xcd_block_id() * (kThreads / kWave) + (threadIdx.x >> 6));
+  const bool chunks_first = (wave & 1u) == 0;
+  for (int phase = 0; phase < 2; ++phase) {
+    if ((phase == 0) == chunks_first) {
+      for (uint32_t c = wave; c < nchunks; c += nwaves)
+        lone_rows<D, P, R>(g, xw, bo, unit_len, c * kWave, wave, hits, nidx, nstart, ncnt, fs);
+    } else {
+      for (uint32_t u = wave; u < nunits; u += nwaves) {
+        const uint2 ud = units[u];
+        unit_rows<D, P, R>(g, xw, bo, __builtin_amdgcn_readfirstlane(ud.x), __builtin_amdgcn_readfirstlane(ud.y),
+                           wave, hits, nidx, nstart, ncnt, fs);
+      }
     }
+  }
+}
+
+// M: particle mode (stencil of single cells) or grid mode (stencil rows).
+template <int D, bool P, bool M>
+__global__ __launch_bounds__(kThreads) void k_fill(GridParams g, const float4* __restrict__ xw,
+                                                   const int32_t* __restrict__ bo,
+                                                   const int32_t* __restrict__ unit_len,
+                                                   const uint2* __restrict__ units,
+                                                   const int32_t* __restrict__ unit_total,
+                                                   int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
+                                                   int32_t* __restrict__ ncnt, FillStripes fs) {
+  __shared__ uint8_t hits[kThreads / kWave][kFillRounds * kWave];
+  uint8_t* mine = hits[threadIdx.x >> 6];
+  const uint32_t nunits = (uint32_t)*unit_total;
+  fill_items<D, P, M ? Walker<D, P>::kCellRanges : Walker<D, P>::kRowRanges>(g, xw, bo, unit_len, units, nunits,
+                                                                             mine, nidx, nstart, ncnt, fs);
+}
+
+// total[0] = in-radius pairs (blocks written or not), total[1] = pairs of
+// the blocks not written, from the counters' words (see FillStripes).  One
+// workgroup of kThreads >= kFillStripes.
+static_assert(kThreads >= kFillStripes, "k_fill_totals reads one counter per thread");
+static __global__ __launch_bounds__(kThreads) void k_fill_totals(const unsigned long long* __restrict__ ctr,
+                                                                 uint32_t stripes,
+                                                                 unsigned long long* __restrict__ total) {
+  __shared__ unsigned long long part[2][kThreads / kWave];
+  const uint32_t s = threadIdx.x;
+  unsigned long long a = 0, o = 0;
+  if (s < stripes) {
+    const unsigned long long* c = ctr + (uint64_t)s * kStripeWords;
+    a = c[0] - c[1] + c[2];
+    o = c[2];
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    a += __shfl_down(a, off, kWave);
+    o += __shfl_down(o, off, kWave);
+  }
+  if (__lane_id() == 0) {
+    part[0][s / kWave] = a;
+    part[1][s / kWave] = o;
+  }
+  __syncthreads();
+  if (s == 0) {
+    unsigned long long sa = 0, so = 0;
+    for (uint32_t w = 0; w < kThreads / kWave; ++w) {
+      sa += part[0][w];
+      so += part[1][w];
+    }
+    total[0] = sa;
+    total[1] = so;
   }
 }
 
@@ -1787,37 +1857,45 @@ void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
 }
 
 constexpr uint32_t kPersistentWorkgroups = 2048;
+// Workgroups of the list fill (timed at cfg5: 4096 beats 2048, 3072 and 6144).
+constexpr uint32_t kFillWorkgroups = 4096;
 
-// Stencil candidate counts of every binned particle (g.cand), and the fill's
-// work split, unit table and stencil ranges in the grid's scratch (read by
-// neighbour_fill).
+// Work split of the list fill (unit table and lone marks, in the grid's
+// scratch), read by neighbour_fill.
 template <int D, bool P>
 void neighbour_candidates(const Grid& g, const int32_t* bo, const float* x, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
-  hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
-  SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_candidates<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, g.packed, g.cand,
-                     g.sparse_len, g.unit_len, g.flags, g.ranges);
+  hipLaunchKernelGGL((k_fill_split<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, x, g.unit_len, g.flags);
   SPHOPS_LAUNCHED();
   run_unit_schedule(g, st);
 }
 
-// Fill the rows (compact, allocated from the counter `used`): cells with
-// several particles (and lone particles with many candidates) cell-major,
-// the other lone particles a lane each, with the work split and ranges
-// neighbour_candidates left in the grid.
+// Fill the rows (compact, allocated from the striped counters) with the work
+// split neighbour_candidates left in the grid; used[0..1] receive the pair
+// totals (k_fill_totals).
 template <int D, bool P>
-void neighbour_fill(const Grid& g, const float* x, int32_t* nstart, int32_t* nidx, int32_t* ncnt,
-                    unsigned long long* used, int64_t cap, hipStream_t st) {
+void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, int32_t* nstart, int32_t* nidx,
+                    int32_t* ncnt, unsigned long long* used, int64_t cap, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
   SPHOPS_LAUNCHED();
-  fill_u32(reinterpret_cast<uint32_t*>(used), 2, 0u, st);
-  hipLaunchKernelGGL((k_unit_fill<D, P>), dim3(kPersistentWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, g.cand,
-                     g.ranges, g.units, g.unit_total, nidx, nstart, ncnt, used, cap);
+  // S slices of at least kStripeMinEntries entries and, for n particles,
+  // about n / (kStripeMinUnits * kUnitParticles) units or more each (one
+  // slice for small buffers)
+  uint32_t S = 1;
+  while (S < kFillStripes && (int64_t)(2 * S) * kStripeMinEntries <= cap &&
+         (uint64_t)(2 * S) * kStripeMinUnits * kUnitParticles <= n)
+    S *= 2;
+  FillStripes fs{g.stripes, S - 1, (uint64_t)(cap / S)};
+  fill_u32(reinterpret_cast<uint32_t*>(g.stripes), (uint64_t)S * kStripeWords * 2, 0u, st);
+  if (g.particle_mode)
+    hipLaunchKernelGGL((k_fill<D, P, true>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, bo,
+                       g.unit_len, g.units, g.unit_total, nidx, nstart, ncnt, fs);
+  else
+    hipLaunchKernelGGL((k_fill<D, P, false>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, bo,
+                       g.unit_len, g.units, g.unit_total, nidx, nstart, ncnt, fs);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_lane_fill<D, P>), grid_for(n), dim3(kThreads), 0, st, g.p, g.packed, g.sparse_len,
-                     g.ranges, nidx, nstart, ncnt, used, cap);
+  hipLaunchKernelGGL(k_fill_totals, dim3(1), dim3(kThreads), 0, st, g.stripes, S, used);
   SPHOPS_LAUNCHED();
 }
 
@@ -1988,7 +2066,7 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a_i
       if (g.n_keys) neighbour_candidates<D, P>(g, bo, a.x, st);
       return;
     case Op::NeighbourFill:
-      if (g.n_keys) neighbour_fill<D, P>(g, a.x, a.iout3, a.iout, a.iout2, a.used, a.cap, st);
+      if (g.n_keys) neighbour_fill<D, P>(g, a.bo, a.x, a.iout3, a.iout, a.iout2, a.used, a.cap, st);
       return;
     case Op::NeighbourTiles:
       if (g.n_keys)

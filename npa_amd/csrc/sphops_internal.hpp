@@ -51,13 +51,11 @@ struct Grid {
   uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
   float4* packed = nullptr;       // B*N (x, y, z|0, weight) read by the pair kernels
   // work split of the neighbour-list fill:
-  int32_t* cand = nullptr;        // B*N: stencil candidates of each particle
-  int32_t* sparse_len = nullptr;  // B*N: candidate count of particles filled a lane each, -1 for the others
-  int32_t* unit_len = nullptr;    // B*N: particles of the unit starting at this particle, 0 if none starts here
+  int32_t* sparse_len = nullptr;  // B*N: list length of the particles outside the cell tiles, -1 for the others
+  int32_t* unit_len = nullptr;    // B*N: particles of the unit starting here (> 0), 0, or -1 (lone particle)
   uint2* units = nullptr;         // B*N: unit descriptors {first particle, particles}
   int32_t* unit_total = nullptr;  // number of units (device)
-  int n_ranges = 0;               // stencil ranges per particle (rows in grid mode, cells in particle mode)
-  uint2* ranges = nullptr;        // B*N*n_ranges: stencil ranges, stored by unit-first and lone particles
+  unsigned long long* stripes = nullptr;  // kFillStripes * kStripeWords: row-allocation counters of the fill
   // (positions, bin_offsets) of the last neighbour_candidates call: the fill
   // reads the work split and ranges that call left and must get the same
   mutable const void* split_key[2] = {nullptr, nullptr};
@@ -168,14 +166,23 @@ uint64_t neighbour_wave_capacity(const Grid& g);
 // particle k with unit_len[k] > 0 (flags[k] = 1 there, 0 elsewhere), in
 // particle order; their number goes to unit_total.  Scans flags in place.
 void run_unit_schedule(const Grid& g, hipStream_t st);
-// Neighbour-list fill: cells of two or more particles, and lone particles
-// with at least kLaneMaxCand stencil candidates, are filled cell-major in
-// units of at most kUnitParticles particles of one cell, one wave per unit;
-// the other lone particles one lane each.
-constexpr int32_t kLaneMaxCand = 64;
+// Neighbour-list fill: cells of two or more particles are filled cell-major
+// in units of at most kUnitParticles particles of one cell, one wave per
+// unit; particles alone in their cell one lane each.
 // Largest neighbour-list index buffer (entries): byte offsets into it fit in 32 bits.
 constexpr int64_t kMaxListEntries = (int64_t)1 << 30;
 constexpr int32_t kUnitParticles = 8;
+// Row allocation of the fill: up to kFillStripes counters, each owning an
+// equal slice of the index buffer of at least kStripeMinEntries entries and
+// serving about kStripeMinUnits units or more (so that slices fill evenly);
+// a wave takes its blocks from counter (wave id mod stripes).  One counter
+// for the whole device serialises the atomics of ~10^5 units; striped, they
+// spread over as many addresses.  Counters lie kStripeWords 64-bit words
+// apart (256 bytes).
+constexpr uint32_t kFillStripes = 256;
+constexpr uint32_t kStripeWords = 32;
+constexpr int64_t kStripeMinEntries = (int64_t)1 << 15;
+constexpr uint64_t kStripeMinUnits = 64;
 // Work classes of the list traversal: class q holds
 // the items whose length is <= t[q] (and above the previous bound), the last
 // class the rest; each class is served by groups of g[q] lanes per particle

@@ -383,8 +383,9 @@ class _HashGridNative:
         wcap = 2 * max(int(_lib.sphops_neighbor_wave_capacity(self._h)), 1)
         waves = torch.empty(wcap, dtype=_I32, device=dev)
         waves2 = torch.empty(wcap, dtype=_I32, device=dev)
-        # device counts: [0:2] in-radius pairs (int64), [2] waves, [3] split
-        # waves, [4] tile units, [5] waves of the particles outside the tiles
+        # device counts: [0:2] in-radius pairs (int64), [2:4] pairs of rows not
+        # stored (int64), [4] waves, [5] split waves, [6] tile units, [7] waves
+        # of the particles outside the tiles
         small = torch.zeros(8, dtype=_I32, device=dev)
         cap = self._capacity(n)
         index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
@@ -395,22 +396,22 @@ class _HashGridNative:
                                          ctypes.c_void_p(small.data_ptr()), st))
         _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
                                              ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
-                                             ctypes.c_void_p(small.data_ptr() + 8), ctypes.c_void_p(waves2.data_ptr()),
-                                             ctypes.c_void_p(small.data_ptr() + 12), st))
+                                             ctypes.c_void_p(small.data_ptr() + 16), ctypes.c_void_p(waves2.data_ptr()),
+                                             ctypes.c_void_p(small.data_ptr() + 20), st))
         if tiles is not None:
             # after the fill: the tile build reuses the grid scratch that holds
             # the fill's work split
             _check(_lib.sphops_neighbor_tiles(
                 self._h, x, bo, ctypes.c_void_p(count.data_ptr()), ctypes.c_void_p(tiles[0].data_ptr()),
-                ctypes.c_void_p(small.data_ptr() + 16), ctypes.c_void_p(tiles[1].data_ptr()),
-                ctypes.c_void_p(tiles[2].data_ptr()), ctypes.c_void_p(small.data_ptr() + 20), st))
+                ctypes.c_void_p(small.data_ptr() + 24), ctypes.c_void_p(tiles[1].data_ptr()),
+                ctypes.c_void_p(tiles[2].data_ptr()), ctypes.c_void_p(small.data_ptr() + 28), st))
         if not capturing:
-            self._start_readback(small)
+            self._start_readback(small, cap)
         e1, e2, e3 = self._wave_estimates(n)
         plan = NeighborPlan(start, count, index, order, waves, e1, waves2, e2, small)
         plan.capacity = cap
         if tiles is not None:
-            plan.tiles = (tiles[0], small[4:5], tiles[1], tiles[2], e3, small[5:6])
+            plan.tiles = (tiles[0], small[6:7], tiles[1], tiles[2], e3, small[7:8])
         self._last_plan = plan
         return plan
 
@@ -441,12 +442,18 @@ class _HashGridNative:
         first = max(n // 8, 1)
         return (first, first, first)
 
-    def _start_readback(self, small):
+    # Index-buffer margin over the last total, as a right shift of the total
+    # (3: 1/8); lowered (a larger margin) when a list did not fit although
+    # its buffer held the total, i.e. the fill's slices were uneven.
+    _slack_shift = 3
+
+    def _start_readback(self, small, cap):
         """Copy the device counts to pinned host memory without waiting."""
         rb = getattr(self, "_rb", None)
         if rb is None:
             self._rb = rb = torch.empty(8, dtype=_I32, pin_memory=True)
         rb.copy_(small, non_blocking=True)
+        self._rb_cap = cap
         self._rb_event = torch.cuda.Event()
         self._rb_event.record()
 
@@ -463,8 +470,11 @@ class _HashGridNative:
             return
         v = self._rb.tolist()
         total = (v[0] & 0xFFFFFFFF) | (v[1] << 32)
-        self._index_capacity = total + total // 8 + 1024
-        self._wave_counts = (v[2], v[3], v[5])
+        unstored = (v[2] & 0xFFFFFFFF) | (v[3] << 32)
+        if unstored and self._rb_cap >= total and self._slack_shift > 1:
+            self._slack_shift -= 1
+        self._index_capacity = total + (total >> self._slack_shift) + 1024
+        self._wave_counts = (v[4], v[5], v[7])
         self._rb_event = None
 
     # Cell tiles for the pass-B backward (sphops_neighbor_tiles): opt-in
@@ -500,15 +510,13 @@ class _HashGridNative:
                                  else (max(n // 8, 1),) * 3)
 
     def list_overflow(self):
-        """True if the last list built did not store every row (its total
-        exceeded the index capacity; those rows were walked on the stencil).
-        Reads the total back (synchronises)."""
+        """True if the last list built did not store every row (its index
+        buffer was too small; those rows were walked on the stencil).  Reads
+        the count back (synchronises)."""
         plan = getattr(self, "_last_plan", None)
         if plan is None:
             return False
-        v = plan[8][:2].cpu().tolist()
-        total = (v[0] & 0xFFFFFFFF) | (v[1] << 32)
-        return total > plan.capacity
+        return int(plan[8][2:4].cpu().view(torch.int64).item()) > 0
 
     def reset_list_overflow(self):
         self._last_plan = None
@@ -567,8 +575,8 @@ class _HashGridNative:
             if len(nbr) > 6:
                 a.nbr_waves_split, a.nbr_wave_count_split = nbr[6].data_ptr(), nbr[7]
             if len(nbr) > 8 and nbr[8] is not None:  # the wave counts on the device
-                a.nbr_wave_count_device = nbr[8].data_ptr() + 8
-                a.nbr_wave_count_split_device = nbr[8].data_ptr() + 12
+                a.nbr_wave_count_device = nbr[8].data_ptr() + 16
+                a.nbr_wave_count_split_device = nbr[8].data_ptr() + 20
             tiles = getattr(nbr, "tiles", None)
             if tiles is not None:
                 a.tile_units, a.tile_unit_count = tiles[0].data_ptr(), tiles[1].data_ptr()

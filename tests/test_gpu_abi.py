@@ -31,7 +31,7 @@ def test_fill_follows_candidates():
     n = xb.shape[0] * xb.shape[1]
     start = torch.empty(n, dtype=torch.int32, device="cuda")
     count = torch.empty(n, dtype=torch.int32, device="cuda")
-    total = torch.zeros(1, dtype=torch.int64, device="cuda")
+    total = torch.zeros(2, dtype=torch.int64, device="cuda")  # pairs found, pairs not stored
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     xp, bp = ctypes.c_void_p(xb.data_ptr()), ctypes.c_void_p(snap.bin_offsets.data_ptr())
     _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, st))
@@ -59,7 +59,7 @@ def test_fill_follows_candidates():
     assert fill(xp, bp, cap) == 0
     torch.cuda.synchronize()
     first = rows()
-    assert int(total.item()) == int(count.sum().item())
+    assert total.tolist() == [int(count.sum().item()), 0]
     assert fill(xp, bp, cap) == 0
     torch.cuda.synchronize()
     assert rows() == first
@@ -70,10 +70,12 @@ def test_fill_follows_candidates():
     stored = ref[1] >= 0
     assert torch.equal(ref[1][stored], count[stored])
     # a buffer one entry short of the total: some row is not stored, and its
-    # count encodes its stencil candidates; the total still counts it
-    need = int(total.item())
+    # count encodes its stencil candidates; the total still counts it, and the
+    # second word counts the pairs of the rows not stored
+    need = int(total[0].item())
     assert fill(xp, bp, need - 1) == 0
     torch.cuda.synchronize()
     c = count.cpu().numpy()
-    assert (c < 0).any() and int(total.item()) == need
+    assert (c < 0).any() and int(total[0].item()) == need
     assert np.all(c[c < 0] <= -2)
+    assert int(total[1].item()) == sum(len(first[k]) for k in np.flatnonzero(c < 0))

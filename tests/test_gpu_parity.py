@@ -370,6 +370,11 @@ def test_neighbor_list(name):
         np.testing.assert_array_equal(gj[o], p.j[sel][r], err_msg=label)
         # the stored rows of all particles lie inside the buffer and do not overlap
         allc = count[: c.B * c.N]
+        # the second count: pairs of the rows not stored
+        unstored = int(nbr[8][2:4].cpu().view(torch.int64).item())
+        assert (unstored == 0) == bool((allc >= 0).all()), label
+        if len(q) == c.B * c.N:
+            assert unstored == int(ref_cnt[~stored].sum()), label
         ks = np.flatnonzero(allc > 0)
         lo, hi = start[ks], start[ks] + allc[ks]
         so = np.argsort(lo)
