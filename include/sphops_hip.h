@@ -73,7 +73,7 @@ int sphops_initialize(sphops_grid* grid, const float* positions, int32_t* permut
  * serving loops, harnesses that forbid hipMalloc.  The grid is described by
  * the arguments of sphops_grid_create; the outputs are sphops_initialize's,
  * bit for bit.  The sort, scan and block-table scratch comes from one static
- * device array per GPU (about 24 MiB, held until the process ends), so
+ * device array per GPU (about 22 MiB, held until the process ends), so
  * batch_size * particle_count must be at most 2^20 and batch_size * cell count
  * at most 2^28; larger grids fail with an error and no work queued.  Calls
  * that overlap on one GPU share the array and race: serialise them (one

@@ -268,22 +268,20 @@ __global__ __launch_bounds__(kThreads) void k_fill_u32(uint32_t* __restrict__ p,
   if (i < n) p[i] = v;
 }
 
-// First and one-past-last sorted position of every non-empty cell chunk.
-__global__ __launch_bounds__(kThreads) void k_chunk_marks(const uint32_t* __restrict__ keys, uint32_t n,
-                                                          uint32_t* __restrict__ cfirst,
-                                                          uint32_t* __restrict__ cend) {
-  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
-  if (k >= n) return;
-  const uint32_t ch = keys[k] >> kChunkLog2;
-  if (k == 0 || (keys[k - 1] >> kChunkLog2) != ch) cfirst[ch] = k;
-  if (k == n - 1 || (keys[k + 1] >> kChunkLog2) != ch) cend[ch] = k + 1;
-}
-
-__global__ __launch_bounds__(kThreads) void k_chunk_counts(const uint32_t* __restrict__ cfirst,
-                                                           const uint32_t* __restrict__ cend,
-                                                           uint32_t* __restrict__ cnt, uint32_t nch) {
-  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-  if (i < nch) cnt[i] = cend[i] - cfirst[i];
+// chunk_lo[c] = number of sorted keys below the first cell of chunk c
+// (c = 0 .. nch), by binary search over the sorted keys.
+__global__ __launch_bounds__(kThreads) void k_chunk_lo(const uint32_t* __restrict__ keys, uint32_t n,
+                                                       uint32_t* __restrict__ chunk_lo, uint32_t nch) {
+  const uint32_t c = blockIdx.x * kThreads + threadIdx.x;
+  if (c > nch) return;
+  const uint64_t target = (uint64_t)c << kChunkLog2;
+  uint32_t lo = 0, hi = n;
+  while (lo < hi) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if ((uint64_t)keys[mid] < target) lo = mid + 1;
+    else hi = mid;
+  }
+  chunk_lo[c] = lo;
 }
 
 // bin_offsets[c] = number of sorted keys < c, for the 1024 cells of a chunk.
@@ -352,46 +350,48 @@ __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint32_t* __rest
   }
 }
 
-__global__ __launch_bounds__(kThreads) void k_permutation(const uint32_t* __restrict__ vals, uint32_t n,
-                                                          uint32_t N, int32_t* __restrict__ perm) {
-  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
-  if (k >= n) return;
-  const uint32_t src = vals[k];
-  perm[src] = (int32_t)(k - (src / N) * N);
-}
-
-// --------------------------------------------------------- block table
-
-__global__ __launch_bounds__(kThreads) void k_block_flags(const uint32_t* __restrict__ keys, uint32_t n,
+// Permutation (destination slot of every input particle) and, in grid mode
+// (flags non-null), the block-start flags of the block table: sorted position
+// k starts a block when its offset in its cell is a multiple of maxp.
+__global__ __launch_bounds__(kThreads) void k_permutation(const uint32_t* __restrict__ keys,
+                                                          const uint32_t* __restrict__ vals, uint32_t n,
+                                                          uint32_t N, int32_t* __restrict__ perm,
                                                           const int32_t* __restrict__ bo, uint32_t maxp,
                                                           uint32_t* __restrict__ flags) {
   const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
   if (k >= n) return;
-  const uint32_t rs = (uint32_t)bo[keys[k]];
-  flags[k] = ((k - rs) % maxp == 0) ? 1u : 0u;
+  const uint32_t src = vals[k];
+  perm[src] = (int32_t)(k - (src / N) * N);
+  if (flags != nullptr) {
+    const uint32_t rs = (uint32_t)bo[keys[k]];
+    flags[k] = ((k - rs) % maxp == 0) ? 1u : 0u;
+  }
 }
 
-// rows {global_cell, offset_in_cell, count, batch} (sphops/utils.cuh:295-301)
+// --------------------------------------------------------- block table
+
+// Rows {global_cell, offset_in_cell, count, batch} (sphops/utils.cuh:295-301)
+// of the blocks starting at sorted position i < n (row rowidx[i]), zero rows
+// r in [total, max_blocks) (thread i handles position i and row i), and the
+// block count into total_out.
 __global__ __launch_bounds__(kThreads) void k_block_rows(const uint32_t* __restrict__ keys, uint32_t n,
                                                          const int32_t* __restrict__ bo,
                                                          const uint32_t* __restrict__ rowidx, uint32_t maxp,
-                                                         uint32_t G, int4* __restrict__ info) {
-  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
-  if (k >= n) return;
+                                                         uint32_t G, int4* __restrict__ info,
+                                                         const uint32_t* __restrict__ total, uint64_t max_blocks,
+                                                         int32_t* __restrict__ total_out) {
+  const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t t = *total;
+  if (i == 0 && total_out) *total_out = (int32_t)t;
+  if (i < max_blocks && i >= t) info[i] = make_int4(0, 0, 0, 0);
+  if (i >= n) return;
+  const uint32_t k = (uint32_t)i;
   const uint32_t key = keys[k];
   const uint32_t rs = (uint32_t)bo[key];
   const uint32_t off = k - rs;
   if (off % maxp != 0) return;
   const uint32_t cnt = (uint32_t)bo[key + 1] - rs;
   info[rowidx[k]] = make_int4((int)key, (int)off, (int)min(maxp, cnt - off), (int)(key / G));
-}
-
-__global__ __launch_bounds__(kThreads) void k_block_tail(const uint32_t* __restrict__ total, uint64_t max_blocks,
-                                                         int4* __restrict__ info, int32_t* __restrict__ total_out) {
-  const uint64_t r = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  const uint32_t t = *total;
-  if (r == 0 && total_out) *total_out = (int32_t)t;
-  if (r < max_blocks && r >= t) info[r] = make_int4(0, 0, 0, 0);
 }
 
 // ----------------------------------------------------------- bin / unbin
@@ -714,34 +714,24 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
 
   // 3. bin_offsets via per-chunk key ranges
   const uint32_t nch = (uint32_t)g.n_chunks;
-  hipLaunchKernelGGL(k_fill_u32, blocks_for(nch), dim3(kThreads), 0, st, g.chunk_first, (uint64_t)nch, 0u);
+  hipLaunchKernelGGL(k_chunk_lo, blocks_for((uint64_t)nch + 1), dim3(kThreads), 0, st, skeys, n, g.chunk_lo, nch);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_fill_u32, blocks_for(nch), dim3(kThreads), 0, st, g.chunk_end, (uint64_t)nch, 0u);
-  SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_chunk_marks, blocks_for(n), dim3(kThreads), 0, st, skeys, n, g.chunk_first, g.chunk_end);
-  SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_chunk_counts, blocks_for(nch), dim3(kThreads), 0, st, g.chunk_first, g.chunk_end,
-                     g.chunk_lo, nch);
-  SPHOPS_LAUNCHED();
-  device_exclusive_scan(g.chunk_lo, g.chunk_lo, nch, g.scan_tmp, g.chunk_lo + nch, st);
   hipLaunchKernelGGL(k_bin_offsets, dim3((nch + kChunksPerBlock - 1) / kChunksPerBlock), dim3(kThreads), 0, st,
                      skeys, g.chunk_lo, nch, bo, ncp1);
   SPHOPS_LAUNCHED();
 
-  // 4. permutation (destination slot of each input particle)
-  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, svals, n, g.p.N, perm);
+  // 4. permutation (destination slot of each input particle), with the
+  // block-start flags in grid mode
+  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, skeys, svals, n, g.p.N, perm, bo,
+                     g.p.maxp, g.particle_mode ? nullptr : g.flags);
   SPHOPS_LAUNCHED();
 
   // 5. block table (grid mode)
   if (!g.particle_mode) {
-    hipLaunchKernelGGL(k_block_flags, blocks_for(n), dim3(kThreads), 0, st, skeys, n, bo, g.p.maxp, g.flags);
-    SPHOPS_LAUNCHED();
     device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, g.flags + n, st);
-    hipLaunchKernelGGL(k_block_rows, blocks_for(n), dim3(kThreads), 0, st, skeys, n, bo, g.flags, g.p.maxp,
-                       g.p.G, reinterpret_cast<int4*>(block_info));
-    SPHOPS_LAUNCHED();
-    hipLaunchKernelGGL(k_block_tail, blocks_for(g.max_blocks), dim3(kThreads), 0, st, g.flags + n, g.max_blocks,
-                       reinterpret_cast<int4*>(block_info), total_blocks);
+    hipLaunchKernelGGL(k_block_rows, blocks_for(std::max<uint64_t>(n, g.max_blocks)), dim3(kThreads), 0, st,
+                       skeys, n, bo, g.flags, g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n,
+                       g.max_blocks, total_blocks);
     SPHOPS_LAUNCHED();
   } else if (total_blocks) {
     fill_u32(reinterpret_cast<uint32_t*>(total_blocks), 1, 0u, st);

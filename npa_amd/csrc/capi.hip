@@ -139,8 +139,6 @@ void free_grid(Grid* g) {
   }
   (void)hipFree(g->hist);
   (void)hipFree(g->scan_tmp);
-  (void)hipFree(g->chunk_first);
-  (void)hipFree(g->chunk_end);
   (void)hipFree(g->chunk_lo);
   (void)hipFree(g->flags);
   (void)hipFree(g->packed);
@@ -272,8 +270,6 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->hist = dalloc<uint32_t>((uint64_t)sphops::kRadixBins * g->n_tiles);
       g->scan_tmp_len = sphops::scan_tmp_elems(sphops::scan_words(*g));
       g->scan_tmp = dalloc<uint32_t>(g->scan_tmp_len);
-      g->chunk_first = dalloc<uint32_t>(g->n_chunks);
-      g->chunk_end = dalloc<uint32_t>(g->n_chunks);
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
       g->flags = dalloc<uint32_t>(BN + 1);
       g->packed = dalloc<float4>(BN);
@@ -935,7 +931,7 @@ constexpr int kNoAllocMaxDevices = 64;
 // Word offsets of the scratch pieces for a grid of n_keys particles, n_tiles
 // radix tiles and n_chunks cell chunks; each piece starts on 256 bytes.
 struct NoAllocLayout {
-  uint64_t keys[2], vals[2], hist, flags, chunk_first, chunk_end, chunk_lo, scan, scan_len, words;
+  uint64_t keys[2], vals[2], hist, flags, chunk_lo, scan, scan_len, words;
 };
 
 constexpr uint64_t pad_words(uint64_t w) { return (w + 63) & ~uint64_t(63); }
@@ -953,10 +949,6 @@ constexpr NoAllocLayout noalloc_layout(uint64_t n_keys, uint64_t n_tiles, uint64
   at += pad_words((uint64_t)sphops::kRadixBins * n_tiles);
   l.flags = at;
   at += pad_words(n_keys + 1);
-  l.chunk_first = at;
-  at += pad_words(n_chunks);
-  l.chunk_end = at;
-  at += pad_words(n_chunks);
   l.chunk_lo = at;
   at += pad_words(n_chunks + 1);
   l.scan = at;
@@ -967,7 +959,7 @@ constexpr NoAllocLayout noalloc_layout(uint64_t n_keys, uint64_t n_tiles, uint64
 }
 
 // Every piece grows with its size, so the largest grid the entry point
-// accepts bounds every layout: about 24 MiB.
+// accepts bounds every layout: about 22 MiB.
 constexpr uint64_t kNoAllocWords =
     noalloc_layout(kNoAllocMaxKeys, (kNoAllocMaxKeys + 4095) / 4096, (kNoAllocMaxCells + 1 + 1023) / 1024).words;
 
@@ -1018,8 +1010,6 @@ int sphops_initialize_noalloc(int dim, int boundary, int mode, const int32_t* gr
     }
     g.hist = s + l.hist;
     g.flags = s + l.flags;
-    g.chunk_first = s + l.chunk_first;
-    g.chunk_end = s + l.chunk_end;
     g.chunk_lo = s + l.chunk_lo;
     g.scan_tmp = s + l.scan;
     g.scan_tmp_len = l.scan_len;

@@ -45,9 +45,7 @@ struct Grid {
   uint32_t* hist = nullptr;       // 256 * n_tiles (+1)
   uint32_t* scan_tmp = nullptr;   // partial sums for device scans
   uint64_t scan_tmp_len = 0;
-  uint32_t* chunk_first = nullptr;
-  uint32_t* chunk_end = nullptr;
-  uint32_t* chunk_lo = nullptr;   // n_chunks + 1
+  uint32_t* chunk_lo = nullptr;   // n_chunks + 1: sorted keys below each chunk's first cell
   uint32_t* flags = nullptr;      // B*N + 1 (block starts, then their scan)
   float4* packed = nullptr;       // B*N (x, y, z|0, weight) read by the pair kernels
   // work split of the neighbour-list fill:
