@@ -45,7 +45,26 @@ def _cases():
     d = H.random_case("dense2d-per", 1, 1000, 16, 2, 8, 0.125, True, "grid", uniform=False, sigma=0.05)
     d.x[..., :2] += 0.5  # the cluster straddles the periodic boundary
     cs.append(d)
+    cs += [_lone_heavy_case(mode) for mode in ("grid", "particle")]
     return cs
+
+
+def _lone_heavy_case(mode):
+    """Particles alone in their cell whose stencil holds more than 64
+    candidates (served by a whole wave, like a unit of one particle): 300
+    particles crowd cell (4, 4, 4) of an 8^3 grid of h = 0.25, each of its 26
+    neighbour cells holds one particle, and 200 more are scattered."""
+    rng = np.random.default_rng(11)
+    h = 0.25
+    crowd = 0.125 + (rng.random((300, 3)) - 0.5) * 0.2
+    offs = np.array([(a, b, c) for a in (-1, 0, 1) for b in (-1, 0, 1) for c in (-1, 0, 1) if (a, b, c) != (0, 0, 0)])
+    lone = 0.125 + offs * h + (rng.random((len(offs), 3)) - 0.5) * 0.2
+    far = (rng.random((200, 3)) - 0.5) * 1.9
+    x = np.concatenate([crowd, lone, far])[None]
+    N = x.shape[1]
+    s = rng.standard_normal((1, N, 16)).astype(np.float32)
+    m = (rng.random((1, N)) + 1e-3).astype(np.float32)
+    return H.Case(f"lone-heavy-{mode}", H.pack_pos(x), s, m, (8, 8, 8), h, False, mode, 64)
 
 
 def _workload_cases():
