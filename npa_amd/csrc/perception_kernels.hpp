@@ -25,6 +25,8 @@
 
 #include "sphops_internal.hpp"
 
+#include <type_traits>
+
 namespace sphops {
 namespace pk {
 
@@ -1165,110 +1167,117 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
       const Row row = Row::of(a, k);
       const int start = row.start;
       const int end = row.end;
-      for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
-        // geometry of the pair this lane owns (all zero for a stencil
-        // candidate out of radius)
-        const int to = t0 + slice * S;
-        uint32_t jo = k;
-        float vo = 0.0f, Wo = 0.0f, t2o = 0.0f, jao = 0.0f, jbo = 0.0f;
-        float rbo[3] = {0.0f, 0.0f, 0.0f}, wo[3] = {0.0f, 0.0f, 0.0f};
-        float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float d2 = 0.0f, r[3] = {0.0f, 0.0f, 0.0f};
-        bool inr = false;
-        if (to < end) {
-          const uint32_t jc = row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
-          pj = xw[jc];
-          float xj[3];
-          unpack(pj, xj);
-          d2 = displacement<D, P>(g, xi, xj, r);
-          inr = !row.stencil || d2 < g.eps2;
-          if (inr) jo = jc;
-        }
-        if (inr) {
-          float xj[3];
-          unpack(pj, xj);
-          vo = pj.w;
-          const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
-          Wo = poly6(g.eps2, db);
-          float d;
-          const float mag = spiky_mag(g.eps, db, &d);
-  #pragma unroll
-          for (int e = 0; e < D; ++e) {
-            wo[e] = mag * rbo[e];
-            wsum[e] += vo * wo[e];
+      // rows walked on the stencil (count < 0, rare) take the general loop;
+      // a wave without them the list-only one
+      auto walk = [&](auto stencil_rows) {
+        constexpr bool ST = decltype(stencil_rows)::value;
+        for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
+          // geometry of the pair this lane owns (all zero for a stencil
+          // candidate out of radius)
+          const int to = t0 + slice * S;
+          uint32_t jo = k;
+          float vo = 0.0f, Wo = 0.0f, t2o = 0.0f, jao = 0.0f, jbo = 0.0f;
+          float rbo[3] = {0.0f, 0.0f, 0.0f}, wo[3] = {0.0f, 0.0f, 0.0f};
+          float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          float d2 = 0.0f, r[3] = {0.0f, 0.0f, 0.0f};
+          bool inr = false;
+          if (to < end) {
+            const uint32_t jc = ST && row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
+            pj = xw[jc];
+            float xj[3];
+            unpack(pj, xj);
+            d2 = displacement<D, P>(g, xi, xj, r);
+            inr = !(ST && row.stencil) || d2 < g.eps2;
+            if (inr) jo = jc;
           }
-          if (db != 0.0f && db < g.eps2) {
-            const float tt = g.eps2 - db;
-            t2o = tt * tt;
-            const float di = fast_rcp(d);
-            jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
-            jbo = 3.0f * (g.eps2 - db) * di * di * di;
-          }
-        }
-  #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (t0 + q * S >= end) break;  // uniform over the quad
-          uint32_t j;
-          float vj, W, t2, ja, jb, rb[3], w[3];
-  #define SPHOPS_QUAD_FETCH(QQ)                                                   \
-    j = quad_get<QQ>(jo);                                                         \
-    vj = quad_get<QQ>(vo);                                                        \
-    W = quad_get<QQ>(Wo);                                                         \
-    t2 = quad_get<QQ>(t2o);                                                       \
-    ja = quad_get<QQ>(jao);                                                       \
-    jb = quad_get<QQ>(jbo);                                                       \
-    for (int e = 0; e < D; ++e) {                                                 \
-      rb[e] = quad_get<QQ>(rbo[e]);                                               \
-      w[e] = quad_get<QQ>(wo[e]);                                                 \
-    }
-          if (q == 0) { SPHOPS_QUAD_FETCH(0) }
-          else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
-          else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
-          else { SPHOPS_QUAD_FETCH(3) }
-  #undef SPHOPS_QUAD_FETCH
-          float gbj[CW], ggj[CW * D];
-          load_span<CW, true>(row_slice<OFF32>(a.g, j, C, c0), gbj);
-          load_span<CW * D, true>(row_slice<OFF32>(a.g2, j, C * D, c0 * D), ggj);
-          if constexpr (!FULL) {
-  #pragma unroll
-            for (int f = 0; f < CW; ++f) {
-              dsb[f] += W * gbj[f];
-  #pragma unroll
-              for (int e = 0; e < D; ++e) dsg[f] += ggj[f * D + e] * w[e];
-            }
-          } else {
-            float sj[CW];
-            load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
-            float A = 0.0f, Bv = 0.0f;
-            float u1[D] = {}, u2[D] = {};
-  #pragma unroll
-            for (int f = 0; f < CW; ++f) {
-              dsb[f] += W * gbj[f];
-              A += gbi[f] * sj[f];
-              Bv += gbj[f] * si[f];
-              const float df = si[f] - sj[f];
-  #pragma unroll
-              for (int e = 0; e < D; ++e) {
-                dsg[f] += ggj[f * D + e] * w[e];
-                u1[e] += df * ggj[f * D + e];
-                u2[e] += df * ggi[f * D + e];
-              }
-            }
-            const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
-            float u[D], uw = 0.0f, rv = 0.0f;
-  #pragma unroll
+          if (inr) {
+            float xj[3];
+            unpack(pj, xj);
+            vo = pj.w;
+            const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
+            Wo = poly6(g.eps2, db);
+            float d;
+            const float mag = spiky_mag(g.eps, db, &d);
+    #pragma unroll
             for (int e = 0; e < D; ++e) {
-              dxb[e] += m6 * rb[e];
-              uw += u1[e] * w[e];
-              u[e] = vi * u1[e] + vj * u2[e];
-              rv += rb[e] * u[e];
+              wo[e] = mag * rbo[e];
+              wsum[e] += vo * wo[e];
             }
-            drg += uw;
-  #pragma unroll
-            for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
+            if (db != 0.0f && db < g.eps2) {
+              const float tt = g.eps2 - db;
+              t2o = tt * tt;
+              const float di = fast_rcp(d);
+              jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
+              jbo = 3.0f * (g.eps2 - db) * di * di * di;
+            }
+          }
+    #pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (t0 + q * S >= end) break;  // uniform over the quad
+            uint32_t j;
+            float vj, W, t2, ja, jb, rb[3], w[3];
+    #define SPHOPS_QUAD_FETCH(QQ)                                                   \
+      j = quad_get<QQ>(jo);                                                         \
+      vj = quad_get<QQ>(vo);                                                        \
+      W = quad_get<QQ>(Wo);                                                         \
+      t2 = quad_get<QQ>(t2o);                                                       \
+      ja = quad_get<QQ>(jao);                                                       \
+      jb = quad_get<QQ>(jbo);                                                       \
+      for (int e = 0; e < D; ++e) {                                                 \
+        rb[e] = quad_get<QQ>(rbo[e]);                                               \
+        w[e] = quad_get<QQ>(wo[e]);                                                 \
+      }
+            if (q == 0) { SPHOPS_QUAD_FETCH(0) }
+            else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
+            else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
+            else { SPHOPS_QUAD_FETCH(3) }
+    #undef SPHOPS_QUAD_FETCH
+            float gbj[CW], ggj[CW * D];
+            load_span<CW, true>(row_slice<OFF32>(a.g, j, C, c0), gbj);
+            load_span<CW * D, true>(row_slice<OFF32>(a.g2, j, C * D, c0 * D), ggj);
+            if constexpr (!FULL) {
+    #pragma unroll
+              for (int f = 0; f < CW; ++f) {
+                dsb[f] += W * gbj[f];
+    #pragma unroll
+                for (int e = 0; e < D; ++e) dsg[f] += ggj[f * D + e] * w[e];
+              }
+            } else {
+              float sj[CW];
+              load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
+              float A = 0.0f, Bv = 0.0f;
+              float u1[D] = {}, u2[D] = {};
+    #pragma unroll
+              for (int f = 0; f < CW; ++f) {
+                dsb[f] += W * gbj[f];
+                A += gbi[f] * sj[f];
+                Bv += gbj[f] * si[f];
+                const float df = si[f] - sj[f];
+    #pragma unroll
+                for (int e = 0; e < D; ++e) {
+                  dsg[f] += ggj[f * D + e] * w[e];
+                  u1[e] += df * ggj[f * D + e];
+                  u2[e] += df * ggi[f * D + e];
+                }
+              }
+              const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
+              float u[D], uw = 0.0f, rv = 0.0f;
+    #pragma unroll
+              for (int e = 0; e < D; ++e) {
+                dxb[e] += m6 * rb[e];
+                uw += u1[e] * w[e];
+                u[e] = vi * u1[e] + vj * u2[e];
+                rv += rb[e] * u[e];
+              }
+              drg += uw;
+    #pragma unroll
+              for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
+            }
           }
         }
-      }
+      };
+      if (__ballot(row.stencil) != 0) walk(std::integral_constant<bool, true>{});
+      else walk(std::integral_constant<bool, false>{});
       if constexpr (FULL) {  // blur's dL/drho: sum_j W_j g_j . s_i = s_i . sum_j W_j g_j
   #pragma unroll
         for (int f = 0; f < CW; ++f) drb += si[f] * dsb[f];
@@ -1308,7 +1317,7 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
 // its channel slice.  The moment matrix is accumulated by the owning lane,
 // reduced over the group and handed to the four slice lanes.
 template <int D, bool P, int CW, bool OFF32>
-__global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
+__global__ __launch_bounds__(kThreads, 8) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
   const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
   const uint32_t stride = schedule_stride(live);
@@ -1335,60 +1344,67 @@ __global__ __launch_bounds__(kThreads) void k_blur_hybrid_fwd_quad(GridParams g,
       const Row row = Row::of(a, k);
       const int start = row.start;
       const int end = row.end;
-      for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
-        const int to = t0 + slice * S;
-        uint32_t jo = k;
-        float wo = 0.0f, to_ = 0.0f, ro[3] = {0.0f, 0.0f, 0.0f};
-        float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float d2 = 0.0f, rr[3] = {0.0f, 0.0f, 0.0f};
-        bool inr = false;
-        if (to < end) {
-          const uint32_t jc = row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
-          pj = xw[jc];
-          float xj[3];
-          unpack(pj, xj);
-          d2 = displacement<D, P>(g, xi, xj, rr);
-          inr = !row.stencil || d2 < g.eps2;
-          if (inr) jo = jc;
-        }
-        if (inr) {
-          ro[0] = rr[0];
-          ro[1] = rr[1];
-          ro[2] = rr[2];
-          wo = poly6(g.eps2, d2) * pj.w;
-          float d;
-          to_ = spiky_mag(g.eps, d2, &d) * pj.w;
-  #pragma unroll
-          for (int p = 0; p < D; ++p)
-  #pragma unroll
-            for (int q = p; q < D; ++q) M[p * D + q] += to_ * ro[p] * ro[q];
-        }
-  #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (t0 + q * S >= end) break;  // uniform over the quad
-          uint32_t j;
-          float w, t, r[3];
-  #define SPHOPS_QUAD_FETCH(QQ)             \
-    j = quad_get<QQ>(jo);                   \
-    w = quad_get<QQ>(wo);                   \
-    t = quad_get<QQ>(to_);                  \
-    for (int e = 0; e < D; ++e) r[e] = quad_get<QQ>(ro[e]);
-          if (q == 0) { SPHOPS_QUAD_FETCH(0) }
-          else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
-          else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
-          else { SPHOPS_QUAD_FETCH(3) }
-  #undef SPHOPS_QUAD_FETCH
-          float sj[CW];
-          load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
-  #pragma unroll
-          for (int f = 0; f < CW; ++f) {
-            blur[f] += w * sj[f];
-            const float qf = t * (sj[f] - si[f]);
-  #pragma unroll
-            for (int e = 0; e < D; ++e) acc[f * D + e] += qf * r[e];
+      // rows walked on the stencil (count < 0, rare) take the general loop;
+      // a wave without them the list-only one
+      auto walk = [&](auto stencil_rows) {
+        constexpr bool ST = decltype(stencil_rows)::value;
+        for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
+          const int to = t0 + slice * S;
+          uint32_t jo = k;
+          float wo = 0.0f, to_ = 0.0f, ro[3] = {0.0f, 0.0f, 0.0f};
+          float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          float d2 = 0.0f, rr[3] = {0.0f, 0.0f, 0.0f};
+          bool inr = false;
+          if (to < end) {
+            const uint32_t jc = ST && row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
+            pj = xw[jc];
+            float xj[3];
+            unpack(pj, xj);
+            d2 = displacement<D, P>(g, xi, xj, rr);
+            inr = !(ST && row.stencil) || d2 < g.eps2;
+            if (inr) jo = jc;
+          }
+          if (inr) {
+            ro[0] = rr[0];
+            ro[1] = rr[1];
+            ro[2] = rr[2];
+            wo = poly6(g.eps2, d2) * pj.w;
+            float d;
+            to_ = spiky_mag(g.eps, d2, &d) * pj.w;
+    #pragma unroll
+            for (int p = 0; p < D; ++p)
+    #pragma unroll
+              for (int q = p; q < D; ++q) M[p * D + q] += to_ * ro[p] * ro[q];
+          }
+    #pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (t0 + q * S >= end) break;  // uniform over the quad
+            uint32_t j;
+            float w, t, r[3];
+    #define SPHOPS_QUAD_FETCH(QQ)             \
+      j = quad_get<QQ>(jo);                   \
+      w = quad_get<QQ>(wo);                   \
+      t = quad_get<QQ>(to_);                  \
+      for (int e = 0; e < D; ++e) r[e] = quad_get<QQ>(ro[e]);
+            if (q == 0) { SPHOPS_QUAD_FETCH(0) }
+            else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
+            else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
+            else { SPHOPS_QUAD_FETCH(3) }
+    #undef SPHOPS_QUAD_FETCH
+            float sj[CW];
+            load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
+    #pragma unroll
+            for (int f = 0; f < CW; ++f) {
+              blur[f] += w * sj[f];
+              const float qf = t * (sj[f] - si[f]);
+    #pragma unroll
+              for (int e = 0; e < D; ++e) acc[f * D + e] += qf * r[e];
+            }
           }
         }
-      }
+      };
+      if (__ballot(row.stencil) != 0) walk(std::integral_constant<bool, true>{});
+      else walk(std::integral_constant<bool, false>{});
     }
     grp_sum_streams(G, blur, acc);
     grp_sum(G, M);
