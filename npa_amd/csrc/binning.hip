@@ -518,19 +518,42 @@ __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restr
   if (threadIdx.x < kNumClasses) cnt[blockIdx.x * kNumClasses + threadIdx.x] = h[threadIdx.x];
 }
 
-// Stable scatter of a tile's items into order, class by class, at the
-// scanned segment offsets.  Same tile walk as the radix scatter: wave w owns
-// items [w*1024, (w+1)*1024) in index order; three ballots identify lanes of
-// the same class.
+// Stable scatter of a tile's items into order, class by class.  The tile
+// first finds its segment offsets (segment s = tile * kNumClasses + class,
+// in tile-major order): the sum of the counts of all earlier tiles, reduced
+// by the workgroup, plus the tile's own earlier classes; it writes them to
+// seg (and the last tile the item total to seg[nseg]).  Same tile walk as the
+// radix scatter: wave w owns items [w*1024, (w+1)*1024) in index order;
+// three ballots identify lanes of the same class.
 template <bool CSR>
 __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __restrict__ src, uint32_t n,
-                                                            ClassBounds cb, const uint32_t* __restrict__ cnt_scan,
+                                                            ClassBounds cb, const uint32_t* __restrict__ cnt,
+                                                            uint32_t* __restrict__ seg,
                                                             int32_t* __restrict__ order) {
   __shared__ uint32_t wcnt[kThreads / 64][kNumClasses];
   __shared__ uint32_t gbase[kNumClasses];
+  __shared__ uint32_t part[kThreads / 64];
   const int wave = threadIdx.x >> 6, lane = __lane_id();
   if (threadIdx.x < (kThreads / 64) * kNumClasses) (&wcnt[0][0])[threadIdx.x] = 0;
-  if (threadIdx.x < kNumClasses) gbase[threadIdx.x] = cnt_scan[blockIdx.x * kNumClasses + threadIdx.x];
+  {
+    const uint32_t before = blockIdx.x * (uint32_t)kNumClasses;
+    uint32_t s = 0;
+    for (uint32_t i = threadIdx.x; i < before; i += kThreads) s += cnt[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+    if (lane == 0) part[wave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t run = 0;
+      for (int w = 0; w < kThreads / 64; ++w) run += part[w];
+      for (int q = 0; q < kNumClasses; ++q) {
+        gbase[q] = run;
+        seg[before + q] = run;
+        run += cnt[before + q];
+      }
+      if (blockIdx.x == gridDim.x - 1) seg[before + kNumClasses] = run;
+    }
+  }
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
   const uint64_t below_mask = lanemask_lt();
@@ -570,23 +593,70 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
   }
 }
 
-// Waves needed by segment s = (tile, class): items / (64 / group size),
-// rounded up.  seg holds nseg + 1 offsets (the last one is the item total).
-__global__ void k_wave_counts(const uint32_t* __restrict__ seg, uint32_t nseg, GroupSizes gs,
-                              uint32_t* __restrict__ wcnt) {
-  const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-  if (s >= nseg) return;
-  const uint32_t lo = seg[s], hi = seg[s + 1];
-  const uint32_t per = (uint32_t)(kWave / gs.g[s % kNumClasses]);
-  wcnt[s] = (hi - lo + per - 1) / per;
+// Waves per segment for one or two group-size tables, scanned into the first
+// wave of every segment (wstart[table * nseg + s]) and the tables' wave totals,
+// by one workgroup (chunks of kThreads * 8 segments with a running carry).
+__global__ __launch_bounds__(kThreads) void k_wave_tables(const uint32_t* __restrict__ seg, uint32_t nseg,
+                                                          GroupSizes gs1, GroupSizes gs2, int tables,
+                                                          uint32_t* __restrict__ wstart,
+                                                          int32_t* __restrict__ total1,
+                                                          int32_t* __restrict__ total2) {
+  __shared__ uint32_t part[kThreads / 64];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  constexpr uint32_t kPer = 8;
+  for (int tb = 0; tb < tables; ++tb) {
+    const GroupSizes& gs = tb == 0 ? gs1 : gs2;
+    uint32_t carry = 0;
+    for (uint32_t c0 = 0; c0 < nseg; c0 += kThreads * kPer) {
+      const uint32_t s0 = c0 + threadIdx.x * kPer;
+      uint32_t v[kPer], run = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < kPer; ++i) {
+        const uint32_t s = s0 + i;
+        uint32_t w = 0;
+        if (s < nseg) {
+          const uint32_t per = (uint32_t)(kWave / gs.g[s % kNumClasses]);
+          w = (seg[s + 1] - seg[s] + per - 1) / per;
+        }
+        v[i] = run;
+        run += w;
+      }
+      uint32_t incl = run;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      if (lane == 63) part[wave] = incl;
+      __syncthreads();
+      uint32_t wbase = 0, chunk = 0;
+#pragma unroll
+      for (int w = 0; w < kThreads / 64; ++w) {
+        if (w < wave) wbase += part[w];
+        chunk += part[w];
+      }
+      __syncthreads();
+      const uint32_t base = carry + wbase + incl - run;
+#pragma unroll
+      for (uint32_t i = 0; i < kPer; ++i)
+        if (s0 + i < nseg) wstart[(uint64_t)tb * nseg + s0 + i] = base + v[i];
+      carry += chunk;
+    }
+    if (threadIdx.x == 0) *(tb == 0 ? total1 : total2) = (int32_t)carry;
+  }
 }
 
-// One workgroup per tile writes the wave descriptors of its segments:
-// {first slot in order, group size << 8 | items in the wave}.
-__global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restrict__ seg,
-                                                        const uint32_t* __restrict__ wstart, GroupSizes gs,
-                                                        uint2* __restrict__ waves) {
+// One workgroup per (tile, table) writes the wave descriptors of its
+// segments: {first slot in order, group size << 8 | items in the wave}.
+__global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restrict__ seg, uint32_t nseg,
+                                                        const uint32_t* __restrict__ wstart_all, GroupSizes gs1,
+                                                        GroupSizes gs2, uint2* __restrict__ waves1,
+                                                        uint2* __restrict__ waves2) {
   const uint32_t t = blockIdx.x;
+  const bool second = blockIdx.y != 0;
+  const GroupSizes& gs = second ? gs2 : gs1;
+  const uint32_t* __restrict__ wstart = wstart_all + (second ? nseg : 0u);
+  uint2* __restrict__ waves = second ? waves2 : waves1;
 #pragma unroll
   for (uint32_t q = 0; q < (uint32_t)kNumClasses; ++q) {
     const uint32_t s = t * kNumClasses + q;
@@ -609,30 +679,24 @@ void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, co
   const uint32_t n = (uint32_t)g.n_keys;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
   const uint32_t nseg = (uint32_t)kNumClasses * ntiles;
-  // hist holds 256 * ntiles words: item offsets per segment (nseg + 1, the
-  // last is the number of scheduled items), then wave offsets per segment
-  uint32_t* seg = g.hist;
-  uint32_t* wcnt = g.hist + nseg + 1;
-  hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg);
+  // hist holds 256 * ntiles words: item counts per segment, their offsets
+  // (nseg + 1, the last is the number of scheduled items), then the first
+  // wave of every segment for each descriptor table
+  uint32_t* cnt = g.hist;
+  uint32_t* seg = cnt + nseg;
+  uint32_t* wstart = seg + nseg + 1;
+  hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt);
   SPHOPS_LAUNCHED();
-  device_exclusive_scan(seg, seg, nseg, g.scan_tmp, seg + nseg, st);
-  hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, seg, order);
+  hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, seg, order);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg, gs,
-                     wcnt);
+  const int tables = waves2 != nullptr ? 2 : 1;  // a second table: same order, other group sizes
+  const GroupSizes gsb = gs2 != nullptr ? *gs2 : gs;
+  hipLaunchKernelGGL(k_wave_tables, dim3(1), dim3(kThreads), 0, st, seg, nseg, gs, gsb, tables, wstart, wave_total,
+                     tables == 2 ? wave_total2 : wave_total);
   SPHOPS_LAUNCHED();
-  device_exclusive_scan(wcnt, wcnt, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total), st);
-  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt, gs, waves);
+  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles, (uint32_t)tables), dim3(kThreads), 0, st, seg, nseg, wstart, gs, gsb,
+                     waves, tables == 2 ? waves2 : waves);
   SPHOPS_LAUNCHED();
-  if (waves2 != nullptr) {  // a second descriptor table over the same order, other group sizes
-    uint32_t* wcnt2 = wcnt + nseg;
-    hipLaunchKernelGGL(k_wave_counts, dim3((nseg + kThreads - 1) / kThreads), dim3(kThreads), 0, st, seg, nseg,
-                       *gs2, wcnt2);
-    SPHOPS_LAUNCHED();
-    device_exclusive_scan(wcnt2, wcnt2, nseg, g.scan_tmp, reinterpret_cast<uint32_t*>(wave_total2), st);
-    hipLaunchKernelGGL(k_wave_fill, dim3(ntiles), dim3(kThreads), 0, st, seg, wcnt2, *gs2, waves2);
-    SPHOPS_LAUNCHED();
-  }
 }
 
 }  // namespace
