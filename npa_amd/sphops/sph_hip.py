@@ -64,6 +64,18 @@ def _validate_shape(t, expected, name):
 _F32, _I32 = torch.float32, torch.int32
 
 
+def next_index_capacity(total, unstored, used_capacity, slack_shift):
+    """Index capacity for the next snapshot's neighbour list from the last
+    list's pair total, the pairs of its rows that were not stored and the
+    capacity it had: the total plus a margin of total >> slack_shift plus
+    1024.  A list that did not fit although its buffer held the total had
+    uneven slices (the fill allocates rows per slice of the buffer), so the
+    margin grows (the shift drops, down to 1).  Returns (capacity, shift)."""
+    if unstored and used_capacity >= total and slack_shift > 1:
+        slack_shift -= 1
+    return total + (total >> slack_shift) + 1024, slack_shift
+
+
 class NeighborPlan(tuple):
     """A snapshot's neighbour list and its schedules (``neighbor_list``):
     the tuple ``(start, count, index, order, waves, wave_count, waves_split,
@@ -471,9 +483,8 @@ class _HashGridNative:
         v = self._rb.tolist()
         total = (v[0] & 0xFFFFFFFF) | (v[1] << 32)
         unstored = (v[2] & 0xFFFFFFFF) | (v[3] << 32)
-        if unstored and self._rb_cap >= total and self._slack_shift > 1:
-            self._slack_shift -= 1
-        self._index_capacity = total + (total >> self._slack_shift) + 1024
+        self._index_capacity, self._slack_shift = next_index_capacity(total, unstored, self._rb_cap,
+                                                                      self._slack_shift)
         self._wave_counts = (v[4], v[5], v[7])
         self._rb_event = None
 

@@ -54,3 +54,23 @@ def test_perception_features_rejects_non_contiguous():
     with pytest.raises(TypeError):
         PF.PerceptionFeatures.apply(s.transpose(1, 2).contiguous().transpose(1, 2), s, None, None, 2, 1.0, 1.0,
                                     4.0, 0)
+
+
+def test_next_index_capacity():
+    """The list's index-buffer policy: the last total plus 1/8 and 1024; a list
+    that overflowed with a buffer smaller than its total keeps the margin, one
+    that overflowed with room for its total (uneven slices) widens it, down to
+    a margin of 1/2."""
+    from npa_amd.sphops.sph_hip import next_index_capacity as nic
+    assert nic(8000, 0, 10000, 3) == (8000 + 1000 + 1024, 3)
+    assert nic(0, 0, 40, 3) == (1024, 3)
+    # too small a buffer: the next one holds the total, margin unchanged
+    cap, s = nic(1 << 20, 5, 1000, 3)
+    assert s == 3 and cap >= 1 << 20
+    # room for the total but rows did not fit: wider margin each time, to 1/2
+    cap, s = nic(1 << 20, 5, 1 << 21, 3)
+    assert s == 2 and cap == (1 << 20) + (1 << 18) + 1024
+    assert nic(1 << 20, 5, 1 << 21, 2)[1] == 1
+    assert nic(1 << 20, 5, 1 << 21, 1) == ((1 << 20) + (1 << 19) + 1024, 1)
+    # totals above 2^31 stay exact (Python integers); the grid caps the buffer later
+    assert nic(3 << 30, 0, 0, 3)[0] == (3 << 30) + (3 << 27) + 1024
