@@ -46,6 +46,12 @@ int sphops_abi_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* sphops_last_error(void);
 
+/* A grid of no particles (particle_count or batch_size 0) is valid: every
+ * call then validates its other arguments and launches nothing, and the
+ * per-particle buffers (positions, states, outputs, block_info with no rows)
+ * may be NULL, as torch passes them for empty tensors.  bin_offsets is
+ * always B*G+1 entries and receives zeros. */
+
 /* HashGrid{2D,3D}{Periodic,Box} / VHashGrid... constructors
  * (sphops/sph_cuda.cu:3049-3093 classes, HashGrid::_init sph_cuda.cu:1836-1899;
  * Python entry sphops/sph.py:48-78).  grid_size has `dim` entries. */

@@ -302,7 +302,8 @@ static void check_initialize_args(const Grid& g, const float* positions, const i
                                   const int32_t* bin_offsets, const int32_t* block_info) {
   require(bin_offsets != nullptr, "bin_offsets must not be NULL");
   require(g.n_keys == 0 || (positions && permutation), "positions and permutation must not be NULL");
-  require(g.particle_mode || block_info != nullptr, "block_info must not be NULL in grid mode");
+  require(g.particle_mode || block_info != nullptr || g.max_blocks == 0,
+          "block_info must not be NULL in grid mode");
   require(sphops::pk::aligned16(bin_offsets), "bin_offsets must be 16-byte aligned");
   require(g.particle_mode || sphops::pk::aligned16(block_info), "block_info must be 16-byte aligned");
   require(g.dim == 2 || sphops::pk::aligned16(positions), "3D positions must be 16-byte aligned");
@@ -345,8 +346,13 @@ int sphops_backward_bin_particles(const sphops_grid* grid, const float* grad_out
 static int fwd_op(const sphops_grid* grid, Op op, const int32_t* bo, OpPtrs a, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
-    require(bo != nullptr && a.x != nullptr && a.out0 != nullptr, "null buffer");
     const bool chan = op == Op::Blur || op == Op::Gradient || op == Op::GradientHybrid || op == Op::BlurGradientHybrid;
+    if (grid->n_keys == 0) {  // no particles: nothing to read or write (empty tensors may be NULL)
+      require(bo != nullptr, "null buffer");
+      if (chan) sphops::check_channels(a.C);
+      return;
+    }
+    require(bo != nullptr && a.x != nullptr && a.out0 != nullptr, "null buffer");
     if (chan) {
       sphops::check_channels(a.C);
       require(a.s != nullptr, "state must not be NULL");
@@ -438,6 +444,11 @@ int sphops_gradient_hybrid_forward(const sphops_grid* grid, const float* x, cons
 static int bwd_op(const sphops_grid* grid, Op op, bool full, const int32_t* bo, OpPtrs a, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
+    if (grid->n_keys == 0) {  // no particles: nothing to read or write (empty tensors may be NULL)
+      require(bo != nullptr, "null buffer");
+      if (op == Op::Blur || op == Op::Gradient || op == Op::BlurGradientHybrid) sphops::check_channels(a.C);
+      return;
+    }
     require(bo != nullptr && a.x != nullptr && a.m != nullptr && a.g != nullptr, "null buffer");
     if (op == Op::Blur || op == Op::Gradient || op == Op::BlurGradientHybrid) {
       sphops::check_channels(a.C);

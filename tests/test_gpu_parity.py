@@ -46,6 +46,12 @@ def _cases():
     d.x[..., :2] += 0.5  # the cluster straddles the periodic boundary
     cs.append(d)
     cs += [_lone_heavy_case(mode) for mode in ("grid", "particle")]
+    # one particle per cloud (its only neighbour is itself), and one crowded
+    # cell split into several units and several blocks (maxp = 16)
+    cs.append(H.random_case("single3d", 2, 1, 16, 3, 8, 0.25, False, "grid"))
+    one = H.random_case("onecell2d", 1, 100, 16, 2, 8, 0.25, True, "grid", maxp=16)
+    one.x[..., :2] = 0.125 + (one.x[..., :2] - 0.0) * 0.05  # inside cell (4, 4)
+    cs.append(one)
     return cs
 
 
