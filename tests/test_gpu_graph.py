@@ -73,6 +73,50 @@ def test_captured_step_replays_match_eager(dim, periodic, mode):
     grid.set_capture_capacity(0)
 
 
+def test_capture_below_the_sizes_still_correct():
+    """Capture mode with sizes far below the step's needs: an index buffer of
+    64 entries (almost every row is walked on the stencil instead) and pair
+    launches sized for a twentieth of the waves (the kernels loop over the
+    true device counts).  Replays still give the eager results, within fp32
+    summation-order differences, and list_overflow reports the small buffer."""
+    import npa_amd.sphops as sp
+    B, N, C, dim = 2, 3000, 16, 3
+    cases = [H.random_case("graph-small", B, N, C, dim, 16, 0.06, False, "grid", uniform=True, sigma=0.45,
+                           seed=seed) for seed in (5, 6)]
+    c0 = cases[0]
+    grid = sp.HashGrid(dim=dim, boundary="clamped", mode="grid", grid_size=list(c0.grid_size), eps=c0.eps,
+                       num_particles=N, batch_size=B, max_particles_per_block=c0.maxp)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    ups = [torch.randn(B, N, C, device="cuda", generator=gen), torch.randn(B, N, C, dim, device="cuda", generator=gen),
+           torch.randn(B, N, dim, device="cuda", generator=gen)]
+    xs = [torch.from_numpy(c.x).cuda() for c in cases]
+    ss = [torch.from_numpy(c.s).cuda() for c in cases]
+    _step(sp, grid, xs[0], ss[0], ups)
+    eager = [[t.clone() for t in _step(sp, grid, x, s, ups)] for x, s in zip(xs, ss)]
+    grid.hashgrid.set_capture_capacity(64, wave_margin=0.05)
+    static_x, static_s = xs[0].clone(), ss[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            _step(sp, grid, static_x, static_s, ups)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = _step(sp, grid, static_x, static_s, ups)
+    names = ["blur", "gradient_hybrid", "density_gradient", "rho", "dL/dx", "dL/ds"]
+    for k in (1, 0):
+        static_x.copy_(xs[k])
+        static_s.copy_(ss[k])
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(names, outs, eager[k]):
+            err = (got - ref).abs().max().item()
+            assert err <= 1e-4 * ref.abs().max().item() + 1e-6, f"replay on case {k}: {name} off by {err}"
+    assert grid.list_overflow()
+    grid.set_capture_capacity(0)
+
+
 class _TinyNPA(torch.nn.Module):
     """The NPA attributes step_euler reads (models/npa.py:15-63), small MLP."""
 
