@@ -398,7 +398,7 @@ class _HashGridNative:
         # device counts: [0:2] in-radius pairs (int64), [2:4] pairs of rows not
         # stored (int64), [4] waves, [5] split waves, [6] tile units, [7] waves
         # of the particles outside the tiles
-        small = torch.zeros(8, dtype=_I32, device=dev)
+        small = torch.empty(8, dtype=_I32, device=dev)  # every word read is written by a kernel
         cap = self._capacity(n)
         index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
         tiles = self._tile_buffers(dev, n, wcap) if self.tiles_enabled else None
@@ -418,7 +418,7 @@ class _HashGridNative:
                 ctypes.c_void_p(small.data_ptr() + 24), ctypes.c_void_p(tiles[1].data_ptr()),
                 ctypes.c_void_p(tiles[2].data_ptr()), ctypes.c_void_p(small.data_ptr() + 28), st))
         if not capturing:
-            self._start_readback(small, cap)
+            self._start_readback(small, cap, tiles is not None)
         e1, e2, e3 = self._wave_estimates(n)
         plan = NeighborPlan(start, count, index, order, waves, e1, waves2, e2, small)
         plan.capacity = cap
@@ -459,13 +459,15 @@ class _HashGridNative:
     # its buffer held the total, i.e. the fill's slices were uneven.
     _slack_shift = 3
 
-    def _start_readback(self, small, cap):
-        """Copy the device counts to pinned host memory without waiting."""
+    def _start_readback(self, small, cap, tiles):
+        """Copy the device counts to pinned host memory without waiting
+        (the tile counts are valid only for a plan with tiles)."""
         rb = getattr(self, "_rb", None)
         if rb is None:
             self._rb = rb = torch.empty(8, dtype=_I32, pin_memory=True)
         rb.copy_(small, non_blocking=True)
         self._rb_cap = cap
+        self._rb_tiles = tiles
         self._rb_event = torch.cuda.Event()
         self._rb_event.record()
 
@@ -485,7 +487,8 @@ class _HashGridNative:
         unstored = (v[2] & 0xFFFFFFFF) | (v[3] << 32)
         self._index_capacity, self._slack_shift = next_index_capacity(total, unstored, self._rb_cap,
                                                                       self._slack_shift)
-        self._wave_counts = (v[4], v[5], v[7])
+        first = max(self._b * self._n // 8, 1)
+        self._wave_counts = (v[4], v[5], v[7] if self._rb_tiles else first)
         self._rb_event = None
 
     # Cell tiles for the pass-B backward (sphops_neighbor_tiles): opt-in
