@@ -29,10 +29,14 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 
 // ------------------------------------------------------------------ keys
 
+// The sort moves one 64-bit word per particle: its cell key in the high half
+// (the sort key) and its index in the low half (B*G and B*N are below 2^32).
+__device__ __forceinline__ uint32_t kv_key(uint64_t v) { return (uint32_t)(v >> 32); }
+__device__ __forceinline__ uint32_t kv_val(uint64_t v) { return (uint32_t)v; }
+
 template <int D, bool PERIODIC>
 __global__ __launch_bounds__(kThreads) void k_cell_keys(GridParams g, const float* __restrict__ pos,
-                                                        uint32_t* __restrict__ keys,
-                                                        uint32_t* __restrict__ vals, uint32_t n) {
+                                                        uint64_t* __restrict__ kv, uint32_t n) {
   const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
   if (k >= n) return;
   float x[3];
@@ -40,8 +44,7 @@ __global__ __launch_bounds__(kThreads) void k_cell_keys(GridParams g, const floa
   int c[3];
   pos2cell<D, PERIODIC>(g, x, c);
   const uint32_t b = k / g.N;
-  keys[k] = b * g.G + cell_hash<D>(g, c);
-  vals[k] = k;
+  kv[k] = ((uint64_t)(b * g.G + cell_hash<D>(g, c)) << 32) | k;
 }
 
 // ------------------------------------------------------- device-wide scan
@@ -183,7 +186,7 @@ void device_exclusive_scan(const uint32_t* in, uint32_t* out, uint64_t n, uint32
 
 // ------------------------------------------------------------ radix sort
 
-__global__ __launch_bounds__(kThreads) void k_radix_hist(const uint32_t* __restrict__ keys, uint32_t n, int shift,
+__global__ __launch_bounds__(kThreads) void k_radix_hist(const uint64_t* __restrict__ kv, uint32_t n, int shift,
                                                          uint32_t* __restrict__ hist, uint32_t ntiles) {
   __shared__ uint32_t h[kBins];
   for (int d = threadIdx.x; d < kBins; d += kThreads) h[d] = 0;
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void k_radix_hist(const uint32_t* __restr
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const uint32_t idx = base + i * kThreads + threadIdx.x;
-    if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & (kBins - 1)], 1u);
+    if (idx < n) atomicAdd(&h[(kv_key(kv[idx]) >> shift) & (kBins - 1)], 1u);
   }
   __syncthreads();
   for (int d = threadIdx.x; d < kBins; d += kThreads) hist[d * ntiles + blockIdx.x] = h[d];
@@ -202,10 +205,8 @@ __global__ __launch_bounds__(kThreads) void k_radix_hist(const uint32_t* __restr
 // [w*1024, (w+1)*1024) and walks them 64 at a time in index order; lanes with
 // equal digits find each other with 8 ballots, so each key's rank among the
 // equal-digit keys before it is exact and no atomics are involved.
-__global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint32_t* __restrict__ kin,
-                                                            const uint32_t* __restrict__ vin,
-                                                            uint32_t* __restrict__ kout,
-                                                            uint32_t* __restrict__ vout, uint32_t n, int shift,
+__global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint64_t* __restrict__ kin,
+                                                            uint64_t* __restrict__ kout, uint32_t n, int shift,
                                                             const uint32_t* __restrict__ hist_scan,
                                                             uint32_t ntiles) {
   __shared__ uint32_t wcnt[kThreads / 64][kBins];
@@ -217,14 +218,14 @@ __global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint32_t* __re
 
   const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
   const uint64_t below_mask = lanemask_lt();
-  uint32_t key[kItems], val[kItems], rank[kItems];
+  uint64_t word[kItems];
+  uint32_t rank[kItems];
 #pragma unroll
   for (int t = 0; t < kItems; ++t) {
     const uint32_t idx = base + t * 64 + lane;
     const bool valid = idx < n;
-    key[t] = valid ? kin[idx] : 0u;
-    val[t] = valid ? vin[idx] : 0u;
-    const uint32_t digit = (key[t] >> shift) & (kBins - 1);
+    word[t] = valid ? kin[idx] : 0ull;
+    const uint32_t digit = (kv_key(word[t]) >> shift) & (kBins - 1);
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < kRadixBits; ++b) {
@@ -253,10 +254,8 @@ __global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint32_t* __re
   for (int t = 0; t < kItems; ++t) {
     const uint32_t idx = base + t * 64 + lane;
     if (idx < n) {
-      const uint32_t digit = (key[t] >> shift) & (kBins - 1);
-      const uint32_t dst = gbase[digit] + wcnt[wave][digit] + rank[t];
-      kout[dst] = key[t];
-      vout[dst] = val[t];
+      const uint32_t digit = (kv_key(word[t]) >> shift) & (kBins - 1);
+      kout[gbase[digit] + wcnt[wave][digit] + rank[t]] = word[t];
     }
   }
 }
@@ -270,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void k_fill_u32(uint32_t* __restrict__ p,
 
 // chunk_lo[c] = number of sorted keys below the first cell of chunk c
 // (c = 0 .. nch), by binary search over the sorted keys.
-__global__ __launch_bounds__(kThreads) void k_chunk_lo(const uint32_t* __restrict__ keys, uint32_t n,
+__global__ __launch_bounds__(kThreads) void k_chunk_lo(const uint64_t* __restrict__ kv, uint32_t n,
                                                        uint32_t* __restrict__ chunk_lo, uint32_t nch) {
   const uint32_t c = blockIdx.x * kThreads + threadIdx.x;
   if (c > nch) return;
@@ -278,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_lo(const uint32_t* __restric
   uint32_t lo = 0, hi = n;
   while (lo < hi) {
     const uint32_t mid = lo + ((hi - lo) >> 1);
-    if ((uint64_t)keys[mid] < target) lo = mid + 1;
+    if ((uint64_t)kv_key(kv[mid]) < target) lo = mid + 1;
     else hi = mid;
   }
   chunk_lo[c] = lo;
@@ -291,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_lo(const uint32_t* __restric
 // cell counts, where the kernel is a 16-byte-per-lane store stream).
 constexpr int kChunksPerBlock = 8;
 
-__global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint32_t* __restrict__ keys,
+__global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint64_t* __restrict__ kv,
                                                           const uint32_t* __restrict__ chunk_lo, uint32_t nch,
                                                           int32_t* __restrict__ bo, uint64_t ncells_p1) {
   __shared__ uint32_t first[kChunk];
@@ -311,8 +310,8 @@ __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint32_t* __rest
       for (int q = 0; q < 4; ++q) first[t * 4 + q] = hi;
       __syncthreads();
       for (uint32_t p = lo + t; p < hi; p += kThreads) {
-        const uint32_t key = keys[p];
-        if (p == lo || keys[p - 1] != key) first[key - (uint32_t)c0] = p;
+        const uint32_t key = kv_key(kv[p]);
+        if (p == lo || kv_key(kv[p - 1]) != key) first[key - (uint32_t)c0] = p;
       }
       __syncthreads();
 #pragma unroll
@@ -353,17 +352,17 @@ __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint32_t* __rest
 // Permutation (destination slot of every input particle) and, in grid mode
 // (flags non-null), the block-start flags of the block table: sorted position
 // k starts a block when its offset in its cell is a multiple of maxp.
-__global__ __launch_bounds__(kThreads) void k_permutation(const uint32_t* __restrict__ keys,
-                                                          const uint32_t* __restrict__ vals, uint32_t n,
+__global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __restrict__ kv, uint32_t n,
                                                           uint32_t N, int32_t* __restrict__ perm,
                                                           const int32_t* __restrict__ bo, uint32_t maxp,
                                                           uint32_t* __restrict__ flags) {
   const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
   if (k >= n) return;
-  const uint32_t src = vals[k];
+  const uint64_t w = kv[k];
+  const uint32_t src = kv_val(w);
   perm[src] = (int32_t)(k - (src / N) * N);
   if (flags != nullptr) {
-    const uint32_t rs = (uint32_t)bo[keys[k]];
+    const uint32_t rs = (uint32_t)bo[kv_key(w)];
     flags[k] = ((k - rs) % maxp == 0) ? 1u : 0u;
   }
 }
@@ -374,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void k_permutation(const uint32_t* __rest
 // of the blocks starting at sorted position i < n (row rowidx[i]), zero rows
 // r in [total, max_blocks) (thread i handles position i and row i), and the
 // block count into total_out.
-__global__ __launch_bounds__(kThreads) void k_block_rows(const uint32_t* __restrict__ keys, uint32_t n,
+__global__ __launch_bounds__(kThreads) void k_block_rows(const uint64_t* __restrict__ kv, uint32_t n,
                                                          const int32_t* __restrict__ bo,
                                                          const uint32_t* __restrict__ rowidx, uint32_t maxp,
                                                          uint32_t G, int4* __restrict__ info,
@@ -386,7 +385,7 @@ __global__ __launch_bounds__(kThreads) void k_block_rows(const uint32_t* __restr
   if (i < max_blocks && i >= t) info[i] = make_int4(0, 0, 0, 0);
   if (i >= n) return;
   const uint32_t k = (uint32_t)i;
-  const uint32_t key = keys[k];
+  const uint32_t key = kv_key(kv[k]);
   const uint32_t rs = (uint32_t)bo[key];
   const uint32_t off = k - rs;
   if (off % maxp != 0) return;
@@ -438,9 +437,9 @@ template <int D>
 void launch_keys(const Grid& g, const float* pos, uint32_t n, hipStream_t st) {
   const dim3 grid((n + kThreads - 1) / kThreads);
   if (g.periodic)
-    hipLaunchKernelGGL((k_cell_keys<D, true>), grid, dim3(kThreads), 0, st, g.p, pos, g.keys[0], g.vals[0], n);
+    hipLaunchKernelGGL((k_cell_keys<D, true>), grid, dim3(kThreads), 0, st, g.p, pos, g.kv[0], n);
   else
-    hipLaunchKernelGGL((k_cell_keys<D, false>), grid, dim3(kThreads), 0, st, g.p, pos, g.keys[0], g.vals[0], n);
+    hipLaunchKernelGGL((k_cell_keys<D, false>), grid, dim3(kThreads), 0, st, g.p, pos, g.kv[0], n);
   SPHOPS_LAUNCHED();
 }
 
@@ -765,28 +764,27 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   int cur = 0;
   for (int p = 0; p < passes; ++p) {
     const int shift = p * kRadixBits;
-    hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kThreads), 0, st, g.keys[cur], n, shift, g.hist, ntiles);
+    hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kThreads), 0, st, g.kv[cur], n, shift, g.hist, ntiles);
     SPHOPS_LAUNCHED();
     device_exclusive_scan(g.hist, g.hist, (uint64_t)kBins * ntiles, g.scan_tmp, nullptr, st);
-    hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kThreads), 0, st, g.keys[cur], g.vals[cur],
-                       g.keys[cur ^ 1], g.vals[cur ^ 1], n, shift, g.hist, ntiles);
+    hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kThreads), 0, st, g.kv[cur], g.kv[cur ^ 1], n, shift,
+                       g.hist, ntiles);
     SPHOPS_LAUNCHED();
     cur ^= 1;
   }
-  const uint32_t* skeys = g.keys[cur];
-  const uint32_t* svals = g.vals[cur];
+  const uint64_t* skv = g.kv[cur];
 
   // 3. bin_offsets via per-chunk key ranges
   const uint32_t nch = (uint32_t)g.n_chunks;
-  hipLaunchKernelGGL(k_chunk_lo, blocks_for((uint64_t)nch + 1), dim3(kThreads), 0, st, skeys, n, g.chunk_lo, nch);
+  hipLaunchKernelGGL(k_chunk_lo, blocks_for((uint64_t)nch + 1), dim3(kThreads), 0, st, skv, n, g.chunk_lo, nch);
   SPHOPS_LAUNCHED();
   hipLaunchKernelGGL(k_bin_offsets, dim3((nch + kChunksPerBlock - 1) / kChunksPerBlock), dim3(kThreads), 0, st,
-                     skeys, g.chunk_lo, nch, bo, ncp1);
+                     skv, g.chunk_lo, nch, bo, ncp1);
   SPHOPS_LAUNCHED();
 
   // 4. permutation (destination slot of each input particle), with the
   // block-start flags in grid mode
-  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, skeys, svals, n, g.p.N, perm, bo,
+  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm, bo,
                      g.p.maxp, g.particle_mode ? nullptr : g.flags);
   SPHOPS_LAUNCHED();
 
@@ -794,7 +792,7 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   if (!g.particle_mode) {
     device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, g.flags + n, st);
     hipLaunchKernelGGL(k_block_rows, blocks_for(std::max<uint64_t>(n, g.max_blocks)), dim3(kThreads), 0, st,
-                       skeys, n, bo, g.flags, g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n,
+                       skv, n, bo, g.flags, g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n,
                        g.max_blocks, total_blocks);
     SPHOPS_LAUNCHED();
   } else if (total_blocks) {

@@ -134,8 +134,7 @@ void setup_grid(Grid& g, int dim, int boundary, int mode, const int32_t* grid_si
 void free_grid(Grid* g) {
   if (!g) return;
   for (int i = 0; i < 2; ++i) {
-    (void)hipFree(g->keys[i]);
-    (void)hipFree(g->vals[i]);
+    (void)hipFree(g->kv[i]);
   }
   (void)hipFree(g->hist);
   (void)hipFree(g->scan_tmp);
@@ -264,8 +263,7 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
     try {
       SPHOPS_HIP(hipGetDevice(&g->device));
       for (int i = 0; i < 2; ++i) {
-        g->keys[i] = dalloc<uint32_t>(BN);
-        g->vals[i] = dalloc<uint32_t>(BN);
+        g->kv[i] = dalloc<uint64_t>(BN);
       }
       g->hist = dalloc<uint32_t>((uint64_t)sphops::kRadixBins * g->n_tiles);
       g->scan_tmp_len = sphops::scan_tmp_elems(sphops::scan_words(*g));
@@ -942,7 +940,7 @@ constexpr int kNoAllocMaxDevices = 64;
 // Word offsets of the scratch pieces for a grid of n_keys particles, n_tiles
 // radix tiles and n_chunks cell chunks; each piece starts on 256 bytes.
 struct NoAllocLayout {
-  uint64_t keys[2], vals[2], hist, flags, chunk_lo, scan, scan_len, words;
+  uint64_t kv[2], hist, flags, chunk_lo, scan, scan_len, words;
 };
 
 constexpr uint64_t pad_words(uint64_t w) { return (w + 63) & ~uint64_t(63); }
@@ -950,11 +948,9 @@ constexpr uint64_t pad_words(uint64_t w) { return (w + 63) & ~uint64_t(63); }
 constexpr NoAllocLayout noalloc_layout(uint64_t n_keys, uint64_t n_tiles, uint64_t n_chunks) {
   NoAllocLayout l{};
   uint64_t at = 0;
-  for (int i = 0; i < 2; ++i) {
-    l.keys[i] = at;
-    at += pad_words(n_keys);
-    l.vals[i] = at;
-    at += pad_words(n_keys);
+  for (int i = 0; i < 2; ++i) {  // 64-bit words
+    l.kv[i] = at;
+    at += pad_words(2 * n_keys);
   }
   l.hist = at;
   at += pad_words((uint64_t)sphops::kRadixBins * n_tiles);
@@ -1016,8 +1012,7 @@ int sphops_initialize_noalloc(int dim, int boundary, int mode, const int32_t* gr
     require(l.words <= kNoAllocWords, "sphops_initialize_noalloc: scratch layout exceeds the static array");
     uint32_t* s = scratch_on_current_device(&g.device);
     for (int i = 0; i < 2; ++i) {
-      g.keys[i] = s + l.keys[i];
-      g.vals[i] = s + l.vals[i];
+      g.kv[i] = reinterpret_cast<uint64_t*>(s + l.kv[i]);
     }
     g.hist = s + l.hist;
     g.flags = s + l.flags;

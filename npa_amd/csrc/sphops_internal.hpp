@@ -40,8 +40,8 @@ struct Grid {
   uint64_t n_cells = 0;       // B*G
   uint64_t n_tiles = 0;       // radix tiles
   uint64_t n_chunks = 0;      // cell chunks for bin_offsets
-  uint32_t* keys[2] = {nullptr, nullptr};
-  uint32_t* vals[2] = {nullptr, nullptr};
+  // radix-sort ping-pong buffers of B*N words (cell key << 32 | particle index)
+  uint64_t* kv[2] = {nullptr, nullptr};
   uint32_t* hist = nullptr;       // 256 * n_tiles (+1)
   uint32_t* scan_tmp = nullptr;   // partial sums for device scans
   uint64_t scan_tmp_len = 0;
