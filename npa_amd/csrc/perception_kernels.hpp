@@ -1317,7 +1317,7 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
 // its channel slice.  The moment matrix is accumulated by the owning lane,
 // reduced over the group and handed to the four slice lanes.
 template <int D, bool P, int CW, bool OFF32>
-__global__ __launch_bounds__(kThreads, 8) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
+__global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
   const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
   const uint32_t stride = schedule_stride(live);
@@ -1348,6 +1348,13 @@ __global__ __launch_bounds__(kThreads, 8) void k_blur_hybrid_fwd_quad(GridParams
       // a wave without them the list-only one
       auto walk = [&](auto stencil_rows) {
         constexpr bool ST = decltype(stencil_rows)::value;
+        // list rows: the next iteration's list entry is loaded one iteration
+        // ahead (clamped into the row), and the body has no branch before
+        // the row loads, so the position and row loads go out together
+        uint32_t jnext = 0u;
+        if constexpr (!ST) {
+          if (end > start) jnext = (uint32_t)nidx[min(start + stream + slice * S, end - 1)];
+        }
         for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
           const int to = t0 + slice * S;
           uint32_t jo = k;
@@ -1355,15 +1362,33 @@ __global__ __launch_bounds__(kThreads, 8) void k_blur_hybrid_fwd_quad(GridParams
           float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
           float d2 = 0.0f, rr[3] = {0.0f, 0.0f, 0.0f};
           bool inr = false;
-          if (to < end) {
-            const uint32_t jc = ST && row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
-            pj = xw[jc];
+          if constexpr (ST) {
+            if (to < end) {
+              const uint32_t jc = row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
+              pj = xw[jc];
+              float xj[3];
+              unpack(pj, xj);
+              d2 = displacement<D, P>(g, xi, xj, rr);
+              inr = !row.stencil || d2 < g.eps2;
+              if (inr) jo = jc;
+            }
+          } else {
+            inr = to < end;
+            if (inr) jo = jnext;
+            jnext = (uint32_t)nidx[min(to + 4 * S, end - 1)];
+            pj = xw[jo];
             float xj[3];
             unpack(pj, xj);
             d2 = displacement<D, P>(g, xi, xj, rr);
-            inr = !(ST && row.stencil) || d2 < g.eps2;
-            if (inr) jo = jc;
           }
+          // all four pairs are taken unconditionally (a pair past the row's
+          // end has j = k and zero weights, so it adds nothing), and their
+          // four row loads are issued before any of them is used
+          float sj[4][CW];
+          load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<0>(jo), C, c0), sj[0]);
+          load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<1>(jo), C, c0), sj[1]);
+          load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<2>(jo), C, c0), sj[2]);
+          load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<3>(jo), C, c0), sj[3]);
           if (inr) {
             ro[0] = rr[0];
             ro[1] = rr[1];
@@ -1378,11 +1403,8 @@ __global__ __launch_bounds__(kThreads, 8) void k_blur_hybrid_fwd_quad(GridParams
           }
     #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            if (t0 + q * S >= end) break;  // uniform over the quad
-            uint32_t j;
             float w, t, r[3];
     #define SPHOPS_QUAD_FETCH(QQ)             \
-      j = quad_get<QQ>(jo);                   \
       w = quad_get<QQ>(wo);                   \
       t = quad_get<QQ>(to_);                  \
       for (int e = 0; e < D; ++e) r[e] = quad_get<QQ>(ro[e]);
@@ -1391,12 +1413,10 @@ __global__ __launch_bounds__(kThreads, 8) void k_blur_hybrid_fwd_quad(GridParams
             else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
             else { SPHOPS_QUAD_FETCH(3) }
     #undef SPHOPS_QUAD_FETCH
-            float sj[CW];
-            load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
     #pragma unroll
             for (int f = 0; f < CW; ++f) {
-              blur[f] += w * sj[f];
-              const float qf = t * (sj[f] - si[f]);
+              blur[f] += w * sj[q][f];
+              const float qf = t * (sj[q][f] - si[f]);
     #pragma unroll
               for (int e = 0; e < D; ++e) acc[f * D + e] += qf * r[e];
             }
