@@ -1052,24 +1052,33 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
           if (d2 < g.eps2) op.pair(g, a, xi, xj, pj.w, r, d2, j);
         }
       }
-      for (; t + G < end; t += 2 * G) {
-        const uint32_t j0 = (uint32_t)nidx[t], j1 = (uint32_t)nidx[t + G];
-        const float4 p0 = xw[j0], p1 = xw[j1];
-        float x0[3], x1[3], r0[3], r1[3];
-        unpack(p0, x0);
-        unpack(p1, x1);
-        const float d0 = displacement<D, P>(g, xi, x0, r0);
-        const float d1 = displacement<D, P>(g, xi, x1, r1);
-        op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
-        op.pair(g, a, xi, x1, p1.w, r1, d1, j1);
-      }
       if (t < end) {
-        const uint32_t j0 = (uint32_t)nidx[t];
-        const float4 p0 = xw[j0];
-        float x0[3], r0[3];
-        unpack(p0, x0);
-        const float d0 = displacement<D, P>(g, xi, x0, r0);
-        op.pair(g, a, xi, x0, p0.w, r0, d0, j0);
+        // list rows: four entries per step, in the order above; their
+        // indices are loaded one step ahead (clamped into the row) and
+        // their positions together, so a step waits for memory once
+        uint32_t jn[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) jn[q] = (uint32_t)nidx[min(t + q * G, end - 1)];
+        for (; t < end; t += 4 * G) {
+          uint32_t j[4];
+          float4 p[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            j[q] = jn[q];
+            jn[q] = (uint32_t)nidx[min(t + (4 + q) * G, end - 1)];
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) p[q] = xw[j[q]];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (t + q * G < end) {
+              float xj[3], r[3];
+              unpack(p[q], xj);
+              const float d2 = displacement<D, P>(g, xi, xj, r);
+              op.pair(g, a, xi, xj, p[q].w, r, d2, j[q]);
+            }
+          }
+        }
       }
     }
     op.reduce(G);
