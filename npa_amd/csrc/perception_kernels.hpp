@@ -564,13 +564,23 @@ struct OpDensityBwd {
     gi = a.g[k];
     mi = a.m[k];
   }
+  struct Nbr {  // the neighbour's upstream, loaded ahead by k_pairs_grouped
+    float g;
+  };
+  __device__ static void fetch(const OpPtrs& a, uint32_t j, Nbr& n) { n.g = a.g[j]; }
   __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float wj,
                        const float* r, float d2, uint32_t j) {
+    Nbr n;
+    fetch(a, j, n);
+    pair(g, a, xi, xj, wj, r, d2, j, n);
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs&, const float* xi, const float* xj, float wj,
+                       const float* r, float d2, uint32_t, const Nbr& n) {
     float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
     if (db == 0.0f || !(db < g.eps2)) return;
     const float t = g.eps2 - db;
-    const float coef = gi * wj + a.g[j] * mi;
+    const float coef = gi * wj + n.g * mi;
     const float mag = -coef * 6.0f * t * t;
 #pragma unroll
     for (int e = 0; e < D; ++e) dx[e] += mag * rb[e];
@@ -590,13 +600,26 @@ struct OpDensityGradientBwd {
     for (int e = 0; e < D; ++e) gi[e] = a.g[(uint64_t)k * D + e];
     mi = a.m[k];
   }
+  struct Nbr {  // the neighbour's upstream, loaded ahead by k_pairs_grouped
+    float g[D];
+  };
+  __device__ static void fetch(const OpPtrs& a, uint32_t j, Nbr& n) {
+#pragma unroll
+    for (int e = 0; e < D; ++e) n.g[e] = a.g[(uint64_t)j * D + e];
+  }
   __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float wj,
                        const float* r, float d2, uint32_t j) {
+    Nbr n;
+    fetch(a, j, n);
+    pair(g, a, xi, xj, wj, r, d2, j, n);
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs&, const float* xi, const float* xj, float wj,
+                       const float* r, float d2, uint32_t, const Nbr& n) {
     float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
     float diff[D];
 #pragma unroll
-    for (int e = 0; e < D; ++e) diff[e] = a.g[(uint64_t)j * D + e] * mi - gi[e] * wj;
+    for (int e = 0; e < D; ++e) diff[e] = n.g[e] * mi - gi[e] * wj;
     spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, diff, dx);
   }
   __device__ void reduce(int G) { grp_sum(G, dx); }
@@ -809,19 +832,33 @@ struct OpDensityPairBwd {
     for (int e = 0; e < D; ++e) gdi[e] = a.g2[(uint64_t)k * D + e];
     mi = a.m[k];
   }
+  struct Nbr {  // the neighbour's two upstreams, loaded ahead by k_pairs_grouped
+    float g, g2[D];
+  };
+  __device__ static void fetch(const OpPtrs& a, uint32_t j, Nbr& n) {
+    n.g = a.g[j];
+#pragma unroll
+    for (int e = 0; e < D; ++e) n.g2[e] = a.g2[(uint64_t)j * D + e];
+  }
   __device__ void pair(const GridParams& g, const OpPtrs& a, const float* xi, const float* xj, float wj,
                        const float* r, float d2, uint32_t j) {
+    Nbr n;
+    fetch(a, j, n);
+    pair(g, a, xi, xj, wj, r, d2, j, n);
+  }
+  __device__ void pair(const GridParams& g, const OpPtrs&, const float* xi, const float* xj, float wj,
+                       const float* r, float d2, uint32_t, const Nbr& n) {
     float rb[3];
     const float db = back_disp<D, P>(g, xi, xj, r, d2, rb);
     if (db != 0.0f && db < g.eps2) {
       const float t = g.eps2 - db;
-      const float mag = -(gi * wj + a.g[j] * mi) * 6.0f * t * t;
+      const float mag = -(gi * wj + n.g * mi) * 6.0f * t * t;
 #pragma unroll
       for (int e = 0; e < D; ++e) dx_w[e] += mag * rb[e];
     }
     float diff[D];
 #pragma unroll
-    for (int e = 0; e < D; ++e) diff[e] = a.g2[(uint64_t)j * D + e] * mi - gdi[e] * wj;
+    for (int e = 0; e < D; ++e) diff[e] = n.g2[e] * mi - gdi[e] * wj;
     spiky_jacobian_apply<D>(rb, db, g.eps, g.eps2, diff, dx_k);
   }
   __device__ void reduce(int G) { grp_sum(G, dx_w, dx_k); }
@@ -1015,6 +1052,13 @@ __device__ __forceinline__ uint32_t schedule_stride(uint32_t live) {
   return schedule_blocks(live) * (kThreads / kWave);
 }
 
+// Ops that declare a neighbour record (Nbr, fetch) have it loaded ahead of
+// their pair() calls by the list loop below.
+template <class T, class = void>
+struct has_nbr : std::false_type {};
+template <class T>
+struct has_nbr<T, std::void_t<typename T::Nbr>> : std::true_type {};
+
 // List traversal with a group of G lanes per particle, G by list-length class:
 // wave w serves the particles a.order[first .. first + n) of its descriptor
 // a.waves[w] = {first, G << 8 | n}; lane `sub` of a group takes pairs sub,
@@ -1069,13 +1113,28 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
           }
 #pragma unroll
           for (int q = 0; q < 4; ++q) p[q] = xw[j[q]];
+          if constexpr (has_nbr<OP>::value) {  // the op's neighbour data too
+            typename OP::Nbr nb[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (t + q * G < end) {
-              float xj[3], r[3];
-              unpack(p[q], xj);
-              const float d2 = displacement<D, P>(g, xi, xj, r);
-              op.pair(g, a, xi, xj, p[q].w, r, d2, j[q]);
+            for (int q = 0; q < 4; ++q) OP::fetch(a, j[q], nb[q]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if (t + q * G < end) {
+                float xj[3], r[3];
+                unpack(p[q], xj);
+                const float d2 = displacement<D, P>(g, xi, xj, r);
+                op.pair(g, a, xi, xj, p[q].w, r, d2, j[q], nb[q]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if (t + q * G < end) {
+                float xj[3], r[3];
+                unpack(p[q], xj);
+                const float d2 = displacement<D, P>(g, xi, xj, r);
+                op.pair(g, a, xi, xj, p[q].w, r, d2, j[q]);
+              }
             }
           }
         }
