@@ -1908,7 +1908,7 @@ __global__ __launch_bounds__(kThreads) void k_fill(GridParams g, const float4* _
 // the blocks not written, from the counters' words (see FillStripes).  One
 // workgroup of kThreads >= kFillStripes.
 static_assert(kThreads >= kFillStripes, "k_fill_totals reads one counter per thread");
-static __global__ __launch_bounds__(kThreads) void k_fill_totals(const unsigned long long* __restrict__ ctr,
+[[maybe_unused]] static __global__ __launch_bounds__(kThreads) void k_fill_totals(const unsigned long long* __restrict__ ctr,
                                                                  uint32_t stripes,
                                                                  unsigned long long* __restrict__ total) {
   __shared__ unsigned long long part[2][kThreads / kWave];

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void k_tile_flags(GridParams g, const int
   tile_flags_of<D, P>(g, bo, k, xi, ncnt, flags, unit_len, sparse_len);
 }
 
-static __global__ __launch_bounds__(kThreads) void k_tile_units(const int32_t* __restrict__ unit_len,
+[[maybe_unused]] static __global__ __launch_bounds__(kThreads) void k_tile_units(const int32_t* __restrict__ unit_len,
                                                          const uint32_t* __restrict__ slot, uint32_t n,
                                                          uint2* __restrict__ units) {
   const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
