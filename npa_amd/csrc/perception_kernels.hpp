@@ -1670,14 +1670,21 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
   const int32_t offs = (int32_t)(lo - pre);
   const int32_t dof = offs - __shfl_up(offs, 1, kWave);
   const int32_t off0 = __builtin_amdgcn_readlane(offs, 0);
-  // wave-uniform values kept in vector registers (the scalar file holds the
-  // unit's positions)
+  // wave-uniform values: in grid mode (R <= 9) kept in vector registers (the
+  // scalar file holds the unit's positions); the 27 single-cell ranges of
+  // particle mode would take 54 vector registers and most of the occupancy,
+  // so they are read into scalar registers
   uint32_t spre[R];
   int32_t sdof[R];
 #pragma unroll
   for (int r = 1; r < R; ++r) {
-    spre[r] = (uint32_t)__shfl((int)pre, r, kWave);
-    sdof[r] = __shfl(dof, r, kWave);
+    if constexpr (R > 9) {
+      spre[r] = (uint32_t)__builtin_amdgcn_readlane((int)pre, r);
+      sdof[r] = __builtin_amdgcn_readlane(dof, r);
+    } else {
+      spre[r] = (uint32_t)__shfl((int)pre, r, kWave);
+      sdof[r] = __shfl(dof, r, kWave);
+    }
   }
   auto candidate = [&](uint32_t p) -> uint32_t {
     int32_t o = off0;
@@ -1792,28 +1799,43 @@ __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __r
   uint32_t cand = 0, c = 0;
   int32_t h0 = 0, h1 = 0, h2 = 0, h3 = 0;
   Walker<D, P> w{};
+  // ranges fetched kFetch at a time (their loads in flight together): three
+  // for the many single-cell ranges of particle mode and periodic grids, one
+  // for the nine stencil rows of a clamped grid, whose register budget the
+  // unit path needs
+  constexpr int kFetch = R > 9 ? 3 : 1;
+  static_assert(R % kFetch == 0, "ranges come in whole fetch groups");
   if (lone) {
     unpack(xw[k], xi);
     w.init(g, xi, k);
 #pragma unroll 1
-    for (int r = 0; r < R; ++r) {
-      w.fetch(g, bo, r);
-      const uint32_t len = w.jend - w.j;
-      const uint32_t take = cand < (uint32_t)kWave ? min(len, (uint32_t)kWave - cand) : 0u;
-      for (uint32_t q = 0; q < take; ++q) {
-        float xj[3], rr[3];
-        unpack(xw[w.j + q], xj);
-        if (displacement<D, P>(g, xi, xj, rr) < g.eps2) {
-          mask |= 1ull << (cand + q);
-          const int32_t j = (int32_t)(w.j + q);
-          h0 = c == 0 ? j : h0;
-          h1 = c == 1 ? j : h1;
-          h2 = c == 2 ? j : h2;
-          h3 = c == 3 ? j : h3;
-          ++c;
-        }
+    for (int r0 = 0; r0 < R; r0 += kFetch) {
+      uint32_t rlo[kFetch], rhi[kFetch];
+#pragma unroll
+      for (int u = 0; u < kFetch; ++u) {
+        w.fetch(g, bo, r0 + u);
+        rlo[u] = w.j;
+        rhi[u] = w.jend;
       }
-      cand += len;
+#pragma unroll
+      for (int u = 0; u < kFetch; ++u) {
+        const uint32_t len = rhi[u] - rlo[u];
+        const uint32_t take = cand < (uint32_t)kWave ? min(len, (uint32_t)kWave - cand) : 0u;
+        for (uint32_t q = 0; q < take; ++q) {
+          float xj[3], rr[3];
+          unpack(xw[rlo[u] + q], xj);
+          if (displacement<D, P>(g, xi, xj, rr) < g.eps2) {
+            mask |= 1ull << (cand + q);
+            const int32_t j = (int32_t)(rlo[u] + q);
+            h0 = c == 0 ? j : h0;
+            h1 = c == 1 ? j : h1;
+            h2 = c == 2 ? j : h2;
+            h3 = c == 3 ? j : h3;
+            ++c;
+          }
+        }
+        cand += len;
+      }
     }
   }
   const bool light = lone && cand <= (uint32_t)kWave;
