@@ -1654,6 +1654,32 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
     lo = w.j;
     len = w.jend - w.j;
   }
+  // Many ranges (particle mode, periodic grids): empty ones are dropped and a
+  // range that starts where the previous kept one ends is merged into it, so
+  // the concatenation (the candidate sequence, rows included) is unchanged
+  // and the mapping below steps over the `nr` kept ranges only.  Kept range
+  // m goes through this wave's LDS area (rewritten by pass one) to lane m.
+  uint32_t nr = (uint32_t)R;
+  if constexpr (R > 9) {
+    const uint64_t below = (1ull << lane) - 1ull;
+    const uint64_t ne = __ballot(len > 0);
+    const uint64_t before = ne & below;
+    const int prev = before ? 63 - __clzll(before) : 0;
+    const uint32_t prev_end = (uint32_t)__shfl((int)(lo + len), prev, kWave);
+    const bool head = len > 0 && (before == 0 || prev_end != lo);
+    const uint64_t heads = __ballot(head);
+    nr = (uint32_t)__popcll(heads);
+    // last nonempty range before the next head: the kept range's end
+    const uint64_t later = heads & ~(below | (1ull << lane));
+    const uint64_t upto = later ? ne & ((1ull << __builtin_ctzll(later)) - 1ull) : ne;
+    const int last = upto ? 63 - __clzll(upto) : 0;
+    const uint32_t end = (uint32_t)__shfl((int)(lo + len), last, kWave);
+    uint2* kept = reinterpret_cast<uint2*>(hits);
+    if (head) kept[__popcll(heads & below)] = make_uint2(lo, end - lo);
+    const uint2 mine = kept[min(lane, (uint32_t)R - 1u)];
+    lo = lane < nr ? mine.x : 0u;
+    len = lane < nr ? mine.y : 0u;
+  }
   // exclusive prefix of the lengths (R <= 32 lanes) and the candidate total
   uint32_t pre = len;
 #pragma unroll
@@ -1689,7 +1715,12 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
   auto candidate = [&](uint32_t p) -> uint32_t {
     int32_t o = off0;
 #pragma unroll
-    for (int r = 1; r < R; ++r) o += p >= spre[r] ? sdof[r] : 0;
+    for (int r = 1; r < R; ++r) {
+      if constexpr (R > 9) {
+        if ((uint32_t)r >= nr) break;  // wave-uniform
+      }
+      o += p >= spre[r] ? sdof[r] : 0;
+    }
     return p < ncand ? (uint32_t)((int32_t)p + o) : i0;
   };
   const uint32_t rounds = (ncand + kWave - 1) / kWave;
@@ -1919,7 +1950,7 @@ __global__ __launch_bounds__(kThreads) void k_fill(GridParams g, const float4* _
                                                    const int32_t* __restrict__ unit_total,
                                                    int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
                                                    int32_t* __restrict__ ncnt, FillStripes fs) {
-  __shared__ uint8_t hits[kThreads / kWave][kFillRounds * kWave];
+  __shared__ __align__(16) uint8_t hits[kThreads / kWave][kFillRounds * kWave];
   uint8_t* mine = hits[threadIdx.x >> 6];
   const uint32_t nunits = (uint32_t)*unit_total;
   fill_items<D, P, M ? Walker<D, P>::kCellRanges : Walker<D, P>::kRowRanges>(g, xw, bo, unit_len, units, nunits,
