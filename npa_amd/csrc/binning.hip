@@ -288,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_lo(const uint64_t* __restric
 // head (suffix minimum), the chunk end being the sentinel.  A workgroup
 // handles kChunksPerBlock consecutive chunks (most of them empty at large
 // cell counts, where the kernel is a 16-byte-per-lane store stream).
-constexpr int kChunksPerBlock = 8;
+constexpr int kChunksPerBlock = 4;
 
 __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint64_t* __restrict__ kv,
                                                           const uint32_t* __restrict__ chunk_lo, uint32_t nch,
