@@ -1426,7 +1426,9 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
         for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
           const int to = t0 + slice * S;
           uint32_t jo = k;
-          float wo = 0.0f, to_ = 0.0f, ro[3] = {0.0f, 0.0f, 0.0f};
+          // owned pair: volume-weighted W, and the volume-weighted spiky
+          // magnitude times r (the moment matrix and gradient factor)
+          float wo = 0.0f, tro[3] = {0.0f, 0.0f, 0.0f};
           float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
           float d2 = 0.0f, rr[3] = {0.0f, 0.0f, 0.0f};
           bool inr = false;
@@ -1458,24 +1460,22 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
           load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<2>(jo), C, c0), sj[2]);
           load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<3>(jo), C, c0), sj[3]);
           if (inr) {
-            ro[0] = rr[0];
-            ro[1] = rr[1];
-            ro[2] = rr[2];
             wo = poly6(g.eps2, d2) * pj.w;
             float d;
-            to_ = spiky_mag(g.eps, d2, &d) * pj.w;
+            const float to_ = spiky_mag(g.eps, d2, &d) * pj.w;
+    #pragma unroll
+            for (int e = 0; e < D; ++e) tro[e] = to_ * rr[e];
     #pragma unroll
             for (int p = 0; p < D; ++p)
     #pragma unroll
-              for (int q = p; q < D; ++q) M[p * D + q] += to_ * ro[p] * ro[q];
+              for (int q = p; q < D; ++q) M[p * D + q] += tro[p] * rr[q];
           }
     #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            float w, t, r[3];
+            float w, tr[3];
     #define SPHOPS_QUAD_FETCH(QQ)             \
       w = quad_get<QQ>(wo);                   \
-      t = quad_get<QQ>(to_);                  \
-      for (int e = 0; e < D; ++e) r[e] = quad_get<QQ>(ro[e]);
+      for (int e = 0; e < D; ++e) tr[e] = quad_get<QQ>(tro[e]);
             if (q == 0) { SPHOPS_QUAD_FETCH(0) }
             else if (q == 1) { SPHOPS_QUAD_FETCH(1) }
             else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
@@ -1484,9 +1484,9 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
     #pragma unroll
             for (int f = 0; f < CW; ++f) {
               blur[f] += w * sj[q][f];
-              const float qf = t * (sj[q][f] - si[f]);
+              const float df = sj[q][f] - si[f];
     #pragma unroll
-              for (int e = 0; e < D; ++e) acc[f * D + e] += qf * r[e];
+              for (int e = 0; e < D; ++e) acc[f * D + e] += df * tr[e];
             }
           }
         }
