@@ -1197,9 +1197,13 @@ __device__ __forceinline__ const float* row_slice(const float* __restrict__ base
   return base + (uint64_t)j * stride + c0;
 }
 
-template <int D, bool P, int CW, bool FULL, bool OFF32>
+// PARTS: 3 for the fused pair, 1 for blur alone (upstream a.g), 2 for the
+// gradient alone (upstream a.g2); the other operator's loads and terms are
+// left out.
+template <int D, bool P, int CW, bool FULL, bool OFF32, int PARTS>
 __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
+  constexpr bool kB = (PARTS & 1) != 0, kG = (PARTS & 2) != 0;
   const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
   const uint32_t stride = schedule_stride(live);
   for (uint32_t wave = schedule_wave(live); wave < live; wave += stride) {
@@ -1215,8 +1219,8 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
     const float4* __restrict__ xw = a.xw;
     float xi[3] = {0.0f, 0.0f, 0.0f};
     float vi = 0.0f, mr2 = 0.0f;
-    float si[FULL ? CW : 1] = {}, gbi[FULL ? CW : 1] = {};
-    float ggi[CW * D] = {};
+    float si[FULL ? CW : 1] = {}, gbi[FULL && kB ? CW : 1] = {};
+    float ggi[kG ? CW * D : 1] = {};
     float dsb[CW] = {}, dsg[CW] = {};
     float wsum[D] = {};
     float dxb[D] = {}, dxg[D] = {};
@@ -1226,11 +1230,9 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
       const float mi = a.m[k], ri = a.rho[k];
       vi = mi / ri;
       mr2 = mi / (ri * ri);
-      load_span<CW * D, true>(a.g2 + ((uint64_t)k * C + c0) * D, ggi);
-      if constexpr (FULL) {
-        load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
-        load_span<CW, true>(a.g + (uint64_t)k * C + c0, gbi);
-      }
+      if constexpr (kG) load_span<CW * D, true>(a.g2 + ((uint64_t)k * C + c0) * D, ggi);
+      if constexpr (FULL) load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
+      if constexpr (FULL && kB) load_span<CW, true>(a.g + (uint64_t)k * C + c0, gbi);
       const int32_t* __restrict__ nidx = a.nidx;
       const Row row = Row::of(a, k);
       const int start = row.start;
@@ -1300,77 +1302,104 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
             else if (q == 2) { SPHOPS_QUAD_FETCH(2) }
             else { SPHOPS_QUAD_FETCH(3) }
     #undef SPHOPS_QUAD_FETCH
-            float gbj[CW], ggj[CW * D];
-            load_span<CW, true>(row_slice<OFF32>(a.g, j, C, c0), gbj);
-            load_span<CW * D, true>(row_slice<OFF32>(a.g2, j, C * D, c0 * D), ggj);
+            float gbj[kB ? CW : 1], ggj[kG ? CW * D : 1];
+            if constexpr (kB) load_span<CW, true>(row_slice<OFF32>(a.g, j, C, c0), gbj);
+            if constexpr (kG) load_span<CW * D, true>(row_slice<OFF32>(a.g2, j, C * D, c0 * D), ggj);
             if constexpr (!FULL) {
     #pragma unroll
               for (int f = 0; f < CW; ++f) {
-                dsb[f] += W * gbj[f];
+                if constexpr (kB) dsb[f] += W * gbj[f];
+                if constexpr (kG) {
     #pragma unroll
-                for (int e = 0; e < D; ++e) dsg[f] += ggj[f * D + e] * w[e];
+                  for (int e = 0; e < D; ++e) dsg[f] += ggj[f * D + e] * w[e];
+                }
               }
             } else {
               float sj[CW];
               load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
-              float A = 0.0f, Bv = 0.0f;
-              float u1[D] = {}, u2[D] = {};
+              if constexpr (kB) {
+                float A = 0.0f, Bv = 0.0f;
     #pragma unroll
-              for (int f = 0; f < CW; ++f) {
-                dsb[f] += W * gbj[f];
-                A += gbi[f] * sj[f];
-                Bv += gbj[f] * si[f];
-                const float df = si[f] - sj[f];
+                for (int f = 0; f < CW; ++f) {
+                  dsb[f] += W * gbj[f];
+                  A += gbi[f] * sj[f];
+                  Bv += gbj[f] * si[f];
+                }
+                const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
+    #pragma unroll
+                for (int e = 0; e < D; ++e) dxb[e] += m6 * rb[e];
+              }
+              if constexpr (kG) {
+                float u1[D] = {}, u2[D] = {};
+    #pragma unroll
+                for (int f = 0; f < CW; ++f) {
+                  const float df = si[f] - sj[f];
+    #pragma unroll
+                  for (int e = 0; e < D; ++e) {
+                    dsg[f] += ggj[f * D + e] * w[e];
+                    u1[e] += df * ggj[f * D + e];
+                    u2[e] += df * ggi[f * D + e];
+                  }
+                }
+                float u[D], uw = 0.0f, rv = 0.0f;
     #pragma unroll
                 for (int e = 0; e < D; ++e) {
-                  dsg[f] += ggj[f * D + e] * w[e];
-                  u1[e] += df * ggj[f * D + e];
-                  u2[e] += df * ggi[f * D + e];
+                  uw += u1[e] * w[e];
+                  u[e] = vi * u1[e] + vj * u2[e];
+                  rv += rb[e] * u[e];
                 }
-              }
-              const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
-              float u[D], uw = 0.0f, rv = 0.0f;
+                drg += uw;
     #pragma unroll
-              for (int e = 0; e < D; ++e) {
-                dxb[e] += m6 * rb[e];
-                uw += u1[e] * w[e];
-                u[e] = vi * u1[e] + vj * u2[e];
-                rv += rb[e] * u[e];
+                for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
               }
-              drg += uw;
-    #pragma unroll
-              for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
             }
           }
         }
       };
       if (__ballot(row.stencil) != 0) walk(std::integral_constant<bool, true>{});
       else walk(std::integral_constant<bool, false>{});
-      if constexpr (FULL) {  // blur's dL/drho: sum_j W_j g_j . s_i = s_i . sum_j W_j g_j
+      if constexpr (FULL && kB) {  // blur's dL/drho: sum_j W_j g_j . s_i = s_i . sum_j W_j g_j
   #pragma unroll
         for (int f = 0; f < CW; ++f) drb += si[f] * dsb[f];
       }
     }
-    grp_sum_streams(G, dsb, dsg);
-    grp_sum(G, wsum);
-    if constexpr (FULL) grp_sum(G, dxb, dxg, drb, drg);
+    if constexpr (kB) grp_sum_streams(G, dsb);
+    if constexpr (kG) {
+      grp_sum_streams(G, dsg);
+      grp_sum(G, wsum);
   #pragma unroll
-    for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
+      for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
+    }
+    if constexpr (FULL && kB) grp_sum(G, dxb, drb);
+    if constexpr (FULL && kG) grp_sum(G, dxg, drg);
     if (active && stream == 0) {
       const float sb = vi * g.c6;
   #pragma unroll
       for (int f = 0; f < CW; ++f) {
-        float t = vi * dsg[f];
+        float o = 0.0f;
+        if constexpr (kB) o = dsb[f] * sb;
+        if constexpr (kG) {
+          float t = vi * dsg[f];
   #pragma unroll
-        for (int e = 0; e < D; ++e) t += ggi[f * D + e] * wsum[e];
-        a.out1[(uint64_t)k * C + c0 + f] = dsb[f] * sb + t * g.cs;
+          for (int e = 0; e < D; ++e) t += ggi[f * D + e] * wsum[e];
+          o = kB ? o + t * g.cs : t * g.cs;
+        }
+        a.out1[(uint64_t)k * C + c0 + f] = o;
       }
       if constexpr (FULL) {
         if (slice == 0) {
-          a.out2[k] = -mr2 * (drb * g.c6 + drg * g.cs);
-          float dx[D];
+          float dr = 0.0f, dx[D] = {};
+          if constexpr (kB) {
+            dr = drb * g.c6;
   #pragma unroll
-          for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6 + dxg[e] * g.cs;
+            for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6;
+          }
+          if constexpr (kG) {
+            dr = kB ? dr + drg * g.cs : drg * g.cs;
+  #pragma unroll
+            for (int e = 0; e < D; ++e) dx[e] = kB ? dx[e] + dxg[e] * g.cs : dxg[e] * g.cs;
+          }
+          a.out2[k] = -mr2 * dr;
           store_pos_grad<D>(a.out0, k, dx, 1.0f);
         }
       }
@@ -2123,27 +2152,30 @@ void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
 }
 
 // The lane-split pass-B backward over the schedule a.waves2 (positions and
-// volumes already packed into a.xw).
-template <int D, bool P, bool FULL>
+// volumes already packed into a.xw); PARTS as for k_blur_hybrid_bwd_quad.
+template <int D, bool P, bool FULL, int PARTS = 3>
 void launch_blur_hybrid_bwd_quad_packed(const Grid& g, const OpPtrs& a, hipStream_t st) {
   const uint32_t wgs = schedule_groups(a.nwaves2, a.nwaves2_dev);
   if (wgs == 0) return;
   const bool off32 = row_offsets_fit_32(g, a.C);
+#define SPHOPS_BWD_QUAD(CW, O32) \
+  hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, CW, FULL, O32, PARTS>), dim3(wgs), dim3(kThreads), 0, st, g.p, a)
   if (a.C == 16) {
-    if (off32) hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 4, FULL, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    else hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 4, FULL, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    if (off32) SPHOPS_BWD_QUAD(4, true);
+    else SPHOPS_BWD_QUAD(4, false);
   } else {
-    if (off32) hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    else hipLaunchKernelGGL((k_blur_hybrid_bwd_quad<D, P, 8, FULL, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    if (off32) SPHOPS_BWD_QUAD(8, true);
+    else SPHOPS_BWD_QUAD(8, false);
   }
+#undef SPHOPS_BWD_QUAD
   SPHOPS_LAUNCHED();
 }
 
-template <int D, bool P, bool FULL>
+template <int D, bool P, bool FULL, int PARTS = 3>
 void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
   pack_for<D, VolumeWeights>(g, a, st);
-  launch_blur_hybrid_bwd_quad_packed<D, P, FULL>(g, a, st);
+  launch_blur_hybrid_bwd_quad_packed<D, P, FULL, PARTS>(g, a, st);
 }
 
 // Pass-B backward with cell tiles: the tiled kernel serves the particles of
@@ -2244,12 +2276,27 @@ void backward_dispatch(const Grid& g, Op op, bool full, const int32_t* bo, const
     case Op::DensityGradient: return launch_pairs<D, P, OpDensityGradientBwd<D, P>>(g, bo, a, st);
     case Op::MomentMatrix: return launch_pairs<D, P, OpMomentMatrixBwd<D, P>>(g, bo, a, st);
     case Op::Blur:
+      // over a neighbour list with 16 or 32 channels: the lane-split kernel
+      // with the blur terms only
+      if (split_ok(a)) {
+        if (full) return launch_blur_hybrid_bwd_quad<D, P, true, 1>(g, a, st);
+        return launch_blur_hybrid_bwd_quad<D, P, false, 1>(g, a, st);
+      }
       if (full) return launch_channels<D, P, BlurBwdFull>(g, bo, a, st);
       return launch_channels<D, P, BlurBwdDs>(g, bo, a, st);
     case Op::Gradient:
-    case Op::GradientHybrid:
+    case Op::GradientHybrid: {
+      // the same with the gradient terms only (its upstream in g2)
+      OpPtrs b = a;
+      b.g2 = a.g;
+      b.g = nullptr;
+      if (split_ok(b)) {
+        if (full) return launch_blur_hybrid_bwd_quad<D, P, true, 2>(g, b, st);
+        return launch_blur_hybrid_bwd_quad<D, P, false, 2>(g, b, st);
+      }
       if (full) return launch_channels<D, P, GradientBwdFull>(g, bo, a, st);
       return launch_channels<D, P, GradientBwdDs>(g, bo, a, st);
+    }
     case Op::DensityPair: return launch_pairs<D, P, OpDensityPairBwd<D, P>>(g, bo, a, st);
     case Op::BlurGradientHybrid: {
       if (split_ok(a) && a.C == 16 && a.tile_units != nullptr && a.waves_sparse != nullptr) {
