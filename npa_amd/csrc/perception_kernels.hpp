@@ -1412,10 +1412,13 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
 // evaluates the q-th of four pairs (index, volume-weighted W and spiky
 // magnitude, r), the quad exchanges them by DPP, and every lane accumulates
 // its channel slice.  The moment matrix is accumulated by the owning lane,
-// reduced over the group and handed to the four slice lanes.
-template <int D, bool P, int CW, bool OFF32>
+// reduced over the group and handed to the four slice lanes.  PARTS: 3 for
+// the fused pair (blur into a.out0, gradient_hybrid into a.out3), 1 for blur
+// alone, 2 for gradient_hybrid alone (into a.out3).
+template <int D, bool P, int CW, bool OFF32, int PARTS>
 __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
+  constexpr bool kB = (PARTS & 1) != 0, kG = (PARTS & 2) != 0;
   const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
   const uint32_t stride = schedule_stride(live);
   for (uint32_t wave = schedule_wave(live); wave < live; wave += stride) {
@@ -1436,7 +1439,7 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
     float M[D * D] = {};
     if (active) {
       unpack(xw[k], xi);
-      load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
+      if constexpr (kG) load_span<CW, true>(a.s + (uint64_t)k * C + c0, si);
       const int32_t* __restrict__ nidx = a.nidx;
       const Row row = Row::of(a, k);
       const int start = row.start;
@@ -1489,15 +1492,17 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
           load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<2>(jo), C, c0), sj[2]);
           load_span<CW, true>(row_slice<OFF32>(a.s, quad_get<3>(jo), C, c0), sj[3]);
           if (inr) {
-            wo = poly6(g.eps2, d2) * pj.w;
-            float d;
-            const float to_ = spiky_mag(g.eps, d2, &d) * pj.w;
+            if constexpr (kB) wo = poly6(g.eps2, d2) * pj.w;
+            if constexpr (kG) {
+              float d;
+              const float to_ = spiky_mag(g.eps, d2, &d) * pj.w;
     #pragma unroll
-            for (int e = 0; e < D; ++e) tro[e] = to_ * rr[e];
+              for (int e = 0; e < D; ++e) tro[e] = to_ * rr[e];
     #pragma unroll
-            for (int p = 0; p < D; ++p)
+              for (int p = 0; p < D; ++p)
     #pragma unroll
-              for (int q = p; q < D; ++q) M[p * D + q] += tro[p] * rr[q];
+                for (int q = p; q < D; ++q) M[p * D + q] += tro[p] * rr[q];
+            }
           }
     #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -1512,10 +1517,12 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
     #undef SPHOPS_QUAD_FETCH
     #pragma unroll
             for (int f = 0; f < CW; ++f) {
-              blur[f] += w * sj[q][f];
-              const float df = sj[q][f] - si[f];
+              if constexpr (kB) blur[f] += w * sj[q][f];
+              if constexpr (kG) {
+                const float df = sj[q][f] - si[f];
     #pragma unroll
-              for (int e = 0; e < D; ++e) acc[f * D + e] += df * tr[e];
+                for (int e = 0; e < D; ++e) acc[f * D + e] += df * tr[e];
+              }
             }
           }
         }
@@ -1523,13 +1530,20 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
       if (__ballot(row.stencil) != 0) walk(std::integral_constant<bool, true>{});
       else walk(std::integral_constant<bool, false>{});
     }
-    grp_sum_streams(G, blur, acc);
-    grp_sum(G, M);
+    if constexpr (kB) grp_sum_streams(G, blur);
+    if constexpr (kG) {
+      grp_sum_streams(G, acc);
+      grp_sum(G, M);
   #pragma unroll
-    for (int q = 0; q < D * D; ++q) M[q] = quad_get<0>(M[q]);  // the group total, to the four slice lanes
+      for (int q = 0; q < D * D; ++q) M[q] = quad_get<0>(M[q]);  // the group total, to the four slice lanes
+    }
     if (active && stream == 0) {
+      if constexpr (kB) {
   #pragma unroll
-      for (int f = 0; f < CW; ++f) a.out0[(uint64_t)k * C + c0 + f] = blur[f] * g.c6;
+        for (int f = 0; f < CW; ++f) a.out0[(uint64_t)k * C + c0 + f] = blur[f] * g.c6;
+      }
+    }
+    if (kG && active && stream == 0) {
       float Ms[D * D], L[D * D];
   #pragma unroll
       for (int p = 0; p < D; ++p)
@@ -2134,20 +2148,24 @@ inline bool row_offsets_fit_32(const Grid& g, uint32_t C) {
   return g.n_keys * (uint64_t)C * 3u * 4u <= 0xFFFFFFFFull;
 }
 
-template <int D, bool P>
+// PARTS as for k_blur_hybrid_fwd_quad.
+template <int D, bool P, int PARTS = 3>
 void launch_blur_hybrid_fwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
   const uint32_t wgs = schedule_groups(a.nwaves2, a.nwaves2_dev);
   pack_for<D, VolumeWeights>(g, a, st);
   if (wgs == 0) return;
   const bool off32 = row_offsets_fit_32(g, a.C);
+#define SPHOPS_FWD_QUAD(CW, O32) \
+  hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, CW, O32, PARTS>), dim3(wgs), dim3(kThreads), 0, st, g.p, a)
   if (a.C == 16) {
-    if (off32) hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 4, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    else hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 4, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    if (off32) SPHOPS_FWD_QUAD(4, true);
+    else SPHOPS_FWD_QUAD(4, false);
   } else {
-    if (off32) hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 8, true>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
-    else hipLaunchKernelGGL((k_blur_hybrid_fwd_quad<D, P, 8, false>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
+    if (off32) SPHOPS_FWD_QUAD(8, true);
+    else SPHOPS_FWD_QUAD(8, false);
   }
+#undef SPHOPS_FWD_QUAD
   SPHOPS_LAUNCHED();
 }
 
@@ -2244,9 +2262,18 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a_i
     case Op::Density: return launch_pairs<D, P, OpDensity<D, P>>(g, bo, a, st);
     case Op::DensityGradient: return launch_pairs<D, P, OpDensityGradient<D, P>>(g, bo, a, st);
     case Op::MomentMatrix: return launch_pairs<D, P, OpMomentMatrix<D, P>>(g, bo, a, st);
+    // blur alone stays on the grouped kernel (a row per lane), which is faster
+    // for it than the lane-split kernel (0.28 against 0.30 ms at cfg5)
     case Op::Blur: return launch_channels<D, P, OpBlur>(g, bo, a, st);
     case Op::Gradient: return launch_channels<D, P, OpGradient>(g, bo, a, st);
-    case Op::GradientHybrid: return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
+    case Op::GradientHybrid: {
+      // over a neighbour list with 16 or 32 channels: the lane-split kernel
+      // with the gradient_hybrid part only (its output in out3)
+      OpPtrs b = a;
+      b.out3 = a.out0;
+      if (split_ok(b)) return launch_blur_hybrid_fwd_quad<D, P, 2>(g, b, st);
+      return launch_channels<D, P, OpGradientHybrid>(g, bo, a, st);
+    }
     case Op::DensityPair: return launch_pairs<D, P, OpDensityPair<D, P>>(g, bo, a, st);
     case Op::BlurGradientHybrid:
       if (split_ok(a)) return launch_blur_hybrid_fwd_quad<D, P>(g, a, st);
