@@ -1266,8 +1266,8 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
             vo = pj.w;
             const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
             Wo = poly6(g.eps2, db);
-            float d;
-            const float mag = spiky_mag(g.eps, db, &d);
+            float d, dinv;
+            const float mag = spiky_mag(g.eps, db, &d, &dinv);
     #pragma unroll
             for (int e = 0; e < D; ++e) {
               wo[e] = mag * rbo[e];
@@ -1276,7 +1276,7 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_q
             if (db != 0.0f && db < g.eps2) {
               const float tt = g.eps2 - db;
               t2o = tt * tt;
-              const float di = fast_rcp(d);
+              const float di = dinv;
               jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
               jbo = 3.0f * (g.eps2 - db) * di * di * di;
             }

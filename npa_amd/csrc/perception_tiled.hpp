@@ -404,8 +404,8 @@ __global__ __launch_bounds__(kTileThreads, 2) void k_blur_hybrid_bwd_tiled(GridP
           const float d2 = displacement<D, P>(g, xi, xj, rr);
           const float db = back_disp<D, P>(g, xi, xj, rr, d2, rbk);
           const float W = poly6(g.eps2, db);
-          float d;
-          const float mag = spiky_mag(g.eps, db, &d);
+          float d, dinv;
+          const float mag = spiky_mag(g.eps, db, &d, &dinv);
           float w[3];
 #pragma unroll
           for (int q = 0; q < D; ++q) {
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void k_blur_hybrid_bwd_tiled(GridP
             if (db != 0.0f && db < g.eps2) {
               const float tt = g.eps2 - db;
               t2 = tt * tt;
-              const float di = fast_rcp(d);
+              const float di = dinv;
               ja = 3.0f * (g.eps - d) * (g.eps - d) * di;
               jb = 3.0f * (g.eps2 - db) * di * di * di;
             }

@@ -146,19 +146,24 @@ __device__ __forceinline__ float poly6(float eps2, float d2) {
   return fmaxf(0.0f, t * t * t);
 }
 
-// Hardware square root and reciprocal (v_sqrt_f32 / v_rcp_f32, 1 ulp): the
-// pair kernels use them for |r| and 1/|r|; the in-radius decision never
-// depends on them (it compares |r|^2 with eps^2).
-__device__ __forceinline__ float fast_sqrt(float v) { return __builtin_amdgcn_sqrtf(v); }
+// Hardware reciprocal square root and reciprocal (v_rsq_f32 / v_rcp_f32,
+// 1 ulp): the pair kernels take 1/|r| from one v_rsq and |r| = |r|^2 / |r|
+// as their product (one quarter-rate instruction instead of v_sqrt and
+// v_rcp); the in-radius decision never depends on them (it compares |r|^2
+// with eps^2).
+__device__ __forceinline__ float fast_rsq(float v) { return __builtin_amdgcn_rsqf(v); }
 __device__ __forceinline__ float fast_rcp(float v) { return __builtin_amdgcn_rcpf(v); }
 
-// Spiky magnitude 3 (h - d)^2 / d for 0 < d < h, else 0; returns d too.
-__device__ __forceinline__ float spiky_mag(float eps, float d2, float* d_out) {
-  const float d = fast_sqrt(d2);
+// Spiky magnitude 3 (h - d)^2 / d for 0 < d < h, else 0; returns d = |r|
+// (0 for d2 = 0) and, if asked, 1/d (meaningful for d2 > 0 only).
+__device__ __forceinline__ float spiky_mag(float eps, float d2, float* d_out, float* di_out = nullptr) {
+  const float di = fast_rsq(d2);
+  const float d = d2 == 0.0f ? 0.0f : d2 * di;
   *d_out = d;
+  if (di_out != nullptr) *di_out = di;
   if (d2 == 0.0f || !(d < eps)) return 0.0f;
   const float t = eps - d;
-  return 3.0f * t * t * fast_rcp(d);
+  return 3.0f * t * t * di;
 }
 
 // grad_out += J(r) * v with J = dK/dr (utils.cuh:242-260); no-op outside (0, h).
@@ -166,8 +171,8 @@ template <int D>
 __device__ __forceinline__ void spiky_jacobian_apply(const float* r, float d2, float eps, float eps2,
                                                      const float* v, float* out) {
   if (d2 == 0.0f || !(d2 < eps2)) return;
-  const float d = fast_sqrt(d2);
-  const float di = fast_rcp(d);
+  const float di = fast_rsq(d2);
+  const float d = d2 * di;
   const float a = 3.0f * (eps - d) * (eps - d) * di;   // diagonal part
   const float b = 3.0f * (eps2 - d2) * di * di * di;   // r r^T part
   float rv = 0.0f;
