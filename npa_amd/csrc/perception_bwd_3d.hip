@@ -1,10 +1,14 @@
-// Backward perception kernels instantiated for 3D (clamped and periodic).
+// Backward perception kernels instantiated for 3D, clamped grids; the
+// periodic ones are instantiated in perception_bwd_3d_periodic.hip, so the
+// two halves compile in parallel.
 #include "perception_kernels.hpp"
 
 namespace sphops {
 
+void run_backward_3d_periodic(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a, hipStream_t st);
+
 void run_backward_3d(const Grid& g, Op op, bool full, const int32_t* bo, const OpPtrs& a, hipStream_t st) {
-  if (g.periodic) pk::backward_dispatch<3, true>(g, op, full, bo, a, st);
+  if (g.periodic) run_backward_3d_periodic(g, op, full, bo, a, st);
   else pk::backward_dispatch<3, false>(g, op, full, bo, a, st);
 }
 
