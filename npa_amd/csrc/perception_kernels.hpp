@@ -1200,8 +1200,11 @@ __device__ __forceinline__ const float* row_slice(const float* __restrict__ base
 // PARTS: 3 for the fused pair, 1 for blur alone (upstream a.g), 2 for the
 // gradient alone (upstream a.g2); the other operator's loads and terms are
 // left out.
+// The launch bound of 3 workgroups per CU (C = 16) still compiles to 122
+// VGPRs and 4 waves per SIMD, but schedules the loop better than a bound of
+// 4: 0.871 against 0.883 ms at cfg5.
 template <int D, bool P, int CW, bool FULL, bool OFF32, int PARTS>
-__global__ __launch_bounds__(kThreads, CW == 4 ? 4 : 2) void k_blur_hybrid_bwd_quad(GridParams g, OpPtrs a) {
+__global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_quad(GridParams g, OpPtrs a) {
   constexpr int C = 4 * CW;
   constexpr bool kB = (PARTS & 1) != 0, kG = (PARTS & 2) != 0;
   const uint32_t live = wave_limit(a.nwaves2, a.nwaves2_dev);
