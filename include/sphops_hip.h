@@ -287,7 +287,10 @@ int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, 
  * other particles get the split schedule of sphops_neighbor_schedule, over
  * their own order: nbr_order_sparse (B*N), nbr_waves_sparse (capacity
  * sphops_neighbor_wave_capacity), wave_count_sparse (device int32).  Needs
- * the snapshot's x_bin, bin_offsets and list lengths (sphops_neighbor_fill). */
+ * the snapshot's x_bin, bin_offsets and list lengths (sphops_neighbor_fill).
+ * It overwrites the fill's work split in the grid scratch: call it after the
+ * snapshot's last fill; a later fill fails until sphops_neighbor_candidates
+ * runs again. */
 int sphops_neighbor_tiles(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
                           const int32_t* nbr_count, uint32_t* tile_units, int32_t* tile_unit_count,
                           int32_t* nbr_order_sparse, uint32_t* nbr_waves_sparse, int32_t* wave_count_sparse,

@@ -727,6 +727,9 @@ int sphops_neighbor_tiles(const sphops_grid* grid, const float* x, const int32_t
     a.waves_sparse = reinterpret_cast<const uint2*>(nbr_waves_sparse);
     a.nwaves_sparse_dev = wave_count_sparse;
     sphops::forward(*grid, Op::NeighbourTiles, bo, a, st);
+    // the tile build overwrote the fill's work split in the grid scratch: a
+    // later fill needs sphops_neighbor_candidates again
+    grid->split_key[0] = grid->split_key[1] = nullptr;
   });
 }
 

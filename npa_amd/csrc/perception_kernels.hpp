@@ -872,21 +872,33 @@ struct OpDensityPairBwd {
 
 // ---- stencil walk for particles whose row did not fit
 
-// Candidate number t (0-based, in stencil order) of particle k, found by
-// walking the stencil ranges from the start.  Slow, and only for particles
-// the fill could not store (count < 0).
+// Candidates of particle k in stencil order, for a lane whose requests never
+// decrease (t, then a larger t, ...): the cursor keeps the range it stopped
+// in, so a row of n candidates costs one walk over its stencil ranges, not
+// one walk per candidate.  Only for particles the fill could not store
+// (count < 0).
 template <int D, bool P>
-__device__ __forceinline__ uint32_t stencil_candidate(const GridParams& g, const int32_t* __restrict__ bo,
-                                                   const float* xi, uint32_t k, uint32_t t) {
+struct StencilCursor {
   Walker<D, P> w;
-  w.init(g, xi, k);
-  for (int r = 0;; ++r) {
-    if (!w.fetch(g, bo, r)) return k;  // past the stencil: cannot happen for t < candidates
-    const uint32_t len = w.jend - w.j;
-    if (t < len) return w.j + t;
-    t -= len;
+  uint32_t before;  // candidates in the ranges before the current one
+
+  __device__ __forceinline__ void init(const GridParams& g, const float* xi, uint32_t k) {
+    w.init(g, xi, k);
+    before = 0;
   }
-}
+  // Candidate number t (0-based); k itself past the stencil, which cannot
+  // happen for t below the particle's candidate count.
+  __device__ __forceinline__ uint32_t at(const GridParams& g, const int32_t* __restrict__ bo, uint32_t k,
+                                         uint32_t t) {
+    while (t - before >= w.jend - w.j) {
+      before += w.jend - w.j;
+      w.j = w.jend = 0;
+      if (!w.fetch(g, bo, w.r)) return k;
+      ++w.r;
+    }
+    return w.j + (t - before);
+  }
+};
 
 // Row of particle k: its list entries, or (count < 0) its stencil candidates.
 struct Row {
@@ -937,8 +949,10 @@ __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t*
   if constexpr (TRAV == kList) {
     const Row row = active ? Row::of(a, k) : Row{0, 0, false};
     if (row.stencil) {
+      StencilCursor<D, P> cur;
+      cur.init(g, xi, k);
       for (int t = 0; t < row.end; ++t) {
-        const uint32_t j = stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)t);
+        const uint32_t j = cur.at(g, a.bo, k, (uint32_t)t);
         const float4 pj = xw[j];
         float xj[3], r[3];
         unpack(pj, xj);
@@ -1087,8 +1101,10 @@ __global__ __launch_bounds__(kThreads) void k_pairs_grouped(GridParams g, OpPtrs
       const int end = row.end;
       int t = row.start + sub;
       if (row.stencil) {
+        StencilCursor<D, P> cur;
+        cur.init(g, xi, k);
         for (; t < end; t += G) {
-          const uint32_t j = stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)t);
+          const uint32_t j = cur.at(g, a.bo, k, (uint32_t)t);
           const float4 pj = xw[j];
           float xj[3], r[3];
           unpack(pj, xj);
@@ -1244,6 +1260,8 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
       // a wave without them the list-only one
       auto walk = [&](auto stencil_rows) {
         constexpr bool ST = decltype(stencil_rows)::value;
+        StencilCursor<D, P> cur;
+        if (ST && row.stencil) cur.init(g, xi, k);
         for (int t0 = start + stream; t0 < end; t0 += 4 * S) {
           // geometry of the pair this lane owns (all zero for a stencil
           // candidate out of radius)
@@ -1255,7 +1273,7 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
           float d2 = 0.0f, r[3] = {0.0f, 0.0f, 0.0f};
           bool inr = false;
           if (to < end) {
-            const uint32_t jc = ST && row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
+            const uint32_t jc = ST && row.stencil ? cur.at(g, a.bo, k, (uint32_t)to) : (uint32_t)nidx[to];
             pj = xw[jc];
             float xj[3];
             unpack(pj, xj);
@@ -1451,6 +1469,8 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
       // a wave without them the list-only one
       auto walk = [&](auto stencil_rows) {
         constexpr bool ST = decltype(stencil_rows)::value;
+        StencilCursor<D, P> cur;
+        if (ST && row.stencil) cur.init(g, xi, k);
         // list rows: the next iteration's list entry is loaded one iteration
         // ahead (clamped into the row), and the body has no branch before
         // the row loads, so the position and row loads go out together
@@ -1469,7 +1489,7 @@ __global__ __launch_bounds__(kThreads, 6) void k_blur_hybrid_fwd_quad(GridParams
           bool inr = false;
           if constexpr (ST) {
             if (to < end) {
-              const uint32_t jc = row.stencil ? stencil_candidate<D, P>(g, a.bo, xi, k, (uint32_t)to) : (uint32_t)nidx[to];
+              const uint32_t jc = row.stencil ? cur.at(g, a.bo, k, (uint32_t)to) : (uint32_t)nidx[to];
               pj = xw[jc];
               float xj[3];
               unpack(pj, xj);
@@ -1618,15 +1638,17 @@ __host__ __device__ constexpr int ranges_per_particle(bool morton) {
 // there.  The buffer is cut into S equal slices of `slen` entries (S a power
 // of two, smask = S - 1), slice s allocated by the counter at
 // stripes[s * kStripeWords], zeroed before the fill; wave w takes its blocks
-// from slice w & smask, or, when a block does not fit there, from one of the
-// next kFillProbes - 1 slices.  Row contents and order (stencil order) are
+// from slice w & smask, or, when a block does not fit there, from one of
+// kFillProbes - 1 further slices spread over the buffer (an odd stride of
+// about S / kFillProbes slices: neighbouring slices serve neighbouring waves,
+// which work on the same dense region and fill up together).  Row contents and order (stencil order) are
 // fixed; only where a row lands depends on the order in which blocks reach a
 // counter, which no result depends on.  A block that fits nowhere is not
 // written: its particles' counts are set to -1 - (their stencil candidates)
-// and the pair kernels walk their stencils instead (stencil_candidate).
+// and the pair kernels walk their stencils instead (StencilCursor).
 // Counter words: [0] entries taken (a failed attempt's block included), [1]
 // entries of failed attempts, [2] entries of blocks not written.
-constexpr uint32_t kFillProbes = 4;
+constexpr uint32_t kFillProbes = 8;
 struct FillStripes {
   unsigned long long* ctr;  // kFillStripes * kStripeWords
   uint32_t smask;
@@ -1638,8 +1660,9 @@ struct FillStripes {
     if (need == 0) return 0;
     const bool first = __lane_id() == 0;
     const uint32_t probes = min(kFillProbes, smask + 1);
+    const uint32_t stride = ((smask + 1) / probes) | 1u;  // odd: the probed slices are distinct
     for (uint32_t i = 0; i < probes; ++i) {
-      const uint32_t s = (wave + i) & smask;
+      const uint32_t s = (wave + i * stride) & smask;
       unsigned long long* c = ctr + (uint64_t)s * kStripeWords;
       unsigned long long b = 0;
       if (first) b = atomicAdd(c, (unsigned long long)need);

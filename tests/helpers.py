@@ -127,3 +127,17 @@ def hybrid_bound(raw, raw_mag, M_mag, L):
     LML = np.einsum("qab,qbc,qcd->qad", aL, M_mag, aL)
     t2 = np.einsum("qfd,qde->qfe", np.abs(raw), LML)
     return t1 + t2
+
+
+def indefinite_matrices(dim, tol=1e-3, seed=8):
+    """Symmetric indefinite matrices Q diag(e) Q^T with one negative
+    eigenvalue: ``big`` has det < -tol (inverted), ``small`` has
+    -tol < det < 0 (the |det| < tol branch gives the identity)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for kind, lo, hi in (("big", 0.05, 2.0), ("small", 1e-4, 2.5e-4)):
+        Q, _ = np.linalg.qr(rng.standard_normal((64, dim, dim)))
+        e = rng.uniform(lo, hi, (64, dim)) ** (1.0 / dim) * rng.choice([1.0, 1.5], (64, dim))
+        e[:, 0] *= -1.0
+        out[kind] = np.einsum("qab,qb,qcb->qac", Q, e, Q)
+    return out

@@ -79,3 +79,40 @@ def test_fill_follows_candidates():
     assert (c < 0).any() and int(total[0].item()) == need
     assert np.all(c[c < 0] <= -2)
     assert int(total[1].item()) == sum(len(first[k]) for k in np.flatnonzero(c < 0))
+
+
+def test_fill_after_tiles_is_refused():
+    """sphops_neighbor_tiles reuses the grid scratch that holds the fill's
+    work split, so a fill after it must be refused until the candidates call
+    runs again (then it works)."""
+    from npa_amd.sphops import _native
+    lib = _native.lib
+    grid, snap, xb = _setup()
+    hg = grid.hashgrid
+    n = xb.shape[0] * xb.shape[1]
+    i32 = dict(dtype=torch.int32, device="cuda")
+    start, count, order = torch.empty(n, **i32), torch.empty(n, **i32), torch.empty(n, **i32)
+    total = torch.zeros(2, dtype=torch.int64, device="cuda")
+    cap = 300 * 300
+    index = torch.empty(cap, **i32)
+    tcap = int(lib.sphops_neighbor_tile_capacity(hg._h))
+    wcap = 2 * int(lib.sphops_neighbor_wave_capacity(hg._h))
+    units, waves = torch.empty(2 * tcap, **i32), torch.empty(wcap, **i32)
+    counts = torch.zeros(2, **i32)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    xp, bp = ctypes.c_void_p(xb.data_ptr()), ctypes.c_void_p(snap.bin_offsets.data_ptr())
+    p = lambda t, off=0: ctypes.c_void_p(t.data_ptr() + off)
+
+    def fill():
+        return lib.sphops_neighbor_fill(hg._h, xp, bp, p(start), p(index), cap, p(count), p(total), st)
+
+    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, st))
+    assert fill() == 0
+    _native.check(lib.sphops_neighbor_tiles(hg._h, xp, bp, p(count), p(units), p(counts), p(order), p(waves),
+                                            p(counts, 4), st))
+    assert fill() != 0
+    assert b"must follow" in lib.sphops_last_error()
+    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, st))
+    assert fill() == 0
+    torch.cuda.synchronize()
+    assert total.tolist() == [int(count.sum().item()), 0]

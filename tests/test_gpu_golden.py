@@ -129,3 +129,22 @@ def test_permute_backward_is_a_gather():
     np.testing.assert_array_equal(x.grad.cpu().numpy(), ux[b, perm])
     np.testing.assert_array_equal(s.grad.cpu().numpy(), us[b, perm])
     np.testing.assert_array_equal(m.grad.cpu().numpy(), um[b, perm])
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_safe_inverse_indefinite(dim):
+    """safe_inv_sym_mat (sphops/sph.py:467-471, sph_cuda.cu:3095-3179) on
+    symmetric indefinite matrices: det < -tol is inverted, -tol < det < 0
+    gives the identity (the |det| < tol branch, sph_cuda.cu:3111, 3152), as
+    the oracle does; positive definite ones are covered by the parity cases."""
+    import npa_amd.sphops as sp
+    from oracle import sph
+    mats = H.indefinite_matrices(dim)
+    M = np.concatenate([mats["big"], mats["small"]]).astype(np.float32)
+    got = sp.safe_inv_sym_mat(dev(M[None]), 1e-3).cpu().numpy()[0]   # (B, N, D, D) as in the reference
+    ref, det = sph.safe_inv_sym(M.astype(np.float64), 1e-3)
+    n = len(mats["big"])
+    assert np.all(det[:n] < -1e-3) and np.all((det[n:] < 0) & (det[n:] > -1e-3))
+    np.testing.assert_array_equal(got[n:], np.broadcast_to(np.eye(dim, dtype=np.float32), got[n:].shape))
+    scale = np.abs(ref) + np.einsum("qab,qbc,qcd->qad", np.abs(ref), np.abs(M), np.abs(ref))
+    H.assert_close(f"safe_inv_indefinite{dim}", got[:n], ref[:n], scale[:n])

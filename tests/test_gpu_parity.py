@@ -87,6 +87,80 @@ CASES = {c.name: c for c in _cases() + _workload_cases()}
 CHAIN_STEPS = 32
 
 
+def _chain_params(wl, seed):
+    """Seeded parameters of the chain's update and loss: a two-layer MLP over
+    the perception features and the loss weights of the final particles."""
+    B, N, C, D = wl.B, wl.N, wl.C, wl.dim
+    gen = torch.Generator().manual_seed(seed)
+    width = 2 * C + C * D + D
+    w1 = (torch.randn(width, 32, generator=gen) / width ** 0.5).cuda()
+    w2 = (torch.randn(32, D + C, generator=gen) / 32 ** 0.5).cuda()
+    u_x = torch.randn(B, N, D, generator=gen).cuda()
+    u_s = torch.randn(B, N, C, generator=gen).cuda()
+    return w1, w2, u_x, u_s
+
+
+def _scaled_features(sb, bl, gh, dg, h, n):
+    """The perception features divided by their natural scales (states and
+    blur O(1), gradients O(1/h), the density gradient O(N/h)), so that fp32
+    rounding of each feature is about 1e-7 of the update's input scale."""
+    return torch.cat([sb, bl, gh.flatten(-2) * h, dg * (h / n)], -1)
+
+
+def _chain_step(grid, wl, x, s, w1, w2, perms=None, scaled=False, step=0.25):
+    """One chain step on the GPU: rebin, NPA.perceive's operators, the
+    NPA-shaped update, the periodic wrap.  Returns the next (x, s), in the
+    step's binned order (step_euler returns the updated particles in binned
+    order, which the next step bins again, models/npa.py:189-204)."""
+    import npa_amd.sphops as sp
+    D = wl.dim
+    with torch.no_grad():
+        snap = grid.instantiate(x)
+    if perms is not None:
+        perms.append(snap.permutation.cpu().numpy())
+    xb, sb = sp.bin_particles(x, s, snap)
+    rho = sp.density(xb, snap)
+    bl = sp.blur(xb, rho, sb, snap)
+    gh = sp.gradient_hybrid(xb, rho, sb, snap)
+    dg = sp.density_gradient(xb, snap)
+    if scaled:
+        z = _scaled_features(sb, bl, gh, dg, wl.h, wl.N)
+    else:
+        z = torch.cat([sb, bl, gh.flatten(-2), dg], -1)
+    y = torch.tanh(z @ w1) @ w2
+    x = grid.wrap_positions(xb + (step * wl.h) * torch.tanh(y[..., :D])).contiguous()
+    s = (sb + 0.1 * torch.tanh(y[..., D:])).contiguous()
+    return x, s
+
+
+def _new_grid(wl):
+    import npa_amd.sphops as sp
+    return sp.HashGrid(dim=wl.dim, boundary="periodic", mode="grid", grid_size=list(wl.grid_size), eps=wl.h,
+                       num_particles=wl.N, batch_size=wl.B, max_particles_per_block=wl.maxp)
+
+
+def _run_chain(wl, steps, seed, scaled=False, step=0.25):
+    """``steps`` chained steps on one grid, then the gradient of the loss
+    ``(x * u_x).sum() + (s * u_s).sum()`` on the final particles with respect
+    to the initial ones, backward through every step.  Returns the inputs
+    (x, s) of every step, the permutation of every step, the gradients and
+    whether every list stored all its rows."""
+    grid = _new_grid(wl)
+    w1, w2, u_x, u_s = _chain_params(wl, seed)
+    x0 = dev(grid.wrap_positions(torch.from_numpy(wl.x))).requires_grad_(True)
+    s0 = dev(wl.s).requires_grad_(True)
+    x, s = x0, s0
+    inputs, perms, stored = [], [], True
+    for _ in range(steps):
+        inputs.append((x.detach().cpu().numpy(), s.detach().cpu().numpy()))
+        x, s = _chain_step(grid, wl, x, s, w1, w2, perms, scaled, step)
+        stored &= not grid.list_overflow()
+    loss = (x * u_x).sum() + (s * u_s).sum()
+    gx, gs = torch.autograd.grad(loss, (x0, s0))
+    torch.cuda.synchronize()
+    return inputs, perms, gx.cpu().numpy(), gs.cpu().numpy(), stored
+
+
 @functools.lru_cache(maxsize=None)
 def _chain(seed=3):
     """cfg2's workload: 32 chained perception + update
@@ -98,41 +172,11 @@ def _chain(seed=3):
     the periodic box after every step.  Returns the inputs (x, s) of every
     step (each in the previous step's binned order) and the gradient of a fixed loss on the final
     particles with respect to the initial ones."""
-    import npa_amd.sphops as sp
     wl = workloads.make("cfg2", 1.0)
-    B, N, C, D = wl.B, wl.N, wl.C, wl.dim
-    print(f"[case] cfg2 chain: {CHAIN_STEPS} steps B={B} N={N} C={C}", flush=True)
-    grid = sp.HashGrid(dim=D, boundary="periodic", mode="grid", grid_size=list(wl.grid_size), eps=wl.h,
-                       num_particles=N, batch_size=B, max_particles_per_block=wl.maxp)
-    gen = torch.Generator().manual_seed(seed)
-    width = 2 * C + C * D + D
-    w1 = (torch.randn(width, 32, generator=gen) / width ** 0.5).cuda()
-    w2 = (torch.randn(32, D + C, generator=gen) / 32 ** 0.5).cuda()
-    u_x = torch.randn(B, N, D, generator=gen).cuda()
-    u_s = torch.randn(B, N, C, generator=gen).cuda()
-    x0 = dev(grid.wrap_positions(torch.from_numpy(wl.x))).requires_grad_(True)
-    s0 = dev(wl.s).requires_grad_(True)
-    x, s = x0, s0
-    inputs = []
-    for _ in range(CHAIN_STEPS):
-        inputs.append((x.detach().cpu().numpy(), s.detach().cpu().numpy()))
-        with torch.no_grad():
-            snap = grid.instantiate(x)
-        xb, sb = sp.bin_particles(x, s, snap)
-        rho = sp.density(xb, snap)
-        bl = sp.blur(xb, rho, sb, snap)
-        gh = sp.gradient_hybrid(xb, rho, sb, snap)
-        dg = sp.density_gradient(xb, snap)
-        z = torch.cat([sb, bl, gh.flatten(-2), dg], -1)
-        y = torch.tanh(z @ w1) @ w2
-        # step_euler returns the updated particles in binned order, which the
-        # next step bins again (models/npa.py:189-204)
-        x = grid.wrap_positions(xb + (0.25 * wl.h) * torch.tanh(y[..., :D])).contiguous()
-        s = (sb + 0.1 * torch.tanh(y[..., D:])).contiguous()
-    loss = (x * u_x).sum() + (s * u_s).sum()
-    gx, gs = torch.autograd.grad(loss, (x0, s0))
-    torch.cuda.synchronize()
-    return wl, inputs, gx.cpu().numpy(), gs.cpu().numpy()
+    print(f"[case] cfg2 chain: {CHAIN_STEPS} steps B={wl.B} N={wl.N} C={wl.C}", flush=True)
+    inputs, _, gx, gs, stored = _run_chain(wl, CHAIN_STEPS, seed)
+    assert stored, "a list of the chain walked rows on the stencil"
+    return wl, inputs, gx, gs
 
 
 def _chain_case(step):
@@ -144,27 +188,35 @@ def _chain_case(step):
     return c
 
 
-def _cfg5_full_case():
-    """cfg5 at its full size (1,048,576 particles, 206 M cells, cells of up to
-    121 particles); perception is checked on a sample of queries: 2000 binned
-    slots drawn uniformly plus every particle of the 16 fullest cells."""
-    wl = workloads.make("cfg5", 1.0)
+def _full_case(name, sample):
+    """A benchmark configuration at its full size:
+    binning is checked bit for bit over every particle and cell; perception
+    on every particle, or with ``sample`` on a sample of queries: that many
+    binned slots drawn uniformly plus every particle of the 16 fullest
+    cells."""
+    wl = workloads.make(name, 1.0)
     c = H.workload_case(wl)
-    c.name = "cfg5-full"
+    c.name = f"{name}-full"
     ob = H.oracle_binning(c)
-    bo = ob["bin_offsets"]
-    cells = np.flatnonzero(np.diff(bo))
-    occ = np.diff(bo)[cells]
-    full = cells[np.argsort(occ, kind="stable")[-16:]]
-    dense = np.concatenate([np.arange(bo[k], bo[k + 1]) for k in full])
-    rng = np.random.default_rng(17)
-    c.queries = np.unique(np.concatenate([rng.choice(c.B * c.N, 2000, replace=False), dense]))
+    if sample:
+        bo = ob["bin_offsets"]
+        cells = np.flatnonzero(np.diff(bo))
+        occ = np.diff(bo)[cells]
+        full = cells[np.argsort(occ, kind="stable")[-16:]]
+        dense = np.concatenate([np.arange(bo[k], bo[k + 1]) for k in full])
+        rng = np.random.default_rng(17)
+        c.queries = np.unique(np.concatenate([rng.choice(c.B * c.N, sample, replace=False), dense]))
     c.extra["binning"] = ob
     return c
 
 
 LAZY = {f"cfg2-chain-step{t}": functools.partial(_chain_case, t) for t in (0, CHAIN_STEPS - 1)}
-LAZY["cfg5-full"] = _cfg5_full_case
+# cfg3: 64 clouds x 512 particles, C = 32, every particle checked;
+# cfg4: 65,536 3D particles, C = 32; cfg5: 1,048,576 3D particles (206 M
+# cells, cells of up to 121 particles), C = 16
+LAZY["cfg3-full"] = functools.partial(_full_case, "cfg3", 0)
+LAZY["cfg4-full"] = functools.partial(_full_case, "cfg4", 8000)
+LAZY["cfg5-full"] = functools.partial(_full_case, "cfg5", 2000)
 
 
 @functools.lru_cache(maxsize=None)
@@ -585,6 +637,99 @@ def test_cfg2_chain_is_deterministic_and_moves():
         last = [r.tobytes() for r in inputs[-1][k].reshape(-1, inputs[-1][k].shape[-1])]
         assert sum(r in first for r in last) < 0.01 * len(last)
     assert np.isfinite(inputs[-1][0]).all() and np.isfinite(inputs[-1][1]).all()
+
+
+def test_cfg2_chain_backward_step_by_step():
+    """The 32-step cfg2 chain's gradient, recomputed one step at a time: each
+    step's vector-Jacobian product is evaluated from the step's recorded
+    inputs on a grid and snapshot of its own, and fed backwards into the step
+    before (train.py:225-238 backpropagates through every step).  Only the
+    chain's autograd graph carries state across snapshots (the per-snapshot
+    neighbour lists, the list sizing read back from the snapshot before, the
+    grid's pass fusion); the recomputation shares none of it, so the two
+    must agree bit for bit.  Step 0 runs on a fresh grid (single operators,
+    as in the chain), the others on a grid that has seen NPA.perceive's
+    calls once (fused passes, as in the chain)."""
+    wl, inputs, gx_chain, gs_chain = _chain()
+    w1, w2, u_x, u_s = _chain_params(wl, 3)
+    warm = _new_grid(wl)
+    with torch.no_grad():
+        _chain_step(warm, wl, dev(inputs[0][0]), dev(inputs[0][1]), w1, w2)
+    gx, gs = u_x, u_s
+    for t in reversed(range(CHAIN_STEPS)):
+        grid = _new_grid(wl) if t == 0 else warm
+        x = dev(inputs[t][0]).requires_grad_(True)
+        s = dev(inputs[t][1]).requires_grad_(True)
+        xn, sn = _chain_step(grid, wl, x, s, w1, w2)
+        assert not grid.list_overflow()
+        if t + 1 < CHAIN_STEPS:  # the recorded input of the next step is this step's output
+            np.testing.assert_array_equal(xn.detach().cpu().numpy(), inputs[t + 1][0])
+            np.testing.assert_array_equal(sn.detach().cpu().numpy(), inputs[t + 1][1])
+        gx, gs = torch.autograd.grad((xn, sn), (x, s), (gx, gs))
+    np.testing.assert_array_equal(gx.cpu().numpy(), gx_chain)
+    np.testing.assert_array_equal(gs.cpu().numpy(), gs_chain)
+
+
+CHAIN_BF_STEPS = 3
+# Position step of the reduced chain, in units of h.
+CHAIN_BF_STEP = 0.05
+# Tolerance of the chained gradient against float64, per element, relative to
+# |ref| plus the tensor's RMS.  fp32 rounding of the positions, the
+# coefficients and the MLP compounds over the steps (measured on an MI355X:
+# about 1e-4 of |ref| + RMS after three steps); a wrong or stale snapshot
+# would differ by O(1).
+CHAIN_BF_RTOL = 1e-3
+
+
+def test_chain_backward_against_float64_bruteforce():
+    """A reduced cfg2 chain (one periodic cloud of 2048 particles, h = 1/17,
+    three steps of 0.05 h at most, each feature divided by its natural scale
+    before the update so that the chain is well conditioned) against float64
+    autograd of the same chain written with the dense all-pairs formulation
+    (oracle/bruteforce.py, torch_sph.py's algorithm): the all-pairs sums do
+    not depend on binning or order, so only the GPU's permutation of each
+    step is replayed (as a gather) to keep the particle order the loss
+    sees."""
+    from oracle import bruteforce as bf
+    wl = workloads.make("cfg2", 2048 / 16384)
+    wl.x, wl.s = wl.x[:1], wl.s[:1]
+    D = wl.dim
+    print(f"[case] cfg2 reduced chain vs float64: N={wl.N} h={wl.h} grid={wl.grid_size}", flush=True)
+    inputs, perms, gx_gpu, gs_gpu, stored = _run_chain(wl, CHAIN_BF_STEPS, 5, scaled=True, step=CHAIN_BF_STEP)
+    assert stored
+    w1, w2, u_x, u_s = (t.cpu().double() for t in _chain_params(wl, 5))
+    h = float(np.float32(wl.h))
+    L = float(wl.grid_size[0]) * h
+    c6, cs = bf.poly6_coef(h, D), bf.spiky_coef(h, D)
+    x0 = torch.from_numpy(inputs[0][0].astype(np.float64)).requires_grad_(True)
+    s0 = torch.from_numpy(inputs[0][1].astype(np.float64)).requires_grad_(True)
+    x, s = x0, s0
+    m = torch.ones(1, wl.N, dtype=torch.float64)
+    for t in range(CHAIN_BF_STEPS):
+        inv = torch.from_numpy(np.argsort(perms[t][0]))  # slot -> particle
+        xb, sb = x[:, inv], s[:, inv]
+        P = bf.Pairs(xb, h, periodic=True, box=[L] * D)
+        rho = bf.density(P, m, c6)
+        bl = bf.blur(P, m, rho, sb, c6)
+        gh = bf.gradient_hybrid(P, m, rho, sb, cs, 1e-3)
+        dg = bf.density_gradient(P, m, cs)
+        z = _scaled_features(sb, bl, gh, dg, wl.h, wl.N)
+        y = torch.tanh(z @ w1) @ w2
+        xn = xb + (CHAIN_BF_STEP * wl.h) * torch.tanh(y[..., :D])
+        x = torch.remainder(xn + 0.5 * L, L) - 0.5 * L
+        s = sb + 0.1 * torch.tanh(y[..., D:])
+        if t + 1 < CHAIN_BF_STEPS:
+            # the GPU's next input (positions modulo the box, states)
+            dx = np.abs(np.mod(inputs[t + 1][0] - x.detach().numpy() + 0.5 * L, L) - 0.5 * L).max()
+            ds = np.abs(inputs[t + 1][1] - s.detach().numpy()).max()
+            print(f"[chain] step {t}: max |x_gpu - x_f64| = {dx:.2e}, max |s_gpu - s_f64| = {ds:.2e}", flush=True)
+            assert dx < 1e-6 * L and ds < 1e-4
+    gx, gs = torch.autograd.grad((x * u_x).sum() + (s * u_s).sum(), (x0, s0))
+    for name, got, ref in (("dx0", gx_gpu, gx.numpy()), ("ds0", gs_gpu, gs.numpy())):
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        print(f"[chain] {name}: |gpu - f64| / |f64| = {rel:.2e}, max error / rms = "
+              f"{np.abs(got - ref).max() / np.sqrt(np.mean(ref ** 2)):.2e}", flush=True)
+        H.assert_close(f"chain:{name}", got, ref, np.zeros_like(ref), rtol=CHAIN_BF_RTOL, atol=CHAIN_BF_RTOL)
 
 
 @pytest.mark.parametrize("name", ["cfg5", "dense2d-per", "dense3d-per-c16", "dense3d-particle-c16", "randn-2d", "cfg1"])

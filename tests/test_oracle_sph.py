@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+import helpers as H
 from oracle import binning, bruteforce as bf, neighbors as nb, sph
 
 
@@ -376,3 +377,22 @@ def test_safe_inverse():
         Z[:, 0, 0] = 1e-4
         Li, _ = sph.safe_inv_sym(Z, 1e-3)
         np.testing.assert_array_equal(Li, np.broadcast_to(np.eye(dim), Li.shape))
+
+
+def test_safe_inverse_indefinite():
+    """The identity branch is taken on |det| < tol, not det < tol
+    (sphops/sph_cuda.cu:3111, 3152): an indefinite matrix with det < -tol is
+    inverted, one with -tol < det < 0 is replaced by the identity."""
+    for dim in (2, 3):
+        mats = H.indefinite_matrices(dim)
+        big, small = mats["big"], mats["small"]
+        dets = np.linalg.det(big)
+        assert np.all(dets < -1e-3)
+        L, det = sph.safe_inv_sym(big, 1e-3)
+        np.testing.assert_allclose(det, dets, rtol=1e-10)
+        np.testing.assert_allclose(L, np.linalg.inv(big), rtol=1e-9, atol=1e-9)
+        dets = np.linalg.det(small)
+        assert np.all((dets < 0) & (dets > -1e-3))
+        L, det = sph.safe_inv_sym(small, 1e-3)
+        np.testing.assert_allclose(det, dets, rtol=1e-9, atol=1e-15)
+        np.testing.assert_array_equal(L, np.broadcast_to(np.eye(dim), L.shape))
