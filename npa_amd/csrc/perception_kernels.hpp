@@ -1242,8 +1242,12 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
     float ggi[kG ? CW * D : 1] = {};
     float dsb[CW] = {}, dsg[CW] = {};
     float wsum[D] = {};
-    float dxb[D] = {}, dxg[D] = {};
+    // dL/dx of both operators in one accumulator, in units of the spiky
+    // coefficient (of poly6's for blur alone): blur's pair term enters
+    // scaled by k6 = -6 c6 / cs
+    float dxm[D] = {};
     float drb = 0.0f, drg = 0.0f;
+    const float k6 = kG ? -6.0f * (g.c6 / g.cs) : -6.0f;
     if (active) {
       unpack(xw[k], xi);
       const float mi = a.m[k], ri = a.rho[k];
@@ -1272,19 +1276,34 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
           float4 pj = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
           float d2 = 0.0f, r[3] = {0.0f, 0.0f, 0.0f};
           bool inr = false;
-          if (to < end) {
-            const uint32_t jc = ST && row.stencil ? cur.at(g, a.bo, k, (uint32_t)to) : (uint32_t)nidx[to];
-            pj = xw[jc];
+          // list rows of the full backward take the pair with no branch (a
+          // lane past the row's end takes the row's last entry; the quad
+          // loop below stops before its pair, and its volume is zeroed for
+          // wsum): 0.878 -> 0.861 ms at cfg5; the dL/ds-only variant, whose
+          // time follows its loads, keeps the branch (0.673 against 0.697)
+          constexpr bool kNoBranch = !ST && FULL;
+          if constexpr (!kNoBranch) {
+            if (to < end) {
+              const uint32_t jc = ST && row.stencil ? cur.at(g, a.bo, k, (uint32_t)to) : (uint32_t)nidx[to];
+              pj = xw[jc];
+              float xj[3];
+              unpack(pj, xj);
+              d2 = displacement<D, P>(g, xi, xj, r);
+              inr = !(ST && row.stencil) || d2 < g.eps2;
+              if (inr) jo = jc;
+            }
+          } else {
+            inr = to < end;
+            jo = (uint32_t)nidx[min(to, end - 1)];
+            pj = xw[jo];
             float xj[3];
             unpack(pj, xj);
             d2 = displacement<D, P>(g, xi, xj, r);
-            inr = !(ST && row.stencil) || d2 < g.eps2;
-            if (inr) jo = jc;
           }
-          if (inr) {
+          if (kNoBranch || inr) {
             float xj[3];
             unpack(pj, xj);
-            vo = pj.w;
+            vo = inr ? pj.w : 0.0f;
             const float db = back_disp<D, P>(g, xi, xj, r, d2, rbo);
             Wo = poly6(g.eps2, db);
             float d, dinv;
@@ -1294,13 +1313,12 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
               wo[e] = mag * rbo[e];
               wsum[e] += vo * wo[e];
             }
-            if (db != 0.0f && db < g.eps2) {
-              const float tt = g.eps2 - db;
-              t2o = tt * tt;
-              const float di = dinv;
-              jao = 3.0f * (g.eps - d) * (g.eps - d) * di;
-              jbo = 3.0f * (g.eps2 - db) * di * di * di;
-            }
+            const bool jac = db != 0.0f && db < g.eps2;  // Jacobian terms vanish outside (0, eps)
+            const float tt = g.eps2 - db;
+            const float di = dinv;
+            t2o = jac ? tt * tt : 0.0f;
+            jao = jac ? 3.0f * (g.eps - d) * (g.eps - d) * di : 0.0f;
+            jbo = jac ? 3.0f * tt * di * di * di : 0.0f;
           }
     #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -1338,6 +1356,7 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
             } else {
               float sj[CW];
               load_span<CW, true>(row_slice<OFF32>(a.s, j, C, c0), sj);
+              float coef = 0.0f;  // the pair's factor of rb in dL/dx
               if constexpr (kB) {
                 float A = 0.0f, Bv = 0.0f;
     #pragma unroll
@@ -1346,9 +1365,11 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
                   A += gbi[f] * sj[f];
                   Bv += gbj[f] * si[f];
                 }
-                const float m6 = -6.0f * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
+                coef = k6 * t2 * (A * vj + Bv * vi);  // t2 = 0 outside (0, eps)
+                if constexpr (!kG) {
     #pragma unroll
-                for (int e = 0; e < D; ++e) dxb[e] += m6 * rb[e];
+                  for (int e = 0; e < D; ++e) dxm[e] += coef * rb[e];
+                }
               }
               if constexpr (kG) {
                 float u1[D] = {}, u2[D] = {};
@@ -1370,8 +1391,9 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
                   rv += rb[e] * u[e];
                 }
                 drg += uw;
+                coef -= jb * rv;
     #pragma unroll
-                for (int e = 0; e < D; ++e) dxg[e] += ja * u[e] - jb * rb[e] * rv;  // ja = jb = 0 outside
+                for (int e = 0; e < D; ++e) dxm[e] += ja * u[e] + coef * rb[e];  // ja = jb = 0 outside
               }
             }
           }
@@ -1391,8 +1413,9 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
   #pragma unroll
       for (int e = 0; e < D; ++e) wsum[e] = quad_get<0>(wsum[e]);  // the group total, to the four slice lanes
     }
-    if constexpr (FULL && kB) grp_sum(G, dxb, drb);
-    if constexpr (FULL && kG) grp_sum(G, dxg, drg);
+    if constexpr (FULL && kB && kG) grp_sum(G, dxm, drb, drg);
+    else if constexpr (FULL && kB) grp_sum(G, dxm, drb);
+    else if constexpr (FULL && kG) grp_sum(G, dxm, drg);
     if (active && stream == 0) {
       const float sb = vi * g.c6;
   #pragma unroll
@@ -1409,17 +1432,11 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
       }
       if constexpr (FULL) {
         if (slice == 0) {
-          float dr = 0.0f, dx[D] = {};
-          if constexpr (kB) {
-            dr = drb * g.c6;
+          float dr = 0.0f, dx[D];
+          if constexpr (kB) dr = drb * g.c6;
+          if constexpr (kG) dr = kB ? dr + drg * g.cs : drg * g.cs;
   #pragma unroll
-            for (int e = 0; e < D; ++e) dx[e] = dxb[e] * g.c6;
-          }
-          if constexpr (kG) {
-            dr = kB ? dr + drg * g.cs : drg * g.cs;
-  #pragma unroll
-            for (int e = 0; e < D; ++e) dx[e] = kB ? dx[e] + dxg[e] * g.cs : dxg[e] * g.cs;
-          }
+          for (int e = 0; e < D; ++e) dx[e] = dxm[e] * (kG ? g.cs : g.c6);
           a.out2[k] = -mr2 * dr;
           store_pos_grad<D>(a.out0, k, dx, 1.0f);
         }
