@@ -276,6 +276,10 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       g->units = dalloc<uint2>(BN);
       g->unit_total = dalloc<int32_t>(1);
       g->stripes = dalloc<unsigned long long>((uint64_t)sphops::kFillStripes * sphops::kStripeWords);
+      // zero once here (and wait, so that a fill on any stream sees it);
+      // every fill's totals kernel leaves them zero again
+      SPHOPS_HIP(hipMemset(g->stripes, 0, sizeof(unsigned long long) * sphops::kFillStripes * sphops::kStripeWords));
+      SPHOPS_HIP(hipDeviceSynchronize());
     } catch (...) {
       sphops::free_grid(g);
       throw;

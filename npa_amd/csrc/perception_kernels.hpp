@@ -1654,7 +1654,7 @@ __host__ __device__ constexpr int ranges_per_particle(bool morton) {
 // the index buffer with an atomic add on a 64-bit counter and writes its rows
 // there.  The buffer is cut into S equal slices of `slen` entries (S a power
 // of two, smask = S - 1), slice s allocated by the counter at
-// stripes[s * kStripeWords], zeroed before the fill; wave w takes its blocks
+// stripes[s * kStripeWords], zero before the fill; wave w takes its blocks
 // from slice w & smask, or, when a block does not fit there, from one of
 // kFillProbes - 1 further slices spread over the buffer (an odd stride of
 // about S / kFillProbes slices: neighbouring slices serve neighbouring waves,
@@ -2044,19 +2044,21 @@ __global__ __launch_bounds__(kThreads) void k_fill(GridParams g, const float4* _
 }
 
 // total[0] = in-radius pairs (blocks written or not), total[1] = pairs of
-// the blocks not written, from the counters' words (see FillStripes).  One
-// workgroup of kThreads >= kFillStripes.
+// the blocks not written, from the counters' words (see FillStripes); the
+// counters are then reset to zero for the next fill.  One workgroup of
+// kThreads >= kFillStripes.
 static_assert(kThreads >= kFillStripes, "k_fill_totals reads one counter per thread");
-[[maybe_unused]] static __global__ __launch_bounds__(kThreads) void k_fill_totals(const unsigned long long* __restrict__ ctr,
+[[maybe_unused]] static __global__ __launch_bounds__(kThreads) void k_fill_totals(unsigned long long* __restrict__ ctr,
                                                                  uint32_t stripes,
                                                                  unsigned long long* __restrict__ total) {
   __shared__ unsigned long long part[2][kThreads / kWave];
   const uint32_t s = threadIdx.x;
   unsigned long long a = 0, o = 0;
   if (s < stripes) {
-    const unsigned long long* c = ctr + (uint64_t)s * kStripeWords;
+    unsigned long long* c = ctr + (uint64_t)s * kStripeWords;
     a = c[0] - c[1] + c[2];
     o = c[2];
+    c[0] = c[1] = c[2] = 0ull;
   }
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -2120,8 +2122,14 @@ template <int D, bool P>
 void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, int32_t* nstart, int32_t* nidx,
                     int32_t* ncnt, unsigned long long* used, int64_t cap, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
-  hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
-  SPHOPS_LAUNCHED();
+  // 3D positions are already 16-byte (x, y, z, w) records; the fill reads
+  // x, y and z only, so they need no packing
+  const float4* xw = reinterpret_cast<const float4*>(x);
+  if constexpr (D == 2) {
+    hipLaunchKernelGGL((k_pack<D, kWNone>), grid_for(n), dim3(kThreads), 0, st, x, nullptr, nullptr, g.packed, n);
+    SPHOPS_LAUNCHED();
+    xw = g.packed;
+  }
   // S slices of at least kStripeMinEntries entries and, for n particles,
   // about n / (kStripeMinUnits * kUnitParticles) units or more each (one
   // slice for small buffers)
@@ -2129,13 +2137,14 @@ void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, int32_t* n
   while (S < kFillStripes && (int64_t)(2 * S) * kStripeMinEntries <= cap &&
          (uint64_t)(2 * S) * kStripeMinUnits * kUnitParticles <= n)
     S *= 2;
+  // the counters are zero here: zeroed at grid creation and by the totals
+  // kernel of every fill
   FillStripes fs{g.stripes, S - 1, (uint64_t)(cap / S)};
-  fill_u32(reinterpret_cast<uint32_t*>(g.stripes), (uint64_t)S * kStripeWords * 2, 0u, st);
   if (g.particle_mode)
-    hipLaunchKernelGGL((k_fill<D, P, true>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, bo,
+    hipLaunchKernelGGL((k_fill<D, P, true>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, xw, bo,
                        g.unit_len, g.units, g.unit_total, nidx, nstart, ncnt, fs);
   else
-    hipLaunchKernelGGL((k_fill<D, P, false>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, g.packed, bo,
+    hipLaunchKernelGGL((k_fill<D, P, false>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, xw, bo,
                        g.unit_len, g.units, g.unit_total, nidx, nstart, ncnt, fs);
   SPHOPS_LAUNCHED();
   hipLaunchKernelGGL(k_fill_totals, dim3(1), dim3(kThreads), 0, st, g.stripes, S, used);
