@@ -349,9 +349,74 @@ __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint64_t* __rest
   }
 }
 
+// First and one-past-last sorted position of the run of `key` (its cell)
+// that contains position k, from the sorted keys alone: a galloping search
+// away from k, then a binary search in the last step's window; about
+// 2 log2(run length) loads, near k.
+__device__ __forceinline__ uint32_t run_start(const uint64_t* __restrict__ kv, uint32_t k, uint32_t key) {
+  uint32_t hi = k, lo = 0, step = 1;  // key(hi) == key; lo: a smaller key, once found
+  bool found = false;
+  while (step <= hi) {
+    const uint32_t probe = hi - step;
+    if (kv_key(kv[probe]) < key) {
+      lo = probe;
+      found = true;
+      break;
+    }
+    hi = probe;
+    step <<= 1;
+  }
+  if (!found) {
+    if (kv_key(kv[0]) == key) return 0;
+    lo = 0;  // key(0) < key
+  }
+  while (hi - lo > 1) {  // key(lo) < key == key(hi)
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (kv_key(kv[mid]) < key) lo = mid;
+    else hi = mid;
+  }
+  return hi;
+}
+
+__device__ __forceinline__ uint32_t run_end(const uint64_t* __restrict__ kv, uint32_t n, uint32_t k,
+                                            uint32_t key) {
+  uint32_t lo = k, hi = n, step = 1;  // key(lo) == key; hi: a larger key, once found
+  bool found = false;
+  while (lo + step < n) {
+    const uint32_t probe = lo + step;
+    if (kv_key(kv[probe]) > key) {
+      hi = probe;
+      found = true;
+      break;
+    }
+    lo = probe;
+    step <<= 1;
+  }
+  if (!found) {
+    if (kv_key(kv[n - 1]) == key) return n;
+    hi = n - 1;  // key(n - 1) > key
+  }
+  while (hi - lo > 1) {  // key(lo) == key < key(hi)
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (kv_key(kv[mid]) > key) hi = mid;
+    else lo = mid;
+  }
+  return hi;
+}
+
+// Cell count from which the permutation and block-row kernels find a cell's
+// bounds in the sorted keys near k (run_start / run_end, which the previous
+// kernels left in cache) instead of loading them from bin_offsets, whose
+// entries are then scattered over a large array (2^22 cells = 16 MB, four
+// times an XCD's L2): 0.339 -> 0.326 ms for instantiate at cfg5, while at
+// cfg1 the dependent loads of the search cost 5 us more than the cached
+// bin_offsets loads.
+constexpr uint64_t kRunSearchMinCells = 1ull << 22;
+
 // Permutation (destination slot of every input particle) and, in grid mode
 // (flags non-null), the block-start flags of the block table: sorted position
-// k starts a block when its offset in its cell is a multiple of maxp.
+// k starts a block when its offset in its cell is a multiple of maxp.  The
+// cell's first position from bin_offsets, or (bo null) from the sorted keys.
 __global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __restrict__ kv, uint32_t n,
                                                           uint32_t N, int32_t* __restrict__ perm,
                                                           const int32_t* __restrict__ bo, uint32_t maxp,
@@ -362,17 +427,18 @@ __global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __rest
   const uint32_t src = kv_val(w);
   perm[src] = (int32_t)(k - (src / N) * N);
   if (flags != nullptr) {
-    const uint32_t rs = (uint32_t)bo[kv_key(w)];
+    const uint32_t key = kv_key(w);
+    const uint32_t rs = bo != nullptr ? (uint32_t)bo[key] : run_start(kv, k, key);
     flags[k] = ((k - rs) % maxp == 0) ? 1u : 0u;
   }
 }
 
-// --------------------------------------------------------- block table
-
 // Rows {global_cell, offset_in_cell, count, batch} (sphops/utils.cuh:295-301)
-// of the blocks starting at sorted position i < n (row rowidx[i]), zero rows
-// r in [total, max_blocks) (thread i handles position i and row i), and the
-// block count into total_out.
+// of the blocks starting at sorted position i < n (row rowidx[i]; position i
+// starts a block when rowidx[i + 1] > rowidx[i], the scan having counted its
+// flag), zero rows r in [total, max_blocks) (thread i handles position i and
+// row i), and the block count into total_out.  Cell bounds as in
+// k_permutation.
 __global__ __launch_bounds__(kThreads) void k_block_rows(const uint64_t* __restrict__ kv, uint32_t n,
                                                          const int32_t* __restrict__ bo,
                                                          const uint32_t* __restrict__ rowidx, uint32_t maxp,
@@ -385,12 +451,13 @@ __global__ __launch_bounds__(kThreads) void k_block_rows(const uint64_t* __restr
   if (i < max_blocks && i >= t) info[i] = make_int4(0, 0, 0, 0);
   if (i >= n) return;
   const uint32_t k = (uint32_t)i;
+  const uint32_t row = rowidx[k];
+  if (rowidx[k + 1] == row) return;  // not a block start
   const uint32_t key = kv_key(kv[k]);
-  const uint32_t rs = (uint32_t)bo[key];
+  const uint32_t rs = bo != nullptr ? (uint32_t)bo[key] : run_start(kv, k, key);
+  const uint32_t re = bo != nullptr ? (uint32_t)bo[key + 1] : run_end(kv, n, k, key);
   const uint32_t off = k - rs;
-  if (off % maxp != 0) return;
-  const uint32_t cnt = (uint32_t)bo[key + 1] - rs;
-  info[rowidx[k]] = make_int4((int)key, (int)off, (int)min(maxp, cnt - off), (int)(key / G));
+  info[row] = make_int4((int)key, (int)off, (int)min(maxp, re - k), (int)(key / G));
 }
 
 // ----------------------------------------------------------- bin / unbin
@@ -784,15 +851,16 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
 
   // 4. permutation (destination slot of each input particle), with the
   // block-start flags in grid mode
-  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm, bo,
-                     g.p.maxp, g.particle_mode ? nullptr : g.flags);
+  const int32_t* cell_bo = g.n_cells >= kRunSearchMinCells ? nullptr : bo;
+  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm, cell_bo, g.p.maxp,
+                     g.particle_mode ? nullptr : g.flags);
   SPHOPS_LAUNCHED();
 
   // 5. block table (grid mode)
   if (!g.particle_mode) {
     device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, g.flags + n, st);
     hipLaunchKernelGGL(k_block_rows, blocks_for(std::max<uint64_t>(n, g.max_blocks)), dim3(kThreads), 0, st,
-                       skv, n, bo, g.flags, g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n,
+                       skv, n, cell_bo, g.flags, g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n,
                        g.max_blocks, total_blocks);
     SPHOPS_LAUNCHED();
   } else if (total_blocks) {
