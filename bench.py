@@ -320,8 +320,10 @@ def measured_copy_gbs(nbytes=COPY_BYTES, reps=20):
 def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps, only=None):
     """Average duration of each native operator call on the path the step
     takes (generic entry points with the snapshot's neighbour list), by HIP
-    events on the current stream around `reps` back-to-back calls.  An
-    operator call is one packing kernel plus one pair kernel."""
+    events on the current stream around `reps` back-to-back calls.  A
+    forward call is one packing kernel plus one pair kernel; a backward call
+    reads the records its forward packed (as in the step) and is the pair
+    kernel alone."""
     import torch
     from npa_amd.sphops import _native as O
     from npa_amd.sphops.sph import _plan
@@ -355,6 +357,13 @@ def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps, only=None):
     bufs = dict(rho=torch.empty_like(rho), blur=torch.empty_like(sb), dg=torch.empty(B, N, D, device=x.device),
                 gh=torch.empty(B, N, C, D, device=x.device), gx=torch.empty_like(xb), gs=torch.empty_like(sb),
                 gr=torch.empty_like(rho))
+    # the (x, weight) records a forward packs for its backward (mass and
+    # volume weights): backward calls read them, as in the step
+    pk_m = torch.empty(B * N, 4, device=x.device)
+    pk_v = torch.empty(B * N, 4, device=x.device)
+    hg.op_forward(O.OP_DENSITY_PAIR, xb, bufs["rho"], bo, mass=m, nbr=nbr, out2=bufs["dg"], packed=pk_m)
+    hg.op_forward(O.OP_BLUR_GRADIENT_HYBRID, xb, bufs["blur"], bo, mass=m, rho=rho, state=sb, nbr=nbr,
+                  out2=bufs["gh"], packed=pk_v)
     calls = {
         "density_fwd": lambda: hg.op_forward(O.OP_DENSITY, xb, bufs["rho"], bo, mass=m, nbr=nbr),
         "density_gradient_fwd": lambda: hg.op_forward(O.OP_DENSITY_GRADIENT, xb, bufs["dg"], bo, mass=m, nbr=nbr),
@@ -363,27 +372,28 @@ def kernel_times(sp, grid, x, s, g_blur, g_hyb, g_dg, full, reps, only=None):
                                                      state=sb, nbr=nbr),
         "blur_bwd": lambda: hg.op_backward(O.OP_BLUR, xb, g_blur, bo, m, rho=rho, state=sb, grad_x=bufs["gx"],
                                            grad_state=bufs["gs"], grad_rho=bufs["gr"], dLdx=full, dLds=True,
-                                           dLdrho=full, nbr=nbr),
+                                           dLdrho=full, nbr=nbr, packed=pk_v),
         "gradient_bwd": lambda: hg.op_backward(O.OP_GRADIENT, xb, g_hyb, bo, m, rho=rho, state=sb, grad_x=bufs["gx"],
                                                grad_state=bufs["gs"], grad_rho=bufs["gr"], dLdx=full, dLds=True,
-                                               dLdrho=full, nbr=nbr),
+                                               dLdrho=full, nbr=nbr, packed=pk_v),
     }
     if full:
         calls["density_gradient_bwd"] = lambda: hg.op_backward(O.OP_DENSITY_GRADIENT, xb, g_dg, bo, m,
-                                                               grad_x=bufs["gx"], nbr=nbr)
-        calls["density_bwd"] = lambda: hg.op_backward(O.OP_DENSITY, xb, rho, bo, m, grad_x=bufs["gx"], nbr=nbr)
+                                                               grad_x=bufs["gx"], nbr=nbr, packed=pk_m)
+        calls["density_bwd"] = lambda: hg.op_backward(O.OP_DENSITY, xb, rho, bo, m, grad_x=bufs["gx"], nbr=nbr,
+                                                      packed=pk_m)
     calls["pass_a_fwd"] = lambda: hg.op_forward(O.OP_DENSITY_PAIR, xb, bufs["rho"], bo, mass=m, nbr=nbr,
                                                 out2=bufs["dg"])
     calls["pass_b_fwd"] = lambda: hg.op_forward(O.OP_BLUR_GRADIENT_HYBRID, xb, bufs["blur"], bo, mass=m, rho=rho,
                                                 state=sb, nbr=nbr, out2=bufs["gh"])
     calls["pass_a_bwd"] = lambda: hg.op_backward(O.OP_DENSITY_PAIR, xb, rho, bo, m, grad_x=bufs["gx"], nbr=nbr,
-                                                 upstream2=g_dg)
+                                                 upstream2=g_dg, packed=pk_m)
     calls["pass_b_bwd"] = lambda: hg.op_backward(O.OP_BLUR_GRADIENT_HYBRID, xb, g_blur, bo, m, rho=rho, state=sb,
                                                  grad_x=bufs["gx"], grad_state=bufs["gs"], grad_rho=bufs["gr"],
-                                                 nbr=nbr, upstream2=g_hyb)
+                                                 nbr=nbr, upstream2=g_hyb, packed=pk_v)
     calls["pass_b_bwd_ds"] = lambda: hg.op_backward(O.OP_BLUR_GRADIENT_HYBRID, xb, g_blur, bo, m, rho=rho,
                                                     state=sb, grad_state=bufs["gs"], dLdx=False, dLdrho=False,
-                                                    nbr=nbr, upstream2=g_hyb)
+                                                    nbr=nbr, upstream2=g_hyb, packed=pk_v)
     for name, fn in calls.items():
         if only is None or name == only:
             timed(name, fn)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 16
+#define SPHOPS_ABI_VERSION 17
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -220,6 +220,16 @@ typedef struct sphops_args {
   const uint32_t* nbr_waves_sparse;
   int32_t nbr_wave_count_sparse;
   const int32_t* nbr_wave_count_sparse_device;
+  /* Optional (x, y, z|0, weight) records of the call's particles, B*N
+   * 16-byte-aligned float4, with the operator's neighbour weight: the mass
+   * for DENSITY, DENSITY_GRADIENT and DENSITY_PAIR, mass / rho for BLUR,
+   * GRADIENT, GRADIENT_HYBRID, MOMENT_MATRIX and BLUR_GRADIENT_HYBRID (no
+   * reference counterpart).  With packed_valid = 0 the call writes them there
+   * instead of the grid's scratch; with packed_valid = 1 it reads them as they
+   * are, which is how a backward reuses what its forward wrote for the same
+   * x, mass and rho (one packing pass fewer).  NULL: the grid's scratch. */
+  float* packed;
+  int32_t packed_valid;
 } sphops_args;
 
 /* Forward operator `op` (SPHOPS_OP_*) on binned particles. */

@@ -571,6 +571,8 @@ static OpPtrs from_args(const sphops_args* a) {
   p.waves_sparse = reinterpret_cast<const uint2*>(a->nbr_waves_sparse);
   p.nwaves_sparse = (uint32_t)std::max(a->nbr_wave_count_sparse, 0);
   p.nwaves_sparse_dev = a->nbr_wave_count_sparse_device;
+  p.xw_buf = reinterpret_cast<float4*>(a->packed);
+  p.xw_ready = a->packed_valid != 0;
   return p;
 }
 
@@ -590,6 +592,8 @@ static void check_list(const sphops_args* a) {
                      a->nbr_waves_sparse != nullptr && a->nbr_waves_split != nullptr),
           "tile_units needs tile_unit_count, nbr_order_sparse, nbr_waves_sparse and the split schedule");
   require(a->nbr_wave_count_sparse >= 0, "negative wave count");
+  require(a->packed == nullptr || sphops::pk::aligned16(a->packed), "packed must be 16-byte aligned");
+  require(a->packed_valid == 0 || a->packed != nullptr, "packed_valid needs packed");
 }
 
 int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream) {

@@ -2092,13 +2092,21 @@ namespace pk {
 
 inline dim3 grid_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) / kThreads)); }
 
+// The (x, weight) records the pair kernels read: packed into the caller's
+// buffer (or the grid's scratch), or the caller's buffer as it is when it
+// already holds them (a backward reusing its forward's records).
 template <int D, class OP>
 void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
+  if (a.xw_buf != nullptr && a.xw_ready) {
+    a.xw = a.xw_buf;
+    return;
+  }
+  float4* dst = a.xw_buf != nullptr ? a.xw_buf : g.packed;
   constexpr int WK = OP::kWeightKind;
-  hipLaunchKernelGGL((k_pack<D, WK>), grid_for(g.n_keys), dim3(kThreads), 0, st, a.x, a.m, a.rho, g.packed,
+  hipLaunchKernelGGL((k_pack<D, WK>), grid_for(g.n_keys), dim3(kThreads), 0, st, a.x, a.m, a.rho, dst,
                      (uint32_t)g.n_keys);
   SPHOPS_LAUNCHED();
-  a.xw = g.packed;
+  a.xw = dst;
 }
 
 constexpr uint32_t kPersistentWorkgroups = 2048;

@@ -124,6 +124,8 @@ struct OpPtrs {
   const int32_t* ncnt = nullptr;  // list length per particle (B*N)
   const int32_t* nidx = nullptr;  // neighbour indices; non-null selects list traversal
   const float4* xw = nullptr;     // packed positions and weights (set by the launcher)
+  float4* xw_buf = nullptr;       // caller's buffer for them (null: the grid's scratch) ...
+  bool xw_ready = false;          // ... already holding this call's records
   const int32_t* order = nullptr; // particles in schedule order (optional, list traversal)
   const uint2* waves = nullptr;   // per-wave descriptors {first slot in order, group size << 8 | particles}
   uint32_t nwaves = 0;

@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -90,7 +90,8 @@ class Args(ctypes.Structure):
                 ("nbr_wave_count_split", ctypes.c_int32), ("upstream2", _p), ("out2", _p),
                 ("nbr_wave_count_device", _p), ("nbr_wave_count_split_device", _p),
                 ("tile_units", _p), ("tile_unit_count", _p), ("nbr_order_sparse", _p), ("nbr_waves_sparse", _p),
-                ("nbr_wave_count_sparse", ctypes.c_int32), ("nbr_wave_count_sparse_device", _p)]
+                ("nbr_wave_count_sparse", ctypes.c_int32), ("nbr_wave_count_sparse_device", _p),
+                ("packed", _p), ("packed_valid", ctypes.c_int32)]
 
 
 (OP_COUNT, OP_DENSITY, OP_DENSITY_GRADIENT, OP_MOMENT_MATRIX, OP_BLUR, OP_GRADIENT, OP_GRADIENT_HYBRID,

@@ -215,16 +215,28 @@ def _plan(snapshot, x_bin):
     return nbr
 
 
-def _fwd(snapshot, op, x_bin, out, mass=None, rho=None, state=None, tol=1e-3):
+def _packed_for(ctx, x_bin):
+    """A (B*N, 4) buffer for the (x, weight) records an operator's forward
+    packs, kept in ``ctx`` so that the backward reads them instead of
+    packing them again (autograd refuses a backward whose saved inputs were
+    modified in place, so the records stay those of its x, mass and rho);
+    None when no input needs a gradient."""
+    n = x_bin.shape[0] * x_bin.shape[1]
+    if n == 0 or not any(ctx.needs_input_grad):
+        return None
+    return torch.empty(n, 4, dtype=torch.float32, device=x_bin.device)
+
+
+def _fwd(snapshot, op, x_bin, out, mass=None, rho=None, state=None, tol=1e-3, packed=None):
     snapshot.grid.op_forward(op, x_bin, out, snapshot.bin_offsets, mass=mass, rho=rho, state=state, tol=tol,
-                             nbr=_plan(snapshot, x_bin))
+                             nbr=_plan(snapshot, x_bin), packed=packed)
 
 
 def _bwd(snapshot, op, x_bin, upstream, mass, rho=None, state=None, grad_x=None, grad_s=None, grad_rho=None,
-         dLdx=True, dLds=True, dLdrho=True, upstream2=None):
+         dLdx=True, dLds=True, dLdrho=True, upstream2=None, packed=None):
     snapshot.grid.op_backward(op, x_bin, _c(upstream), snapshot.bin_offsets, mass, rho=rho, state=state,
                               grad_x=grad_x, grad_state=grad_s, grad_rho=grad_rho, dLdx=dLdx, dLds=dLds,
-                              dLdrho=dLdrho, nbr=_plan(snapshot, x_bin), upstream2=upstream2)
+                              dLdrho=dLdrho, nbr=_plan(snapshot, x_bin), upstream2=upstream2, packed=packed)
 
 
 class Count(torch.autograd.Function):
@@ -248,7 +260,8 @@ class Density(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, mass, snapshot):
         rho = torch.empty(x_bin.shape[:-1], dtype=torch.float32, device=x_bin.device)
-        _fwd(snapshot, _OP.OP_DENSITY, x_bin, rho, mass=mass)
+        ctx.packed = _packed_for(ctx, x_bin)
+        _fwd(snapshot, _OP.OP_DENSITY, x_bin, rho, mass=mass, packed=ctx.packed)
         ctx.save_for_backward(x_bin, mass)
         ctx.snapshot = snapshot
         ctx.dLdx = x_bin.requires_grad
@@ -260,7 +273,7 @@ class Density(torch.autograd.Function):
             return None, None, None
         x_bin, mass = ctx.saved_tensors
         grad_x = torch.empty_like(x_bin)
-        _bwd(ctx.snapshot, _OP.OP_DENSITY, x_bin, grad_output, mass, grad_x=grad_x)
+        _bwd(ctx.snapshot, _OP.OP_DENSITY, x_bin, grad_output, mass, grad_x=grad_x, packed=ctx.packed)
         return grad_x, None, None
 
 
@@ -273,7 +286,8 @@ class Blur(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, s_bin, rho, mass, snapshot):
         s_blur = torch.empty_like(s_bin)
-        _fwd(snapshot, _OP.OP_BLUR, x_bin, s_blur, mass=mass, rho=rho, state=s_bin)
+        ctx.packed = _packed_for(ctx, x_bin)
+        _fwd(snapshot, _OP.OP_BLUR, x_bin, s_blur, mass=mass, rho=rho, state=s_bin, packed=ctx.packed)
         ctx.save_for_backward(x_bin, s_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
@@ -292,7 +306,7 @@ def _state_backward(ctx, op, grad_output, grad_output2=None):
     grad_rho = None if ds_only else torch.empty_like(rho)
     _bwd(ctx.snapshot, op, x_bin, grad_output, mass, rho=rho, state=s_bin, grad_x=grad_x, grad_s=grad_s,
          grad_rho=grad_rho, dLdx=ctx.dLdx, dLds=ctx.dLds, dLdrho=ctx.dLdrho,
-         upstream2=None if grad_output2 is None else _c(grad_output2))
+         upstream2=None if grad_output2 is None else _c(grad_output2), packed=ctx.packed)
     return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
             grad_rho if ctx.dLdrho else None, None, None)
 
@@ -306,7 +320,8 @@ class Gradient(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, s_bin, rho, mass, snapshot):
         grad_s = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
-        _fwd(snapshot, _OP.OP_GRADIENT, x_bin, grad_s, mass=mass, rho=rho, state=s_bin)
+        ctx.packed = _packed_for(ctx, x_bin)
+        _fwd(snapshot, _OP.OP_GRADIENT, x_bin, grad_s, mass=mass, rho=rho, state=s_bin, packed=ctx.packed)
         ctx.save_for_backward(x_bin, s_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
@@ -326,7 +341,8 @@ class DensityGradient(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, mass, snapshot):
         out = torch.empty(*x_bin.shape[:-1], snapshot.dim, dtype=torch.float32, device=x_bin.device)
-        _fwd(snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, out, mass=mass)
+        ctx.packed = _packed_for(ctx, x_bin)
+        _fwd(snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, out, mass=mass, packed=ctx.packed)
         ctx.save_for_backward(x_bin, mass)
         ctx.snapshot = snapshot
         ctx.dLdx = x_bin.requires_grad
@@ -338,7 +354,7 @@ class DensityGradient(torch.autograd.Function):
             return None, None, None
         x_bin, mass = ctx.saved_tensors
         grad_x = torch.empty_like(x_bin)
-        _bwd(ctx.snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, grad_output, mass, grad_x=grad_x)
+        _bwd(ctx.snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, grad_output, mass, grad_x=grad_x, packed=ctx.packed)
         return grad_x, None, None
 
 
@@ -352,7 +368,8 @@ class MomentMatrix(torch.autograd.Function):
     def forward(ctx, x_bin, rho, mass, snapshot):
         D = snapshot.dim
         M = torch.empty(*x_bin.shape[:-1], D, D, dtype=torch.float32, device=x_bin.device)
-        _fwd(snapshot, _OP.OP_MOMENT_MATRIX, x_bin, M, mass=mass, rho=rho)
+        ctx.packed = _packed_for(ctx, x_bin)
+        _fwd(snapshot, _OP.OP_MOMENT_MATRIX, x_bin, M, mass=mass, rho=rho, packed=ctx.packed)
         ctx.save_for_backward(x_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLdrho = x_bin.requires_grad, rho.requires_grad
@@ -364,7 +381,7 @@ class MomentMatrix(torch.autograd.Function):
         grad_x = torch.empty_like(x_bin)
         grad_rho = torch.empty_like(rho)
         _bwd(ctx.snapshot, _OP.OP_MOMENT_MATRIX, x_bin, grad_output, mass, rho=rho, grad_x=grad_x,
-             grad_rho=grad_rho, dLdx=ctx.dLdx, dLdrho=ctx.dLdrho)
+             grad_rho=grad_rho, dLdx=ctx.dLdx, dLdrho=ctx.dLdrho, packed=ctx.packed)
         return grad_x if ctx.dLdx else None, grad_rho if ctx.dLdrho else None, None, None
 
 
@@ -390,7 +407,9 @@ class GradientHybrid(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x_bin, s_bin, rho, mass, snapshot, tol):
         out = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
-        _fwd(snapshot, _OP.OP_GRADIENT_HYBRID, x_bin, out, mass=mass, rho=rho, state=s_bin, tol=tol)
+        ctx.packed = _packed_for(ctx, x_bin)
+        _fwd(snapshot, _OP.OP_GRADIENT_HYBRID, x_bin, out, mass=mass, rho=rho, state=s_bin, tol=tol,
+             packed=ctx.packed)
         ctx.save_for_backward(x_bin, s_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad
@@ -428,8 +447,9 @@ class DensityPair(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         rho = torch.empty(x_bin.shape[:-1], dtype=torch.float32, device=x_bin.device)
         grad_rho = torch.empty(*x_bin.shape[:-1], snapshot.dim, dtype=torch.float32, device=x_bin.device)
+        ctx.packed = _packed_for(ctx, x_bin)
         snapshot.grid.op_forward(_OP.OP_DENSITY_PAIR, x_bin, rho, snapshot.bin_offsets, mass=mass,
-                                 nbr=_plan(snapshot, x_bin), out2=grad_rho)
+                                 nbr=_plan(snapshot, x_bin), out2=grad_rho, packed=ctx.packed)
         ctx.save_for_backward(x_bin, mass)
         ctx.snapshot = snapshot
         ctx.dLdx = x_bin.requires_grad
@@ -442,12 +462,13 @@ class DensityPair(torch.autograd.Function):
         x_bin, mass = ctx.saved_tensors
         grad_x = torch.empty_like(x_bin)
         if g_grad_rho is None:
-            _bwd(ctx.snapshot, _OP.OP_DENSITY, x_bin, g_rho, mass, grad_x=grad_x)
+            _bwd(ctx.snapshot, _OP.OP_DENSITY, x_bin, g_rho, mass, grad_x=grad_x, packed=ctx.packed)
         elif g_rho is None:
-            _bwd(ctx.snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, g_grad_rho, mass, grad_x=grad_x)
+            _bwd(ctx.snapshot, _OP.OP_DENSITY_GRADIENT, x_bin, g_grad_rho, mass, grad_x=grad_x, packed=ctx.packed)
         else:
             ctx.snapshot.grid.op_backward(_OP.OP_DENSITY_PAIR, x_bin, _c(g_rho), ctx.snapshot.bin_offsets, mass,
-                                          grad_x=grad_x, nbr=_plan(ctx.snapshot, x_bin), upstream2=_c(g_grad_rho))
+                                          grad_x=grad_x, nbr=_plan(ctx.snapshot, x_bin), upstream2=_c(g_grad_rho),
+                                          packed=ctx.packed)
         return grad_x, None, None
 
 
@@ -461,8 +482,10 @@ class BlurGradientHybrid(torch.autograd.Function):
         ctx.set_materialize_grads(False)
         s_blur = torch.empty_like(s_bin)
         hyb = torch.empty(*s_bin.shape, snapshot.dim, dtype=torch.float32, device=x_bin.device)
+        ctx.packed = _packed_for(ctx, x_bin)
         snapshot.grid.op_forward(_OP.OP_BLUR_GRADIENT_HYBRID, x_bin, s_blur, snapshot.bin_offsets, mass=mass,
-                                 rho=rho, state=s_bin, tol=tol, nbr=_plan(snapshot, x_bin), out2=hyb)
+                                 rho=rho, state=s_bin, tol=tol, nbr=_plan(snapshot, x_bin), out2=hyb,
+                                 packed=ctx.packed)
         ctx.save_for_backward(x_bin, s_bin, rho, mass)
         ctx.snapshot = snapshot
         ctx.dLdx, ctx.dLds, ctx.dLdrho = x_bin.requires_grad, s_bin.requires_grad, rho.requires_grad

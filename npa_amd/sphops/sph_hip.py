@@ -550,9 +550,12 @@ class _HashGridNative:
             n *= C if d == "C" else self._dim
         return n
 
-    def _args(self, op, x, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, **buffers):
+    def _args(self, op, x, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, packed=None,
+              packed_valid=False, **buffers):
         """Build ``sphops_args``; every buffer is checked for dtype, device,
-        contiguity and element count against ``op``'s output shapes."""
+        contiguity and element count against ``op``'s output shapes.
+        ``packed`` ((B*N, 4) float32) receives the operator's (x, weight)
+        records, or with ``packed_valid`` already holds them."""
         if op not in self._OUT_DIMS:
             raise RuntimeError(f"unknown operator {op}")
         a = _native.Args()
@@ -582,6 +585,15 @@ class _HashGridNative:
             if sizes[name] is None or t.numel() != sizes[name]:
                 raise RuntimeError(f"{name}: expected {sizes[name]} elements, got {t.numel()}")
             setattr(a, "out" if name == "grad_x" else name, t.data_ptr())
+        if packed is not None:
+            if (packed.dtype != _F32 or not packed.is_contiguous() or packed.device.type != "cuda"
+                    or packed.data_ptr() % 16):
+                raise TypeError("packed: expected a contiguous, 16-byte aligned float32 GPU tensor")
+            if packed.numel() != 4 * BN:
+                raise RuntimeError(f"packed: expected {4 * BN} elements, got {packed.numel()}")
+            a.packed, a.packed_valid = packed.data_ptr(), int(bool(packed_valid))
+        elif packed_valid:
+            raise RuntimeError("packed_valid needs packed")
         if nbr is not None:
             a.nbr_start, a.nbr_count, a.nbr_index = nbr[0].data_ptr(), nbr[1].data_ptr(), nbr[2].data_ptr()
             if len(nbr) > 3:
@@ -598,18 +610,24 @@ class _HashGridNative:
                 a.nbr_wave_count_sparse, a.nbr_wave_count_sparse_device = tiles[4], tiles[5].data_ptr()
         return a
 
-    def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None):
+    def op_forward(self, op, x, out, bin_offsets, mass=None, rho=None, state=None, tol=1e-3, nbr=None, out2=None,
+                   packed=None):
         """Forward of operator ``op`` (``_native.OP_*``) into ``out`` (and
-        ``out2`` for the fused codes), optionally over a neighbour list."""
-        a = self._args(op, x, bin_offsets, mass, rho, state, tol=tol, nbr=nbr, out=out, out2=out2)
+        ``out2`` for the fused codes), optionally over a neighbour list;
+        ``packed``, if given, receives the (x, weight) records for the
+        backward to reuse."""
+        a = self._args(op, x, bin_offsets, mass, rho, state, tol=tol, nbr=nbr, packed=packed, out=out, out2=out2)
         _check(_lib.sphops_forward(self._h, op, ctypes.byref(a), _stream(x)))
 
     def op_backward(self, op, x, upstream, bin_offsets, mass, rho=None, state=None, grad_x=None, grad_state=None,
-                    grad_rho=None, dLdx=True, dLds=True, dLdrho=True, nbr=None, upstream2=None):
+                    grad_rho=None, dLdx=True, dLds=True, dLdrho=True, nbr=None, upstream2=None, packed=None):
         """Backward of operator ``op``: gradients w.r.t. x, state and rho
-        written into the given buffers according to the flags."""
-        a = self._args(op, x, bin_offsets, mass, rho, state, nbr=nbr, upstream=upstream, upstream2=upstream2,
-                       grad_x=grad_x, grad_state=grad_state, grad_rho=grad_rho)
+        written into the given buffers according to the flags; ``packed``,
+        if given, holds the records the forward wrote for the same x, mass
+        and rho."""
+        a = self._args(op, x, bin_offsets, mass, rho, state, nbr=nbr, packed=packed, packed_valid=packed is not None,
+                       upstream=upstream, upstream2=upstream2, grad_x=grad_x, grad_state=grad_state,
+                       grad_rho=grad_rho)
         _check(_lib.sphops_backward(self._h, op, int(bool(dLdx)), int(bool(dLds)), int(bool(dLdrho)),
                                     ctypes.byref(a), _stream(x)))
 

@@ -1,6 +1,7 @@
-"""C-ABI contract checks of the neighbour-list fill that need a grid on the GPU:
-the fill must follow the candidates call for the same positions and
-bin_offsets, and its index buffer is limited to 2^30 entries."""
+"""C-ABI contract checks that need a grid on the GPU: the neighbour-list fill
+must follow the candidates call for the same positions and bin_offsets, and
+its index buffer is limited to 2^30 entries; a backward can reuse the
+(x, weight) records its forward packed."""
 import ctypes
 
 import numpy as np
@@ -116,3 +117,47 @@ def test_fill_after_tiles_is_refused():
     assert fill() == 0
     torch.cuda.synchronize()
     assert total.tolist() == [int(count.sum().item()), 0]
+
+
+def test_packed_records_reused_by_backward():
+    """sphops_args.packed: a forward writes its (x, weight) records there and
+    a backward given them (packed_valid) skips its own packing; its results
+    equal, bit for bit, those of a backward that packs again.  A backward
+    claiming valid records without a buffer, or a misaligned buffer, fails."""
+    import npa_amd.sphops as sp
+    from npa_amd.sphops import _native as O
+    grid, snap, xb = _setup()
+    hg = grid.hashgrid
+    B, N = xb.shape[:2]
+    C = 16
+    g = torch.Generator(device="cuda").manual_seed(3)
+    sb = torch.randn(B, N, C, device="cuda", generator=g)
+    m = torch.rand(B, N, device="cuda", generator=g) + 0.5
+    bo = snap.bin_offsets
+    from npa_amd.sphops.sph import _plan
+    nbr = _plan(snap, xb)
+    rho = torch.empty(B, N, device="cuda")
+    hg.op_forward(O.OP_DENSITY, xb, rho, bo, mass=m, nbr=nbr)
+    up1 = torch.randn(B, N, C, device="cuda", generator=g)
+    up2 = torch.randn(B, N, C, 3, device="cuda", generator=g)
+    packed = torch.empty(B * N, 4, device="cuda")
+    blur, hyb = torch.empty_like(sb), torch.empty(B, N, C, 3, device="cuda")
+    hg.op_forward(O.OP_BLUR_GRADIENT_HYBRID, xb, blur, bo, mass=m, rho=rho, state=sb, nbr=nbr, out2=hyb,
+                  packed=packed)
+
+    def bwd(pk):
+        gx, gs, gr = torch.empty_like(xb), torch.empty_like(sb), torch.empty_like(rho)
+        # the grid's scratch holds other records in between (mass-weighted)
+        hg.op_forward(O.OP_DENSITY, xb, torch.empty_like(rho), bo, mass=m, nbr=nbr)
+        hg.op_backward(O.OP_BLUR_GRADIENT_HYBRID, xb, up1, bo, m, rho=rho, state=sb, grad_x=gx, grad_state=gs,
+                       grad_rho=gr, nbr=nbr, upstream2=up2, packed=pk)
+        torch.cuda.synchronize()
+        return gx, gs, gr
+
+    for a, b in zip(bwd(packed), bwd(None)):
+        assert torch.equal(a, b)
+    with pytest.raises(RuntimeError, match="packed_valid needs packed"):
+        hg._args(O.OP_BLUR, xb, bo, m, rho, sb, packed=None, packed_valid=True)
+    bad = torch.empty(B * N * 4 + 1, device="cuda")[1:].view(B * N, 4)
+    with pytest.raises(TypeError, match="16-byte aligned"):
+        hg._args(O.OP_BLUR, xb, bo, m, rho, sb, packed=bad, packed_valid=True)
