@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 17
+#define SPHOPS_ABI_VERSION 18
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -246,8 +246,16 @@ int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLd
 /* First step of the neighbour list: the split of the fill's work (units of
  * up to 8 particles of one cell with two or more particles, which share the
  * cell's 3^D stencil, the cells the reference traverses; particles alone in
- * their cell), left in the grid's scratch for sphops_neighbor_fill. */
-int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bin_offsets, void* stream);
+ * their cell), left in the grid's scratch for sphops_neighbor_fill.  The
+ * split depends on the cell runs alone, and sphops_initialize derives it from
+ * the sorted keys as it writes bin_offsets: with split_from_initialize = 1
+ * the caller states that bin_offsets is, unmodified, what this grid's last
+ * sphops_initialize wrote, and the call then reuses that split (no kernel
+ * runs); with 0, or when the grid's scratch no longer holds that split (a
+ * later build on another bin_offsets, sphops_neighbor_tiles), it is computed
+ * from x and bin_offsets. */
+int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
+                               int split_from_initialize, void* stream);
 
 /* In-radius neighbours (pairs |r| < eps incl. self) of every binned particle,
  * in stencil order: row i is nbr_index[nbr_start[i] .. nbr_start[i] +

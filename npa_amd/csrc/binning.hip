@@ -51,43 +51,46 @@ __global__ __launch_bounds__(kThreads) void k_cell_keys(GridParams g, const floa
 
 // Exclusive scan of the 4096 values owned by one workgroup (16 consecutive
 // values per thread).  Returns the workgroup total; `vals` are replaced by
-// their exclusive prefix.
-__device__ uint32_t block_exclusive_scan(uint32_t (&v)[kItems], uint32_t* sm /*[kThreads/64]*/) {
-  uint32_t run = 0;
+// their exclusive prefix.  T: uint32_t, or uint64_t for two 32-bit counts
+// scanned together (low and high halves; neither total reaches 2^32).
+template <class T>
+__device__ T block_exclusive_scan(T (&v)[kItems], T* sm /*[kThreads/64]*/) {
+  T run = 0;
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
-    uint32_t t = v[i];
+    T t = v[i];
     v[i] = run;
     run += t;
   }
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
-  uint32_t incl = run;
+  T incl = run;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    uint32_t y = __shfl_up(incl, off, 64);
+    T y = __shfl_up(incl, off, 64);
     if (lane >= off) incl += y;
   }
   if (lane == 63) sm[wave] = incl;
   __syncthreads();
-  uint32_t wave_base = 0, total = 0;
+  T wave_base = 0, total = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) {
-    uint32_t s = sm[w];
+    T s = sm[w];
     if (w < wave) wave_base += s;
     total += s;
   }
   __syncthreads();
-  const uint32_t base = wave_base + incl - run;
+  const T base = wave_base + incl - run;
 #pragma unroll
   for (int i = 0; i < kItems; ++i) v[i] += base;
   return total;
 }
 
-__global__ __launch_bounds__(kThreads) void k_scan_reduce(const uint32_t* __restrict__ in, uint64_t n,
-                                                          uint32_t* __restrict__ partials) {
-  __shared__ uint32_t sm[kThreads / 64];
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_scan_reduce(const T* __restrict__ in, uint64_t n,
+                                                          T* __restrict__ partials) {
+  __shared__ T sm[kThreads / 64];
   const uint64_t base = (uint64_t)blockIdx.x * kTile + (uint64_t)threadIdx.x * kItems;
-  uint32_t s = 0;
+  T s = 0;
 #pragma unroll
   for (int i = 0; i < kItems; ++i)
     if (base + i < n) s += in[base + i];
@@ -97,7 +100,7 @@ __global__ __launch_bounds__(kThreads) void k_scan_reduce(const uint32_t* __rest
   if (lane == 0) sm[wave] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t t = 0;
+    T t = 0;
     for (int w = 0; w < kThreads / 64; ++w) t += sm[w];
     partials[blockIdx.x] = t;
   }
@@ -105,16 +108,16 @@ __global__ __launch_bounds__(kThreads) void k_scan_reduce(const uint32_t* __rest
 
 // Scan one tile in place-or-out, adding partials[tile] (if given).  When
 // `total_out` is non-null the grand total is stored there by the last tile.
-__global__ __launch_bounds__(kThreads) void k_scan_apply(const uint32_t* in, uint32_t* out, uint64_t n,
-                                                         const uint32_t* __restrict__ partials,
-                                                         uint32_t* total_out) {
-  __shared__ uint32_t sm[kThreads / 64];
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_scan_apply(const T* in, T* out, uint64_t n,
+                                                         const T* __restrict__ partials, T* total_out) {
+  __shared__ T sm[kThreads / 64];
   const uint64_t base = (uint64_t)blockIdx.x * kTile + (uint64_t)threadIdx.x * kItems;
-  uint32_t v[kItems];
+  T v[kItems];
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) v[i] = (base + i < n) ? in[base + i] : 0u;
-  const uint32_t tot = block_exclusive_scan(v, sm);
-  const uint32_t off = partials ? partials[blockIdx.x] : 0u;
+  for (int i = 0; i < kItems; ++i) v[i] = (base + i < n) ? in[base + i] : T(0);
+  const T tot = block_exclusive_scan<T>(v, sm);
+  const T off = partials ? partials[blockIdx.x] : T(0);
 #pragma unroll
   for (int i = 0; i < kItems; ++i)
     if (base + i < n) out[base + i] = v[i] + off;
@@ -123,27 +126,27 @@ __global__ __launch_bounds__(kThreads) void k_scan_apply(const uint32_t* in, uin
 
 // Scan one tile with its offset computed in place: the sum of partials[0 ..
 // tile), reduced by the workgroup (no separate scan of the partials).
-__global__ __launch_bounds__(kThreads) void k_scan_apply_flat(const uint32_t* in, uint32_t* out, uint64_t n,
-                                                              const uint32_t* __restrict__ partials,
-                                                              uint32_t* total_out) {
-  __shared__ uint32_t sm[kThreads / 64];
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_scan_apply_flat(const T* in, T* out, uint64_t n,
+                                                              const T* __restrict__ partials, T* total_out) {
+  __shared__ T sm[kThreads / 64];
   const uint32_t tile = blockIdx.x;
-  uint32_t pre = 0;
+  T pre = 0;
   for (uint32_t i = threadIdx.x; i < tile; i += kThreads) pre += partials[i];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) pre += __shfl_down(pre, off, 64);
   if (lane == 0) sm[wave] = pre;
   __syncthreads();
-  uint32_t off = 0;
+  T off = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) off += sm[w];
   __syncthreads();
   const uint64_t base = (uint64_t)tile * kTile + (uint64_t)threadIdx.x * kItems;
-  uint32_t v[kItems];
+  T v[kItems];
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) v[i] = (base + i < n) ? in[base + i] : 0u;
-  const uint32_t tot = block_exclusive_scan(v, sm);
+  for (int i = 0; i < kItems; ++i) v[i] = (base + i < n) ? in[base + i] : T(0);
+  const T tot = block_exclusive_scan<T>(v, sm);
 #pragma unroll
   for (int i = 0; i < kItems; ++i)
     if (base + i < n) out[base + i] = v[i] + off;
@@ -167,20 +170,46 @@ void device_exclusive_scan(const uint32_t* in, uint32_t* out, uint64_t n, uint32
   if (n == 0) return;
   const uint64_t tiles = (n + kTile - 1) / kTile;
   if (tiles == 1) {
-    hipLaunchKernelGGL(k_scan_apply, dim3(1), dim3(kThreads), 0, st, in, out, n, nullptr, total);
+    hipLaunchKernelGGL(k_scan_apply<uint32_t>, dim3(1), dim3(kThreads), 0, st, in, out, n, nullptr, total);
     SPHOPS_LAUNCHED();
     return;
   }
   uint32_t* partials = tmp;
-  hipLaunchKernelGGL(k_scan_reduce, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, n, partials);
+  hipLaunchKernelGGL(k_scan_reduce<uint32_t>, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, n, partials);
   SPHOPS_LAUNCHED();
   if (tiles <= kFlatScanTiles) {
-    hipLaunchKernelGGL(k_scan_apply_flat, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n, partials, total);
+    hipLaunchKernelGGL(k_scan_apply_flat<uint32_t>, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n,
+                       partials, total);
     SPHOPS_LAUNCHED();
     return;
   }
   device_exclusive_scan(partials, partials, tiles, tmp + tiles + kTile, nullptr, st);
-  hipLaunchKernelGGL(k_scan_apply, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n, partials, total);
+  hipLaunchKernelGGL(k_scan_apply<uint32_t>, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n, partials,
+                     total);
+  SPHOPS_LAUNCHED();
+}
+
+// The same over 64-bit words, for at most kFlatScanTiles tiles: the partial
+// sums take 2 * tiles words of `tmp` (dual_scan_fits checks both bounds).
+bool dual_scan_fits(const Grid& g, uint64_t n) {
+  const uint64_t tiles = (n + kTile - 1) / kTile;
+  return tiles <= kFlatScanTiles && 2 * tiles <= g.scan_tmp_len;
+}
+
+void device_exclusive_scan64(const uint64_t* in, uint64_t* out, uint64_t n, uint32_t* tmp, uint64_t* total,
+                             hipStream_t st) {
+  if (n == 0) return;
+  const uint64_t tiles = (n + kTile - 1) / kTile;
+  if (tiles == 1) {
+    hipLaunchKernelGGL(k_scan_apply<uint64_t>, dim3(1), dim3(kThreads), 0, st, in, out, n, nullptr, total);
+    SPHOPS_LAUNCHED();
+    return;
+  }
+  uint64_t* partials = reinterpret_cast<uint64_t*>(tmp);
+  hipLaunchKernelGGL(k_scan_reduce<uint64_t>, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, n, partials);
+  SPHOPS_LAUNCHED();
+  hipLaunchKernelGGL(k_scan_apply_flat<uint64_t>, dim3((uint32_t)tiles), dim3(kThreads), 0, st, in, out, n,
+                     partials, total);
   SPHOPS_LAUNCHED();
 }
 
@@ -413,23 +442,51 @@ __device__ __forceinline__ uint32_t run_end(const uint64_t* __restrict__ kv, uin
 // bin_offsets loads.
 constexpr uint64_t kRunSearchMinCells = 1ull << 22;
 
-// Permutation (destination slot of every input particle) and, in grid mode
-// (flags non-null), the block-start flags of the block table: sorted position
-// k starts a block when its offset in its cell is a multiple of maxp.  The
-// cell's first position from bin_offsets, or (bo null) from the sorted keys.
+// Permutation (destination slot of every input particle), in grid mode
+// (BLOCKS) the block-start flags of the block table: sorted position k starts
+// a block when its offset in its cell is a multiple of maxp; and with UNITS
+// the work split of the neighbour-list fill, which depends on the cell runs
+// alone: unit_len[k] = particles of the unit starting at k (a run of up to
+// kUnitParticles particles of a cell with two or more, starting at a
+// multiple of kUnitParticles in the cell), 0 for the other particles of such
+// a cell, -1 for a particle alone in its cell; the unit-start flag is 1
+// where unit_len > 0.  Flags go to flags64 (block flag in the low half, unit
+// flag in the high half) when both are made, else to flags32.  The cell's
+// first position comes from bin_offsets or, with bo null, from the sorted
+// keys.
+template <bool BLOCKS, bool UNITS>
 __global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __restrict__ kv, uint32_t n,
                                                           uint32_t N, int32_t* __restrict__ perm,
                                                           const int32_t* __restrict__ bo, uint32_t maxp,
-                                                          uint32_t* __restrict__ flags) {
+                                                          uint32_t* __restrict__ flags32,
+                                                          uint64_t* __restrict__ flags64,
+                                                          int32_t* __restrict__ unit_len) {
   const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
   if (k >= n) return;
   const uint64_t w = kv[k];
   const uint32_t src = kv_val(w);
   perm[src] = (int32_t)(k - (src / N) * N);
-  if (flags != nullptr) {
+  if constexpr (BLOCKS || UNITS) {
     const uint32_t key = kv_key(w);
     const uint32_t rs = bo != nullptr ? (uint32_t)bo[key] : run_start(kv, k, key);
-    flags[k] = ((k - rs) % maxp == 0) ? 1u : 0u;
+    const uint32_t bf = BLOCKS && (k - rs) % maxp == 0 ? 1u : 0u;
+    uint32_t uf = 0;
+    if constexpr (UNITS) {
+      const bool alone = k == rs && (k + 1 == n || kv_key(kv[k + 1]) != key);
+      int32_t ul = -1;
+      if (!alone) {
+        ul = 0;
+        if ((k - rs) % (uint32_t)kUnitParticles == 0) {
+          uint32_t len = 1;
+          while (len < (uint32_t)kUnitParticles && k + len < n && kv_key(kv[k + len]) == key) ++len;
+          ul = (int32_t)len;
+          uf = 1;
+        }
+      }
+      unit_len[k] = ul;
+    }
+    if constexpr (BLOCKS && UNITS) flags64[k] = (uint64_t)bf | ((uint64_t)uf << 32);
+    else flags32[k] = BLOCKS ? bf : uf;
   }
 }
 
@@ -438,21 +495,41 @@ __global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __rest
 // starts a block when rowidx[i + 1] > rowidx[i], the scan having counted its
 // flag), zero rows r in [total, max_blocks) (thread i handles position i and
 // row i), and the block count into total_out.  Cell bounds as in
-// k_permutation.
+// k_permutation.  With UNITS the scan is the two-count one of k_permutation
+// (rowidx the low halves, unit slots the high halves, n + 1 words with the
+// totals last): the fill's units are written too, units[slot] = {k,
+// unit_len[k]}, and their number into unit_total.
+template <bool UNITS>
 __global__ __launch_bounds__(kThreads) void k_block_rows(const uint64_t* __restrict__ kv, uint32_t n,
                                                          const int32_t* __restrict__ bo,
-                                                         const uint32_t* __restrict__ rowidx, uint32_t maxp,
+                                                         const uint32_t* __restrict__ rowidx32,
+                                                         const uint64_t* __restrict__ scan64, uint32_t maxp,
                                                          uint32_t G, int4* __restrict__ info,
-                                                         const uint32_t* __restrict__ total, uint64_t max_blocks,
-                                                         int32_t* __restrict__ total_out) {
+                                                         const uint32_t* __restrict__ total32, uint64_t max_blocks,
+                                                         int32_t* __restrict__ total_out,
+                                                         const int32_t* __restrict__ unit_len,
+                                                         uint2* __restrict__ units, int32_t* __restrict__ unit_total) {
   const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  const uint32_t t = *total;
-  if (i == 0 && total_out) *total_out = (int32_t)t;
+  const uint32_t t = UNITS ? (uint32_t)scan64[n] : *total32;
+  if (i == 0) {
+    if (total_out) *total_out = (int32_t)t;
+    if constexpr (UNITS) *unit_total = (int32_t)(scan64[n] >> 32);
+  }
   if (i < max_blocks && i >= t) info[i] = make_int4(0, 0, 0, 0);
   if (i >= n) return;
   const uint32_t k = (uint32_t)i;
-  const uint32_t row = rowidx[k];
-  if (rowidx[k + 1] == row) return;  // not a block start
+  uint32_t row, next;
+  if constexpr (UNITS) {
+    const uint64_t sk = scan64[k];
+    const int32_t ul = unit_len[k];
+    if (ul > 0) units[(uint32_t)(sk >> 32)] = make_uint2(k, (uint32_t)ul);
+    row = (uint32_t)sk;
+    next = (uint32_t)scan64[k + 1];
+  } else {
+    row = rowidx32[k];
+    next = rowidx32[k + 1];
+  }
+  if (next == row) return;  // not a block start
   const uint32_t key = kv_key(kv[k]);
   const uint32_t rs = bo != nullptr ? (uint32_t)bo[key] : run_start(kv, k, key);
   const uint32_t re = bo != nullptr ? (uint32_t)bo[key + 1] : run_end(kv, n, k, key);
@@ -850,22 +927,52 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   SPHOPS_LAUNCHED();
 
   // 4. permutation (destination slot of each input particle), with the
-  // block-start flags in grid mode
+  // block-start flags in grid mode and, when the grid has the fill's
+  // buffers, the fill's work split (unit_len, the units and their count)
   const int32_t* cell_bo = g.n_cells >= kRunSearchMinCells ? nullptr : bo;
-  hipLaunchKernelGGL(k_permutation, blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm, cell_bo, g.p.maxp,
-                     g.particle_mode ? nullptr : g.flags);
+  const bool units = g.unit_len != nullptr && g.units != nullptr && g.unit_total != nullptr;
+  const bool dual = units && !g.particle_mode && dual_scan_fits(g, n);
+  uint64_t* f64 = g.kv[cur ^ 1];  // free after the sort; n + 1 words
+#define SPHOPS_PERM(BL, UN, F32, F64)                                                                          \
+  hipLaunchKernelGGL((k_permutation<BL, UN>), blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm, cell_bo, \
+                     g.p.maxp, F32, F64, UN ? g.unit_len : nullptr)
+  if (g.particle_mode) {
+    if (units) SPHOPS_PERM(false, true, g.flags, nullptr);
+    else SPHOPS_PERM(false, false, nullptr, nullptr);
+  } else {
+    if (dual) SPHOPS_PERM(true, true, nullptr, f64);
+    else SPHOPS_PERM(true, false, g.flags, nullptr);
+  }
+#undef SPHOPS_PERM
   SPHOPS_LAUNCHED();
 
-  // 5. block table (grid mode)
+  // 5. block table (grid mode) and the fill's units
   if (!g.particle_mode) {
-    device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, g.flags + n, st);
-    hipLaunchKernelGGL(k_block_rows, blocks_for(std::max<uint64_t>(n, g.max_blocks)), dim3(kThreads), 0, st,
-                       skv, n, cell_bo, g.flags, g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n,
-                       g.max_blocks, total_blocks);
+    const dim3 rows_grid = blocks_for(std::max<uint64_t>(n, g.max_blocks));
+    if (dual) {
+      device_exclusive_scan64(f64, f64, n, g.scan_tmp, f64 + n, st);
+      hipLaunchKernelGGL(k_block_rows<true>, rows_grid, dim3(kThreads), 0, st, skv, n, cell_bo, nullptr, f64,
+                         g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), nullptr, g.max_blocks, total_blocks,
+                         g.unit_len, g.units, g.unit_total);
+    } else {
+      device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, g.flags + n, st);
+      hipLaunchKernelGGL(k_block_rows<false>, rows_grid, dim3(kThreads), 0, st, skv, n, cell_bo, g.flags, nullptr,
+                         g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n, g.max_blocks,
+                         total_blocks, nullptr, nullptr, nullptr);
+    }
     SPHOPS_LAUNCHED();
-  } else if (total_blocks) {
-    fill_u32(reinterpret_cast<uint32_t*>(total_blocks), 1, 0u, st);
+  } else {
+    if (units) {
+      device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, reinterpret_cast<uint32_t*>(g.unit_total), st);
+      hipLaunchKernelGGL(k_unit_write, blocks_for(n), dim3(kThreads), 0, st, g.unit_len, g.flags, n, g.units);
+      SPHOPS_LAUNCHED();
+    }
+    if (total_blocks) fill_u32(reinterpret_cast<uint32_t*>(total_blocks), 1, 0u, st);
   }
+  // the fill's work split now describes this snapshot's cell runs (and a
+  // fill prepared for an earlier snapshot must be prepared again)
+  g.split_key[0] = g.split_key[1] = nullptr;
+  g.split_bo = (units && (dual || g.particle_mode)) ? bo : nullptr;
 }
 
 void run_bin_particles(const Grid& g, const float* in_pos, const float* in_state, const float* in_mass,

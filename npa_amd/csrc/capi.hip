@@ -263,7 +263,7 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
     try {
       SPHOPS_HIP(hipGetDevice(&g->device));
       for (int i = 0; i < 2; ++i) {
-        g->kv[i] = dalloc<uint64_t>(BN);
+        g->kv[i] = dalloc<uint64_t>(BN + 1);
       }
       g->hist = dalloc<uint32_t>((uint64_t)sphops::kRadixBins * g->n_tiles);
       g->scan_tmp_len = sphops::scan_tmp_elems(sphops::scan_words(*g));
@@ -645,15 +645,22 @@ int sphops_backward(const sphops_grid* grid, int op, int dLdx, int dLds, int dLd
   }
 }
 
-int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bo, void* stream) {
+int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const int32_t* bo, int split_from_initialize,
+                               void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
     require(bo != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
     require(grid->dim == 2 || sphops::pk::aligned16(x), "3D positions must be 16-byte aligned");
     if (grid->n_keys == 0) return;
-    OpPtrs a;
-    a.x = x;
-    sphops::forward(*grid, Op::NeighbourCandidates, bo, a, sphops::as_stream(stream));
+    // the split depends on the cell runs alone: the grid still holds the one
+    // its last instantiate derived when the caller vouches for bo and no
+    // build has replaced it since
+    if (!split_from_initialize || grid->split_bo != bo) {
+      OpPtrs a;
+      a.x = x;
+      sphops::forward(*grid, Op::NeighbourCandidates, bo, a, sphops::as_stream(stream));
+      grid->split_bo = nullptr;
+    }
     grid->split_key[0] = x;
     grid->split_key[1] = bo;
   });
@@ -738,6 +745,7 @@ int sphops_neighbor_tiles(const sphops_grid* grid, const float* x, const int32_t
     // the tile build overwrote the fill's work split in the grid scratch: a
     // later fill needs sphops_neighbor_candidates again
     grid->split_key[0] = grid->split_key[1] = nullptr;
+    grid->split_bo = nullptr;
   });
 }
 
@@ -961,7 +969,7 @@ constexpr NoAllocLayout noalloc_layout(uint64_t n_keys, uint64_t n_tiles, uint64
   uint64_t at = 0;
   for (int i = 0; i < 2; ++i) {  // 64-bit words
     l.kv[i] = at;
-    at += pad_words(2 * n_keys);
+    at += pad_words(2 * (n_keys + 1));
   }
   l.hist = at;
   at += pad_words((uint64_t)sphops::kRadixBins * n_tiles);

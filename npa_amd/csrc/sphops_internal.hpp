@@ -40,7 +40,8 @@ struct Grid {
   uint64_t n_cells = 0;       // B*G
   uint64_t n_tiles = 0;       // radix tiles
   uint64_t n_chunks = 0;      // cell chunks for bin_offsets
-  // radix-sort ping-pong buffers of B*N words (cell key << 32 | particle index)
+  // radix-sort ping-pong buffers of B*N + 1 words (cell key << 32 | particle
+  // index); after the sort the free one holds instantiate's flag scan
   uint64_t* kv[2] = {nullptr, nullptr};
   uint32_t* hist = nullptr;       // 256 * n_tiles (+1)
   uint32_t* scan_tmp = nullptr;   // partial sums for device scans
@@ -57,6 +58,10 @@ struct Grid {
   // (positions, bin_offsets) of the last neighbour_candidates call: the fill
   // reads the work split and ranges that call left and must get the same
   mutable const void* split_key[2] = {nullptr, nullptr};
+  // bin_offsets written by the last instantiate when the work split
+  // (unit_len, units, unit_total) still holds what that call derived from the
+  // sorted keys; null once a build has replaced it
+  mutable const int32_t* split_bo = nullptr;
 };
 
 // binning.hip

@@ -18,6 +18,7 @@ returns without synchronising.
 """
 import ctypes
 import os
+import weakref
 
 import torch
 
@@ -223,6 +224,9 @@ class _HashGridNative:
         if total_blocks is not None:
             tb = _arr(total_blocks, "total_blocks", _I32, 1)
         _check(_lib.sphops_initialize(self._h, x, pm, bo, bi, tb, _stream(positions)))
+        # the library derived the list fill's work split from the same sorted
+        # keys; a list built on this very tensor, unmodified, reuses it
+        self._split_source = (weakref.ref(bin_offsets), bin_offsets._version)
 
     def bin_particles(self, input_positions, input_state, input_mass, permutation, output_positions,
                       output_state, output_mass):
@@ -402,7 +406,9 @@ class _HashGridNative:
         cap = self._capacity(n)
         index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
         tiles = self._tile_buffers(dev, n, wcap) if self.tiles_enabled else None
-        _check(_lib.sphops_neighbor_candidates(self._h, x, bo, st))
+        src = getattr(self, "_split_source", None)
+        reuse = src is not None and src[0]() is bin_offsets and bin_offsets._version == src[1]
+        _check(_lib.sphops_neighbor_candidates(self._h, x, bo, 1 if reuse else 0, st))
         _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
                                          ctypes.c_void_p(index.data_ptr()), cap, ctypes.c_void_p(count.data_ptr()),
                                          ctypes.c_void_p(small.data_ptr()), st))

@@ -35,7 +35,7 @@ def test_fill_follows_candidates():
     total = torch.zeros(2, dtype=torch.int64, device="cuda")  # pairs found, pairs not stored
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     xp, bp = ctypes.c_void_p(xb.data_ptr()), ctypes.c_void_p(snap.bin_offsets.data_ptr())
-    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, st))
+    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, 0, st))
     cap = 300 * 300
     index = torch.empty(cap, dtype=torch.int32, device="cuda")
 
@@ -107,16 +107,84 @@ def test_fill_after_tiles_is_refused():
     def fill():
         return lib.sphops_neighbor_fill(hg._h, xp, bp, p(start), p(index), cap, p(count), p(total), st)
 
-    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, st))
+    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, 1, st))
     assert fill() == 0
     _native.check(lib.sphops_neighbor_tiles(hg._h, xp, bp, p(count), p(units), p(counts), p(order), p(waves),
                                             p(counts, 4), st))
     assert fill() != 0
     assert b"must follow" in lib.sphops_last_error()
-    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, st))
+    # the tile build replaced the split instantiate derived: vouching for
+    # bin_offsets no longer skips the work, and the fill is complete
+    _native.check(lib.sphops_neighbor_candidates(hg._h, xp, bp, 1, st))
     assert fill() == 0
     torch.cuda.synchronize()
     assert total.tolist() == [int(count.sum().item()), 0]
+    ref = hg.neighbor_list(xb, snap.bin_offsets)
+    torch.cuda.synchronize()
+    stored = ref[1] >= 0
+    assert torch.equal(ref[1][stored], count[stored])
+
+
+def _rows(start, count, index):
+    """Rows of a list; None for a row that was not stored."""
+    s, c, idx = start.cpu().numpy(), count.cpu().numpy(), index.cpu().numpy()
+    return [idx[s[k]:s[k] + c[k]].tolist() if c[k] >= 0 else None for k in range(len(c))]
+
+
+def _same_stored(rows, ref):
+    assert len(rows) == len(ref)
+    assert all(r is None or r == q for r, q in zip(rows, ref))
+
+
+@pytest.mark.parametrize("mode", ["grid", "particle"])
+def test_split_from_initialize(mode):
+    """sphops_initialize derives the fill's work split from the sorted keys;
+    a candidates call that vouches for the bin_offsets that call wrote
+    reuses it, and the rows equal those of a split computed from the
+    positions.  After another snapshot on the same grid the older
+    bin_offsets no longer matches, and the split is computed again (the
+    Python layer vouches only for the tensor the last initialize wrote)."""
+    import npa_amd.sphops as sp
+    from npa_amd.sphops import _native
+    lib = _native.lib
+    c = H.random_case("split3d", 2, 400, 4, 3, 8, 0.25, False, mode, uniform=False, sigma=0.2)
+    grid = sp.HashGrid(dim=3, boundary="clamped", mode=mode, grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    hg = grid.hashgrid
+    n = c.B * c.N
+    i32 = dict(dtype=torch.int32, device="cuda")
+    cap = n * n
+    bufs = [(torch.empty(n, **i32), torch.empty(n, **i32), torch.empty(cap, **i32)) for _ in range(2)]
+    total = torch.zeros(2, dtype=torch.int64, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def build(xb, bo, vouch, out):
+        start, count, index = out
+        _native.check(lib.sphops_neighbor_candidates(hg._h, p(xb), p(bo), vouch, st))
+        _native.check(lib.sphops_neighbor_fill(hg._h, p(xb), p(bo), p(start), p(index), cap, p(count), p(total),
+                                               st))
+        torch.cuda.synchronize()
+        assert int(total[1].item()) == 0
+        return _rows(start, count, index)
+
+    x1 = torch.from_numpy(c.x).cuda()
+    snap1 = grid.instantiate(x1)
+    xb1 = sp.bin_particles(x1, torch.zeros(c.B, c.N, 4, device="cuda"), snap1)[0].contiguous()
+    reused = build(xb1, snap1.bin_offsets, 1, bufs[0])
+    computed = build(xb1, snap1.bin_offsets, 0, bufs[1])
+    assert reused == computed
+    # a second snapshot (other positions) on the same grid
+    x2 = x1.flip(1).contiguous() * 0.9
+    snap2 = grid.instantiate(x2)
+    xb2 = sp.bin_particles(x2, torch.zeros(c.B, c.N, 4, device="cuda"), snap2)[0].contiguous()
+    assert build(xb1, snap1.bin_offsets, 1, bufs[0]) == computed
+    second = build(xb2, snap2.bin_offsets, 0, bufs[1])
+    plan1 = hg.neighbor_list(xb1, snap1.bin_offsets)
+    plan2 = hg.neighbor_list(xb2, snap2.bin_offsets)
+    torch.cuda.synchronize()
+    _same_stored(_rows(plan1[0], plan1[1], plan1[2]), computed)
+    _same_stored(_rows(plan2[0], plan2[1], plan2[2]), second)
 
 
 def test_packed_records_reused_by_backward():
