@@ -661,40 +661,83 @@ __global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restr
   if (threadIdx.x < kNumClasses) cnt[blockIdx.x * kNumClasses + threadIdx.x] = h[threadIdx.x];
 }
 
-// Stable scatter of a tile's items into order, class by class.  The tile
-// first finds its segment offsets (segment s = tile * kNumClasses + class,
-// in tile-major order): the sum of the counts of all earlier tiles, reduced
-// by the workgroup, plus the tile's own earlier classes; it writes them to
-// seg (and the last tile the item total to seg[nseg]).  Same tile walk as the
-// radix scatter: wave w owns items [w*1024, (w+1)*1024) in index order;
-// three ballots identify lanes of the same class.
+// Waves of a segment of c items at g lanes per item (64 / g items a wave).
+__device__ __forceinline__ uint32_t seg_waves(uint32_t c, int32_t g) {
+  const uint32_t per = (uint32_t)(kWave / g);
+  return (c + per - 1) / per;
+}
+
+// Stable scatter of a tile's items into order, class by class, and the wave
+// descriptors of the tile's segments.  The tile first finds its segment
+// offsets (segment s = tile * kNumClasses + class, in tile-major order): the
+// sum of the counts of all earlier tiles, reduced by the workgroup, plus the
+// tile's own earlier classes; it writes them to seg (and the last tile the
+// item total to seg[nseg]).  The same reduction gives the first wave of each
+// of its segments in the descriptor table of each group-size table (the
+// waves of all earlier segments), and the last tile writes the tables' wave
+// totals.  Same tile walk as the radix scatter: wave w owns items
+// [w*1024, (w+1)*1024) in index order; three ballots identify lanes of the
+// same class.  Descriptor {first slot in order, group size << 8 | items}:
+// one per 64-lane wave of a segment.
 template <bool CSR>
 __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __restrict__ src, uint32_t n,
                                                             ClassBounds cb, const uint32_t* __restrict__ cnt,
                                                             uint32_t* __restrict__ seg,
-                                                            int32_t* __restrict__ order) {
+                                                            int32_t* __restrict__ order, GroupSizes gs1,
+                                                            GroupSizes gs2, int tables, uint2* __restrict__ waves1,
+                                                            uint2* __restrict__ waves2,
+                                                            int32_t* __restrict__ total1,
+                                                            int32_t* __restrict__ total2) {
   __shared__ uint32_t wcnt[kThreads / 64][kNumClasses];
-  __shared__ uint32_t gbase[kNumClasses];
-  __shared__ uint32_t part[kThreads / 64];
+  __shared__ uint32_t gbase[kNumClasses], gcnt[kNumClasses];
+  __shared__ uint32_t wbase[2][kNumClasses];
+  __shared__ uint32_t part[3][kThreads / 64];
   const int wave = threadIdx.x >> 6, lane = __lane_id();
   if (threadIdx.x < (kThreads / 64) * kNumClasses) (&wcnt[0][0])[threadIdx.x] = 0;
   {
     const uint32_t before = blockIdx.x * (uint32_t)kNumClasses;
-    uint32_t s = 0;
-    for (uint32_t i = threadIdx.x; i < before; i += kThreads) s += cnt[i];
+    uint32_t s = 0, w1 = 0, w2 = 0;
+    for (uint32_t i = threadIdx.x; i < before; i += kThreads) {
+      const uint32_t c = cnt[i];
+      s += c;
+      w1 += seg_waves(c, gs1.g[i % kNumClasses]);
+      if (tables == 2) w2 += seg_waves(c, gs2.g[i % kNumClasses]);
+    }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
-    if (lane == 0) part[wave] = s;
+    for (int off = 32; off > 0; off >>= 1) {
+      s += __shfl_down(s, off, 64);
+      w1 += __shfl_down(w1, off, 64);
+      w2 += __shfl_down(w2, off, 64);
+    }
+    if (lane == 0) {
+      part[0][wave] = s;
+      part[1][wave] = w1;
+      part[2][wave] = w2;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-      uint32_t run = 0;
-      for (int w = 0; w < kThreads / 64; ++w) run += part[w];
-      for (int q = 0; q < kNumClasses; ++q) {
-        gbase[q] = run;
-        seg[before + q] = run;
-        run += cnt[before + q];
+      uint32_t run = 0, r1 = 0, r2 = 0;
+      for (int w = 0; w < kThreads / 64; ++w) {
+        run += part[0][w];
+        r1 += part[1][w];
+        r2 += part[2][w];
       }
-      if (blockIdx.x == gridDim.x - 1) seg[before + kNumClasses] = run;
+      for (int q = 0; q < kNumClasses; ++q) {
+        const uint32_t c = cnt[before + q];
+        gbase[q] = run;
+        gcnt[q] = c;
+        seg[before + q] = run;
+        run += c;
+        wbase[0][q] = r1;
+        r1 += seg_waves(c, gs1.g[q]);
+        wbase[1][q] = r2;
+        if (tables == 2) r2 += seg_waves(c, gs2.g[q]);
+      }
+      if (blockIdx.x == gridDim.x - 1) {
+        seg[before + kNumClasses] = run;
+        *total1 = (int32_t)r1;
+        if (tables == 2) *total2 = (int32_t)r2;
+      }
     }
   }
   __syncthreads();
@@ -734,81 +777,17 @@ __global__ __launch_bounds__(kThreads) void k_class_scatter(const int32_t* __res
     const uint32_t idx = base + t * 64 + lane;
     if (idx < n && item_length<CSR>(src, idx) >= 0) order[gbase[cls[t]] + wcnt[wave][cls[t]] + rank[t]] = (int32_t)idx;
   }
-}
-
-// Waves per segment for one or two group-size tables, scanned into the first
-// wave of every segment (wstart[table * nseg + s]) and the tables' wave totals,
-// by one workgroup (chunks of kThreads * 8 segments with a running carry).
-__global__ __launch_bounds__(kThreads) void k_wave_tables(const uint32_t* __restrict__ seg, uint32_t nseg,
-                                                          GroupSizes gs1, GroupSizes gs2, int tables,
-                                                          uint32_t* __restrict__ wstart,
-                                                          int32_t* __restrict__ total1,
-                                                          int32_t* __restrict__ total2) {
-  __shared__ uint32_t part[kThreads / 64];
-  const int lane = __lane_id(), wave = threadIdx.x >> 6;
-  constexpr uint32_t kPer = 8;
+  // the descriptors of the tile's segments, table by table
   for (int tb = 0; tb < tables; ++tb) {
     const GroupSizes& gs = tb == 0 ? gs1 : gs2;
-    uint32_t carry = 0;
-    for (uint32_t c0 = 0; c0 < nseg; c0 += kThreads * kPer) {
-      const uint32_t s0 = c0 + threadIdx.x * kPer;
-      uint32_t v[kPer], run = 0;
+    uint2* __restrict__ waves = tb == 0 ? waves1 : waves2;
 #pragma unroll
-      for (uint32_t i = 0; i < kPer; ++i) {
-        const uint32_t s = s0 + i;
-        uint32_t w = 0;
-        if (s < nseg) {
-          const uint32_t per = (uint32_t)(kWave / gs.g[s % kNumClasses]);
-          w = (seg[s + 1] - seg[s] + per - 1) / per;
-        }
-        v[i] = run;
-        run += w;
-      }
-      uint32_t incl = run;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
-      }
-      if (lane == 63) part[wave] = incl;
-      __syncthreads();
-      uint32_t wbase = 0, chunk = 0;
-#pragma unroll
-      for (int w = 0; w < kThreads / 64; ++w) {
-        if (w < wave) wbase += part[w];
-        chunk += part[w];
-      }
-      __syncthreads();
-      const uint32_t base = carry + wbase + incl - run;
-#pragma unroll
-      for (uint32_t i = 0; i < kPer; ++i)
-        if (s0 + i < nseg) wstart[(uint64_t)tb * nseg + s0 + i] = base + v[i];
-      carry += chunk;
-    }
-    if (threadIdx.x == 0) *(tb == 0 ? total1 : total2) = (int32_t)carry;
-  }
-}
-
-// One workgroup per (tile, table) writes the wave descriptors of its
-// segments: {first slot in order, group size << 8 | items in the wave}.
-__global__ __launch_bounds__(kThreads) void k_wave_fill(const uint32_t* __restrict__ seg, uint32_t nseg,
-                                                        const uint32_t* __restrict__ wstart_all, GroupSizes gs1,
-                                                        GroupSizes gs2, uint2* __restrict__ waves1,
-                                                        uint2* __restrict__ waves2) {
-  const uint32_t t = blockIdx.x;
-  const bool second = blockIdx.y != 0;
-  const GroupSizes& gs = second ? gs2 : gs1;
-  const uint32_t* __restrict__ wstart = wstart_all + (second ? nseg : 0u);
-  uint2* __restrict__ waves = second ? waves2 : waves1;
-#pragma unroll
-  for (uint32_t q = 0; q < (uint32_t)kNumClasses; ++q) {
-    const uint32_t s = t * kNumClasses + q;
-    const uint32_t lo = seg[s], hi = seg[s + 1];
-    const uint32_t per = (uint32_t)(kWave / gs.g[q]);
-    const uint32_t nw = (hi - lo + per - 1) / per;
-    for (uint32_t u = threadIdx.x; u < nw; u += blockDim.x) {
-      const uint32_t first = lo + u * per;
-      waves[wstart[s] + u] = make_uint2(first, ((uint32_t)gs.g[q] << 8) | min(per, hi - first));
+    for (int q = 0; q < kNumClasses; ++q) {
+      const uint32_t lo = gbase[q], c = gcnt[q];
+      const uint32_t per = (uint32_t)(kWave / gs.g[q]);
+      const uint32_t nw = (c + per - 1) / per;
+      for (uint32_t u = threadIdx.x; u < nw; u += kThreads)
+        waves[wbase[tb][q] + u] = make_uint2(lo + u * per, ((uint32_t)gs.g[q] << 8) | min(per, c - u * per));
     }
   }
 }
@@ -822,23 +801,17 @@ void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, co
   const uint32_t n = (uint32_t)g.n_keys;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
   const uint32_t nseg = (uint32_t)kNumClasses * ntiles;
-  // hist holds 256 * ntiles words: item counts per segment, their offsets
-  // (nseg + 1, the last is the number of scheduled items), then the first
-  // wave of every segment for each descriptor table
+  // hist holds 256 * ntiles words: item counts per segment, then their
+  // offsets (nseg + 1, the last is the number of scheduled items)
   uint32_t* cnt = g.hist;
   uint32_t* seg = cnt + nseg;
-  uint32_t* wstart = seg + nseg + 1;
   hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt);
-  SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, seg, order);
   SPHOPS_LAUNCHED();
   const int tables = waves2 != nullptr ? 2 : 1;  // a second table: same order, other group sizes
   const GroupSizes gsb = gs2 != nullptr ? *gs2 : gs;
-  hipLaunchKernelGGL(k_wave_tables, dim3(1), dim3(kThreads), 0, st, seg, nseg, gs, gsb, tables, wstart, wave_total,
+  hipLaunchKernelGGL((k_class_scatter<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt, seg, order, gs,
+                     gsb, tables, waves, tables == 2 ? waves2 : waves, wave_total,
                      tables == 2 ? wave_total2 : wave_total);
-  SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_wave_fill, dim3(ntiles, (uint32_t)tables), dim3(kThreads), 0, st, seg, nseg, wstart, gs, gsb,
-                     waves, tables == 2 ? waves2 : waves);
   SPHOPS_LAUNCHED();
 }
 
