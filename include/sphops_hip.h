@@ -95,7 +95,10 @@ int sphops_bin_particles(const sphops_grid* grid, const float* in_pos, const flo
                          float* out_mass, uint32_t feature_dim, void* stream);
 
 /* HashGrid::backward_bin_particles (sph_cuda.cu:2026-2056): out[b,i] = in[b, perm[b,i]]
- * (also the reference's unbin_particles, sphops/sph.py:187-198). */
+ * (also the reference's unbin_particles, sphops/sph.py:187-198).  In both
+ * directions the two mass pointers may be NULL together (no reference
+ * counterpart): the mass rows are then not moved, as for a backward whose
+ * mass needs no gradient. */
 int sphops_backward_bin_particles(const sphops_grid* grid, const float* grad_out_pos,
                                   const float* grad_out_state, const float* grad_out_mass,
                                   const int32_t* permutation, float* grad_in_pos, float* grad_in_state,

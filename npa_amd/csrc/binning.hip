@@ -541,6 +541,7 @@ __global__ __launch_bounds__(kThreads) void k_block_rows(const uint64_t* __restr
 
 // One group of `lanes` threads moves one particle row.  forward: scatter
 // in[b,i] -> out[b,perm[b,i]];  backward: gather out[b,i] = in[b,perm[b,i]].
+// Null mass pointers leave the mass rows out.
 template <int P, bool VEC4>
 __global__ __launch_bounds__(kThreads) void k_move_rows(const float* __restrict__ in_pos,
                                                         const float* __restrict__ in_state,
@@ -562,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void k_move_rows(const float* __restrict_
       reinterpret_cast<float2*>(out_pos)[dst] = reinterpret_cast<const float2*>(in_pos)[src];
     else
       reinterpret_cast<float4*>(out_pos)[dst] = reinterpret_cast<const float4*>(in_pos)[src];
-    out_mass[dst] = in_mass[src];
+    if (in_mass != nullptr) out_mass[dst] = in_mass[src];
   }
   const uint32_t lanes = 1u << lanes_log2;
   if constexpr (VEC4) {

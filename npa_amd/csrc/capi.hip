@@ -326,7 +326,8 @@ static int move_rows(const sphops_grid* grid, const float* ip, const float* is, 
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
     sphops::check_channels(C == 0 ? 1 : C);
-    require(grid->n_keys == 0 || (ip && is && im && perm && op && os && om), "null buffer");
+    require(grid->n_keys == 0 || (ip && is && perm && op && os), "null buffer");
+    require((im == nullptr) == (om == nullptr), "the mass rows are moved both or neither (both NULL)");
     sphops::run_bin_particles(*grid, ip, is, im, perm, op, os, om, C, fwd, sphops::as_stream(stream));
   });
 }

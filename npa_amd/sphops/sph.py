@@ -150,43 +150,54 @@ def _c(t):
 
 
 class Permute(torch.autograd.Function):
+    """Binning of x, s and mass (sphops/sph.py:148-175).  With mass None
+    (unit masses that the caller does not get back) the mass rows are not
+    moved, and only x_bin and s_bin are returned."""
+
     @staticmethod
     def forward(ctx, x, s, mass, snapshot):
         x_bin = torch.empty_like(x)
         s_bin = torch.empty_like(s)
-        mass_bin = torch.empty_like(mass)
+        mass_bin = None if mass is None else torch.empty_like(mass)
         snapshot.grid.bin_particles(x, s, mass, snapshot.permutation, x_bin, s_bin, mass_bin)
         ctx.snapshot = snapshot
-        ctx.x_shape, ctx.s_shape, ctx.m_shape = x.shape, s.shape, mass.shape
+        ctx.x_shape, ctx.s_shape = x.shape, s.shape
+        ctx.m_shape = None if mass is None else mass.shape
         ctx.dtype, ctx.device = x.dtype, x.device
-        ctx.dLdx, ctx.dLds, ctx.dLdm = x.requires_grad, s.requires_grad, mass.requires_grad
+        ctx.dLdx, ctx.dLds = x.requires_grad, s.requires_grad
+        ctx.dLdm = mass is not None and mass.requires_grad
+        if mass is None:
+            return x_bin, s_bin
         return x_bin, s_bin, mass_bin
 
     @staticmethod
-    def backward(ctx, dL_dx_bin, dL_ds_bin, dL_dm_bin):
+    def backward(ctx, dL_dx_bin, dL_ds_bin, dL_dm_bin=None):
         if dL_dx_bin is None:
             dL_dx_bin = torch.zeros(ctx.x_shape, dtype=ctx.dtype, device=ctx.device)
         if dL_ds_bin is None:
             dL_ds_bin = torch.zeros(ctx.s_shape, dtype=ctx.dtype, device=ctx.device)
-        if dL_dm_bin is None:
-            dL_dm_bin = torch.zeros(ctx.m_shape, dtype=ctx.dtype, device=ctx.device)
-        dL_dx_bin, dL_ds_bin, dL_dm_bin = _c(dL_dx_bin), _c(dL_ds_bin), _c(dL_dm_bin)
+        # a mass that needs no gradient moves no rows (no zeros to gather)
+        grad_m = None
+        if ctx.dLdm:
+            if dL_dm_bin is None:
+                dL_dm_bin = torch.zeros(ctx.m_shape, dtype=ctx.dtype, device=ctx.device)
+            dL_dm_bin = _c(dL_dm_bin)
+            grad_m = torch.empty_like(dL_dm_bin)
+        else:
+            dL_dm_bin = None
+        dL_dx_bin, dL_ds_bin = _c(dL_dx_bin), _c(dL_ds_bin)
         grad_x = torch.empty_like(dL_dx_bin)
         grad_s = torch.empty_like(dL_ds_bin)
-        grad_m = torch.empty_like(dL_dm_bin)
         ctx.snapshot.grid.backward_bin_particles(dL_dx_bin, dL_ds_bin, dL_dm_bin, ctx.snapshot.permutation,
                                                  grad_x, grad_s, grad_m)
-        return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None,
-                grad_m if ctx.dLdm else None, None)
+        return (grad_x if ctx.dLdx else None, grad_s if ctx.dLds else None, grad_m, None)
 
 
 def bin_particles(x, s, snapshot, mass=None):
-    mass_is_none = mass is None
+    if mass is None:  # unit masses: nothing to move (the operators default to them too)
+        return Permute.apply(x, s, None, snapshot)
     mass = _default_mass(x, mass)
-    x_bin, s_bin, mass_bin = Permute.apply(x, s, mass, snapshot)
-    if mass_is_none:
-        return x_bin, s_bin
-    return x_bin, s_bin, mass_bin
+    return Permute.apply(x, s, mass, snapshot)
 
 
 def unbin_particles(x_bin, s_bin, snapshot, mass_bin=None):

@@ -247,10 +247,14 @@ class _HashGridNative:
         _check(_lib.sphops_backward_bin_particles(self._h, *args, C, _stream(grad_output_positions)))
 
     def _move_args(self, ip, is_, im, perm, op, os_, om, C, names):
-        out = [self._pos(ip, names[0]), self._state(is_, names[1], C), self._bn(im, names[2])]
+        # the masses may be None together: their rows are not moved
+        if (im is None) != (om is None):
+            raise ValueError(f"{names[2]} and {names[6]} must both be tensors or both be None")
+        bn = lambda t, name: ctypes.c_void_p() if t is None else self._bn(t, name)
+        out = [self._pos(ip, names[0]), self._state(is_, names[1], C), bn(im, names[2])]
         out.append(_arr(perm, names[3], _I32, 2))
         _validate_shape(perm, (self._b, self._n), names[3])
-        out += [self._pos(op, names[4]), self._state(os_, names[5], C), self._bn(om, names[6])]
+        out += [self._pos(op, names[4]), self._state(os_, names[5], C), bn(om, names[6])]
         return out
 
     # ---- forward operators (sph_cuda.cu:2058-2499)

@@ -111,24 +111,48 @@ def test_wrap_positions(boundary):
         np.testing.assert_array_equal(out, ref)
 
 
-def test_permute_backward_is_a_gather():
+@pytest.mark.parametrize("mass_grad", [True, False])
+def test_permute_backward_is_a_gather(mass_grad):
     """bin_particles' backward returns upstream[b, perm[b, i]] for x, s and
-    mass (sphops/sph.py:148-175), bit for bit."""
+    mass (sphops/sph.py:148-175), bit for bit; a mass that needs no gradient
+    gets none, and its rows are not moved (both mass pointers NULL), while a
+    single NULL mass pointer is refused."""
+    import ctypes
     import npa_amd.sphops as sp
+    from npa_amd.sphops import _native
     c = H.random_case("perm", 2, 300, 5, 3, 8, 0.25, False, "grid", sigma=0.8)
     grid = sp.HashGrid(dim=3, boundary="clamped", mode="grid", grid_size=list(c.grid_size), eps=c.eps,
                        num_particles=c.N, batch_size=c.B)
-    x, s, m = (dev(a).requires_grad_(True) for a in (c.x, c.s, c.m))
+    x, s = (dev(a).requires_grad_(True) for a in (c.x, c.s))
+    m = dev(c.m).requires_grad_(mass_grad)
     snap = grid.instantiate(x.detach())
     xb, sb, mb = sp.bin_particles(x, s, snap, m)
     rng = np.random.default_rng(4)
     ux, us, um = (rng.standard_normal(t.shape).astype(np.float32) for t in (xb, sb, mb))
-    ((xb * dev(ux)).sum() + (sb * dev(us)).sum() + (mb * dev(um)).sum()).backward()
+    loss = (xb * dev(ux)).sum() + (sb * dev(us)).sum()
+    if mass_grad:
+        loss = loss + (mb * dev(um)).sum()
+    loss.backward()
     perm = snap.permutation.cpu().numpy()
     b = np.arange(c.B)[:, None]
     np.testing.assert_array_equal(x.grad.cpu().numpy(), ux[b, perm])
     np.testing.assert_array_equal(s.grad.cpu().numpy(), us[b, perm])
-    np.testing.assert_array_equal(m.grad.cpu().numpy(), um[b, perm])
+    if mass_grad:
+        np.testing.assert_array_equal(m.grad.cpu().numpy(), um[b, perm])
+    else:
+        assert m.grad is None
+        lib, hg = _native.lib, grid.hashgrid
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        gx, gs, gm = torch.empty_like(xb), torch.empty_like(sb), torch.full_like(mb, 7.0)
+        assert lib.sphops_backward_bin_particles(hg._h, p(xb), p(sb), ctypes.c_void_p(), p(snap.permutation), p(gx),
+                                                 p(gs), p(gm), 5, st) != 0
+        assert b"both or neither" in lib.sphops_last_error()
+        assert lib.sphops_backward_bin_particles(hg._h, p(xb), p(sb), ctypes.c_void_p(), p(snap.permutation), p(gx),
+                                                 p(gs), ctypes.c_void_p(), 5, st) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(gx, x.detach()) and torch.equal(gs, s.detach())
+        assert bool((gm == 7.0).all())
 
 
 @pytest.mark.parametrize("dim", [2, 3])
