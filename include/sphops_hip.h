@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 18
+#define SPHOPS_ABI_VERSION 19
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -322,6 +322,15 @@ int64_t sphops_neighbor_tile_capacity(const sphops_grid* grid);
 
 /* Number of wave descriptors nbr_waves must hold for this grid (B*N + 8 per tile of 4096). */
 int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid);
+
+/* Copy of `words` (at most 256) 32-bit words from device memory into pinned
+ * host memory allocated with hipHostMalloc (torch's pin_memory), written by
+ * one small kernel on `stream` with system-scope stores (no reference
+ * counterpart): the host reads them once an event recorded after the call
+ * has completed.  The Python layer reads the list totals back this way;
+ * unlike an asynchronous device-to-host copy it adds no copy engine
+ * dependency to the stream. */
+int sphops_copy_words_to_host(const void* device_src, void* host_dst, uint32_t words, void* stream);
 
 /* Module function safe_inv_sym_mat (sph_cuda.cu:3181-3226): `count` symmetric
  * dim x dim matrices (dim 2 or 3), identity where |det| < tol. */

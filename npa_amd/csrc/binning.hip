@@ -592,6 +592,22 @@ inline dim3 blocks_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) /
 
 }  // namespace
 
+namespace {
+// Words from device memory into (device-visible) pinned host memory, with
+// system-scope stores so that the host sees them once the kernel is done.
+__global__ __launch_bounds__(kThreads) void k_words_to_host(const uint32_t* __restrict__ src, uint32_t* dst,
+                                                            uint32_t words) {
+  const uint32_t i = threadIdx.x;
+  if (i < words) __hip_atomic_store(dst + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+}  // namespace
+
+void copy_words_to_host(const uint32_t* src, uint32_t* dst_device_view, uint32_t words, hipStream_t st) {
+  if (words == 0) return;
+  hipLaunchKernelGGL(k_words_to_host, dim3(1), dim3(kThreads), 0, st, src, dst_device_view, words);
+  SPHOPS_LAUNCHED();
+}
+
 // A fill kernel rather than hipMemsetAsync, so that a step captured in a HIP
 // graph holds no memset nodes.
 void fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t st) {

@@ -766,6 +766,18 @@ int64_t sphops_neighbor_wave_capacity(const sphops_grid* grid) {
   return (int64_t)sphops::neighbour_wave_capacity(*grid);
 }
 
+int sphops_copy_words_to_host(const void* device_src, void* host_dst, uint32_t words, void* stream) {
+  return guarded([&] {
+    require(words <= 256, "sphops_copy_words_to_host: at most 256 words");
+    if (words == 0) return;
+    require(device_src != nullptr && host_dst != nullptr, "null buffer");
+    void* dev_view = nullptr;
+    SPHOPS_HIP(hipHostGetDevicePointer(&dev_view, host_dst, 0));
+    sphops::copy_words_to_host(static_cast<const uint32_t*>(device_src), static_cast<uint32_t*>(dev_view), words,
+                               sphops::as_stream(stream));
+  });
+}
+
 int sphops_safe_inv_sym_mat(const float* in, float* out, int64_t count, int dim, float tol, void* stream) {
   return guarded([&] {
     require(dim == 2 || dim == 3, "safe_inverse only supports 2x2 or 3x3 matrices.");

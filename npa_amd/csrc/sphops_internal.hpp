@@ -209,6 +209,8 @@ constexpr GroupSizes kListGroups{{1, 1, 2, 4, 8, 16, 32, 64}};
 constexpr GroupSizes kSplitGroups{{4, 4, 4, 4, 16, 32, 64, 64}};
 void run_safe_inv(const float* in, float* out, uint64_t count, int dim, float tol, hipStream_t st);
 void fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t st);
+// words (<= 256) from device memory to pinned host memory (its device view)
+void copy_words_to_host(const uint32_t* src, uint32_t* dst_device_view, uint32_t words, hipStream_t st);
 // perceive_glue.hip: perception features of NPA.perceive (include/sphops_hip.h)
 void run_glue_forward(int dim, const float* s, const float* blur, const float* grad_s, const float* grad_rho,
                       float* z, uint64_t n, uint32_t C, float coef_s, float coef_rho, float total_mass, int flags,

@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -73,6 +73,7 @@ _SIGNATURES = {
     "sphops_forward": ([_p, _i32, _p, _p], _i32),
     "sphops_backward": ([_p, _i32, _i32, _i32, _i32, _p, _p], _i32),
     "sphops_neighbor_candidates": ([_p, _p, _p, _i32, _p], _i32),
+    "sphops_copy_words_to_host": ([_p, _p, _u32, _p], _i32),
     "sphops_neighbor_fill": ([_p, _p, _p, _p, _p, _i64, _p, _p, _p], _i32),
     "sphops_neighbor_schedule": ([_p, _p, _p, _p, _p, _p, _p, _p], _i32),
     "sphops_neighbor_tiles": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p], _i32),

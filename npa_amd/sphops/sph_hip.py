@@ -475,7 +475,10 @@ class _HashGridNative:
         rb = getattr(self, "_rb", None)
         if rb is None:
             self._rb = rb = torch.empty(8, dtype=_I32, pin_memory=True)
-        rb.copy_(small, non_blocking=True)
+        # a small kernel writes them into the pinned buffer (no copy-engine
+        # transfer on the stream)
+        _check(_lib.sphops_copy_words_to_host(ctypes.c_void_p(small.data_ptr()), ctypes.c_void_p(rb.data_ptr()), 8,
+                                              _stream(small)))
         self._rb_cap = cap
         self._rb_tiles = tiles
         self._rb_event = torch.cuda.Event()

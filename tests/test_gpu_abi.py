@@ -229,3 +229,24 @@ def test_packed_records_reused_by_backward():
     bad = torch.empty(B * N * 4 + 1, device="cuda")[1:].view(B * N, 4)
     with pytest.raises(TypeError, match="16-byte aligned"):
         hg._args(O.OP_BLUR, xb, bo, m, rho, sb, packed=bad, packed_valid=True)
+
+
+def test_copy_words_to_host():
+    """sphops_copy_words_to_host writes device words into pinned host memory
+    (the list totals' read-back), visible once the stream is synchronised;
+    more than 256 words are refused."""
+    from npa_amd.sphops import _native
+    lib = _native.lib
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    src = torch.randint(-2**31, 2**31 - 1, (256,), dtype=torch.int32, device="cuda")
+    dst = torch.zeros(256, dtype=torch.int32, pin_memory=True)
+    for words in (8, 1, 256):
+        dst.zero_()
+        _native.check(lib.sphops_copy_words_to_host(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                                                    words, st))
+        torch.cuda.synchronize()
+        assert torch.equal(dst[:words], src[:words].cpu())
+        assert not bool(dst[words:].any())
+    assert lib.sphops_copy_words_to_host(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), 257,
+                                         st) != 0
+    assert b"at most 256" in lib.sphops_last_error()
