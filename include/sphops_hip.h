@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 19
+#define SPHOPS_ABI_VERSION 20
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -233,6 +233,16 @@ typedef struct sphops_args {
    * x, mass and rho (one packing pass fewer).  NULL: the grid's scratch. */
   float* packed;
   int32_t packed_valid;
+  /* Optional cell tiles from sphops_neighbor_fill_tiled (no reference
+   * counterpart; all three or none): the own-cell entry counts, the cell
+   * table ({first particle, particles} pairs) and its device count.  The
+   * BLUR, GRADIENT(_HYBRID) and BLUR_GRADIENT_HYBRID backward with 16
+   * channels on 3D clamped grids then take each tiled cell's inner pairs from
+   * a kernel that evaluates each pair once for both ends; every other
+   * operator reads the rows whole. */
+  const int32_t* nbr_own;
+  const uint32_t* cells;
+  const int32_t* cell_count;
 } sphops_args;
 
 /* Forward operator `op` (SPHOPS_OP_*) on binned particles. */
@@ -281,6 +291,24 @@ int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const in
 int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bin_offsets, int32_t* nbr_start,
                          int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, int64_t* nbr_total,
                          void* stream);
+
+/* sphops_neighbor_fill with cell tiles (no reference counterpart): the rows
+ * of the particles of every cell holding 8 to 128 particles keep their
+ * own-cell entries (self included) last, in stencil order like the rest of
+ * the row; nbr_own (B*N) receives how many (0 for every other particle and for
+ * rows not stored), cells (capacity sphops_neighbor_cell_capacity pairs) one
+ * {first particle, particles} pair per such cell in no fixed order, and
+ * cell_count (one device int32) their number.  The rows hold the same
+ * entries as sphops_neighbor_fill's, so every operator accepts the list;
+ * the backward operators that know the tiles (sphops_args.nbr_own) skip the
+ * last nbr_own entries and evaluate those pairs per cell instead. */
+int sphops_neighbor_fill_tiled(const sphops_grid* grid, const float* x, const int32_t* bin_offsets,
+                               int32_t* nbr_start, int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count,
+                               int64_t* nbr_total, int32_t* nbr_own, uint32_t* cells, int32_t* cell_count,
+                               void* stream);
+
+/* Capacity (cell descriptors) the cells buffer of sphops_neighbor_fill_tiled needs. */
+int64_t sphops_neighbor_cell_capacity(const sphops_grid* grid);
 
 /* Schedule for list traversal.  The binned particles are cut into tiles of
  * 4096; within a tile they are partitioned (stably) by list length into eight

@@ -574,6 +574,9 @@ static OpPtrs from_args(const sphops_args* a) {
   p.nwaves_sparse_dev = a->nbr_wave_count_sparse_device;
   p.xw_buf = reinterpret_cast<float4*>(a->packed);
   p.xw_ready = a->packed_valid != 0;
+  p.nown = a->nbr_own;
+  p.cells = reinterpret_cast<const uint2*>(a->cells);
+  p.cell_count = a->cell_count;
   return p;
 }
 
@@ -595,6 +598,9 @@ static void check_list(const sphops_args* a) {
   require(a->nbr_wave_count_sparse >= 0, "negative wave count");
   require(a->packed == nullptr || sphops::pk::aligned16(a->packed), "packed must be 16-byte aligned");
   require(a->packed_valid == 0 || a->packed != nullptr, "packed_valid needs packed");
+  const int cell_ptrs = (a->nbr_own != nullptr) + (a->cells != nullptr) + (a->cell_count != nullptr);
+  require(cell_ptrs == 0 || cell_ptrs == 3, "nbr_own, cells and cell_count go together");
+  require(cell_ptrs == 0 || a->nbr_index != nullptr, "cell tiles need the neighbour list (nbr_index)");
 }
 
 int sphops_forward(const sphops_grid* grid, int op, const sphops_args* args, void* stream) {
@@ -667,9 +673,9 @@ int sphops_neighbor_candidates(const sphops_grid* grid, const float* x, const in
   });
 }
 
-int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* nbr_start,
+static int neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* nbr_start,
                          int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, int64_t* nbr_total,
-                         void* stream) {
+                         const sphops::FillTiles& ft, void* stream) {
   return guarded([&] {
     require(grid != nullptr, "grid must not be NULL");
     require(bo != nullptr && nbr_total != nullptr && (x != nullptr || grid->n_keys == 0), "null buffer");
@@ -693,8 +699,45 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
     a.iout2 = nbr_count;
     a.used = reinterpret_cast<unsigned long long*>(nbr_total);
     a.cap = index_capacity;
+    a.fill_tiles = ft;
     sphops::forward(*grid, Op::NeighbourFill, bo, a, st);
   });
+}
+
+int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* nbr_start,
+                         int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, int64_t* nbr_total,
+                         void* stream) {
+  return neighbor_fill(grid, x, bo, nbr_start, nbr_index, index_capacity, nbr_count, nbr_total, sphops::FillTiles{},
+                       stream);
+}
+
+int sphops_neighbor_fill_tiled(const sphops_grid* grid, const float* x, const int32_t* bo, int32_t* nbr_start,
+                               int32_t* nbr_index, int64_t index_capacity, int32_t* nbr_count, int64_t* nbr_total,
+                               int32_t* nbr_own, uint32_t* cells, int32_t* cell_count, void* stream) {
+  int st = guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    require(cell_count != nullptr && (grid->n_keys == 0 || (nbr_own != nullptr && cells != nullptr)),
+            "null buffer");
+    if (grid->n_keys == 0) sphops::fill_u32(reinterpret_cast<uint32_t*>(cell_count), 1, 0u, sphops::as_stream(stream));
+  });
+  if (st) return st;
+  sphops::FillTiles ft{};
+  if (grid->n_keys != 0) {
+    ft.own = nbr_own;
+    ft.cells = reinterpret_cast<uint2*>(cells);
+    ft.count = cell_count;
+    ft.tmin = (uint32_t)sphops::pk::kCellMin;
+    ft.tmax = (uint32_t)sphops::pk::kCellMax;
+  }
+  return neighbor_fill(grid, x, bo, nbr_start, nbr_index, index_capacity, nbr_count, nbr_total, ft, stream);
+}
+
+int64_t sphops_neighbor_cell_capacity(const sphops_grid* grid) {
+  if (grid == nullptr) {
+    sphops::g_last_error = "grid must not be NULL";
+    return -1;
+  }
+  return (int64_t)(grid->n_keys / sphops::pk::kCellMin + 1);
 }
 
 int sphops_neighbor_schedule(const sphops_grid* grid, const int32_t* nbr_count, int32_t* nbr_order,

@@ -1259,7 +1259,9 @@ __global__ __launch_bounds__(kThreads, CW == 4 ? 3 : 2) void k_blur_hybrid_bwd_q
       const int32_t* __restrict__ nidx = a.nidx;
       const Row row = Row::of(a, k);
       const int start = row.start;
-      const int end = row.end;
+      // with cell tiles the row's last nown[k] entries (its own cell) are
+      // served by k_cell_pairs_bwd
+      const int end = row.end - (a.nown != nullptr ? a.nown[k] : 0);
       // rows walked on the stencil (count < 0, rare) take the general loop;
       // a wave without them the list-only one
       auto walk = [&](auto stencil_rows) {
@@ -1716,12 +1718,13 @@ constexpr int kFillRounds = 48;
 // particles its candidate hit (`hits`, this wave's kFillRounds * 64 bytes of
 // LDS); the unit takes one block of the index buffer; pass two writes each
 // particle's row, ranking the hits of a round with mbcnt.
-template <int D, bool P, int R>
+template <int D, bool P, int R, bool OT>
 __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __restrict__ xw,
                                           const int32_t* __restrict__ bo, uint32_t i0, uint32_t ni,
                                           uint32_t wave, uint8_t* __restrict__ hits,
                                           int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
-                                          int32_t* __restrict__ ncnt, const FillStripes& fs) {
+                                          int32_t* __restrict__ ncnt, const FillStripes& fs,
+                                          const FillTiles& ft) {
   const uint32_t lane = (uint32_t)__lane_id();
   const float4 pt = xw[i0 + min(lane, ni - 1u)];
   float xs[kUnitParticles][3];
@@ -1739,6 +1742,18 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
     w.fetch(g, bo, (int)lane);
     lo = w.j;
     len = w.jend - w.j;
+  }
+  // the unit's own cell [cs, ce) and whether it is a tile (wave-uniform)
+  uint32_t cs = 0, ce = 0;
+  bool tiled = false;
+  if constexpr (OT) {
+    Walker<D, P> w;
+    w.init(g, xs[0], i0);
+    const uint32_t h = w.base + cell_hash<D>(g, w.c);
+    cs = (uint32_t)__builtin_amdgcn_readfirstlane(bo[h]);
+    ce = (uint32_t)__builtin_amdgcn_readfirstlane(bo[h + 1]);
+    tiled = ce - cs >= ft.tmin && ce - cs <= ft.tmax;
+    if (tiled && i0 == cs && lane == 0) ft.cells[atomicAdd(ft.count, 1)] = make_uint2(cs, ce - cs);
   }
   // Many ranges (particle mode, periodic grids): empty ones are dropped and a
   // range that starts where the previous kept one ends is merged into it, so
@@ -1775,6 +1790,18 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
   }
   const uint32_t ncand = (uint32_t)__builtin_amdgcn_readlane((int)pre, 31);
   pre -= len;
+  // a tile's own cell is one contiguous piece of one stencil range: its
+  // candidate positions [po0, po0 + ce - cs), so only the rounds overlapping
+  // it count and place own-cell hits apart
+  uint32_t po0 = 0, po1 = 0;
+  if constexpr (OT) {
+    if (tiled) {
+      const uint64_t at_r = __ballot((int)lane < 32 && len > 0 && cs >= lo && cs < lo + len);
+      const int r0 = at_r ? __builtin_ctzll(at_r) : 0;
+      po0 = (uint32_t)__shfl((int)(pre + cs - lo), r0, kWave);
+      po1 = po0 + (ce - cs);
+    }
+  }
   // candidate at position p < ncand: p + offs of the last range starting at
   // or before p.  The starts do not decrease, so that offset is offs of range
   // 0 plus the steps dof[r] = offs[r] - offs[r - 1] of the ranges 1 .. r
@@ -1812,14 +1839,19 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
   const uint32_t rounds = (ncand + kWave - 1) / kWave;
   // pass one: count, keeping the hit bytes; the next round's positions are
   // loaded while this round is tested
-  uint32_t cnt[kUnitParticles] = {};
-  float4 nx = xw[candidate(lane)];
+  uint32_t cnt[kUnitParticles] = {}, cown[kUnitParticles] = {};
+  uint32_t jn = candidate(lane);
+  float4 nx = xw[jn];
   for (uint32_t rd = 0; rd < rounds; ++rd) {
     const uint32_t p = rd * kWave + lane;
     float xj[3];
     unpack(nx, xj);
     if (p >= ncand) xj[0] = __int_as_float(0x7FC00000);  // NaN: never in radius
-    if (rd + 1 < rounds) nx = xw[candidate(p + kWave)];
+    const bool own = OT && tiled && jn >= cs && jn < ce;
+    if (rd + 1 < rounds) {
+      jn = candidate(p + kWave);
+      nx = xw[jn];
+    }
     uint32_t bits = 0;
 #pragma unroll
     for (int t = 0; t < kUnitParticles; ++t) {
@@ -1827,6 +1859,10 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
         float r[3];
         const bool in = displacement<D, P>(g, xs[t], xj, r) < g.eps2;
         cnt[t] += (uint32_t)__popcll(__ballot(in));
+        if constexpr (OT) {
+          if (tiled && rd * kWave < po1 && rd * kWave + kWave > po0)
+            cown[t] += (uint32_t)__popcll(__ballot(in && own));
+        }
         bits |= (in ? 1u : 0u) << t;
       }
     }
@@ -1841,20 +1877,25 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
     if (lane < ni) {
       nstart[i0 + lane] = 0;
       ncnt[i0 + lane] = -1 - (int32_t)ncand;
+      if constexpr (OT) ft.own[i0 + lane] = 0;
     }
     return;
   }
-  uint32_t at[kUnitParticles];
-  int32_t mine_start = 0, mine_cnt = 0;
+  // at[t]: next slot of particle t's row; ao[t]: next slot of its own-cell
+  // entries, which a tile's rows keep last
+  uint32_t at[kUnitParticles], ao[kUnitParticles];
+  int32_t mine_start = 0, mine_cnt = 0, mine_own = 0;
   {
     uint32_t run = (uint32_t)b;
 #pragma unroll
     for (int t = 0; t < kUnitParticles; ++t) {
       at[t] = run;
       run += cnt[t];
+      ao[t] = run - cown[t];
       if ((int)lane == t) {
         mine_start = (int32_t)at[t];
         mine_cnt = (int32_t)cnt[t];
+        mine_own = (int32_t)cown[t];
       }
     }
   }
@@ -1876,6 +1917,23 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
         if (t < (int)ni && displacement<D, P>(g, xs[t], xj, r) < g.eps2) bits |= 1u << t;
       }
     }
+    if (OT && tiled && rd * kWave < po1 && rd * kWave + kWave > po0) {
+      const bool own = j >= cs && j < ce;
+#pragma unroll
+      for (int t = 0; t < kUnitParticles; ++t) {
+        if (t < (int)ni) {
+          const bool in = (bits >> t) & 1u;
+          const uint64_t m = __ballot(in && !own), mo = __ballot(in && own);
+          const uint64_t mm = own ? mo : m;
+          const uint32_t rank =
+              __builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
+          if (in) store_entry(nidx, (own ? ao[t] : at[t]) + rank, (int32_t)j);
+          at[t] += (uint32_t)__popcll(m);
+          ao[t] += (uint32_t)__popcll(mo);
+        }
+      }
+      continue;
+    }
 #pragma unroll
     for (int t = 0; t < kUnitParticles; ++t) {
       if (t < (int)ni) {
@@ -1891,6 +1949,7 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
   if (lane < ni) {
     nstart[i0 + lane] = mine_start;
     ncnt[i0 + lane] = mine_cnt;
+    if constexpr (OT) ft.own[i0 + lane] = mine_own;
   }
 }
 
@@ -1901,12 +1960,13 @@ __device__ __forceinline__ void unit_rows(const GridParams& g, const float4* __r
 // written from the registers or, for more than four hits, by a second walk.
 // A lone particle with more than 64 candidates is served afterwards by the
 // whole wave (unit_rows, ni = 1).
-template <int D, bool P, int R>
+template <int D, bool P, int R, bool OT>
 __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __restrict__ xw,
                                           const int32_t* __restrict__ bo, const int32_t* __restrict__ unit_len,
                                           uint32_t k0, uint32_t wave, uint8_t* __restrict__ hits,
                                           int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
-                                          int32_t* __restrict__ ncnt, const FillStripes& fs) {
+                                          int32_t* __restrict__ ncnt, const FillStripes& fs,
+                                          const FillTiles& ft) {
   const uint32_t n = g.B * g.N;
   const uint32_t lane = (uint32_t)__lane_id();
   const uint32_t k = k0 + lane;
@@ -1957,6 +2017,9 @@ __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __r
   }
   const bool light = lone && cand <= (uint32_t)kWave;
   const uint32_t cnt = light ? c : 0u;
+  if constexpr (OT) {
+    if (lone) ft.own[k] = 0;  // a lone particle's cell is never a tile
+  }
   uint32_t incl = cnt;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
@@ -1993,7 +2056,7 @@ __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __r
   while (heavy) {
     const uint32_t l = (uint32_t)__builtin_ctzll(heavy);
     heavy &= heavy - 1;
-    unit_rows<D, P, R>(g, xw, bo, k0 + l, 1, wave, hits, nidx, nstart, ncnt, fs);
+    unit_rows<D, P, R, OT>(g, xw, bo, k0 + l, 1, wave, hits, nidx, nstart, ncnt, fs, ft);
   }
 }
 
@@ -2002,12 +2065,13 @@ __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __r
 // and the chunks of 64 particles c = wave, wave + (waves in the grid), ...
 // (k0 = 64 c).  Even waves take their chunks first, odd waves their units
 // first, so that the memory-bound lone walks overlap the ALU-bound units.
-template <int D, bool P, int R>
+template <int D, bool P, int R, bool OT>
 __device__ __forceinline__ void fill_items(const GridParams& g, const float4* __restrict__ xw,
                                            const int32_t* __restrict__ bo, const int32_t* __restrict__ unit_len,
                                            const uint2* __restrict__ units, uint32_t nunits, uint8_t* hits,
                                            int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
-                                           int32_t* __restrict__ ncnt, const FillStripes& fs) {
+                                           int32_t* __restrict__ ncnt, const FillStripes& fs,
+                                           const FillTiles& ft) {
   const uint32_t n = g.B * g.N;
   const uint32_t nchunks = (n + kWave - 1) / kWave;
   const uint32_t nwaves = gridDim.x * (kThreads / kWave);
@@ -2016,31 +2080,32 @@ __device__ __forceinline__ void fill_items(const GridParams& g, const float4* __
   for (int phase = 0; phase < 2; ++phase) {
     if ((phase == 0) == chunks_first) {
       for (uint32_t c = wave; c < nchunks; c += nwaves)
-        lone_rows<D, P, R>(g, xw, bo, unit_len, c * kWave, wave, hits, nidx, nstart, ncnt, fs);
+        lone_rows<D, P, R, OT>(g, xw, bo, unit_len, c * kWave, wave, hits, nidx, nstart, ncnt, fs, ft);
     } else {
       for (uint32_t u = wave; u < nunits; u += nwaves) {
         const uint2 ud = units[u];
-        unit_rows<D, P, R>(g, xw, bo, __builtin_amdgcn_readfirstlane(ud.x), __builtin_amdgcn_readfirstlane(ud.y),
-                           wave, hits, nidx, nstart, ncnt, fs);
+        unit_rows<D, P, R, OT>(g, xw, bo, __builtin_amdgcn_readfirstlane(ud.x),
+                               __builtin_amdgcn_readfirstlane(ud.y), wave, hits, nidx, nstart, ncnt, fs, ft);
       }
     }
   }
 }
 
-// M: particle mode (stencil of single cells) or grid mode (stencil rows).
-template <int D, bool P, bool M>
+// M: particle mode (stencil of single cells) or grid mode (stencil rows);
+// OT: cell tiles (FillTiles).
+template <int D, bool P, bool M, bool OT>
 __global__ __launch_bounds__(kThreads) void k_fill(GridParams g, const float4* __restrict__ xw,
                                                    const int32_t* __restrict__ bo,
                                                    const int32_t* __restrict__ unit_len,
                                                    const uint2* __restrict__ units,
                                                    const int32_t* __restrict__ unit_total,
                                                    int32_t* __restrict__ nidx, int32_t* __restrict__ nstart,
-                                                   int32_t* __restrict__ ncnt, FillStripes fs) {
+                                                   int32_t* __restrict__ ncnt, FillStripes fs, FillTiles ft) {
   __shared__ __align__(16) uint8_t hits[kThreads / kWave][kFillRounds * kWave];
   uint8_t* mine = hits[threadIdx.x >> 6];
   const uint32_t nunits = (uint32_t)*unit_total;
-  fill_items<D, P, M ? Walker<D, P>::kCellRanges : Walker<D, P>::kRowRanges>(g, xw, bo, unit_len, units, nunits,
-                                                                             mine, nidx, nstart, ncnt, fs);
+  fill_items<D, P, M ? Walker<D, P>::kCellRanges : Walker<D, P>::kRowRanges, OT>(
+      g, xw, bo, unit_len, units, nunits, mine, nidx, nstart, ncnt, fs, ft);
 }
 
 // total[0] = in-radius pairs (blocks written or not), total[1] = pairs of
@@ -2086,6 +2151,7 @@ static_assert(kThreads >= kFillStripes, "k_fill_totals reads one counter per thr
 }  // namespace sphops
 
 #include "perception_tiled.hpp"
+#include "perception_cells.hpp"
 
 namespace sphops {
 namespace pk {
@@ -2126,9 +2192,11 @@ void neighbour_candidates(const Grid& g, const int32_t* bo, const float* x, hipS
 // Fill the rows (compact, allocated from the striped counters) with the work
 // split neighbour_candidates left in the grid; used[0..1] receive the pair
 // totals (k_fill_totals).
+// With ft.own set, the rows keep the own-cell entries of the tiles last
+// (FillTiles); ft.count is cleared here.
 template <int D, bool P>
 void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, int32_t* nstart, int32_t* nidx,
-                    int32_t* ncnt, unsigned long long* used, int64_t cap, hipStream_t st) {
+                    int32_t* ncnt, unsigned long long* used, int64_t cap, const FillTiles& ft, hipStream_t st) {
   const uint32_t n = (uint32_t)g.n_keys;
   // 3D positions are already 16-byte (x, y, z, w) records; the fill reads
   // x, y and z only, so they need no packing
@@ -2148,12 +2216,19 @@ void neighbour_fill(const Grid& g, const int32_t* bo, const float* x, int32_t* n
   // the counters are zero here: zeroed at grid creation and by the totals
   // kernel of every fill
   FillStripes fs{g.stripes, S - 1, (uint64_t)(cap / S)};
-  if (g.particle_mode)
-    hipLaunchKernelGGL((k_fill<D, P, true>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, xw, bo,
-                       g.unit_len, g.units, g.unit_total, nidx, nstart, ncnt, fs);
-  else
-    hipLaunchKernelGGL((k_fill<D, P, false>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, xw, bo,
-                       g.unit_len, g.units, g.unit_total, nidx, nstart, ncnt, fs);
+  const bool ot = ft.own != nullptr;
+  if (ot) fill_u32(reinterpret_cast<uint32_t*>(ft.count), 1, 0u, st);
+#define SPHOPS_FILL(M, OT)                                                                                      \
+  hipLaunchKernelGGL((k_fill<D, P, M, OT>), dim3(kFillWorkgroups), dim3(kThreads), 0, st, g.p, xw, bo, g.unit_len, \
+                     g.units, g.unit_total, nidx, nstart, ncnt, fs, ft)
+  if (g.particle_mode) {
+    if (ot) SPHOPS_FILL(true, true);
+    else SPHOPS_FILL(true, false);
+  } else {
+    if (ot) SPHOPS_FILL(false, true);
+    else SPHOPS_FILL(false, false);
+  }
+#undef SPHOPS_FILL
   SPHOPS_LAUNCHED();
   hipLaunchKernelGGL(k_fill_totals, dim3(1), dim3(kThreads), 0, st, g.stripes, S, used);
   SPHOPS_LAUNCHED();
@@ -2253,7 +2328,19 @@ template <int D, bool P, bool FULL, int PARTS = 3>
 void launch_blur_hybrid_bwd_quad(const Grid& g, OpPtrs a, hipStream_t st) {
   if (g.n_keys == 0) return;
   pack_for<D, VolumeWeights>(g, a, st);
+  // the cell kernel serves the tiles' own-cell pairs (3D clamped grids, C =
+  // 16); otherwise the rows are read whole
+  const bool cells = a.nown != nullptr && a.cells != nullptr && a.cell_count != nullptr && D == 3 && !P &&
+                     a.C == 16 && aligned16(a.out1);
+  if (!cells) a.nown = nullptr;
   launch_blur_hybrid_bwd_quad_packed<D, P, FULL, PARTS>(g, a, st);
+  if constexpr (D == 3 && !P) {
+    if (cells) {
+      hipLaunchKernelGGL((k_cell_pairs_bwd<D, FULL, PARTS>), dim3(kCellWorkgroups), dim3(kCellThreads), 0, st, g.p,
+                         a);
+      SPHOPS_LAUNCHED();
+    }
+  }
 }
 
 // Pass-B backward with cell tiles: the tiled kernel serves the particles of
@@ -2342,7 +2429,7 @@ void forward_dispatch(const Grid& g, Op op, const int32_t* bo, const OpPtrs& a_i
       if (g.n_keys) neighbour_candidates<D, P>(g, bo, a.x, st);
       return;
     case Op::NeighbourFill:
-      if (g.n_keys) neighbour_fill<D, P>(g, a.bo, a.x, a.iout3, a.iout, a.iout2, a.used, a.cap, st);
+      if (g.n_keys) neighbour_fill<D, P>(g, a.bo, a.x, a.iout3, a.iout, a.iout2, a.used, a.cap, a.fill_tiles, st);
       return;
     case Op::NeighbourTiles:
       if (g.n_keys)

@@ -108,6 +108,22 @@ enum class Op : int {
   NeighbourTiles = 11,      // cell tiles of the pass-B backward and the schedule of the other particles
 };
 
+// Cell tiles of the list (OT = true in the fill): the rows of the particles
+// of a cell holding tmin .. tmax particles keep their own-cell entries (self
+// included) last, own[k] receives their number (0 for every other particle
+// and for rows walked on the stencil), and each such cell is appended to
+// cells as {first particle, particles}, count[0] cells in all (appended in
+// no fixed order; capacity B*N / tmin).  The pair kernels that know the
+// cells (the pass-B backward) skip a row's last own[k] entries and take
+// those pairs from the cell kernel, which evaluates each pair of a cell once
+// for both of its ends; the other kernels read the whole row.
+struct FillTiles {
+  int32_t* own;
+  uint2* cells;
+  int32_t* count;
+  uint32_t tmin, tmax;
+};
+
 struct OpPtrs {
   const float* x = nullptr;
   const float* m = nullptr;
@@ -148,6 +164,12 @@ struct OpPtrs {
   const uint2* waves_sparse = nullptr;
   uint32_t nwaves_sparse = 0;
   const int32_t* nwaves_sparse_dev = nullptr;
+  // cell tiles: written by the list fill (fill_tiles.own non-null) and read
+  // by the pass-B backward (nown, cells, cell_count, all three or none)
+  FillTiles fill_tiles{};
+  const int32_t* nown = nullptr;
+  const uint2* cells = nullptr;
+  const int32_t* cell_count = nullptr;
   uint32_t C = 0;
   float tol = 1e-3f;
 };

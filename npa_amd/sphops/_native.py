@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -75,6 +75,8 @@ _SIGNATURES = {
     "sphops_neighbor_candidates": ([_p, _p, _p, _i32, _p], _i32),
     "sphops_copy_words_to_host": ([_p, _p, _u32, _p], _i32),
     "sphops_neighbor_fill": ([_p, _p, _p, _p, _p, _i64, _p, _p, _p], _i32),
+    "sphops_neighbor_fill_tiled": ([_p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p], _i32),
+    "sphops_neighbor_cell_capacity": ([_p], _i64),
     "sphops_neighbor_schedule": ([_p, _p, _p, _p, _p, _p, _p, _p], _i32),
     "sphops_neighbor_tiles": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p], _i32),
     "sphops_neighbor_tile_capacity": ([_p], _i64),
@@ -92,7 +94,8 @@ class Args(ctypes.Structure):
                 ("nbr_wave_count_device", _p), ("nbr_wave_count_split_device", _p),
                 ("tile_units", _p), ("tile_unit_count", _p), ("nbr_order_sparse", _p), ("nbr_waves_sparse", _p),
                 ("nbr_wave_count_sparse", ctypes.c_int32), ("nbr_wave_count_sparse_device", _p),
-                ("packed", _p), ("packed_valid", ctypes.c_int32)]
+                ("packed", _p), ("packed_valid", ctypes.c_int32), ("nbr_own", _p), ("cells", _p),
+                ("cell_count", _p)]
 
 
 (OP_COUNT, OP_DENSITY, OP_DENSITY_GRADIENT, OP_MOMENT_MATRIX, OP_BLUR, OP_GRADIENT, OP_GRADIENT_HYBRID,

@@ -83,12 +83,15 @@ class NeighborPlan(tuple):
     wave_count_split[, device counts])``, plus ``tiles``: the cell tiles of
     the pass-B backward ``(units, unit count (device), order of the other
     particles, their split waves, their wave count (host bound), its device
-    copy)``, or None."""
+    copy)``, or None; and ``cells``: the cell tiles of
+    ``sphops_neighbor_fill_tiled`` ``(own-cell entries per particle, cell
+    table, its count (device))``, or None."""
 
     def __new__(cls, *items):
         return super().__new__(cls, items)
 
     tiles = None
+    cells = None
     capacity = 0
 
 
@@ -405,17 +408,29 @@ class _HashGridNative:
         waves2 = torch.empty(wcap, dtype=_I32, device=dev)
         # device counts: [0:2] in-radius pairs (int64), [2:4] pairs of rows not
         # stored (int64), [4] waves, [5] split waves, [6] tile units, [7] waves
-        # of the particles outside the tiles
-        small = torch.empty(8, dtype=_I32, device=dev)  # every word read is written by a kernel
+        # of the particles outside the tiles, [8] cell tiles
+        small = torch.empty(9, dtype=_I32, device=dev)  # every word read is written by a kernel
         cap = self._capacity(n)
         index = torch.empty(max(cap, 1), dtype=_I32, device=dev)
         tiles = self._tile_buffers(dev, n, wcap) if self.tiles_enabled else None
         src = getattr(self, "_split_source", None)
         reuse = src is not None and src[0]() is bin_offsets and bin_offsets._version == src[1]
         _check(_lib.sphops_neighbor_candidates(self._h, x, bo, 1 if reuse else 0, st))
-        _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
-                                         ctypes.c_void_p(index.data_ptr()), cap, ctypes.c_void_p(count.data_ptr()),
-                                         ctypes.c_void_p(small.data_ptr()), st))
+        cells = None
+        if tiles is None and self._cells_wanted():
+            ccap = max(int(_lib.sphops_neighbor_cell_capacity(self._h)), 1)
+            cells = (torch.empty(max(n, 1), dtype=_I32, device=dev), torch.empty(2 * ccap, dtype=_I32, device=dev),
+                     small[8:9])
+            _check(_lib.sphops_neighbor_fill_tiled(
+                self._h, x, bo, ctypes.c_void_p(start.data_ptr()), ctypes.c_void_p(index.data_ptr()), cap,
+                ctypes.c_void_p(count.data_ptr()), ctypes.c_void_p(small.data_ptr()),
+                ctypes.c_void_p(cells[0].data_ptr()), ctypes.c_void_p(cells[1].data_ptr()),
+                ctypes.c_void_p(small.data_ptr() + 32), st))
+        else:
+            _check(_lib.sphops_neighbor_fill(self._h, x, bo, ctypes.c_void_p(start.data_ptr()),
+                                             ctypes.c_void_p(index.data_ptr()), cap,
+                                             ctypes.c_void_p(count.data_ptr()), ctypes.c_void_p(small.data_ptr()),
+                                             st))
         _check(_lib.sphops_neighbor_schedule(self._h, ctypes.c_void_p(count.data_ptr()),
                                              ctypes.c_void_p(order.data_ptr()), ctypes.c_void_p(waves.data_ptr()),
                                              ctypes.c_void_p(small.data_ptr() + 16), ctypes.c_void_p(waves2.data_ptr()),
@@ -434,6 +449,7 @@ class _HashGridNative:
         plan.capacity = cap
         if tiles is not None:
             plan.tiles = (tiles[0], small[6:7], tiles[1], tiles[2], e3, small[7:8])
+        plan.cells = cells
         self._last_plan = plan
         return plan
 
@@ -509,6 +525,16 @@ class _HashGridNative:
     # kernel is slower than the lane-split list kernel it replaces for
     # well-filled cells.
     tiles_enabled = os.environ.get("NPA_SPHOPS_TILES", "0") == "1"
+
+    # Cell pairs of sphops_neighbor_fill_tiled: the pass-B backward evaluates
+    # each pair inside a cell of 8 to 128 particles once for both ends (3D
+    # clamped grids).  Opt-in (NPA_SPHOPS_CELLS=1, or this attribute): at cfg5
+    # the list kernel spends only 0.09 ms on those pairs, whose rows it finds
+    # in L1, and the cell kernel takes 0.47 ms for them.
+    cells_enabled = os.environ.get("NPA_SPHOPS_CELLS", "0") == "1"
+
+    def _cells_wanted(self):
+        return self.cells_enabled and self._dim == 3 and self._boundary == CLAMPED
 
     def _tile_buffers(self, dev, n, wcap):
         cap = max(int(_lib.sphops_neighbor_tile_capacity(self._h)), 1)
@@ -616,6 +642,9 @@ class _HashGridNative:
             if len(nbr) > 8 and nbr[8] is not None:  # the wave counts on the device
                 a.nbr_wave_count_device = nbr[8].data_ptr() + 16
                 a.nbr_wave_count_split_device = nbr[8].data_ptr() + 20
+            cells = getattr(nbr, "cells", None)
+            if cells is not None:
+                a.nbr_own, a.cells, a.cell_count = cells[0].data_ptr(), cells[1].data_ptr(), cells[2].data_ptr()
             tiles = getattr(nbr, "tiles", None)
             if tiles is not None:
                 a.tile_units, a.tile_unit_count = tiles[0].data_ptr(), tiles[1].data_ptr()

@@ -42,6 +42,11 @@ def _cases():
     cs.append(d3)
     cs.append(H.random_case("dense3d-particle-c16", 1, 1500, 16, 3, 8, 0.25, False, "particle", uniform=False,
                             sigma=0.08))
+    # 3D clamped clouds at C = 16 whose crowded cells hold 8 to ~30 particles
+    # (the cell pairs of the pass-B backward)
+    for mode in ("grid", "particle"):
+        cs.append(H.random_case(f"cells3d-{mode}-c16", 1, 1500, 16, 3, 8, 0.25, False, mode, uniform=False,
+                                sigma=0.4))
     d = H.random_case("dense2d-per", 1, 1000, 16, 2, 8, 0.125, True, "grid", uniform=False, sigma=0.05)
     d.x[..., :2] += 0.5  # the cluster straddles the periodic boundary
     cs.append(d)
@@ -771,3 +776,55 @@ def test_cell_tiles_backward(name):
             (ra, ma), (rb, mb_) = ora["b_blur"][i], ora["b_grad"][i]
             H.assert_close(f"{name}:tiles.d{k}", _flat(got[k].cpu().numpy(), q, D if k == "x" else None), ra + rb,
                            ma + mb_)
+
+
+@pytest.mark.parametrize("name", ["cells3d-grid-c16", "cells3d-particle-c16", "cfg5", "cfg5-full"])
+def test_cell_pairs_backward(name):
+    """The opt-in cell pairs of the pass-B backward (sphops_neighbor_fill_tiled
+    keeps each tiled cell's own-cell entries last, the list kernel skips them
+    and k_cell_pairs_bwd evaluates each pair inside a cell once for both
+    ends) against the oracle: the fused backward with every gradient and
+    with dL/ds alone, and the single blur and gradient_hybrid backward."""
+    import npa_amd.sphops as sp
+    from npa_amd.sphops.sph import BlurGradientHybrid, GradientHybrid, Blur, _plan
+    c, res, ora = run(name)
+    q = ora["q"]
+    D = c.dim
+    grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    grid.hashgrid.cells_enabled = True
+    snap = grid.instantiate(dev(c.x))
+    xb, sb, mb, rho = dev(res["xb"]), dev(res["sb"]), dev(res["mb"]), dev(res["rho"])
+    rng = np.random.default_rng(11)
+    B, N, C = c.B, c.N, c.C
+    rng.standard_normal((B, N))
+    g_blur = rng.standard_normal((B, N, C)).astype(np.float32)
+    g_grad = rng.standard_normal((B, N, C, D)).astype(np.float32)
+    plan = _plan(snap, xb)
+    assert plan.cells is not None
+    cells = int(plan.cells[2].item())
+    own = plan.cells[0][: B * N].cpu().numpy()
+    assert cells > 0 and (own > 0).any(), f"{name}: no cell holds 8 to 128 particles"
+    for need in (("x", "s", "rho"), ("s",)):
+        xr = xb.detach().clone().requires_grad_("x" in need)
+        sr = sb.detach().clone().requires_grad_(True)
+        rr = rho.detach().clone().requires_grad_("rho" in need)
+        torch.autograd.backward(BlurGradientHybrid.apply(xr, sr, rr, mb, snap, 1e-3), [dev(g_blur), dev(g_grad)])
+        got = {"x": xr.grad, "s": sr.grad, "rho": rr.grad}
+        for i, k in enumerate(("x", "s", "rho")):
+            if k not in need:
+                continue
+            (ra, ma), (rb, mb_) = ora["b_blur"][i], ora["b_grad"][i]
+            H.assert_close(f"{name}:cells.d{k}", _flat(got[k].cpu().numpy(), q, D if k == "x" else None), ra + rb,
+                           ma + mb_)
+    for key, fn, up in (("b_blur", lambda x, s, r: Blur.apply(x, s, r, mb, snap), g_blur),
+                        ("b_grad", lambda x, s, r: GradientHybrid.apply(x, s, r, mb, snap, 1e-3), g_grad)):
+        xr = xb.detach().clone().requires_grad_(True)
+        sr = sb.detach().clone().requires_grad_(True)
+        rr = rho.detach().clone().requires_grad_(True)
+        torch.autograd.backward(fn(xr, sr, rr), [dev(up)])
+        got = {"x": xr.grad, "s": sr.grad, "rho": rr.grad}
+        for i, k in enumerate(("x", "s", "rho")):
+            ref, mag = ora[key][i]  # gradient_hybrid's backward is the raw gradient's (straight-through)
+            H.assert_close(f"{name}:cells.{key}.d{k}", _flat(got[k].cpu().numpy(), q, D if k == "x" else None), ref,
+                           mag)
