@@ -293,7 +293,7 @@ int sphops_neighbor_fill(const sphops_grid* grid, const float* x, const int32_t*
                          void* stream);
 
 /* sphops_neighbor_fill with cell tiles (no reference counterpart): the rows
- * of the particles of every cell holding 8 to 128 particles keep their
+ * of the particles of every cell holding 16 to 64 particles keep their
  * own-cell entries (self included) last, in stencil order like the rest of
  * the row; nbr_own (B*N) receives how many (0 for every other particle and for
  * rows not stored), cells (capacity sphops_neighbor_cell_capacity pairs) one

@@ -39,8 +39,10 @@
 namespace sphops {
 namespace pk {
 
-constexpr int kCellMax = 128;        // particles per tiled cell (8 blocks of 16)
-constexpr int kCellMin = 8;          // cells with fewer particles keep their pairs in the list
+// Cells of 16 to 64 particles (the best of the thresholds measured at cfg5:
+// 8-128 with two workgroups per CU, 16-128, and 16-64 with four).
+constexpr int kCellMax = 64;         // particles per tiled cell (4 blocks of 16)
+constexpr int kCellMin = 16;         // cells with fewer particles keep their pairs in the list
 constexpr int kCellThreads = 256;    // four waves: up to four block pairs per round
 constexpr uint32_t kCellWorkgroups = 1024;
 
@@ -246,9 +248,9 @@ __device__ __forceinline__ void cell_block_pair(const GridParams& g, CellLds<D, 
 
 // PARTS and FULL as for k_blur_hybrid_bwd_quad (C = 16, clamped grids).
 template <int D, bool FULL, int PARTS>
-__global__ __launch_bounds__(kCellThreads, 2) void k_cell_pairs_bwd(GridParams g, OpPtrs a) {
+__global__ __launch_bounds__(kCellThreads, 4) void k_cell_pairs_bwd(GridParams g, OpPtrs a) {
   constexpr bool kB = (PARTS & 1) != 0, kG = (PARTS & 2) != 0;
-  constexpr int C = 16, CW = 4;
+  constexpr int CW = 4;
   __shared__ CellLds<D, FULL, PARTS> L;
   const uint32_t ncells = (uint32_t)*a.cell_count;
   const int tid = threadIdx.x, wv = tid >> 6;

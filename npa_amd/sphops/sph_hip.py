@@ -527,10 +527,11 @@ class _HashGridNative:
     tiles_enabled = os.environ.get("NPA_SPHOPS_TILES", "0") == "1"
 
     # Cell pairs of sphops_neighbor_fill_tiled: the pass-B backward evaluates
-    # each pair inside a cell of 8 to 128 particles once for both ends (3D
+    # each pair inside a cell of 16 to 64 particles once for both ends (3D
     # clamped grids).  Opt-in (NPA_SPHOPS_CELLS=1, or this attribute): at cfg5
-    # the list kernel spends only 0.09 ms on those pairs, whose rows it finds
-    # in L1, and the cell kernel takes 0.47 ms for them.
+    # the list kernel spends little on those pairs, whose rows it finds in
+    # L1, and the pass-B backward takes 0.96 ms with them against 0.85 ms
+    # without.
     cells_enabled = os.environ.get("NPA_SPHOPS_CELLS", "0") == "1"
 
     def _cells_wanted(self):

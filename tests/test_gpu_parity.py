@@ -804,7 +804,7 @@ def test_cell_pairs_backward(name):
     assert plan.cells is not None
     cells = int(plan.cells[2].item())
     own = plan.cells[0][: B * N].cpu().numpy()
-    assert cells > 0 and (own > 0).any(), f"{name}: no cell holds 8 to 128 particles"
+    assert cells > 0 and (own > 0).any(), f"{name}: no cell holds 16 to 64 particles"
     for need in (("x", "s", "rho"), ("s",)):
         xr = xb.detach().clone().requires_grad_("x" in need)
         sr = sb.detach().clone().requires_grad_(True)
