@@ -828,3 +828,48 @@ def test_cell_pairs_backward(name):
             ref, mag = ora[key][i]  # gradient_hybrid's backward is the raw gradient's (straight-through)
             H.assert_close(f"{name}:cells.{key}.d{k}", _flat(got[k].cpu().numpy(), q, D if k == "x" else None), ref,
                            mag)
+
+
+@pytest.mark.parametrize("name", ["cells3d-grid-c16", "ref3d-clamp-grid"])
+def test_cell_pairs_replay_and_empty(name):
+    """Cell pairs on: two backward calls on one snapshot agree bit for bit
+    (fixed sum order, no atomics), and a cloud with no cell of 16 to 64
+    particles (ref3d: at most a few per cell) leaves an empty cell table and
+    the same results as the whole-row path."""
+    import npa_amd.sphops as sp
+    from npa_amd.sphops.sph import BlurGradientHybrid, _plan
+    c, res, _ = run(name)
+    D = c.dim
+    rng = np.random.default_rng(5)
+    g_blur = dev(rng.standard_normal((c.B, c.N, c.C)).astype(np.float32))
+    g_grad = dev(rng.standard_normal((c.B, c.N, c.C, D)).astype(np.float32))
+    outs = {}
+    for cells in (True, False):
+        grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
+                           num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+        grid.hashgrid.cells_enabled = cells
+        snap = grid.instantiate(dev(c.x))
+        xb, sb, mb, rho = dev(res["xb"]), dev(res["sb"]), dev(res["mb"]), dev(res["rho"])
+        got = []
+        for _ in range(2):
+            xr = xb.detach().clone().requires_grad_(True)
+            sr = sb.detach().clone().requires_grad_(True)
+            rr = rho.detach().clone().requires_grad_(True)
+            torch.autograd.backward(BlurGradientHybrid.apply(xr, sr, rr, mb, snap, 1e-3), [g_blur, g_grad])
+            got.append([t.grad.cpu().numpy() for t in (xr, sr, rr)])
+        for a, b in zip(got[0], got[1]):
+            assert np.array_equal(a, b), f"{name}: replay differs (cells={cells})"
+        outs[cells] = got[0]
+        if cells:
+            plan = _plan(snap, xb)
+            ncells = int(plan.cells[2].item())
+            own = plan.cells[0][: c.B * c.N].cpu().numpy()
+            if name.startswith("ref3d"):
+                assert ncells == 0 and not own.any(), f"{name}: unexpected tiled cells"
+            else:
+                assert ncells > 0 and own.any()
+    for a, b in zip(outs[True], outs[False]):
+        scale = np.abs(b).max() + 1e-30
+        assert np.abs(a - b).max() <= 1e-4 * scale, f"{name}: cell pairs and whole rows disagree"
+        if name.startswith("ref3d"):
+            assert np.array_equal(a, b), f"{name}: no tiled cell, yet the results changed"
