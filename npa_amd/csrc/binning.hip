@@ -319,14 +319,14 @@ __global__ __launch_bounds__(kThreads) void k_chunk_lo(const uint64_t* __restric
 // cell counts, where the kernel is a 16-byte-per-lane store stream).
 constexpr int kChunksPerBlock = 4;
 
-__global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint64_t* __restrict__ kv,
-                                                          const uint32_t* __restrict__ chunk_lo, uint32_t nch,
-                                                          int32_t* __restrict__ bo, uint64_t ncells_p1) {
+__device__ __forceinline__ void bin_offsets_block(const uint64_t* __restrict__ kv,
+                                                  const uint32_t* __restrict__ chunk_lo, uint32_t nch,
+                                                  int32_t* __restrict__ bo, uint64_t ncells_p1, uint32_t blk) {
   __shared__ uint32_t first[kChunk];
   __shared__ uint32_t wmin[kThreads / 64];
   const int t = threadIdx.x;
   for (int i = 0; i < kChunksPerBlock; ++i) {
-    const uint32_t ch = blockIdx.x * kChunksPerBlock + (uint32_t)i;
+    const uint32_t ch = blk * kChunksPerBlock + (uint32_t)i;
     if (ch >= nch) break;  // uniform over the workgroup
     const uint32_t lo = chunk_lo[ch], hi = chunk_lo[ch + 1];
     const uint64_t c0 = (uint64_t)ch << kChunkLog2;
@@ -376,6 +376,12 @@ __global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint64_t* __rest
         if (c + q < ncells_p1) bo[c + q] = (int)s[q];
     }
   }
+}
+
+__global__ __launch_bounds__(kThreads) void k_bin_offsets(const uint64_t* __restrict__ kv,
+                                                          const uint32_t* __restrict__ chunk_lo, uint32_t nch,
+                                                          int32_t* __restrict__ bo, uint64_t ncells_p1) {
+  bin_offsets_block(kv, chunk_lo, nch, bo, ncells_p1, blockIdx.x);
 }
 
 // First and one-past-last sorted position of the run of `key` (its cell)
@@ -455,13 +461,12 @@ constexpr uint64_t kRunSearchMinCells = 1ull << 22;
 // first position comes from bin_offsets or, with bo null, from the sorted
 // keys.
 template <bool BLOCKS, bool UNITS>
-__global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __restrict__ kv, uint32_t n,
-                                                          uint32_t N, int32_t* __restrict__ perm,
-                                                          const int32_t* __restrict__ bo, uint32_t maxp,
-                                                          uint32_t* __restrict__ flags32,
-                                                          uint64_t* __restrict__ flags64,
-                                                          int32_t* __restrict__ unit_len) {
-  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+__device__ __forceinline__ void permutation_block(const uint64_t* __restrict__ kv, uint32_t n, uint32_t N,
+                                                  int32_t* __restrict__ perm, const int32_t* __restrict__ bo,
+                                                  uint32_t maxp, uint32_t* __restrict__ flags32,
+                                                  uint64_t* __restrict__ flags64, int32_t* __restrict__ unit_len,
+                                                  uint32_t blk) {
+  const uint32_t k = blk * kThreads + threadIdx.x;
   if (k >= n) return;
   const uint64_t w = kv[k];
   const uint32_t src = kv_val(w);
@@ -487,6 +492,38 @@ __global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __rest
     }
     if constexpr (BLOCKS && UNITS) flags64[k] = (uint64_t)bf | ((uint64_t)uf << 32);
     else flags32[k] = BLOCKS ? bf : uf;
+  }
+}
+
+template <bool BLOCKS, bool UNITS>
+__global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __restrict__ kv, uint32_t n,
+                                                          uint32_t N, int32_t* __restrict__ perm,
+                                                          const int32_t* __restrict__ bo, uint32_t maxp,
+                                                          uint32_t* __restrict__ flags32,
+                                                          uint64_t* __restrict__ flags64,
+                                                          int32_t* __restrict__ unit_len) {
+  permutation_block<BLOCKS, UNITS>(kv, n, N, perm, bo, maxp, flags32, flags64, unit_len, blockIdx.x);
+}
+
+// bin_offsets and the permutation in one launch, for grids whose permutation
+// finds cell bounds in the sorted keys (it does not read bin_offsets): one
+// permutation workgroup after every `every` chunk workgroups, so that the
+// latency-bound permutation runs under the bin_offsets store stream instead
+// of after it (the dispatcher starts workgroups in order; with all
+// permutation workgroups first the two did not overlap).
+template <bool BLOCKS, bool UNITS>
+__global__ __launch_bounds__(kThreads) void k_offsets_permutation(
+    const uint64_t* __restrict__ kv, const uint32_t* __restrict__ chunk_lo, uint32_t nch, int32_t* __restrict__ bo,
+    uint64_t ncells_p1, uint32_t nb_bo, uint32_t n, uint32_t N, int32_t* __restrict__ perm, uint32_t maxp,
+    uint32_t* __restrict__ flags32, uint64_t* __restrict__ flags64, int32_t* __restrict__ unit_len,
+    uint32_t nb_perm, uint32_t every) {
+  const uint32_t b = blockIdx.x, q = b / (every + 1), r = b % (every + 1);
+  if (q < nb_perm) {
+    if (r == every) permutation_block<BLOCKS, UNITS>(kv, n, N, perm, nullptr, maxp, flags32, flags64, unit_len, q);
+    else if (q * every + r < nb_bo) bin_offsets_block(kv, chunk_lo, nch, bo, ncells_p1, q * every + r);
+  } else {
+    const uint32_t c = nb_perm * every + (b - nb_perm * (every + 1));
+    if (c < nb_bo) bin_offsets_block(kv, chunk_lo, nch, bo, ncells_p1, c);
   }
 }
 
@@ -912,20 +949,36 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   const uint32_t nch = (uint32_t)g.n_chunks;
   hipLaunchKernelGGL(k_chunk_lo, blocks_for((uint64_t)nch + 1), dim3(kThreads), 0, st, skv, n, g.chunk_lo, nch);
   SPHOPS_LAUNCHED();
-  hipLaunchKernelGGL(k_bin_offsets, dim3((nch + kChunksPerBlock - 1) / kChunksPerBlock), dim3(kThreads), 0, st,
-                     skv, g.chunk_lo, nch, bo, ncp1);
-  SPHOPS_LAUNCHED();
+  const uint32_t nb_bo = (nch + kChunksPerBlock - 1) / kChunksPerBlock;
 
   // 4. permutation (destination slot of each input particle), with the
   // block-start flags in grid mode and, when the grid has the fill's
-  // buffers, the fill's work split (unit_len, the units and their count)
+  // buffers, the fill's work split (unit_len, the units and their count);
+  // on large grids it takes cell bounds from the sorted keys and runs in
+  // the bin_offsets launch
   const int32_t* cell_bo = g.n_cells >= kRunSearchMinCells ? nullptr : bo;
   const bool units = g.unit_len != nullptr && g.units != nullptr && g.unit_total != nullptr;
   const bool dual = units && !g.particle_mode && dual_scan_fits(g, n);
   uint64_t* f64 = g.kv[cur ^ 1];  // free after the sort; n + 1 words
-#define SPHOPS_PERM(BL, UN, F32, F64)                                                                          \
-  hipLaunchKernelGGL((k_permutation<BL, UN>), blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm, cell_bo, \
-                     g.p.maxp, F32, F64, UN ? g.unit_len : nullptr)
+  const uint32_t nb_perm = blocks_for(n).x;
+  if (cell_bo != nullptr) {
+    hipLaunchKernelGGL(k_bin_offsets, dim3(nb_bo), dim3(kThreads), 0, st, skv, g.chunk_lo, nch, bo, ncp1);
+    SPHOPS_LAUNCHED();
+  }
+  const uint32_t every = std::max<uint32_t>(1u, nb_bo / std::max<uint32_t>(nb_perm, 1u));
+  // the interleaved launch covers nb_perm * (every + 1) workgroups, or more
+  // when the chunks outnumber the permutation's (every rounds down)
+  const uint32_t nb_all = std::max(nb_bo + nb_perm, nb_perm * (every + 1));
+#define SPHOPS_PERM(BL, UN, F32, F64)                                                                              \
+  do {                                                                                                              \
+    if (cell_bo != nullptr)                                                                                         \
+      hipLaunchKernelGGL((k_permutation<BL, UN>), blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm,       \
+                         cell_bo, g.p.maxp, F32, F64, UN ? g.unit_len : nullptr);                                   \
+    else                                                                                                            \
+      hipLaunchKernelGGL((k_offsets_permutation<BL, UN>), dim3(nb_all), dim3(kThreads), 0, st, skv, g.chunk_lo,    \
+                         nch, bo, ncp1, nb_bo, n, g.p.N, perm, g.p.maxp, F32, F64, UN ? g.unit_len : nullptr,       \
+                         nb_perm, every);                                                                           \
+  } while (0)
   if (g.particle_mode) {
     if (units) SPHOPS_PERM(false, true, g.flags, nullptr);
     else SPHOPS_PERM(false, false, nullptr, nullptr);
