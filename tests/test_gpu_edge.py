@@ -75,3 +75,29 @@ def test_large_grid_cell_bounds(layout):
     np.testing.assert_array_equal(snap.bin_offsets.cpu().numpy(), ref["bin_offsets"])
     np.testing.assert_array_equal(snap.block_info.cpu().numpy(), ref["block_info"])
     assert int(snap.total_blocks.item()) == ref["total_blocks"]
+
+
+def test_large_grid_many_particles():
+    """Above 2^22 cells the permutation runs inside the bin_offsets launch,
+    one permutation workgroup after every few chunk workgroups; here the
+    permutation's workgroups outnumber the chunks' (300,000 particles on
+    4.35 M cells), the case where the interleave takes one chunk workgroup per
+    permutation workgroup and the launch grows to cover them all: every
+    binning output bit-exact against the oracle."""
+    import numpy as np
+    import helpers as H
+    import npa_amd.sphops as sp
+    rng = np.random.default_rng(29)
+    gs, eps, B, N = (170, 160, 160), 0.01, 1, 300_000
+    half = np.array(gs) * eps / 2
+    x = (rng.random((B, N, 3)) - 0.5) * 2 * (half - 1e-3)
+    c = _binning_case("cells-many", x, gs, eps, 16, B)
+    print("[case] large-grid many particles", flush=True)
+    grid = sp.HashGrid(dim=3, boundary="clamped", mode="grid", grid_size=list(gs), eps=eps, num_particles=N,
+                       batch_size=B, max_particles_per_block=16)
+    snap = grid.instantiate(torch.from_numpy(c.x).cuda())
+    ref = H.oracle_binning(c)
+    np.testing.assert_array_equal(snap.permutation.cpu().numpy(), ref["permutation"])
+    np.testing.assert_array_equal(snap.bin_offsets.cpu().numpy(), ref["bin_offsets"])
+    np.testing.assert_array_equal(snap.block_info.cpu().numpy(), ref["block_info"])
+    assert int(snap.total_blocks.item()) == ref["total_blocks"]
