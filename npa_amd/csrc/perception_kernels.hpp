@@ -1979,8 +1979,10 @@ __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __r
   // ranges fetched kFetch at a time (their loads in flight together): three
   // for the many single-cell ranges of particle mode and periodic grids, one
   // for the nine stencil rows of a clamped grid, whose register budget the
-  // unit path needs
+  // unit path needs; a clamped grid's walk loads two candidate positions
+  // at a time instead (more would cost the unit path a wave per SIMD)
   constexpr int kFetch = R > 9 ? 3 : 1;
+  constexpr int kLoneLoads = R > 9 ? 1 : 2;
   static_assert(R % kFetch == 0, "ranges come in whole fetch groups");
   if (lone) {
     unpack(xw[k], xi);
@@ -1998,17 +2000,25 @@ __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __r
       for (int u = 0; u < kFetch; ++u) {
         const uint32_t len = rhi[u] - rlo[u];
         const uint32_t take = cand < (uint32_t)kWave ? min(len, (uint32_t)kWave - cand) : 0u;
-        for (uint32_t q = 0; q < take; ++q) {
-          float xj[3], rr[3];
-          unpack(xw[rlo[u] + q], xj);
-          if (displacement<D, P>(g, xi, xj, rr) < g.eps2) {
-            mask |= 1ull << (cand + q);
-            const int32_t j = (int32_t)(rlo[u] + q);
-            h0 = c == 0 ? j : h0;
-            h1 = c == 1 ? j : h1;
-            h2 = c == 2 ? j : h2;
-            h3 = c == 3 ? j : h3;
-            ++c;
+        // kLoneLoads candidate positions in flight per step (the last one
+        // repeated past the range's end, so every load stays in it)
+        for (uint32_t q = 0; q < take; q += kLoneLoads) {
+          float4 pj[kLoneLoads];
+#pragma unroll
+          for (int v = 0; v < kLoneLoads; ++v) pj[v] = xw[rlo[u] + min(q + (uint32_t)v, take - 1u)];
+#pragma unroll
+          for (int v = 0; v < kLoneLoads; ++v) {
+            float xj[3], rr[3];
+            unpack(pj[v], xj);
+            if (q + (uint32_t)v < take && displacement<D, P>(g, xi, xj, rr) < g.eps2) {
+              mask |= 1ull << (cand + q + (uint32_t)v);
+              const int32_t j = (int32_t)(rlo[u] + q + (uint32_t)v);
+              h0 = c == 0 ? j : h0;
+              h1 = c == 1 ? j : h1;
+              h2 = c == 2 ? j : h2;
+              h3 = c == 3 ? j : h3;
+              ++c;
+            }
           }
         }
         cand += len;
