@@ -369,7 +369,11 @@ __device__ __forceinline__ void bin_offsets_block(const uint64_t* __restrict__ k
     }
     const uint64_t c = c0 + (uint64_t)t * 4;
     if (c + 3 < ncells_p1) {
-      *reinterpret_cast<int4*>(bo + c) = make_int4((int)s[0], (int)s[1], (int)s[2], (int)s[3]);
+      // non-temporal: the table is far larger than the caches, and kept out
+      // of them it leaves no dirty lines for the kernels after it to evict
+      typedef int v4i __attribute__((ext_vector_type(4)));
+      const v4i v = {(int)s[0], (int)s[1], (int)s[2], (int)s[3]};
+      __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(bo + c));
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
