@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SPHOPS_ABI_VERSION 20
+#define SPHOPS_ABI_VERSION 21
 
 #define SPHOPS_CLAMPED 0
 #define SPHOPS_PERIODIC 1
@@ -72,6 +72,17 @@ int sphops_grid_coefficients(const sphops_grid* grid, float* poly6, float* spiky
  * per snapshot instead of inside the grid. */
 int sphops_initialize(sphops_grid* grid, const float* positions, int32_t* permutation, int32_t* bin_offsets,
                       int32_t* block_info, int32_t* total_blocks, void* stream);
+
+/* sphops_initialize that also writes the inverse permutation (B,N int32):
+ * inverse[b*N + i] = the index within cloud b of the particle binned to slot
+ * i, so permutation[b*N + inverse[b*N + i]] == i.  No counterpart in the
+ * reference.  sphops_bin_particles with the inverse in place of the
+ * permutation is then the unbin (sphops_backward_bin_particles) done as a
+ * scatter, which moves the rows faster than the gather.  The outputs other
+ * than inverse are sphops_initialize's, bit for bit. */
+int sphops_initialize_inverse(sphops_grid* grid, const float* positions, int32_t* permutation,
+                              int32_t* inverse, int32_t* bin_offsets, int32_t* block_info,
+                              int32_t* total_blocks, void* stream);
 
 /* sphops_initialize without a grid object and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate device

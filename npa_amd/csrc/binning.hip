@@ -469,12 +469,14 @@ __device__ __forceinline__ void permutation_block(const uint64_t* __restrict__ k
                                                   int32_t* __restrict__ perm, const int32_t* __restrict__ bo,
                                                   uint32_t maxp, uint32_t* __restrict__ flags32,
                                                   uint64_t* __restrict__ flags64, int32_t* __restrict__ unit_len,
-                                                  uint32_t blk) {
+                                                  int32_t* __restrict__ inv, uint32_t blk) {
   const uint32_t k = blk * kThreads + threadIdx.x;
   if (k >= n) return;
   const uint64_t w = kv[k];
   const uint32_t src = kv_val(w);
-  perm[src] = (int32_t)(k - (src / N) * N);
+  const uint32_t cloud = (src / N) * N;
+  perm[src] = (int32_t)(k - cloud);
+  if (inv != nullptr) inv[k] = (int32_t)(src - cloud);
   if constexpr (BLOCKS || UNITS) {
     const uint32_t key = kv_key(w);
     const uint32_t rs = bo != nullptr ? (uint32_t)bo[key] : run_start(kv, k, key);
@@ -505,8 +507,9 @@ __global__ __launch_bounds__(kThreads) void k_permutation(const uint64_t* __rest
                                                           const int32_t* __restrict__ bo, uint32_t maxp,
                                                           uint32_t* __restrict__ flags32,
                                                           uint64_t* __restrict__ flags64,
-                                                          int32_t* __restrict__ unit_len) {
-  permutation_block<BLOCKS, UNITS>(kv, n, N, perm, bo, maxp, flags32, flags64, unit_len, blockIdx.x);
+                                                          int32_t* __restrict__ unit_len,
+                                                          int32_t* __restrict__ inv) {
+  permutation_block<BLOCKS, UNITS>(kv, n, N, perm, bo, maxp, flags32, flags64, unit_len, inv, blockIdx.x);
 }
 
 // bin_offsets and the permutation in one launch, for grids whose permutation
@@ -520,10 +523,11 @@ __global__ __launch_bounds__(kThreads) void k_offsets_permutation(
     const uint64_t* __restrict__ kv, const uint32_t* __restrict__ chunk_lo, uint32_t nch, int32_t* __restrict__ bo,
     uint64_t ncells_p1, uint32_t nb_bo, uint32_t n, uint32_t N, int32_t* __restrict__ perm, uint32_t maxp,
     uint32_t* __restrict__ flags32, uint64_t* __restrict__ flags64, int32_t* __restrict__ unit_len,
-    uint32_t nb_perm, uint32_t every) {
+    int32_t* __restrict__ inv, uint32_t nb_perm, uint32_t every) {
   const uint32_t b = blockIdx.x, q = b / (every + 1), r = b % (every + 1);
   if (q < nb_perm) {
-    if (r == every) permutation_block<BLOCKS, UNITS>(kv, n, N, perm, nullptr, maxp, flags32, flags64, unit_len, q);
+    if (r == every)
+      permutation_block<BLOCKS, UNITS>(kv, n, N, perm, nullptr, maxp, flags32, flags64, unit_len, inv, q);
     else if (q * every + r < nb_bo) bin_offsets_block(kv, chunk_lo, nch, bo, ncells_p1, q * every + r);
   } else {
     const uint32_t c = nb_perm * every + (b - nb_perm * (every + 1));
@@ -912,7 +916,7 @@ void exclusive_scan_u32(const Grid& g, uint32_t* data, uint64_t n, uint32_t* tot
 }
 
 void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int32_t* block_info,
-                     int32_t* total_blocks, hipStream_t st) {
+                     int32_t* total_blocks, hipStream_t st, int32_t* inv) {
   const uint32_t n = (uint32_t)g.n_keys;
   const uint64_t ncp1 = g.n_cells + 1;
   if (n == 0) {
@@ -977,10 +981,10 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   do {                                                                                                              \
     if (cell_bo != nullptr)                                                                                         \
       hipLaunchKernelGGL((k_permutation<BL, UN>), blocks_for(n), dim3(kThreads), 0, st, skv, n, g.p.N, perm,       \
-                         cell_bo, g.p.maxp, F32, F64, UN ? g.unit_len : nullptr);                                   \
+                         cell_bo, g.p.maxp, F32, F64, UN ? g.unit_len : nullptr, inv);                              \
     else                                                                                                            \
       hipLaunchKernelGGL((k_offsets_permutation<BL, UN>), dim3(nb_all), dim3(kThreads), 0, st, skv, g.chunk_lo,    \
-                         nch, bo, ncp1, nb_bo, n, g.p.N, perm, g.p.maxp, F32, F64, UN ? g.unit_len : nullptr,       \
+                         nch, bo, ncp1, nb_bo, n, g.p.N, perm, g.p.maxp, F32, F64, UN ? g.unit_len : nullptr, inv,  \
                          nb_perm, every);                                                                           \
   } while (0)
   if (g.particle_mode) {

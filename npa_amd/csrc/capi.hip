@@ -321,6 +321,18 @@ int sphops_initialize(sphops_grid* grid, const float* positions, int32_t* permut
   });
 }
 
+int sphops_initialize_inverse(sphops_grid* grid, const float* positions, int32_t* permutation,
+                              int32_t* inverse, int32_t* bin_offsets, int32_t* block_info,
+                              int32_t* total_blocks, void* stream) {
+  return guarded([&] {
+    require(grid != nullptr, "grid must not be NULL");
+    check_initialize_args(*grid, positions, permutation, bin_offsets, block_info);
+    require(grid->n_keys == 0 || inverse != nullptr, "inverse must not be NULL");
+    sphops::run_instantiate(*grid, positions, permutation, bin_offsets, block_info, total_blocks,
+                            sphops::as_stream(stream), inverse);
+  });
+}
+
 static int move_rows(const sphops_grid* grid, const float* ip, const float* is, const float* im, const int32_t* perm,
                      float* op, float* os, float* om, uint32_t C, bool fwd, void* stream) {
   return guarded([&] {

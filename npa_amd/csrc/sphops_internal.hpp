@@ -65,8 +65,10 @@ struct Grid {
 };
 
 // binning.hip
+// inv (B*N, or null): the inverse permutation, inv[b*N + slot] = the index
+// within cloud b of the particle binned to that slot
 void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bin_offsets,
-                     int32_t* block_info, int32_t* total_blocks, hipStream_t st);
+                     int32_t* block_info, int32_t* total_blocks, hipStream_t st, int32_t* inv = nullptr);
 void run_bin_particles(const Grid& g, const float* in_pos, const float* in_state, const float* in_mass,
                        const int32_t* perm, float* out_pos, float* out_state, float* out_mass,
                        uint32_t C, bool forward, hipStream_t st);

@@ -10,7 +10,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "SPHOPS_HIP_LIB", os.path.join(os.path.dirname(_HERE), "_lib", "libsphops_hip.so"))
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -35,6 +35,7 @@ _SIGNATURES = {
     "sphops_grid_max_blocks": ([_p], _i64),
     "sphops_grid_coefficients": ([_p, ctypes.POINTER(_f32), ctypes.POINTER(_f32)], _i32),
     "sphops_initialize": ([_p, _p, _p, _p, _p, _p, _p], _i32),
+    "sphops_initialize_inverse": ([_p, _p, _p, _p, _p, _p, _p, _p], _i32),
     "sphops_initialize_noalloc": ([_i32, _i32, _i32, ctypes.POINTER(ctypes.c_int32), _f32, _u32, _u32, _u32,
                                    _p, _p, _p, _p, _p, _p], _i32),
     "sphops_bin_particles": ([_p, _p, _p, _p, _p, _p, _p, _p, _u32, _p], _i32),

@@ -213,7 +213,10 @@ class _HashGridNative:
         return ctypes.c_void_p(t.data_ptr())
 
     # ---- binning (sph_cuda.cu:1926-2056)
-    def initialize(self, positions, permutation, bin_offsets, block_info, total_blocks=None):
+    def initialize(self, positions, permutation, bin_offsets, block_info, total_blocks=None, inverse=None):
+        """``inverse`` (B, N) int32, optional: receives the inverse permutation
+        (``sphops_initialize_inverse``), with which ``bin_particles`` performs
+        the unbin as a scatter."""
         x = self._pos(positions, "positions")
         bo = self._offsets(bin_offsets)
         pm = _arr(permutation, "permutation", _I32, 2)
@@ -226,7 +229,12 @@ class _HashGridNative:
         tb = ctypes.c_void_p()
         if total_blocks is not None:
             tb = _arr(total_blocks, "total_blocks", _I32, 1)
-        _check(_lib.sphops_initialize(self._h, x, pm, bo, bi, tb, _stream(positions)))
+        if inverse is None:
+            _check(_lib.sphops_initialize(self._h, x, pm, bo, bi, tb, _stream(positions)))
+        else:
+            iv = _arr(inverse, "inverse", _I32, 2)
+            _validate_shape(inverse, (self._b, self._n), "inverse")
+            _check(_lib.sphops_initialize_inverse(self._h, x, pm, iv, bo, bi, tb, _stream(positions)))
         # the library derived the list fill's work split from the same sorted
         # keys; a list built on this very tensor, unmodified, reuses it
         self._split_source = (weakref.ref(bin_offsets), bin_offsets._version)

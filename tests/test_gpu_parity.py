@@ -246,7 +246,8 @@ def run(name):
     x, s, m = dev(c.x), dev(c.s), dev(c.m)
     snap = grid.instantiate(x)
     xb, sb, mb = sp.bin_particles(x, s, snap, m)
-    res = dict(perm=snap.permutation.cpu().numpy(), bo=snap.bin_offsets.cpu().numpy(),
+    res = dict(perm=snap.permutation.cpu().numpy(), inv=snap.inverse.cpu().numpy(),
+               bo=snap.bin_offsets.cpu().numpy(),
                bi=snap.block_info.cpu().numpy(), tb=int(snap.total_blocks.item()),
                xb=xb.cpu().numpy(), sb=sb.cpu().numpy(), mb=mb.cpu().numpy())
     xu, su, mu = sp.unbin_particles(xb, sb, snap, mb)
@@ -344,6 +345,11 @@ def test_binning_bit_exact(name):
     c, res, ora = run(name)
     ob = ora["binning"]
     np.testing.assert_array_equal(res["perm"], ob["permutation"])
+    # the inverse permutation instantiate writes beside it (the unbin below
+    # runs as a scatter by it)
+    slots = np.broadcast_to(np.arange(c.N, dtype=np.int64), (c.B, c.N))
+    inv_then_perm = np.take_along_axis(ob["permutation"].astype(np.int64), res["inv"].astype(np.int64), 1)
+    np.testing.assert_array_equal(inv_then_perm, slots)
     np.testing.assert_array_equal(res["bo"], ob["bin_offsets"])
     if c.mode == "grid":
         np.testing.assert_array_equal(res["bi"], ob["block_info"])
@@ -604,6 +610,49 @@ def test_stencil_methods_match_oracle(name):
         H.assert_close(f"{name}:grad.{key}", _flat(got.cpu().numpy(), q, D if key == "dx" else None), ref, mag)
     hg.gradient_backward(xb, rho, mb, sb, g_grad, gx, gs, gr, bo, bi, False, True, False)
     H.assert_close(f"{name}:grad_ds.ds", _flat(gs.cpu().numpy(), q), *ora["b_grad"][1])
+
+
+@pytest.mark.parametrize("name", ["ref2d-per-particle", "ref3d-clamp-grid", "cfg5"])
+def test_unbin_scatter_and_gather_agree(name):
+    """The unbin runs as a scatter by the snapshot's inverse permutation while
+    the permutation and the inverse are unmodified, and as the gather by the
+    permutation once either has been written to; both give the input rows
+    back bit for bit, through unbin_particles and through the bin's autograd
+    backward."""
+    import npa_amd.sphops as sp
+    c = case(name)
+    grid = sp.HashGrid(dim=c.dim, boundary=c.boundary, mode=c.mode, grid_size=list(c.grid_size), eps=c.eps,
+                       num_particles=c.N, batch_size=c.B, max_particles_per_block=c.maxp)
+    x, s, m = dev(c.x), dev(c.s), dev(c.m)
+    calls = {"scatter": 0, "gather": 0}
+    hg = grid.hashgrid
+    orig_bin, orig_gather = hg.bin_particles, hg.backward_bin_particles
+
+    def counted(kind, fn):
+        def wrapped(*a):
+            calls[kind] += 1
+            return fn(*a)
+        return wrapped
+
+    hg.bin_particles = counted("scatter", orig_bin)
+    hg.backward_bin_particles = counted("gather", orig_gather)
+    try:
+        for edit in (False, True):
+            snap = grid.instantiate(x)
+            if edit:
+                snap.permutation.add_(0)  # same values, a new version: the inverse no longer vouched for
+            xr, sr = x.clone().requires_grad_(True), s.clone().requires_grad_(True)
+            xb, sb, mb = sp.bin_particles(xr, sr, snap, m)
+            before = dict(calls)
+            xu, su, mu = sp.unbin_particles(xb.detach(), sb.detach(), snap, mb.detach())
+            torch.autograd.backward([xb, sb], [xb.detach() * 2, sb.detach() * 3])
+            torch.cuda.synchronize()
+            kind = "gather" if edit else "scatter"
+            assert calls[kind] - before[kind] == 2, (edit, calls, before)
+            assert torch.equal(xu, x) and torch.equal(su, s) and torch.equal(mu, m)
+            assert torch.equal(xr.grad, x * 2) and torch.equal(sr.grad, s * 3)
+    finally:
+        hg.bin_particles, hg.backward_bin_particles = orig_bin, orig_gather
 
 
 @pytest.mark.parametrize("name", ["ref2d-clamp-grid", "cfg5"])
