@@ -230,6 +230,44 @@ __global__ __launch_bounds__(kThreads) void k_radix_hist(const uint64_t* __restr
   for (int d = threadIdx.x; d < kBins; d += kThreads) hist[d * ntiles + blockIdx.x] = h[d];
 }
 
+// Per digit d (a wave each, four digits a workgroup): the tile counts
+// hist[d * ntiles + t] are replaced by their exclusive prefix over the tiles,
+// and the digit's total goes to tot[d].  The scatter adds the totals of the
+// smaller digits, which gives the exclusive prefix over digit-major order
+// that a device-wide scan of the histograms would.
+__global__ __launch_bounds__(kThreads) void k_radix_colscan(uint32_t* __restrict__ hist, uint32_t ntiles,
+                                                            uint32_t* __restrict__ tot) {
+  const uint32_t d = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (d >= (uint32_t)kBins) return;  // wave-uniform
+  const uint32_t lane = __lane_id();
+  uint32_t* __restrict__ h = hist + (uint64_t)d * ntiles;
+  uint32_t carry = 0;
+  for (uint32_t t0 = 0; t0 < ntiles; t0 += 4 * 64) {
+    uint32_t v[4], sum = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t t = t0 + lane * 4 + u;
+      v[u] = t < ntiles ? h[t] : 0u;
+      sum += v[u];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = __shfl_up(incl, off, 64);
+      if ((int)lane >= off) incl += y;
+    }
+    uint32_t run = carry + incl - sum;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t t = t0 + lane * 4 + u;
+      if (t < ntiles) h[t] = run;
+      run += v[u];
+    }
+    carry += (uint32_t)__shfl(incl, 63, 64);
+  }
+  if (lane == 0) tot[d] = carry;
+}
+
 // Stable scatter of one radix digit.  Wave w of the tile owns keys
 // [w*1024, (w+1)*1024) and walks them 64 at a time in index order; lanes with
 // equal digits find each other with 8 ballots, so each key's rank among the
@@ -237,12 +275,40 @@ __global__ __launch_bounds__(kThreads) void k_radix_hist(const uint64_t* __restr
 __global__ __launch_bounds__(kThreads) void k_radix_scatter(const uint64_t* __restrict__ kin,
                                                             uint64_t* __restrict__ kout, uint32_t n, int shift,
                                                             const uint32_t* __restrict__ hist_scan,
-                                                            uint32_t ntiles) {
+                                                            const uint32_t* __restrict__ tot, uint32_t ntiles) {
+  static_assert(kBins == 4 * kThreads, "four digits a thread in the digit prefix");
   __shared__ uint32_t wcnt[kThreads / 64][kBins];
   __shared__ uint32_t gbase[kBins];
+  __shared__ uint32_t wsum[kThreads / 64];
   const int wave = threadIdx.x >> 6, lane = __lane_id();
   for (int i = threadIdx.x; i < (kThreads / 64) * kBins; i += kThreads) (&wcnt[0][0])[i] = 0;
-  for (int d = threadIdx.x; d < kBins; d += kThreads) gbase[d] = hist_scan[d * ntiles + blockIdx.x];
+  {
+    // digit d's first slot: the totals of the digits below d (exclusive
+    // prefix over the workgroup, four consecutive digits a thread) plus the
+    // counts of d in the tiles before this one
+    const int d0 = 4 * threadIdx.x;
+    uint32_t v[4], sum = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v[u] = tot[d0 + u];
+      sum += v[u];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    uint32_t run = incl - sum;
+    for (int w = 0; w < wave; ++w) run += wsum[w];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      gbase[d0 + u] = run + hist_scan[(uint64_t)(d0 + u) * ntiles + blockIdx.x];
+      run += v[u];
+    }
+  }
   __syncthreads();
 
   const uint32_t base = blockIdx.x * kTile + wave * (kTile / (kThreads / 64));
@@ -460,10 +526,13 @@ constexpr uint64_t kRunSearchMinCells = 1ull << 22;
 // kUnitParticles particles of a cell with two or more, starting at a
 // multiple of kUnitParticles in the cell), 0 for the other particles of such
 // a cell, -1 for a particle alone in its cell; the unit-start flag is 1
-// where unit_len > 0.  Flags go to flags64 (block flag in the low half, unit
-// flag in the high half) when both are made, else to flags32.  The cell's
-// first position comes from bin_offsets or, with bo null, from the sorted
-// keys.
+// where unit_len > 0.  When both are made they go to flags64 as masks, per
+// wave of 64 sorted positions w: flags64[2w] the block starts, flags64[2w + 1]
+// the unit starts (bit l: position 64w + l), and flags64[2 nw + w] their
+// counts (blocks in the low half, units in the high half; nw = the number of
+// waves), which one scan of nw words turns into each wave's first block row
+// and unit slot; else one flag per position to flags32.  The cell's first
+// position comes from bin_offsets or, with bo null, from the sorted keys.
 template <bool BLOCKS, bool UNITS>
 __device__ __forceinline__ void permutation_block(const uint64_t* __restrict__ kv, uint32_t n, uint32_t N,
                                                   int32_t* __restrict__ perm, const int32_t* __restrict__ bo,
@@ -496,8 +565,20 @@ __device__ __forceinline__ void permutation_block(const uint64_t* __restrict__ k
       }
       unit_len[k] = ul;
     }
-    if constexpr (BLOCKS && UNITS) flags64[k] = (uint64_t)bf | ((uint64_t)uf << 32);
-    else flags32[k] = BLOCKS ? bf : uf;
+    if constexpr (BLOCKS && UNITS) {
+      // k runs over 64 consecutive positions a wave (kThreads is a multiple
+      // of 64): its lane 0 holds the wave's first position, which is below n
+      // whenever any lane of the wave is
+      const uint64_t bm = __ballot(bf != 0u), um = __ballot(uf != 0u);
+      if (__lane_id() == 0) {
+        const uint32_t w = k >> 6, nw = (n + 63) >> 6;
+        flags64[2 * (uint64_t)w] = bm;
+        flags64[2 * (uint64_t)w + 1] = um;
+        flags64[2 * (uint64_t)nw + w] = (uint64_t)__popcll(bm) | ((uint64_t)__popcll(um) << 32);
+      }
+    } else {
+      flags32[k] = BLOCKS ? bf : uf;
+    }
   }
 }
 
@@ -540,14 +621,16 @@ __global__ __launch_bounds__(kThreads) void k_offsets_permutation(
 // starts a block when rowidx[i + 1] > rowidx[i], the scan having counted its
 // flag), zero rows r in [total, max_blocks) (thread i handles position i and
 // row i), and the block count into total_out.  Cell bounds as in
-// k_permutation.  With UNITS the scan is the two-count one of k_permutation
-// (rowidx the low halves, unit slots the high halves, n + 1 words with the
-// totals last): the fill's units are written too, units[slot] = {k,
+// k_permutation.  With UNITS the flags are k_permutation's masks (`masks`,
+// 2 nw words) and the scan its per-wave counts (`scan64`, nw + 1 words, the
+// totals last; a position's row and slot are its wave's plus the starts
+// below it in the wave): the fill's units are written too, units[slot] = {k,
 // unit_len[k]}, and their number into unit_total.
 template <bool UNITS>
 __global__ __launch_bounds__(kThreads) void k_block_rows(const uint64_t* __restrict__ kv, uint32_t n,
                                                          const int32_t* __restrict__ bo,
                                                          const uint32_t* __restrict__ rowidx32,
+                                                         const uint64_t* __restrict__ masks,
                                                          const uint64_t* __restrict__ scan64, uint32_t maxp,
                                                          uint32_t G, int4* __restrict__ info,
                                                          const uint32_t* __restrict__ total32, uint64_t max_blocks,
@@ -555,26 +638,28 @@ __global__ __launch_bounds__(kThreads) void k_block_rows(const uint64_t* __restr
                                                          const int32_t* __restrict__ unit_len,
                                                          uint2* __restrict__ units, int32_t* __restrict__ unit_total) {
   const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  const uint32_t t = UNITS ? (uint32_t)scan64[n] : *total32;
+  const uint32_t nw = (n + 63) >> 6;
+  const uint32_t t = UNITS ? (uint32_t)scan64[nw] : *total32;
   if (i == 0) {
     if (total_out) *total_out = (int32_t)t;
-    if constexpr (UNITS) *unit_total = (int32_t)(scan64[n] >> 32);
+    if constexpr (UNITS) *unit_total = (int32_t)(scan64[nw] >> 32);
   }
   if (i < max_blocks && i >= t) info[i] = make_int4(0, 0, 0, 0);
   if (i >= n) return;
   const uint32_t k = (uint32_t)i;
-  uint32_t row, next;
+  uint32_t row;
   if constexpr (UNITS) {
-    const uint64_t sk = scan64[k];
-    const int32_t ul = unit_len[k];
-    if (ul > 0) units[(uint32_t)(sk >> 32)] = make_uint2(k, (uint32_t)ul);
-    row = (uint32_t)sk;
-    next = (uint32_t)scan64[k + 1];
+    const uint32_t w = k >> 6;
+    const uint64_t below = (1ull << (k & 63u)) - 1ull;
+    const uint64_t bm = masks[2 * (uint64_t)w], um = masks[2 * (uint64_t)w + 1], sk = scan64[w];
+    if ((um >> (k & 63u)) & 1ull)
+      units[(uint32_t)(sk >> 32) + (uint32_t)__popcll(um & below)] = make_uint2(k, (uint32_t)unit_len[k]);
+    if (((bm >> (k & 63u)) & 1ull) == 0ull) return;  // not a block start
+    row = (uint32_t)sk + (uint32_t)__popcll(bm & below);
   } else {
     row = rowidx32[k];
-    next = rowidx32[k + 1];
+    if (rowidx32[k + 1] == row) return;  // not a block start
   }
-  if (next == row) return;  // not a block start
   const uint32_t key = kv_key(kv[k]);
   const uint32_t rs = bo != nullptr ? (uint32_t)bo[key] : run_start(kv, k, key);
   const uint32_t re = bo != nullptr ? (uint32_t)bo[key + 1] : run_end(kv, n, k, key);
@@ -940,14 +1025,17 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   while (bits < 32 && (g.n_cells - 1) >> bits) ++bits;
   const int passes = (bits + kRadixBits - 1) / kRadixBits;
   const uint32_t ntiles = (uint32_t)g.n_tiles;
+  uint32_t* digit_totals = g.hist + (uint64_t)kBins * ntiles;  // the histograms' last kBins words
   int cur = 0;
   for (int p = 0; p < passes; ++p) {
     const int shift = p * kRadixBits;
     hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kThreads), 0, st, g.kv[cur], n, shift, g.hist, ntiles);
     SPHOPS_LAUNCHED();
-    device_exclusive_scan(g.hist, g.hist, (uint64_t)kBins * ntiles, g.scan_tmp, nullptr, st);
+    hipLaunchKernelGGL(k_radix_colscan, dim3(kBins / (kThreads / 64)), dim3(kThreads), 0, st, g.hist, ntiles,
+                       digit_totals);
+    SPHOPS_LAUNCHED();
     hipLaunchKernelGGL(k_radix_scatter, dim3(ntiles), dim3(kThreads), 0, st, g.kv[cur], g.kv[cur ^ 1], n, shift,
-                       g.hist, ntiles);
+                       g.hist, digit_totals, ntiles);
     SPHOPS_LAUNCHED();
     cur ^= 1;
   }
@@ -966,8 +1054,11 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   // the bin_offsets launch
   const int32_t* cell_bo = g.n_cells >= kRunSearchMinCells ? nullptr : bo;
   const bool units = g.unit_len != nullptr && g.units != nullptr && g.unit_total != nullptr;
-  const bool dual = units && !g.particle_mode && dual_scan_fits(g, n);
-  uint64_t* f64 = g.kv[cur ^ 1];  // free after the sort; n + 1 words
+  // the masks of the block and unit starts and their per-wave counts take
+  // 3 nw + 1 words of the other sort buffer (n + 1 words, free after the sort)
+  const uint32_t nw = (n + 63) / 64;
+  const bool dual = units && !g.particle_mode && n >= 64 && dual_scan_fits(g, nw);
+  uint64_t* f64 = g.kv[cur ^ 1];
   const uint32_t nb_perm = blocks_for(n).x;
   if (cell_bo != nullptr) {
     hipLaunchKernelGGL(k_bin_offsets, dim3(nb_bo), dim3(kThreads), 0, st, skv, g.chunk_lo, nch, bo, ncp1);
@@ -1001,13 +1092,15 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   if (!g.particle_mode) {
     const dim3 rows_grid = blocks_for(std::max<uint64_t>(n, g.max_blocks));
     if (dual) {
-      device_exclusive_scan64(f64, f64, n, g.scan_tmp, f64 + n, st);
-      hipLaunchKernelGGL(k_block_rows<true>, rows_grid, dim3(kThreads), 0, st, skv, n, cell_bo, nullptr, f64,
+      uint64_t* counts = f64 + 2 * (uint64_t)nw;
+      device_exclusive_scan64(counts, counts, nw, g.scan_tmp, counts + nw, st);
+      hipLaunchKernelGGL(k_block_rows<true>, rows_grid, dim3(kThreads), 0, st, skv, n, cell_bo, nullptr, f64, counts,
                          g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), nullptr, g.max_blocks, total_blocks,
                          g.unit_len, g.units, g.unit_total);
     } else {
       device_exclusive_scan(g.flags, g.flags, n, g.scan_tmp, g.flags + n, st);
       hipLaunchKernelGGL(k_block_rows<false>, rows_grid, dim3(kThreads), 0, st, skv, n, cell_bo, g.flags, nullptr,
+                         nullptr,
                          g.p.maxp, g.p.G, reinterpret_cast<int4*>(block_info), g.flags + n, g.max_blocks,
                          total_blocks, nullptr, nullptr, nullptr);
     }

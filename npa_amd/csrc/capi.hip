@@ -265,7 +265,7 @@ int sphops_grid_create(int dim, int boundary, int mode, const int32_t* grid_size
       for (int i = 0; i < 2; ++i) {
         g->kv[i] = dalloc<uint64_t>(BN + 1);
       }
-      g->hist = dalloc<uint32_t>((uint64_t)sphops::kRadixBins * g->n_tiles);
+      g->hist = dalloc<uint32_t>(sphops::hist_words(*g));
       g->scan_tmp_len = sphops::scan_tmp_elems(sphops::scan_words(*g));
       g->scan_tmp = dalloc<uint32_t>(g->scan_tmp_len);
       g->chunk_lo = dalloc<uint32_t>(g->n_chunks + 1);
@@ -1040,7 +1040,7 @@ constexpr NoAllocLayout noalloc_layout(uint64_t n_keys, uint64_t n_tiles, uint64
     at += pad_words(2 * (n_keys + 1));
   }
   l.hist = at;
-  at += pad_words((uint64_t)sphops::kRadixBins * n_tiles);
+  at += pad_words(sphops::hist_words(n_tiles));
   l.flags = at;
   at += pad_words(n_keys + 1);
   l.chunk_lo = at;

@@ -287,5 +287,9 @@ void run_relu_linear_input_grad(const float* dy, const float* w, const float* h,
 
 constexpr uint32_t kMaxChannels = 64;
 constexpr int kRadixBins = 1024;  // digit values per radix-sort pass (10 bits)
+// Words of the radix histograms: kRadixBins tile counts per tile of 4096
+// keys, then the kRadixBins digit totals.
+constexpr uint64_t hist_words(uint64_t n_tiles) { return (uint64_t)kRadixBins * (n_tiles + 1); }
+inline uint64_t hist_words(const Grid& g) { return hist_words(g.n_tiles); }
 
 }  // namespace sphops
