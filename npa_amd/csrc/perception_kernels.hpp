@@ -2070,11 +2070,18 @@ __device__ __forceinline__ void lone_rows(const GridParams& g, const float4* __r
   }
 }
 
-// The list fill: a persistent grid whose waves take the units u = wave,
-// wave + (waves in the grid), ... (units[u] = {first particle, particles})
-// and the chunks of 64 particles c = wave, wave + (waves in the grid), ...
-// (k0 = 64 c).  Even waves take their chunks first, odd waves their units
-// first, so that the memory-bound lone walks overlap the ALU-bound units.
+// The list fill: a persistent grid whose waves take the chunks of 64
+// particles c = wave, wave + (waves in the grid), ... (k0 = 64 c) and the
+// units (units[u] = {first particle, particles}) from kFillStripes queues:
+// queue q holds the units u = q, q + kFillStripes, ... (a sample of the whole
+// cloud, so the queues carry about equal work), its counter at word
+// kUnitQueueWord of stripe q, and the waves w = q mod kFillStripes take its
+// units one at a time until it is empty.  A unit's cost runs from one round
+// to dozens (crowded cells sit together), so a fixed share per wave leaves
+// the waves that drew crowded cells running long after the others.  Even
+// waves take their chunks first, odd waves their units first, so that the
+// memory-bound lone walks overlap the ALU-bound units.  Which wave writes a
+// row changes only where the row lands in the index buffer.
 template <int D, bool P, int R, bool OT>
 __device__ __forceinline__ void fill_items(const GridParams& g, const float4* __restrict__ xw,
                                            const int32_t* __restrict__ bo, const int32_t* __restrict__ unit_len,
@@ -2092,8 +2099,15 @@ __device__ __forceinline__ void fill_items(const GridParams& g, const float4* __
       for (uint32_t c = wave; c < nchunks; c += nwaves)
         lone_rows<D, P, R, OT>(g, xw, bo, unit_len, c * kWave, wave, hits, nidx, nstart, ncnt, fs, ft);
     } else {
-      for (uint32_t u = wave; u < nunits; u += nwaves) {
-        const uint2 ud = units[u];
+      const uint32_t q = wave & (kFillStripes - 1u);
+      const uint32_t in_queue = q < nunits ? (nunits - q + kFillStripes - 1u) / kFillStripes : 0u;
+      unsigned long long* __restrict__ next = fs.ctr + (uint64_t)q * kStripeWords + kUnitQueueWord;
+      for (;;) {
+        uint32_t i = 0;
+        if (__lane_id() == 0) i = (uint32_t)atomicAdd(next, 1ull);
+        i = (uint32_t)__builtin_amdgcn_readfirstlane((int)__shfl((int)i, 0, kWave));
+        if (i >= in_queue) break;
+        const uint2 ud = units[i * kFillStripes + q];
         unit_rows<D, P, R, OT>(g, xw, bo, __builtin_amdgcn_readfirstlane(ud.x),
                                __builtin_amdgcn_readfirstlane(ud.y), wave, hits, nidx, nstart, ncnt, fs, ft);
       }
@@ -2120,7 +2134,8 @@ __global__ __launch_bounds__(kThreads) void k_fill(GridParams g, const float4* _
 
 // total[0] = in-radius pairs (blocks written or not), total[1] = pairs of
 // the blocks not written, from the counters' words (see FillStripes); the
-// counters are then reset to zero for the next fill.  One workgroup of
+// counters, and the unit queues of all kFillStripes stripes, are then reset
+// to zero for the next fill.  One workgroup of
 // kThreads >= kFillStripes.
 static_assert(kThreads >= kFillStripes, "k_fill_totals reads one counter per thread");
 [[maybe_unused]] static __global__ __launch_bounds__(kThreads) void k_fill_totals(unsigned long long* __restrict__ ctr,
@@ -2135,6 +2150,7 @@ static_assert(kThreads >= kFillStripes, "k_fill_totals reads one counter per thr
     o = c[2];
     c[0] = c[1] = c[2] = 0ull;
   }
+  if (s < kFillStripes) ctr[(uint64_t)s * kStripeWords + kUnitQueueWord] = 0ull;  // the fill's unit queues
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {
     a += __shfl_down(a, off, kWave);
@@ -2188,6 +2204,7 @@ void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
 constexpr uint32_t kPersistentWorkgroups = 2048;
 // Workgroups of the list fill (timed at cfg5: 4096 beats 2048, 3072 and 6144).
 constexpr uint32_t kFillWorkgroups = 4096;
+static_assert(kFillWorkgroups * (kThreads / kWave) >= kFillStripes, "every unit queue of the fill has a wave");
 
 // Work split of the list fill (unit table and lone marks, in the grid's
 // scratch), read by neighbour_fill.

@@ -210,6 +210,10 @@ constexpr int32_t kUnitParticles = 8;
 // apart (256 bytes).
 constexpr uint32_t kFillStripes = 256;
 constexpr uint32_t kStripeWords = 32;
+// word of a stripe's 256-byte record that counts the units taken from the
+// list fill's unit queue of that stripe (a cache line apart from the row
+// counters at words 0-2)
+constexpr uint32_t kUnitQueueWord = 16;
 constexpr int64_t kStripeMinEntries = (int64_t)1 << 15;
 constexpr uint64_t kStripeMinUnits = 64;
 // Work classes of the list traversal: class q holds
