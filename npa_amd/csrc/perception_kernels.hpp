@@ -2202,7 +2202,8 @@ void pack_for(const Grid& g, OpPtrs& a, hipStream_t st) {
 }
 
 constexpr uint32_t kPersistentWorkgroups = 2048;
-// Workgroups of the list fill (timed at cfg5: 4096 beats 2048, 3072 and 6144).
+// Workgroups of the list fill (timed at cfg5, with the unit queues too: 4096
+// beats 2048, 3072, 6144 and 8192).
 constexpr uint32_t kFillWorkgroups = 4096;
 static_assert(kFillWorkgroups * (kThreads / kWave) >= kFillStripes, "every unit queue of the fill has a wave");
 
