@@ -1048,9 +1048,10 @@ __device__ __forceinline__ uint32_t wave_limit(uint32_t host, const int32_t* dev
 }
 
 // The schedule's waves are served in rounds of (at most) the launched waves:
-// this wave's first index, with the XCD-contiguous block mapping taken over
-// the workgroups the round needs, so that a launch larger than the schedule
-// still spreads its live waves over all eight XCDs; and the round's stride.
+// this wave's first index, with the XCD mapping in chunks (xcd_block_id_chunked)
+// taken over the workgroups the round needs, so that a launch larger than the
+// schedule still spreads its live waves over all eight XCDs, and every XCD
+// serves a share of every region of space; and the round's stride.
 // Any launch (a multiple of eight workgroups) serves every live wave, so the
 // launch can be sized from an estimate and the count read on the device.
 __device__ __forceinline__ uint32_t schedule_blocks(uint32_t live) {
@@ -1059,7 +1060,7 @@ __device__ __forceinline__ uint32_t schedule_blocks(uint32_t live) {
 }
 __device__ __forceinline__ uint32_t schedule_wave(uint32_t live) {
   const uint32_t per = kThreads / kWave;
-  const uint32_t b = xcd_block_id(schedule_blocks(live));
+  const uint32_t b = xcd_block_id_chunked(schedule_blocks(live));
   return b == 0xFFFFFFFFu ? b : b * per + (threadIdx.x >> 6);
 }
 __device__ __forceinline__ uint32_t schedule_stride(uint32_t live) {

@@ -203,6 +203,25 @@ __device__ __forceinline__ uint32_t xcd_block_id(uint32_t nb_live) {
   return k < q + (xcd < rem ? 1u : 0u) ? xcd * q + min(xcd, rem) + k : 0xFFFFFFFFu;
 }
 
+// The first nb_live logical ids dealt to the eight XCDs in chunks of
+// kXcdChunk consecutive ids, the XCDs taking turns chunk by chunk: a chunk
+// keeps neighbouring ids (neighbouring space) on one XCD's L2, and the turns
+// give every XCD a share of every part of the id range, so that no XCD draws
+// only the costly ones (contiguous eighths leave the XCDs that get the sparse
+// regions idle for up to half the launch).  Workgroup x runs on XCD x mod 8
+// and is its XCD's (x / 8)-th; a launch of at least 8 * ceil(nb_live / 8)
+// workgroups covers every id, the workgroups past them get UINT32_MAX.
+constexpr uint32_t kXcdChunk = 64;
+__device__ __forceinline__ uint32_t xcd_block_id_chunked(uint32_t nb_live) {
+  const uint32_t x = blockIdx.x, xcd = x & 7u, k = x >> 3;
+  const uint32_t per_xcd = (nb_live + 7u) >> 3;
+  if (k >= per_xcd) return 0xFFFFFFFFu;
+  const uint32_t whole = per_xcd / kXcdChunk * kXcdChunk;  // ids of each XCD in whole chunks
+  const uint32_t id = k < whole ? ((k / kXcdChunk) * 8u + xcd) * kXcdChunk + k % kXcdChunk
+                                : 8u * whole + xcd * (per_xcd - whole) + (k - whole);
+  return id < nb_live ? id : 0xFFFFFFFFu;
+}
+
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 }  // namespace sphops
