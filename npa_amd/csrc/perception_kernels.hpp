@@ -937,7 +937,10 @@ __device__ __forceinline__ void unpack(const float4 v, float* p) {
 template <int D, bool P, int TRAV, class OP>
 __global__ __launch_bounds__(kThreads) void k_pairs(GridParams g, const int32_t* __restrict__ bo, OpPtrs a) {
   const uint32_t n = g.B * g.N;
-  const uint32_t k = xcd_block_id() * kThreads + threadIdx.x;
+  // particles dealt to the XCDs in chunks (xcd_block_id_chunked), as the
+  // schedules are: contiguous eighths would give some XCDs only sparse regions
+  const uint32_t b = xcd_block_id_chunked((n + kThreads - 1) / kThreads);
+  const uint32_t k = b == 0xFFFFFFFFu ? n : b * kThreads + threadIdx.x;
   const bool active = k < n;
   const float4* __restrict__ xw = a.xw;
   OP op;
@@ -2184,6 +2187,9 @@ namespace sphops {
 namespace pk {
 
 inline dim3 grid_for(uint64_t n) { return dim3((uint32_t)((n + kThreads - 1) / kThreads)); }
+// One workgroup per kThreads items, rounded up to a multiple of the eight
+// XCDs (what xcd_block_id_chunked needs to cover every item).
+inline dim3 grid_for_xcds(uint64_t n) { return dim3((uint32_t)(((n + kThreads - 1) / kThreads + 7) / 8 * 8)); }
 
 // The (x, weight) records the pair kernels read: packed into the caller's
 // buffer (or the grid's scratch), or the caller's buffer as it is when it
@@ -2289,11 +2295,11 @@ void launch_pairs(const Grid& g, const int32_t* bo, OpPtrs a, hipStream_t st) {
     if (wgs == 0) return;
     hipLaunchKernelGGL((k_pairs_grouped<D, P, OP>), dim3(wgs), dim3(kThreads), 0, st, g.p, a);
   } else if (a.nidx != nullptr) {
-    hipLaunchKernelGGL((k_pairs<D, P, kList, OP>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, a);
+    hipLaunchKernelGGL((k_pairs<D, P, kList, OP>), grid_for_xcds(n), dim3(kThreads), 0, st, g.p, bo, a);
   } else if (OP::kChannels) {
-    hipLaunchKernelGGL((k_pairs<D, P, kStencil2, OP>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, a);
+    hipLaunchKernelGGL((k_pairs<D, P, kStencil2, OP>), grid_for_xcds(n), dim3(kThreads), 0, st, g.p, bo, a);
   } else {
-    hipLaunchKernelGGL((k_pairs<D, P, kStencil, OP>), grid_for(n), dim3(kThreads), 0, st, g.p, bo, a);
+    hipLaunchKernelGGL((k_pairs<D, P, kStencil, OP>), grid_for_xcds(n), dim3(kThreads), 0, st, g.p, bo, a);
   }
   SPHOPS_LAUNCHED();
 }
