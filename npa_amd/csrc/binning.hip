@@ -35,17 +35,38 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 __device__ __forceinline__ uint32_t kv_key(uint64_t v) { return (uint32_t)(v >> 32); }
 __device__ __forceinline__ uint32_t kv_val(uint64_t v) { return (uint32_t)v; }
 
+// Keys of the kTile particles of radix tile blockIdx.x, and the tile's counts
+// of the first radix digit (the low kRadixBits of the key), laid out as
+// k_radix_hist writes them: the sort's first pass then needs no pass of its
+// own over the keys to count them.
+// One workgroup of kKeyThreads a tile: a tile's worth of position loads in
+// flight takes more waves than the sort's tile kernels have.
+constexpr int kKeyThreads = 1024;
+constexpr int kKeyItems = kTile / kKeyThreads;
+static_assert(kKeyItems * kKeyThreads == kTile, "a key workgroup covers one radix tile");
 template <int D, bool PERIODIC>
-__global__ __launch_bounds__(kThreads) void k_cell_keys(GridParams g, const float* __restrict__ pos,
-                                                        uint64_t* __restrict__ kv, uint32_t n) {
-  const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
-  if (k >= n) return;
-  float x[3];
-  load_pos<D>(pos, k, x);
-  int c[3];
-  pos2cell<D, PERIODIC>(g, x, c);
-  const uint32_t b = k / g.N;
-  kv[k] = ((uint64_t)(b * g.G + cell_hash<D>(g, c)) << 32) | k;
+__global__ __launch_bounds__(kKeyThreads) void k_cell_keys(GridParams g, const float* __restrict__ pos,
+                                                           uint64_t* __restrict__ kv, uint32_t n,
+                                                           uint32_t* __restrict__ hist, uint32_t ntiles) {
+  __shared__ uint32_t h[kBins];
+  for (int d = threadIdx.x; d < kBins; d += kKeyThreads) h[d] = 0;
+  __syncthreads();
+  const uint32_t base = blockIdx.x * kTile;
+#pragma unroll
+  for (int i = 0; i < kKeyItems; ++i) {
+    const uint32_t k = base + i * kKeyThreads + threadIdx.x;
+    if (k < n) {
+      float x[3];
+      load_pos<D>(pos, k, x);
+      int c[3];
+      pos2cell<D, PERIODIC>(g, x, c);
+      const uint32_t key = (k / g.N) * g.G + cell_hash<D>(g, c);
+      kv[k] = ((uint64_t)key << 32) | k;
+      atomicAdd(&h[key & (kBins - 1)], 1u);
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < kBins; d += kKeyThreads) hist[d * ntiles + blockIdx.x] = h[d];
 }
 
 // ------------------------------------------------------- device-wide scan
@@ -711,11 +732,13 @@ __global__ __launch_bounds__(kThreads) void k_move_rows(const float* __restrict_
 
 template <int D>
 void launch_keys(const Grid& g, const float* pos, uint32_t n, hipStream_t st) {
-  const dim3 grid((n + kThreads - 1) / kThreads);
+  const uint32_t ntiles = (uint32_t)g.n_tiles;
   if (g.periodic)
-    hipLaunchKernelGGL((k_cell_keys<D, true>), grid, dim3(kThreads), 0, st, g.p, pos, g.kv[0], n);
+    hipLaunchKernelGGL((k_cell_keys<D, true>), dim3(ntiles), dim3(kKeyThreads), 0, st, g.p, pos, g.kv[0], n, g.hist,
+                       ntiles);
   else
-    hipLaunchKernelGGL((k_cell_keys<D, false>), grid, dim3(kThreads), 0, st, g.p, pos, g.kv[0], n);
+    hipLaunchKernelGGL((k_cell_keys<D, false>), dim3(ntiles), dim3(kKeyThreads), 0, st, g.p, pos, g.kv[0], n, g.hist,
+                       ntiles);
   SPHOPS_LAUNCHED();
 }
 
@@ -1017,7 +1040,8 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
     if (total_blocks) fill_u32(reinterpret_cast<uint32_t*>(total_blocks), 1, 0u, st);
     return;
   }
-  // 1. keys
+  // 1. keys, with the first pass's digit counts
+  if ((uint64_t)n > g.n_tiles * kTile) throw Error("instantiate: more keys than radix tiles");
   if (g.dim == 2) launch_keys<2>(g, pos, n, st);
   else launch_keys<3>(g, pos, n, st);
 
@@ -1030,8 +1054,10 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   int cur = 0;
   for (int p = 0; p < passes; ++p) {
     const int shift = p * kRadixBits;
-    hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kThreads), 0, st, g.kv[cur], n, shift, g.hist, ntiles);
-    SPHOPS_LAUNCHED();
+    if (p > 0) {  // the first pass's counts come from k_cell_keys
+      hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kThreads), 0, st, g.kv[cur], n, shift, g.hist, ntiles);
+      SPHOPS_LAUNCHED();
+    }
     hipLaunchKernelGGL(k_radix_colscan, dim3(kBins / (kThreads / 64)), dim3(kThreads), 0, st, g.hist, ntiles,
                        digit_totals);
     SPHOPS_LAUNCHED();
