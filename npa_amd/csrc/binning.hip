@@ -1,6 +1,7 @@
 // Spatial-hash binning for gfx950: cell keys, a stable LSD radix sort (per
-// pass: tile histograms, a per-digit scan over the tiles, a ballot-ranked
-// scatter), bin_offsets from sorted run heads, the grid-mode block table, the
+// pass: tile histograms, the first pass's counted with the keys, a per-digit
+// scan over the tiles, a ballot-ranked scatter), bin_offsets from sorted run
+// heads, the grid-mode block table, the
 // permutation and its inverse, and the bin/unbin row moves.
 //
 // Replaces the reference's atomic counting sort (sphops/sph_cuda.cu:32-206,
