@@ -36,26 +36,28 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 __device__ __forceinline__ uint32_t kv_key(uint64_t v) { return (uint32_t)(v >> 32); }
 __device__ __forceinline__ uint32_t kv_val(uint64_t v) { return (uint32_t)v; }
 
+// The tile-counting kernels (keys, radix and class histograms) run one
+// workgroup of kCountThreads per tile: a tile's loads in flight need more
+// waves than one 256-thread workgroup per CU has.
+constexpr int kCountThreads = 1024;
+constexpr int kCountItems = kTile / kCountThreads;
+static_assert(kCountItems * kCountThreads == kTile, "a counting workgroup covers one tile");
+
 // Keys of the kTile particles of radix tile blockIdx.x, and the tile's counts
 // of the first radix digit (the low kRadixBits of the key), laid out as
 // k_radix_hist writes them: the sort's first pass then needs no pass of its
 // own over the keys to count them.
-// One workgroup of kKeyThreads a tile: a tile's worth of position loads in
-// flight takes more waves than the sort's tile kernels have.
-constexpr int kKeyThreads = 1024;
-constexpr int kKeyItems = kTile / kKeyThreads;
-static_assert(kKeyItems * kKeyThreads == kTile, "a key workgroup covers one radix tile");
 template <int D, bool PERIODIC>
-__global__ __launch_bounds__(kKeyThreads) void k_cell_keys(GridParams g, const float* __restrict__ pos,
+__global__ __launch_bounds__(kCountThreads) void k_cell_keys(GridParams g, const float* __restrict__ pos,
                                                            uint64_t* __restrict__ kv, uint32_t n,
                                                            uint32_t* __restrict__ hist, uint32_t ntiles) {
   __shared__ uint32_t h[kBins];
-  for (int d = threadIdx.x; d < kBins; d += kKeyThreads) h[d] = 0;
+  for (int d = threadIdx.x; d < kBins; d += kCountThreads) h[d] = 0;
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile;
 #pragma unroll
-  for (int i = 0; i < kKeyItems; ++i) {
-    const uint32_t k = base + i * kKeyThreads + threadIdx.x;
+  for (int i = 0; i < kCountItems; ++i) {
+    const uint32_t k = base + i * kCountThreads + threadIdx.x;
     if (k < n) {
       float x[3];
       load_pos<D>(pos, k, x);
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(kKeyThreads) void k_cell_keys(GridParams g, const f
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < kBins; d += kKeyThreads) hist[d * ntiles + blockIdx.x] = h[d];
+  for (int d = threadIdx.x; d < kBins; d += kCountThreads) hist[d * ntiles + blockIdx.x] = h[d];
 }
 
 // ------------------------------------------------------- device-wide scan
@@ -238,19 +240,20 @@ void device_exclusive_scan64(const uint64_t* in, uint64_t* out, uint64_t n, uint
 
 // ------------------------------------------------------------ radix sort
 
-__global__ __launch_bounds__(kThreads) void k_radix_hist(const uint64_t* __restrict__ kv, uint32_t n, int shift,
-                                                         uint32_t* __restrict__ hist, uint32_t ntiles) {
+__global__ __launch_bounds__(kCountThreads) void k_radix_hist(const uint64_t* __restrict__ kv, uint32_t n,
+                                                              int shift, uint32_t* __restrict__ hist,
+                                                              uint32_t ntiles) {
   __shared__ uint32_t h[kBins];
-  for (int d = threadIdx.x; d < kBins; d += kThreads) h[d] = 0;
+  for (int d = threadIdx.x; d < kBins; d += kCountThreads) h[d] = 0;
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile;
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const uint32_t idx = base + i * kThreads + threadIdx.x;
+  for (int i = 0; i < kCountItems; ++i) {
+    const uint32_t idx = base + i * kCountThreads + threadIdx.x;
     if (idx < n) atomicAdd(&h[(kv_key(kv[idx]) >> shift) & (kBins - 1)], 1u);
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < kBins; d += kThreads) hist[d * ntiles + blockIdx.x] = h[d];
+  for (int d = threadIdx.x; d < kBins; d += kCountThreads) hist[d * ntiles + blockIdx.x] = h[d];
 }
 
 // Per digit d (a wave each, four digits a workgroup): the tile counts
@@ -735,10 +738,10 @@ template <int D>
 void launch_keys(const Grid& g, const float* pos, uint32_t n, hipStream_t st) {
   const uint32_t ntiles = (uint32_t)g.n_tiles;
   if (g.periodic)
-    hipLaunchKernelGGL((k_cell_keys<D, true>), dim3(ntiles), dim3(kKeyThreads), 0, st, g.p, pos, g.kv[0], n, g.hist,
+    hipLaunchKernelGGL((k_cell_keys<D, true>), dim3(ntiles), dim3(kCountThreads), 0, st, g.p, pos, g.kv[0], n, g.hist,
                        ntiles);
   else
-    hipLaunchKernelGGL((k_cell_keys<D, false>), dim3(ntiles), dim3(kKeyThreads), 0, st, g.p, pos, g.kv[0], n, g.hist,
+    hipLaunchKernelGGL((k_cell_keys<D, false>), dim3(ntiles), dim3(kCountThreads), 0, st, g.p, pos, g.kv[0], n, g.hist,
                        ntiles);
   SPHOPS_LAUNCHED();
 }
@@ -805,16 +808,16 @@ __device__ __forceinline__ int32_t item_length(const int32_t* __restrict__ src, 
 // cnt[tile * kNumClasses + class].
 // Items of negative length are skipped: they get no class and no slot.
 template <bool CSR>
-__global__ __launch_bounds__(kThreads) void k_class_count(const int32_t* __restrict__ src, uint32_t n,
-                                                          ClassBounds cb, uint32_t* __restrict__ cnt) {
+__global__ __launch_bounds__(kCountThreads) void k_class_count(const int32_t* __restrict__ src, uint32_t n,
+                                                               ClassBounds cb, uint32_t* __restrict__ cnt) {
   __shared__ uint32_t h[kNumClasses];
   if (threadIdx.x < kNumClasses) h[threadIdx.x] = 0;
   __syncthreads();
   const uint32_t base = blockIdx.x * kTile;
   uint32_t c[kNumClasses] = {};
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const uint32_t idx = base + i * kThreads + threadIdx.x;
+  for (int i = 0; i < kCountItems; ++i) {
+    const uint32_t idx = base + i * kCountThreads + threadIdx.x;
     const int32_t len = idx < n ? item_length<CSR>(src, idx) : -1;
     if (len >= 0) {
       const uint32_t k = length_class(len, cb);
@@ -977,7 +980,7 @@ void tiled_schedule(const Grid& g, const int32_t* src, const ClassBounds& cb, co
   // offsets (nseg + 1, the last is the number of scheduled items)
   uint32_t* cnt = g.hist;
   uint32_t* seg = cnt + nseg;
-  hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kThreads), 0, st, src, n, cb, cnt);
+  hipLaunchKernelGGL((k_class_count<CSR>), dim3(ntiles), dim3(kCountThreads), 0, st, src, n, cb, cnt);
   SPHOPS_LAUNCHED();
   const int tables = waves2 != nullptr ? 2 : 1;  // a second table: same order, other group sizes
   const GroupSizes gsb = gs2 != nullptr ? *gs2 : gs;
@@ -1056,7 +1059,8 @@ void run_instantiate(Grid& g, const float* pos, int32_t* perm, int32_t* bo, int3
   for (int p = 0; p < passes; ++p) {
     const int shift = p * kRadixBits;
     if (p > 0) {  // the first pass's counts come from k_cell_keys
-      hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kThreads), 0, st, g.kv[cur], n, shift, g.hist, ntiles);
+      hipLaunchKernelGGL(k_radix_hist, dim3(ntiles), dim3(kCountThreads), 0, st, g.kv[cur], n, shift, g.hist,
+                         ntiles);
       SPHOPS_LAUNCHED();
     }
     hipLaunchKernelGGL(k_radix_colscan, dim3(kBins / (kThreads / 64)), dim3(kThreads), 0, st, g.hist, ntiles,
